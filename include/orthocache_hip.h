@@ -1,0 +1,204 @@
+/*
+ * orthocache_hip.h -- C ABI of liborthocache_hip.so, the MI355X (gfx950)
+ * implementation of OrthoCache's spectral-gated decode attention.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * returns an int status (OC_OK = 0) and never lets a C++ exception or a
+ * host allocation cross the boundary.  Work is enqueued on the hipStream_t
+ * passed in (`stream`, NULL = the default stream); nothing synchronises.
+ * oc_last_error() returns a thread-local message for the last failure.
+ *
+ * Reference interfaces replaced (paths relative to
+ * src/orthocache_gpu/triton_kernels/ of the reference tree):
+ *   oc_score_tiles  <- _fwht_eviction_kernel launch of triton_fwht_eviction
+ *                      (fwht_fused_prototype.py:255-322, launch :305-318)
+ *   oc_fwht_tiles   <- the W @ K_tile product that every kernel computes
+ *                      (fwht_fused_prototype.py:160-162, fused_eviction.py:268)
+ *   oc_decode       <- the main-kernel + reduce-kernel pair of
+ *                      fused_orthocache_attention (fused_eviction.py:773-786),
+ *                      fused_orthocache_attention_v2 (fused_eviction.py:657-680),
+ *                      fused_orthocache_attention_v3_gqa (gqa_eviction.py:603-625),
+ *                      fused_orthocache_attention_paged (paged_eviction.py:404-433)
+ *   oc_lse_merge    <- _splitk_reduce_kernel (fused_eviction.py:316-373),
+ *                      _gqa_splitk_reduce_kernel (gqa_eviction.py:458-495),
+ *                      _paged_splitk_reduce_kernel (paged_eviction.py:195-237)
+ *   oc_device_cu_count <- torch.cuda.get_device_properties(...).multi_processor_count
+ *                      as read by _auto_num_splits (fused_eviction.py:556-570)
+ */
+#ifndef ORTHOCACHE_HIP_H
+#define ORTHOCACHE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OC_ABI_VERSION 1
+
+/* status codes */
+#define OC_OK 0
+#define OC_ERR_INVALID 1      /* bad argument (shape, dtype, stride, size) */
+#define OC_ERR_UNSUPPORTED 2  /* valid but not implemented by these kernels */
+#define OC_ERR_HIP 3          /* a HIP runtime call failed */
+#define OC_ERR_WORKSPACE 4    /* workspace too small */
+
+/* element types of K/V (all four) and of q/out (the first three) */
+#define OC_F32 0
+#define OC_F16 1
+#define OC_BF16 2
+#define OC_FP8_E4M3FN 3
+
+/* tile gates */
+#define OC_GATE_NONE 0  /* dense decode: every tile retained                    */
+#define OC_GATE_ZETA 1  /* retain iff !(e_high/(e_low+1e-6) > threshold)        */
+#define OC_GATE_CS 2    /* retain iff !(max_g ||q_g|| * sqrt(e_high) <= threshold) */
+
+/* where tile scores come from */
+#define OC_MODE_SINGLE_PASS 0 /* scores computed from K inside the decode kernel  */
+#define OC_MODE_CACHED 1      /* scores read from score_e_low/score_e_high; K and
+                                 V are read for retained tiles only               */
+
+/* K dequantisation */
+#define OC_KSCALE_NONE 0     /* k = float(k_elem)                                   */
+#define OC_KSCALE_Q_FOLD 1   /* q := round_qdtype(float(q) * k_scale), k = float(k_elem)
+                                (fused_eviction.py:619-621, gqa_eviction.py:565-567) */
+#define OC_KSCALE_ELEM_QDTYPE 2 /* k = round_qdtype(float(k_elem) * k_scale), q unscaled
+                                (paged fp8 path, paged_eviction.py:354-357)          */
+#define OC_KSCALE_TILE 3     /* k = float(k_elem) * k_scales[row, tile]   (extension) */
+
+/* V dequantisation */
+#define OC_VSCALE_NONE 0
+#define OC_VSCALE_TILE 1     /* v = float(v_elem) * v_scales[row, tile]   (extension) */
+
+/*
+ * KV layout.  A "row" is one (sequence, kv head) pair; rows are decoded
+ * independently.  Tiles are 64 consecutive tokens of a row.
+ *
+ * paged == 0: element (row r, token t, dim c) of K is at
+ *             k + (r * k_row_stride + t * k_token_stride + c) elements.
+ * paged == 1: row r = b * num_kv_heads + h; token t of sequence b lives in
+ *             physical block p = block_tables[b * bt_stride + t / block_size]
+ *             at k + (p * k_block_stride + h * k_head_stride
+ *                     + (t % block_size) * k_token_stride + c) elements.
+ *             Block ids outside [0, num_blocks) make the call fail with
+ *             OC_ERR_INVALID reported through `error_flag`.
+ * lengths:    NULL, or int32 token counts indexed by r / rows_per_length;
+ *             a row has ceil(len/64) tiles (at most num_tiles).  Full tiles
+ *             are scored; a partial tail tile is always retained and its
+ *             tokens past len are masked.  (extension)
+ */
+typedef struct oc_kv_desc {
+  const void* k;
+  const void* v;
+  int32_t dtype;        /* OC_F32 .. OC_FP8_E4M3FN, same for K and V */
+  int32_t head_dim;     /* 64 or 128 */
+  int32_t num_rows;
+  int32_t num_tiles;    /* tiles per row (upper bound when lengths != NULL) */
+  int64_t k_row_stride, k_token_stride;
+  int64_t v_row_stride, v_token_stride;
+  int32_t paged;
+  int32_t block_size;   /* power of two >= 8 */
+  int32_t num_kv_heads;
+  int32_t rows_per_length;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int64_t num_blocks;
+  int64_t k_block_stride, k_head_stride;
+  int64_t v_block_stride, v_head_stride;
+  const int32_t* lengths;
+  int32_t k_scale_mode;     /* OC_KSCALE_* */
+  float k_scale;            /* scalar for Q_FOLD / ELEM_QDTYPE */
+  const float* k_scales;    /* (num_rows, >= num_tiles) for OC_KSCALE_TILE */
+  int64_t k_scales_row_stride;
+  int32_t v_scale_mode;     /* OC_VSCALE_* */
+  int32_t reserved0;
+  const float* v_scales;
+  int64_t v_scales_row_stride;
+  int32_t* error_flag;      /* optional int32 set non-zero on a bad block id */
+} oc_kv_desc;
+
+/*
+ * oc_score_tiles -- per-(row, tile) band energies of the 64-point Walsh-
+ * Hadamard transform along the token axis (natural-order rows [1,8) and
+ * [32,64), fwht_fused_prototype.py:44-50), zeta = e_high/(e_low+1e-6) and
+ * keep = !(zeta > zeta_max).  Outputs are (num_rows, num_tiles) row-major
+ * with row stride `out_row_stride`; any output pointer may be NULL.
+ * A partial tail tile gets e_low = e_high = zeta = 0 and keep = 1; tiles
+ * past a row's length get keep = 0.
+ * Replaces the launch in triton_fwht_eviction (fwht_fused_prototype.py:305-318).
+ */
+int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e_high,
+                   float* zeta, uint8_t* keep, int64_t out_row_stride, void* stream);
+
+/*
+ * oc_fwht_tiles -- the full transform X = W64 @ K_tile (float32) of every
+ * tile of every row, written to out[((r * num_tiles + t) * 64 + s) * head_dim + c].
+ * Replaces the W @ K products (fwht_fused_prototype.py:160-162).
+ */
+int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream);
+
+/* decode parameters; see oc_decode */
+typedef struct oc_decode_params {
+  oc_kv_desc kv;
+  const void* q;            /* (num_rows * G, head_dim) */
+  int32_t q_dtype;          /* OC_F32 / OC_F16 / OC_BF16 */
+  int32_t G;                /* query heads per row, 1..64 */
+  int64_t q_row_stride;     /* elements */
+  int32_t gate;             /* OC_GATE_* */
+  int32_t mode;             /* OC_MODE_* */
+  double threshold;         /* zeta_max or tau */
+  const float* score_e_low; /* cached mode: (num_rows, num_tiles) */
+  const float* score_e_high;
+  int64_t score_row_stride;
+  int32_t num_splits;       /* P >= 1: split s owns tiles {s + kP} */
+  int32_t out_dtype;        /* OC_F32 / OC_F16 / OC_BF16 */
+  void* out;                /* (num_rows * G, head_dim) */
+  int64_t out_row_stride;
+  uint8_t* keep_out;        /* optional (num_rows, num_tiles): 1 = retained */
+  int64_t keep_row_stride;
+  int32_t* split_counts;    /* optional (num_rows, P): retained tiles per split */
+  float* partial_m;         /* optional (num_rows * G, P); NULL = workspace */
+  float* partial_l;         /* optional (num_rows * G, P) */
+  float* partial_acc;       /* optional (num_rows * G, P, head_dim) */
+  void* workspace;          /* device memory, oc_decode_workspace_size() bytes */
+  size_t workspace_bytes;
+} oc_decode_params;
+
+/* bytes of device workspace oc_decode needs for `p` (0 when partials are given) */
+size_t oc_decode_workspace_size(const oc_decode_params* p);
+
+/*
+ * oc_decode -- gated split-K flash-decode plus the log-sum-exp merge.
+ * For every row r and split s, the online-softmax state of each of its G
+ * query heads over the retained tiles {s + kP} (fused_eviction.py:259) is
+ * formed in float32 (m0 = -1e9), then the P states are merged and
+ * out = acc / max(l, 1e-9) is written in out_dtype.
+ */
+int oc_decode(const oc_decode_params* p, void* stream);
+
+/*
+ * oc_lse_merge -- out[r, :] = merge over s of (m[r,s], l[r,s], acc[r,s,:]),
+ * acc/max(l, 1e-9), written in out_dtype with row stride out_row_stride.
+ */
+int oc_lse_merge(const float* m, const float* l, const float* acc, int32_t rows,
+                 int32_t num_splits, int32_t head_dim, void* out, int32_t out_dtype,
+                 int64_t out_row_stride, void* stream);
+
+/* sizeof(oc_kv_desc) and sizeof(oc_decode_params) as compiled into the
+ * library, so that a binding can check its own struct layout (no
+ * counterpart in the reference, which has no native ABI) */
+int oc_abi_sizes(size_t* kv_desc_bytes, size_t* decode_params_bytes);
+
+/* number of compute units of the current device (256 on MI355X) */
+int oc_device_cu_count(int32_t* cus);
+
+const char* oc_version(void);
+const char* oc_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORTHOCACHE_HIP_H */

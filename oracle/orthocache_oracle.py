@@ -1,0 +1,535 @@
+"""CPU oracle for OrthoCache's spectral-gated decode attention.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker that the HIP kernels
+are compared against.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it; the product package
+(``orthocache-gpu_amd/orthocache_gpu``) never does, and it never serves as a
+fallback for the product path.
+
+It restates, in numpy float32, the reference's CPU ("PyTorch fallback")
+paths with the same per-head, per-tile loop structure:
+
+* ``walsh_matrix``            <- fwht_fused_prototype.py:57-80
+* ``fwht_scores``             <- fwht_fused_prototype.py:199-248
+* ``fused_v1``                <- fused_eviction.py:460-549 (+ wrapper :698-755)
+* ``fused_v2``                <- fused_eviction.py:380-457 (+ wrapper :573-628)
+* ``gqa_v3``                  <- gqa_eviction.py:87-276    (+ wrapper :511-574)
+* ``paged``                   <- paged_eviction.py:244-316 (+ wrapper :323-368)
+* ``auto_num_splits``         <- fused_eviction.py:556-570
+* ``dense_decode``            <- pipeline.py:558-568 (fp32 form)
+
+(all paths relative to ``src/orthocache_gpu/triton_kernels/`` or
+``src/orthocache_gpu/`` of the reference tree).
+
+Extensions that the reference does not have (per-(row, tile) fp32 K/V
+scales, per-sequence ``context_lens`` and GQA for the paged layout, the
+cached-score gate and per-split partial states) are restated in the same
+style and marked "extension" in their docstrings.
+
+Pinning (how each function is checked, see tests/test_oracle.py):
+
+* ``walsh_matrix``: closed form (-1)^popcount(i&j)/8, orthogonality,
+  symmetry (the reference's own test_fused_kernel.py:45-92 properties).
+* ``fwht_scores``: textbook radix-2 butterfly in float64, the closed forms
+  E_high = 1/2 sum ||k_u - k_{u+32}||^2 and
+  E_low = 1/8 sum_r ||S_r||^2 - 1/64 ||sum_t k_t||^2, integer-valued
+  known-answer tiles (exact in any summation order), and golden vectors
+  written by the reference's own CPU code (tests/golden/).
+* ``fused_v1`` / ``fused_v2`` / ``gqa_v3`` / ``paged``: golden vectors
+  from the reference, float64 brute-force softmax over the retained tokens,
+  zero-eviction == dense, total eviction == 0.
+* split partials: the LSE merge of the per-split partials equals the
+  single-split result (float64), and the tile sets are {s + kP}.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+TILE_SIZE = 64
+BAND_LOW_64 = (1, 8)
+BAND_HIGH_64 = (32, 64)
+
+F32 = np.float32
+_EPS_ZETA = F32(1e-6)          # `e_low + 1e-6` evaluated in float32
+_M0 = F32(-1e9)                 # online-softmax initial max
+_L_MIN = F32(1e-9)              # clamp(l, min=1e-9)
+_CS_CLAMP = 1e-38               # subnormal clamp of the CS gate
+
+
+# ---------------------------------------------------------------------------
+# Walsh matrix and tile scores
+# ---------------------------------------------------------------------------
+
+def walsh_matrix(n: int = TILE_SIZE) -> np.ndarray:
+    """Sylvester Hadamard matrix scaled by 1/sqrt(n), float32.
+
+    Follows generate_walsh_matrix (fwht_fused_prototype.py:57-80):
+    H_{2m} = [[H, H], [H, -H]], then H / n**0.5.
+    """
+    assert n > 0 and (n & (n - 1)) == 0, f"n must be a power of 2, got {n}"
+    h = np.ones((1, 1), dtype=F32)
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]]).astype(F32)
+    return (h / F32(n ** 0.5)).astype(F32)
+
+
+def _as_f32(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=F32))
+
+
+def tile_energies(k_tile: np.ndarray, w: np.ndarray) -> Tuple[F32, F32]:
+    """(E_low, E_high) of one 64xd fp32 tile: X = W @ K, row-energies summed
+    over head_dim, bands [1,8) and [32,64) (fused_eviction.py:424-427)."""
+    spec = w @ k_tile
+    eps = np.sum(spec * spec, axis=1, dtype=F32)
+    e_low = np.sum(eps[BAND_LOW_64[0]:BAND_LOW_64[1]], dtype=F32)
+    e_high = np.sum(eps[BAND_HIGH_64[0]:BAND_HIGH_64[1]], dtype=F32)
+    return F32(e_low), F32(e_high)
+
+
+def zeta_of(e_low: F32, e_high: F32) -> F32:
+    """zeta = e_high / (e_low + 1e-6) in float32 (fused_eviction.py:428)."""
+    return F32(F32(e_high) / F32(F32(e_low) + _EPS_ZETA))
+
+
+def fwht_scores(keys: np.ndarray, zeta_max: float, tile_size: int = TILE_SIZE):
+    """Batched tile scores for a (num_tiles*64, d) key matrix.
+
+    Follows _pytorch_fwht_eviction (fwht_fused_prototype.py:199-248):
+    returns (keep mask [True = retain, zeta <= zeta_max], zeta, e_low, e_high).
+    """
+    keys = _as_f32(keys)
+    n, d = keys.shape
+    t = n // tile_size
+    assert n == t * tile_size
+    w = walsh_matrix(tile_size)
+    tiles = keys.reshape(t, tile_size, d)
+    spec = np.matmul(w[None], tiles)
+    eps = np.sum(spec * spec, axis=2, dtype=F32)
+    e_low = np.sum(eps[:, BAND_LOW_64[0]:BAND_LOW_64[1]], axis=1, dtype=F32)
+    e_high = np.sum(eps[:, BAND_HIGH_64[0]:BAND_HIGH_64[1]], axis=1, dtype=F32)
+    zeta = (e_high / (e_low + _EPS_ZETA)).astype(F32)
+    keep = zeta.astype(np.float64) <= float(zeta_max)
+    return keep, zeta, e_low, e_high
+
+
+def cs_keep(e_high: F32, q_group: np.ndarray, tau: float) -> bool:
+    """Cauchy-Schwarz gate of gqa_eviction.py:222-239.
+
+    k_high_norm = ||X[32:64]||_F (0 if < 1e-38); q_norms = ||q_g||_2 (0 if
+    < 1e-38); evicted iff max_g(q_norm_g * k_high_norm) <= tau.  The norm is
+    taken as sqrt of the band energy (the Frobenius norm's definition).
+    Returns True when the tile is retained.
+    """
+    kn = F32(np.sqrt(F32(e_high)))
+    if float(kn) < _CS_CLAMP:
+        kn = F32(0.0)
+    qn = q_norms(q_group)
+    cs = (qn * kn).astype(F32)
+    mx = float(np.max(cs)) if cs.size else float("-inf")
+    if math.isnan(mx):
+        return True
+    return not (mx <= float(tau))
+
+
+def q_norms(q_group: np.ndarray) -> np.ndarray:
+    """||q_g||_2 per row in float32 with the <1e-38 clamp (gqa_eviction.py:231-233)."""
+    q = _as_f32(q_group)
+    qn = np.sqrt(np.sum(q * q, axis=1, dtype=F32)).astype(F32)
+    return np.where(qn < _CS_CLAMP, F32(0.0), qn).astype(F32)
+
+
+# ---------------------------------------------------------------------------
+# dtype helpers (the reference's q*k_scale is computed in q's dtype)
+# ---------------------------------------------------------------------------
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to `dtype` ('f32', 'f16', 'bf16') with RNE and
+    return them as float32."""
+    x = _as_f32(x)
+    if dtype == "f32":
+        return x
+    if dtype == "f16":
+        return x.astype(np.float16).astype(F32)
+    if dtype == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        nan = np.isnan(x)
+        lsb = (u >> 16) & 1
+        r = ((u + 0x7FFF + lsb) >> 16) << 16
+        out = (r & 0xFFFFFFFF).astype(np.uint32).view(F32)
+        return np.where(nan, x, out).astype(F32)
+    raise ValueError(dtype)
+
+
+def fp8_e4m3fn_table() -> np.ndarray:
+    """float value of each of the 256 OCP e4m3fn codes (0x7f/0xff are NaN)."""
+    out = np.zeros(256, dtype=F32)
+    for code in range(256):
+        s = -1.0 if code & 0x80 else 1.0
+        e = (code >> 3) & 0xF
+        m = code & 0x7
+        if e == 0xF and m == 0x7:
+            out[code] = np.nan
+        elif e == 0:
+            out[code] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            out[code] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return out
+
+
+def fp8_encode(x: np.ndarray) -> np.ndarray:
+    """Round float32 to the nearest e4m3fn code (RNE, saturating at 448)."""
+    table = fp8_e4m3fn_table()
+    finite = np.where(np.isnan(table), np.inf, table)
+    pos = np.argsort(finite[:128])
+    vals = finite[:128][pos]
+    x = _as_f32(x)
+    ax = np.minimum(np.abs(x), F32(448.0))
+    idx = np.searchsorted(vals, ax)
+    idx = np.clip(idx, 1, len(vals) - 1)
+    lo, hi = vals[idx - 1], vals[idx]
+    code_lo, code_hi = pos[idx - 1], pos[idx]
+    d_lo, d_hi = ax - lo, hi - ax
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (code_hi % 2 == 0))
+    code = np.where(pick_hi, code_hi, code_lo).astype(np.uint8)
+    code = np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
+    return code
+
+
+# ---------------------------------------------------------------------------
+# Online-softmax tile update (fused_eviction.py:434-445)
+# ---------------------------------------------------------------------------
+
+class _State:
+    __slots__ = ("m", "l", "acc")
+
+    def __init__(self, d: int):
+        self.m = _M0
+        self.l = F32(0.0)
+        self.acc = np.zeros(d, dtype=F32)
+
+
+def _update(st: _State, q_row: np.ndarray, k_tile: np.ndarray, v_tile: np.ndarray,
+            scale: F32, valid: Optional[int] = None) -> None:
+    logits = (k_tile @ q_row).astype(F32) * scale
+    if valid is not None and valid < logits.shape[0]:
+        logits = logits.copy()
+        logits[valid:] = F32(-np.inf)
+    local_max = F32(np.max(logits))
+    new_max = F32(max(st.m, local_max)) if not np.isnan(local_max) else local_max
+    p = np.exp((logits - new_max).astype(F32)).astype(F32)
+    s = np.sum(p, dtype=F32)
+    alpha = F32(np.exp(F32(st.m - new_max)))
+    st.l = F32(st.l * alpha + s)
+    st.acc = (st.acc * alpha + (p @ v_tile).astype(F32)).astype(F32)
+    st.m = new_max
+
+
+def _finish(st: _State) -> np.ndarray:
+    return (st.acc / max(st.l, _L_MIN)).astype(F32)
+
+
+def _scale_of(d: int) -> F32:
+    return F32(1.0 / (d ** 0.5))
+
+
+# ---------------------------------------------------------------------------
+# Reference CPU paths
+# ---------------------------------------------------------------------------
+
+def fused_v1(q, keys, values, zeta_max: float, tile_size: int = TILE_SIZE,
+             return_mask: bool = False, k_scale: float = 1.0, q_dtype: str = "f32"):
+    """Single-head zeta-gated decode.
+
+    Follows fused_orthocache_attention (fused_eviction.py:698-755) and its
+    CPU body _pytorch_fused_orthocache_attention (:460-549).  `q` is the
+    (1, d) query already decoded to float32; `q_dtype` names its storage
+    dtype so that `q * k_scale` is rounded like the reference
+    (fused_eviction.py:746-748).  Returns (out (1, d) float32, metadata).
+    """
+    q = _as_f32(q)
+    if k_scale != 1.0:
+        q = round_to(q * F32(k_scale), q_dtype)
+    keys, values = _as_f32(keys), _as_f32(values)
+    d = q.shape[-1]
+    t_count = keys.shape[0] // tile_size
+    w = walsh_matrix(tile_size)
+    scale = _scale_of(d)
+    st = _State(d)
+    mask = np.zeros(t_count, dtype=bool)
+    kept = ev = 0
+    for t in range(t_count):
+        kt = keys[t * tile_size:(t + 1) * tile_size]
+        el, eh = tile_energies(kt, w)
+        if float(zeta_of(el, eh)) > zeta_max:
+            ev += 1
+            continue
+        mask[t] = True
+        kept += 1
+        _update(st, q[0], kt, values[t * tile_size:(t + 1) * tile_size], scale)
+    meta = {"tiles_retained": kept, "tiles_evicted": ev,
+            "eviction_rate": ev / max(1, t_count)}
+    if return_mask:
+        meta["eviction_mask"] = mask
+    return _finish(st)[None, :], meta
+
+
+def fused_v2(q, keys, values, zeta_max: float, tile_size: int = TILE_SIZE,
+             k_scale: float = 1.0, q_dtype: str = "f32"):
+    """Multi-head zeta-gated decode; q (H, d), keys/values (H, S, d).
+
+    Follows fused_orthocache_attention_v2 (fused_eviction.py:573-628) and
+    _pytorch_fused_orthocache_multihead (:380-457).  Returns (out (H, d)
+    float32, metadata, keep mask (H, T))."""
+    q = _as_f32(q)
+    if k_scale != 1.0:
+        q = round_to(q * F32(k_scale), q_dtype)
+    keys, values = _as_f32(keys), _as_f32(values)
+    h_count, s_len, d = keys.shape
+    t_count = s_len // tile_size
+    w = walsh_matrix(tile_size)
+    scale = _scale_of(d)
+    outs = []
+    kept = ev = 0
+    mask = np.zeros((h_count, t_count), dtype=bool)
+    for h in range(h_count):
+        st = _State(d)
+        for t in range(t_count):
+            kt = keys[h, t * tile_size:(t + 1) * tile_size]
+            el, eh = tile_energies(kt, w)
+            if float(zeta_of(el, eh)) > zeta_max:
+                ev += 1
+                continue
+            kept += 1
+            mask[h, t] = True
+            _update(st, q[h], kt, values[h, t * tile_size:(t + 1) * tile_size], scale)
+        outs.append(_finish(st))
+    meta = {"tiles_retained": kept, "tiles_evicted": ev,
+            "eviction_rate": ev / max(1, t_count * h_count)}
+    return np.stack(outs), meta, mask
+
+
+def gqa_v3(q, keys, values, tau: float, num_query_groups: int,
+           tile_size: int = TILE_SIZE, k_scale: float = 1.0, q_dtype: str = "f32"):
+    """GQA decode with the Cauchy-Schwarz gate; q (Hkv*G, d), K/V (Hkv, S, d).
+
+    Follows fused_orthocache_attention_v3_gqa (gqa_eviction.py:511-574) and
+    _pytorch_gqa_cauchy_schwarz_attention (:87-276): one gate decision per
+    (kv head, tile) from max_g ||q_g|| * ||X[32:64]||_F <= tau, then a
+    separate online softmax per query head g (:249-259).
+    Returns (out (Hq, d) float32, metadata, keep mask (Hkv, T))."""
+    q = _as_f32(q)
+    if k_scale != 1.0:
+        q = round_to(q * F32(k_scale), q_dtype)
+    keys, values = _as_f32(keys), _as_f32(values)
+    hkv, s_len, d = keys.shape
+    g_count = num_query_groups
+    assert q.shape[0] == hkv * g_count, (
+        f"num_query_heads ({q.shape[0]}) != num_kv_heads ({hkv}) × G ({g_count})")
+    t_count = s_len // tile_size
+    w = walsh_matrix(tile_size)
+    scale = _scale_of(d)
+    outs = []
+    kept = ev = 0
+    mask = np.zeros((hkv, t_count), dtype=bool)
+    for kv in range(hkv):
+        qg = q[kv * g_count:(kv + 1) * g_count]
+        sts = [_State(d) for _ in range(g_count)]
+        for t in range(t_count):
+            kt = keys[kv, t * tile_size:(t + 1) * tile_size]
+            _, eh = tile_energies(kt, w)
+            if not cs_keep(eh, qg, tau):
+                ev += 1
+                continue
+            kept += 1
+            mask[kv, t] = True
+            vt = values[kv, t * tile_size:(t + 1) * tile_size]
+            for g in range(g_count):
+                _update(sts[g], qg[g], kt, vt, scale)
+        outs.extend(_finish(s) for s in sts)
+    meta = {"tiles_retained": kept, "tiles_evicted": ev,
+            "eviction_rate": ev / max(1, t_count * hkv),
+            "num_kv_heads": hkv, "num_query_groups": g_count,
+            "gate_type": "cauchy_schwarz"}
+    return np.stack(outs), meta, mask
+
+
+def paged(q, k_cache, v_cache, block_tables, zeta_max: float,
+          tile_size: int = TILE_SIZE, k_scale: float = 1.0, q_dtype: str = "f32",
+          k_is_fp8: bool = False):
+    """Paged zeta-gated decode; q (B, H, d), caches (NB, H, bs, d).
+
+    Follows fused_orthocache_attention_paged (paged_eviction.py:323-368) and
+    _pytorch_paged_orthocache_attention (:244-316): every sequence is read
+    for max_blocks*bs tokens through its block-table row; an fp8 key cache
+    is first converted to q's dtype and multiplied by k_scale in that dtype
+    (:354-357).  `k_cache` holds the decoded float32 values of the stored
+    elements.  Returns (out (B, H, d) float32, {}, keep mask (B, H, T))."""
+    q = _as_f32(q)
+    k_cache, v_cache = _as_f32(k_cache), _as_f32(v_cache)
+    if k_is_fp8:
+        k_cache = round_to(round_to(k_cache, q_dtype) * F32(k_scale), q_dtype)
+        k_scale = 1.0
+    if k_scale != 1.0:
+        q = round_to(q * F32(k_scale), q_dtype)
+    bt = np.asarray(block_tables, dtype=np.int64)
+    b_count, h_count, d = q.shape
+    bs = k_cache.shape[2]
+    t_count = (bt.shape[1] * bs) // tile_size
+    w = walsh_matrix(tile_size)
+    scale = _scale_of(d)
+    out = np.zeros((b_count, h_count, d), dtype=F32)
+    mask = np.zeros((b_count, h_count, t_count), dtype=bool)
+    for b in range(b_count):
+        for h in range(h_count):
+            kh = np.concatenate([k_cache[bt[b, j], h] for j in range(bt.shape[1])])
+            vh = np.concatenate([v_cache[bt[b, j], h] for j in range(bt.shape[1])])
+            st = _State(d)
+            for t in range(t_count):
+                kt = kh[t * tile_size:(t + 1) * tile_size]
+                el, eh = tile_energies(kt, w)
+                if float(zeta_of(el, eh)) > zeta_max:
+                    continue
+                mask[b, h, t] = True
+                _update(st, q[b, h], kt, vh[t * tile_size:(t + 1) * tile_size], scale)
+            out[b, h] = _finish(st)
+    return out, {}, mask
+
+
+def auto_num_splits(num_tiles: int, num_cus: Optional[int]) -> int:
+    """P = min(#CU, max(1, T//4), T), and 1 off-device (fused_eviction.py:556-570)."""
+    if num_cus is None:
+        return 1
+    return max(1, min(num_cus, max(1, num_tiles // 4), num_tiles))
+
+
+# ---------------------------------------------------------------------------
+# Generalised decode (extensions): GQA x {none, zeta, cs} gate x scales x
+# context lengths x per-split partials.  With G=1 / gate='zeta' / no scales /
+# full-length rows it reduces to fused_v2; with gate='cs' to gqa_v3.
+# ---------------------------------------------------------------------------
+
+def decode_rows(q, keys, values, *, gate: str, threshold: float, G: int,
+                tile_size: int = TILE_SIZE, k_scales=None, v_scales=None,
+                lengths: Optional[Sequence[int]] = None,
+                num_splits: Optional[int] = None, want_partials: bool = False):
+    """Extension: gated decode over `rows` independent (batch, kv-head) rows.
+
+    q (rows*G, d) float32; keys/values (rows, S, d) float32 (decoded element
+    values); k_scales/v_scales (rows, T) float32 or None: the tile's value is
+    element * scale (one float32 multiply).  lengths[r] (tokens, <= S): only
+    tiles fully inside the length are scored; a partial tail tile is always
+    retained and its tokens past the length are masked out of the softmax.
+    gate in {'none', 'zeta', 'cs'}.
+
+    The tile loop follows the reference's per-tile order; when num_splits is
+    given the tiles of split s are {s + kP} (fused_eviction.py:259) and the
+    per-split partial states (m, l, acc) are returned as well.
+    Returns dict(out (rows*G, d), keep (rows, T), e_low, e_high,
+    retained, evicted, [M, L, ACC])."""
+    q = _as_f32(q)
+    keys, values = _as_f32(keys), _as_f32(values)
+    rows, s_len, d = keys.shape
+    t_count = s_len // tile_size
+    w = walsh_matrix(tile_size)
+    scale = _scale_of(d)
+    p_count = 1 if num_splits is None else num_splits
+    keep = np.zeros((rows, t_count), dtype=bool)
+    e_low = np.zeros((rows, t_count), dtype=F32)
+    e_high = np.zeros((rows, t_count), dtype=F32)
+    m_out = np.full((rows * G, p_count), _M0, dtype=F32)
+    l_out = np.zeros((rows * G, p_count), dtype=F32)
+    acc_out = np.zeros((rows * G, p_count, d), dtype=F32)
+    out = np.zeros((rows * G, d), dtype=F32)
+    kept = ev = 0
+    for r in range(rows):
+        length = s_len if lengths is None else int(lengths[r])
+        n_tiles = min(t_count, -(-length // tile_size))
+        qg = q[r * G:(r + 1) * G]
+        for s in range(p_count):
+            sts = [_State(d) for _ in range(G)]
+            for t in range(s, n_tiles, p_count):
+                kt = keys[r, t * tile_size:(t + 1) * tile_size]
+                vt = values[r, t * tile_size:(t + 1) * tile_size]
+                if k_scales is not None:
+                    kt = (kt * F32(k_scales[r, t])).astype(F32)
+                if v_scales is not None:
+                    vt = (vt * F32(v_scales[r, t])).astype(F32)
+                valid = length - t * tile_size
+                full = valid >= tile_size
+                el, eh = tile_energies(kt, w) if full else (F32(0), F32(0))
+                e_low[r, t], e_high[r, t] = el, eh
+                if not full or gate == "none":
+                    k_ok = True
+                elif gate == "zeta":
+                    k_ok = not (float(zeta_of(el, eh)) > threshold)
+                elif gate == "cs":
+                    k_ok = cs_keep(eh, qg, threshold)
+                else:
+                    raise ValueError(gate)
+                keep[r, t] = k_ok
+                if not k_ok:
+                    ev += 1
+                    continue
+                kept += 1
+                for g in range(G):
+                    _update(sts[g], qg[g], kt, vt, scale,
+                            valid=None if full else valid)
+            for g in range(G):
+                m_out[r * G + g, s] = sts[g].m
+                l_out[r * G + g, s] = sts[g].l
+                acc_out[r * G + g, s] = sts[g].acc
+    for i in range(rows * G):
+        out[i] = lse_merge(m_out[i], l_out[i], acc_out[i])
+    res = {"out": out, "keep": keep, "e_low": e_low, "e_high": e_high,
+           "retained": kept, "evicted": ev}
+    if want_partials:
+        res.update(M=m_out, L=l_out, ACC=acc_out)
+    return res
+
+
+def lse_merge(m: np.ndarray, l: np.ndarray, acc: np.ndarray) -> np.ndarray:
+    """Sequential log-sum-exp merge of split partials (fused_eviction.py:316-373):
+    m' = max, l = l*e^(m-m') + l_s*e^(m_s-m'), acc likewise; acc/max(l,1e-9)."""
+    m_run, l_run, a_run = F32(m[0]), F32(l[0]), acc[0].astype(F32)
+    for s in range(1, len(m)):
+        nm = F32(max(m_run, F32(m[s])))
+        a1 = F32(np.exp(F32(m_run - nm)))
+        a2 = F32(np.exp(F32(F32(m[s]) - nm)))
+        l_run = F32(l_run * a1 + F32(l[s]) * a2)
+        a_run = (a_run * a1 + acc[s].astype(F32) * a2).astype(F32)
+        m_run = nm
+    return (a_run / max(l_run, _L_MIN)).astype(F32)
+
+
+def dense_decode(q, keys, values) -> np.ndarray:
+    """Dense softmax decode in float64 over every token (the comparator of
+    pipeline.py:558-568 / profile_multihead.py:127-146); q (R, d), K/V (R, S, d)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(keys, dtype=np.float64)
+    v = np.asarray(values, dtype=np.float64)
+    logits = np.einsum("rd,rsd->rs", q, k) / math.sqrt(q.shape[-1])
+    logits -= logits.max(axis=1, keepdims=True)
+    p = np.exp(logits)
+    p /= p.sum(axis=1, keepdims=True)
+    return np.einsum("rs,rsd->rd", p, v)
+
+
+def fwht64_butterfly(x: np.ndarray) -> np.ndarray:
+    """Textbook radix-2 FWHT along axis 0 in float64, natural (Sylvester)
+    order, scaled by 1/8: the six-stage butterfly of
+    test_fused_kernel.py:103-139."""
+    x = np.array(x, dtype=np.float64)
+    n = x.shape[0]
+    h = 1
+    while h < n:
+        y = x.reshape(n // (2 * h), 2, h, *x.shape[1:])
+        a, b = y[:, 0].copy(), y[:, 1].copy()
+        y[:, 0], y[:, 1] = a + b, a - b
+        x = y.reshape(x.shape)
+        h *= 2
+    return x / math.sqrt(n)

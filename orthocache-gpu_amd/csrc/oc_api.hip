@@ -1,0 +1,344 @@
+// C ABI of liborthocache_hip (declared in include/orthocache_hip.h):
+// argument validation, workspace carving, kernel dispatch and the
+// log-sum-exp merge kernel.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "oc_kernels.h"
+#include "orthocache_hip.h"
+
+namespace oc {
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+static int hip_fail(hipError_t e, const char* what) {
+  return fail(OC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static int elem_size(int dt) {
+  switch (dt) {
+    case OC_F32: return 4;
+    case OC_F16: case OC_BF16: return 2;
+    case OC_FP8_E4M3FN: return 1;
+    default: return 0;
+  }
+}
+
+static bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+// Validates the KV descriptor and fills the layout part of DecodeArgs.
+static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
+  if (!kv) return fail(OC_ERR_INVALID, "kv descriptor is NULL");
+  const int es = elem_size(kv->dtype);
+  if (!es) return fail(OC_ERR_INVALID, "unknown K/V dtype %d", kv->dtype);
+  if (kv->head_dim != 64 && kv->head_dim != 128)
+    return fail(OC_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", kv->head_dim);
+  if (kv->num_rows < 0 || kv->num_tiles < 0) return fail(OC_ERR_INVALID, "negative sizes");
+  if (kv->num_rows > 65535) return fail(OC_ERR_UNSUPPORTED, "num_rows %d > 65535", kv->num_rows);
+  if (!kv->k) return fail(OC_ERR_INVALID, "K pointer is NULL");
+  const int64_t lb = (int64_t)(kv->head_dim / 16) * es;  // bytes per lane per token row
+  const int64_t al = lb < 16 ? lb : 16;
+  auto chk = [&](int64_t stride_el, const char* what) -> int {
+    if ((stride_el * es) % al) return fail(OC_ERR_INVALID, "%s stride %lld not a multiple of %lld bytes",
+                                           what, (long long)stride_el, (long long)al);
+    return OC_OK;
+  };
+  if (!aligned(kv->k, al) || (kv->v && !aligned(kv->v, al)))
+    return fail(OC_ERR_INVALID, "K/V base pointers must be %lld-byte aligned", (long long)al);
+  int rc;
+  if ((rc = chk(kv->k_token_stride, "K token"))) return rc;
+  if ((rc = chk(kv->v_token_stride, "V token"))) return rc;
+  memset(&a, 0, sizeof a);
+  a.k = (const char*)kv->k;
+  a.v = (const char*)kv->v;
+  a.k_tok_stride = kv->k_token_stride * es;
+  a.v_tok_stride = kv->v_token_stride * es;
+  a.paged = kv->paged ? 1 : 0;
+  if (!a.paged) {
+    if ((rc = chk(kv->k_row_stride, "K row"))) return rc;
+    if ((rc = chk(kv->v_row_stride, "V row"))) return rc;
+    a.k_row_stride = kv->k_row_stride * es;
+    a.v_row_stride = kv->v_row_stride * es;
+  } else {
+    const int bs = kv->block_size;
+    if (bs < 4 || (bs & (bs - 1))) return fail(OC_ERR_INVALID, "block_size %d must be a power of 2 >= 4", bs);
+    if (kv->num_kv_heads <= 0 || kv->num_rows % kv->num_kv_heads)
+      return fail(OC_ERR_INVALID, "num_rows %d not a multiple of num_kv_heads %d", kv->num_rows, kv->num_kv_heads);
+    if (!kv->block_tables) return fail(OC_ERR_INVALID, "block_tables is NULL");
+    if ((rc = chk(kv->k_block_stride, "K block"))) return rc;
+    if ((rc = chk(kv->k_head_stride, "K head"))) return rc;
+    if ((rc = chk(kv->v_block_stride, "V block"))) return rc;
+    if ((rc = chk(kv->v_head_stride, "V head"))) return rc;
+    int l2 = 0;
+    while ((1 << l2) < bs) ++l2;
+    a.bs_log2 = l2;
+    a.nkv = kv->num_kv_heads;
+    a.bt = kv->block_tables;
+    a.bt_stride = kv->bt_stride;
+    a.num_blocks = kv->num_blocks;
+    a.k_blk_stride = kv->k_block_stride * es;
+    a.k_head_stride = kv->k_head_stride * es;
+    a.v_blk_stride = kv->v_block_stride * es;
+    a.v_head_stride = kv->v_head_stride * es;
+  }
+  a.rows_per_length = kv->rows_per_length > 0 ? kv->rows_per_length : 1;
+  a.lengths = kv->lengths;
+  a.num_rows = kv->num_rows;
+  a.num_tiles = kv->num_tiles;
+  a.k_scale_mode = kv->k_scale_mode;
+  a.v_scale_mode = kv->v_scale_mode;
+  a.k_scale = kv->k_scale;
+  a.k_scales = kv->k_scales;
+  a.ks_stride = kv->k_scales_row_stride;
+  a.v_scales = kv->v_scales;
+  a.vs_stride = kv->v_scales_row_stride;
+  a.error_flag = kv->error_flag;
+  if (a.k_scale_mode < OC_KSCALE_NONE || a.k_scale_mode > OC_KSCALE_TILE)
+    return fail(OC_ERR_INVALID, "k_scale_mode %d", a.k_scale_mode);
+  if (a.k_scale_mode == OC_KSCALE_TILE && !a.k_scales) return fail(OC_ERR_INVALID, "k_scales is NULL");
+  if (a.v_scale_mode == OC_VSCALE_TILE && !a.v_scales) return fail(OC_ERR_INVALID, "v_scales is NULL");
+  if (a.v_scale_mode != OC_VSCALE_NONE && a.v_scale_mode != OC_VSCALE_TILE)
+    return fail(OC_ERR_INVALID, "v_scale_mode %d", a.v_scale_mode);
+  return OC_OK;
+}
+
+template <int DT>
+hipError_t launch_decode(const DecodeArgs& a, int head_dim, int gt, int gchunks, hipStream_t st);
+template <int DT>
+hipError_t launch_score(const DecodeArgs& a, int head_dim, hipStream_t st);
+template <int DT>
+hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
+
+static hipError_t dispatch_decode(int dt, const DecodeArgs& a, int hd, int gt, int gc, hipStream_t st) {
+  switch (dt) {
+    case OC_F32: return launch_decode<OC_F32>(a, hd, gt, gc, st);
+    case OC_F16: return launch_decode<OC_F16>(a, hd, gt, gc, st);
+    case OC_BF16: return launch_decode<OC_BF16>(a, hd, gt, gc, st);
+    default: return launch_decode<OC_FP8_E4M3FN>(a, hd, gt, gc, st);
+  }
+}
+
+static hipError_t dispatch_score(int dt, const DecodeArgs& a, int hd, hipStream_t st) {
+  switch (dt) {
+    case OC_F32: return launch_score<OC_F32>(a, hd, st);
+    case OC_F16: return launch_score<OC_F16>(a, hd, st);
+    case OC_BF16: return launch_score<OC_BF16>(a, hd, st);
+    default: return launch_score<OC_FP8_E4M3FN>(a, hd, st);
+  }
+}
+
+static hipError_t dispatch_fwht(int dt, const DecodeArgs& a, int hd, hipStream_t st) {
+  switch (dt) {
+    case OC_F32: return launch_fwht<OC_F32>(a, hd, st);
+    case OC_F16: return launch_fwht<OC_F16>(a, hd, st);
+    case OC_BF16: return launch_fwht<OC_BF16>(a, hd, st);
+    default: return launch_fwht<OC_FP8_E4M3FN>(a, hd, st);
+  }
+}
+
+// ---------------------------------------------------------------- merge
+
+__device__ __forceinline__ float block_reduce(float x, bool is_max, float* red) {
+  x = is_max ? wave_max(x) : wave_sum(x);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  x = red[0];
+  for (int i = 1; i < nw; ++i) x = is_max ? fmaxf(x, red[i]) : x + red[i];
+  __syncthreads();
+  return x;
+}
+
+// One workgroup per query-head row: out = sum_s e^(m_s-M) acc_s / max(sum_s e^(m_s-M) l_s, 1e-9)
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ m, const float* __restrict__ l,
+                                                    const float* __restrict__ acc, int P, int D, char* out,
+                                                    int out_dtype, int64_t out_row_stride) {
+  extern __shared__ float sw[];
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const float* mr = m + r * P;
+  const float* lr = l + r * P;
+  float mx = -__builtin_inff();
+  for (int s = threadIdx.x; s < P; s += blockDim.x) mx = fmaxf(mx, mr[s]);
+  mx = block_reduce(mx, true, red);
+  float ls = 0.f;
+  for (int s = threadIdx.x; s < P; s += blockDim.x) {
+    const float w = __expf(mr[s] - mx);
+    sw[s] = w;
+    ls = __builtin_fmaf(w, lr[s], ls);
+  }
+  ls = block_reduce(ls, false, red);  // contains the barrier that publishes sw
+  const float inv_l = fmaxf(ls, 1e-9f);
+  const int es = out_dtype == OC_F32 ? 4 : 2;
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    const float* ap = acc + r * P * D + c;
+    float x = 0.f;
+    for (int s = 0; s < P; ++s) x = __builtin_fmaf(ap[(int64_t)s * D], sw[s], x);
+    store_scalar(out + r * out_row_stride + (int64_t)c * es, out_dtype, x / inv_l);
+  }
+}
+
+static int launch_merge(const float* m, const float* l, const float* acc, int rows, int P, int D, void* out,
+                        int out_dtype, int64_t out_row_stride_el, hipStream_t st) {
+  if (rows == 0) return OC_OK;
+  const int es = out_dtype == OC_F32 ? 4 : 2;
+  hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), (size_t)P * sizeof(float), st, m, l, acc, P, D,
+                     (char*)out, out_dtype, out_row_stride_el * es);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "merge launch");
+}
+
+}  // namespace oc
+
+using namespace oc;
+
+static size_t partial_floats(const oc_decode_params* p) {
+  const size_t rq = (size_t)p->kv.num_rows * (size_t)p->G * (size_t)p->num_splits;
+  return rq * (2 + (size_t)p->kv.head_dim);
+}
+
+extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
+  if (!p || p->num_splits <= 0 || p->G <= 0) return 0;
+  if (p->partial_m && p->partial_l && p->partial_acc) return 0;
+  return partial_floats(p) * sizeof(float) + 256;
+}
+
+extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
+  if (!p) return fail(OC_ERR_INVALID, "params is NULL");
+  DecodeArgs a;
+  int rc = fill_kv(&p->kv, a);
+  if (rc) return rc;
+  if (!p->kv.v) return fail(OC_ERR_INVALID, "V pointer is NULL");
+  const int D = p->kv.head_dim;
+  if (p->G < 1 || p->G > 64) return fail(OC_ERR_UNSUPPORTED, "G=%d outside 1..64", p->G);
+  if (p->num_splits < 1 || p->num_splits > 8192) return fail(OC_ERR_INVALID, "num_splits %d outside 1..8192", p->num_splits);
+  if (p->q_dtype != OC_F32 && p->q_dtype != OC_F16 && p->q_dtype != OC_BF16)
+    return fail(OC_ERR_INVALID, "q dtype %d", p->q_dtype);
+  if (p->out_dtype != OC_F32 && p->out_dtype != OC_F16 && p->out_dtype != OC_BF16)
+    return fail(OC_ERR_INVALID, "out dtype %d", p->out_dtype);
+  if (!p->q || !p->out) return fail(OC_ERR_INVALID, "q/out pointer is NULL");
+  if (p->gate < OC_GATE_NONE || p->gate > OC_GATE_CS) return fail(OC_ERR_INVALID, "gate %d", p->gate);
+  if (p->mode != OC_MODE_SINGLE_PASS && p->mode != OC_MODE_CACHED) return fail(OC_ERR_INVALID, "mode %d", p->mode);
+  if (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE) {
+    if (!p->score_e_high || (p->gate == OC_GATE_ZETA && !p->score_e_low))
+      return fail(OC_ERR_INVALID, "cached mode needs score_e_high (and score_e_low for the zeta gate)");
+  }
+  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) a.q_dtype = p->q_dtype;
+  const int qes = p->q_dtype == OC_F32 ? 4 : 2;
+  a.q = (const char*)p->q;
+  a.q_row_stride = p->q_row_stride * qes;
+  a.q_dtype = p->q_dtype;
+  a.G = p->G;
+  a.gate = p->gate;
+  a.mode = p->mode;
+  a.thr = p->threshold;
+  a.sc_el = p->score_e_low;
+  a.sc_eh = p->score_e_high;
+  a.sc_stride = p->score_row_stride;
+  a.P = p->num_splits;
+  a.keep_out = p->keep_out;
+  a.keep_stride = p->keep_row_stride;
+  a.split_counts = p->split_counts;
+  a.scale = (float)(1.0 / std::sqrt((double)D));
+  if (p->partial_m && p->partial_l && p->partial_acc) {
+    a.pm = p->partial_m;
+    a.pl = p->partial_l;
+    a.pacc = p->partial_acc;
+  } else {
+    const size_t need = oc_decode_workspace_size(p);
+    if (!p->workspace || p->workspace_bytes < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+    char* w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
+    const size_t rq = (size_t)p->kv.num_rows * p->G * p->num_splits;
+    a.pacc = (float*)w;
+    a.pm = a.pacc + rq * D;
+    a.pl = a.pm + rq;
+  }
+  if (a.num_rows == 0) return OC_OK;
+  const int gt = p->G >= 8 ? 8 : (p->G >= 4 ? (p->G == 4 ? 4 : 8) : (p->G == 3 ? 4 : p->G));
+  const int gchunks = (p->G + gt - 1) / gt;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, p->num_splits, D, p->out, p->out_dtype,
+                      p->out_row_stride, st);
+}
+
+extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e_high, float* zeta,
+                              uint8_t* keep, int64_t out_row_stride, void* stream) {
+  DecodeArgs a;
+  int rc = fill_kv(kv, a);
+  if (rc) return rc;
+  a.thr = zeta_max;
+  a.o_el = e_low;
+  a.o_eh = e_high;
+  a.o_z = zeta;
+  a.o_keep = keep;
+  a.o_stride = out_row_stride;
+  a.q_dtype = OC_F32;
+  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) return fail(OC_ERR_INVALID, "ELEM_QDTYPE scaling needs a q dtype");
+  if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
+  const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
+}
+
+extern "C" int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream) {
+  DecodeArgs a;
+  int rc = fill_kv(kv, a);
+  if (rc) return rc;
+  if (!out) return fail(OC_ERR_INVALID, "out is NULL");
+  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) return fail(OC_ERR_INVALID, "ELEM_QDTYPE scaling needs a q dtype");
+  a.lengths = nullptr;
+  a.o_fwht = out;
+  if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
+  const hipError_t e = dispatch_fwht(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? OC_OK : hip_fail(e, "fwht launch");
+}
+
+extern "C" int oc_lse_merge(const float* m, const float* l, const float* acc, int32_t rows, int32_t num_splits,
+                            int32_t head_dim, void* out, int32_t out_dtype, int64_t out_row_stride, void* stream) {
+  if (!m || !l || !acc || !out) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (rows < 0 || num_splits < 1 || num_splits > 8192 || head_dim < 1 || head_dim > 1024)
+    return fail(OC_ERR_INVALID, "bad sizes");
+  if (out_dtype != OC_F32 && out_dtype != OC_F16 && out_dtype != OC_BF16)
+    return fail(OC_ERR_INVALID, "out dtype %d", out_dtype);
+  return launch_merge(m, l, acc, rows, num_splits, head_dim, out, out_dtype, out_row_stride,
+                      (hipStream_t)stream);
+}
+
+extern "C" int oc_abi_sizes(size_t* kv_desc_bytes, size_t* decode_params_bytes) {
+  if (kv_desc_bytes) *kv_desc_bytes = sizeof(oc_kv_desc);
+  if (decode_params_bytes) *decode_params_bytes = sizeof(oc_decode_params);
+  return OC_OK;
+}
+
+extern "C" int oc_device_cu_count(int32_t* cus) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  int n = 0;
+  e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+  if (cus) *cus = n;
+  return OC_OK;
+}
+
+extern "C" const char* oc_version(void) { return "orthocache_hip 0.1.0 (gfx950, abi 1)"; }
+
+extern "C" const char* oc_last_error(void) { return g_last_error.c_str(); }

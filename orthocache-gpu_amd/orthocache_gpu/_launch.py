@@ -1,0 +1,371 @@
+"""Host-side plumbing shared by the drop-in entry points: tensor checks,
+KV descriptors, workspace reuse and the oc_decode / oc_score_tiles calls.
+
+torch is used for device memory and the current stream only; every
+computation on the path runs in liborthocache_hip.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _native as N
+
+TILE_SIZE = 64
+MAX_SPLITS = 8192
+
+_DTYPE_CODES = {
+    torch.float32: N.OC_F32,
+    torch.float16: N.OC_F16,
+    torch.bfloat16: N.OC_BF16,
+    torch.float8_e4m3fn: N.OC_FP8_E4M3FN,
+}
+
+
+def dtype_code(dt: torch.dtype, what: str, allow_fp8: bool = True) -> int:
+    code = _DTYPE_CODES.get(dt)
+    if code is None or (code == N.OC_FP8_E4M3FN and not allow_fp8):
+        raise TypeError(f"orthocache_gpu: unsupported {what} dtype {dt}")
+    return code
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "orthocache_gpu runs on an AMD GPU only: got a tensor on "
+                f"'{t.device}'. Move the inputs to the GPU (there is no CPU fallback).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"orthocache_gpu: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _aligned(t: torch.Tensor, nbytes: int) -> bool:
+    return t.data_ptr() % nbytes == 0
+
+
+def _kv_align(head_dim: int, es: int) -> int:
+    return min(16, (head_dim // 16) * es)
+
+
+def last_dim_ready(t: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """Returns `t` if its last dimension is contiguous and every other stride
+    and the base pointer keep the kernel's vector loads aligned; otherwise a
+    contiguous copy (the reference wrappers always copy, fused_eviction.py:636-638)."""
+    es = t.element_size()
+    al = _kv_align(head_dim, es)
+    ok = t.stride(-1) == 1 and _aligned(t, al)
+    if ok:
+        for s in t.stride()[:-1]:
+            if (s * es) % al:
+                ok = False
+    return t if ok else t.contiguous()
+
+
+# ---------------------------------------------------------------- descriptors
+
+@dataclass
+class KVLayout:
+    """Everything oc_kv_desc carries, plus the tensors it points to."""
+    k: torch.Tensor
+    v: Optional[torch.Tensor]
+    head_dim: int
+    num_rows: int
+    num_tiles: int
+    k_row_stride: int = 0
+    k_token_stride: int = 0
+    v_row_stride: int = 0
+    v_token_stride: int = 0
+    paged: bool = False
+    block_size: int = 0
+    num_kv_heads: int = 0
+    block_tables: Optional[torch.Tensor] = None
+    num_blocks: int = 0
+    k_block_stride: int = 0
+    k_head_stride: int = 0
+    v_block_stride: int = 0
+    v_head_stride: int = 0
+    lengths: Optional[torch.Tensor] = None
+    rows_per_length: int = 1
+    k_scale_mode: int = N.OC_KSCALE_NONE
+    k_scale: float = 1.0
+    k_scales: Optional[torch.Tensor] = None
+    v_scale_mode: int = N.OC_VSCALE_NONE
+    v_scales: Optional[torch.Tensor] = None
+    error_flag: Optional[torch.Tensor] = None
+
+    def struct(self) -> N.OcKvDesc:
+        d = N.OcKvDesc()
+        d.k = _ptr(self.k)
+        d.v = _ptr(self.v)
+        d.dtype = dtype_code(self.k.dtype, "K")
+        if self.v is not None and self.v.dtype != self.k.dtype:
+            raise TypeError(f"orthocache_gpu: K and V dtypes differ ({self.k.dtype} vs {self.v.dtype})")
+        d.head_dim = self.head_dim
+        d.num_rows = self.num_rows
+        d.num_tiles = self.num_tiles
+        d.k_row_stride, d.k_token_stride = self.k_row_stride, self.k_token_stride
+        d.v_row_stride, d.v_token_stride = self.v_row_stride, self.v_token_stride
+        d.paged = 1 if self.paged else 0
+        d.block_size = self.block_size
+        d.num_kv_heads = self.num_kv_heads
+        d.rows_per_length = self.rows_per_length
+        d.block_tables = _ptr(self.block_tables)
+        d.bt_stride = 0 if self.block_tables is None else self.block_tables.stride(0)
+        d.num_blocks = self.num_blocks
+        d.k_block_stride, d.k_head_stride = self.k_block_stride, self.k_head_stride
+        d.v_block_stride, d.v_head_stride = self.v_block_stride, self.v_head_stride
+        d.lengths = _ptr(self.lengths)
+        d.k_scale_mode = self.k_scale_mode
+        d.k_scale = float(self.k_scale)
+        d.k_scales = _ptr(self.k_scales)
+        d.k_scales_row_stride = 0 if self.k_scales is None else self.k_scales.stride(0)
+        d.v_scale_mode = self.v_scale_mode
+        d.v_scales = _ptr(self.v_scales)
+        d.v_scales_row_stride = 0 if self.v_scales is None else self.v_scales.stride(0)
+        d.error_flag = _ptr(self.error_flag)
+        return d
+
+
+def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor]) -> KVLayout:
+    """(rows, S, d) K/V views (last dimension contiguous, any other strides)."""
+    rows, s_len, d = keys.shape
+    if values is not None and values.shape != keys.shape:
+        raise ValueError(f"keys {tuple(keys.shape)} and values {tuple(values.shape)} must have the same shape")
+    keys = last_dim_ready(keys, d)
+    if values is not None:
+        values = last_dim_ready(values, d)
+    return KVLayout(
+        k=keys, v=values, head_dim=d, num_rows=rows, num_tiles=s_len // TILE_SIZE,
+        k_row_stride=keys.stride(0), k_token_stride=keys.stride(1),
+        v_row_stride=0 if values is None else values.stride(0),
+        v_token_stride=0 if values is None else values.stride(1))
+
+
+def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
+                 num_tiles: int) -> KVLayout:
+    """(num_blocks, num_kv_heads, block_size, d) caches + int32 block table."""
+    nb, hkv, bs, d = k_cache.shape
+    if v_cache.shape != k_cache.shape:
+        raise ValueError(f"k_cache {tuple(k_cache.shape)} and v_cache {tuple(v_cache.shape)} must have the same shape")
+    if block_tables.dim() != 2:
+        raise ValueError("block_tables must be 2-D (num_seqs, max_blocks)")
+    k_cache = last_dim_ready(k_cache, d)
+    v_cache = last_dim_ready(v_cache, d)
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if block_tables.stride(-1) != 1:
+        block_tables = block_tables.contiguous()
+    return KVLayout(
+        k=k_cache, v=v_cache, head_dim=d, num_rows=block_tables.shape[0] * hkv, num_tiles=num_tiles,
+        k_token_stride=k_cache.stride(2), v_token_stride=v_cache.stride(2),
+        paged=True, block_size=bs, num_kv_heads=hkv, block_tables=block_tables, num_blocks=nb,
+        k_block_stride=k_cache.stride(0), k_head_stride=k_cache.stride(1),
+        v_block_stride=v_cache.stride(0), v_head_stride=v_cache.stride(1),
+        rows_per_length=hkv)
+
+
+# ---------------------------------------------------------------- workspace
+
+_WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """A reusable device buffer per (device, stream); calls on one stream are
+    ordered, so they can share it."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def current_stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ---------------------------------------------------------------- split count
+
+_CU_COUNT: Dict[int, int] = {}
+
+
+def cu_count(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNT.get(idx)
+    if n is None:
+        n = torch.cuda.get_device_properties(idx).multi_processor_count
+        _CU_COUNT[idx] = n
+    return n
+
+
+def auto_num_splits(num_tiles: int, device: torch.device) -> int:
+    """P = max(1, min(#CU, max(1, T // 4), T)) (fused_eviction.py:556-570)."""
+    return max(1, min(cu_count(device), max(1, num_tiles // 4), num_tiles))
+
+
+# ---------------------------------------------------------------- calls
+
+@dataclass
+class DecodeResult:
+    out: torch.Tensor
+    keep: Optional[torch.Tensor] = None          # (rows, T) uint8
+    split_counts: Optional[torch.Tensor] = None  # (rows, P) int32
+    num_splits: int = 1
+    partials: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None
+
+
+def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float, mode: int = N.OC_MODE_SINGLE_PASS,
+           scores: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_splits: Optional[int] = None,
+           out_dtype: torch.dtype, want_keep: bool = False, want_partials: bool = False,
+           out: Optional[torch.Tensor] = None) -> DecodeResult:
+    """One oc_decode call.  q is (rows*G, d) with a contiguous last dimension."""
+    device = require_gpu(q, kv.k, kv.v)
+    d = kv.head_dim
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    P = num_splits if num_splits is not None else auto_num_splits(kv.num_tiles, device)
+    if not 1 <= P <= MAX_SPLITS:
+        raise ValueError(f"num_splits {P} outside 1..{MAX_SPLITS}")
+    rows_q = kv.num_rows * G
+    if q.dim() != 2 or q.shape[0] != rows_q or q.shape[1] != d:
+        raise ValueError(f"q must be ({rows_q}, {d}) for {kv.num_rows} kv rows x G={G}, got {tuple(q.shape)}")
+    if out is None:
+        out = torch.empty((rows_q, d), dtype=out_dtype, device=device)
+    elif out.shape != (rows_q, d) or out.stride(-1) != 1 or out.device != device:
+        raise ValueError(f"out must be a ({rows_q}, {d}) tensor on {device} with a contiguous last dim")
+    keep = None
+    if want_keep:
+        keep = torch.zeros((kv.num_rows, max(kv.num_tiles, 1)), dtype=torch.uint8, device=device)
+    p = N.OcDecodeParams()
+    p.kv = kv.struct()
+    p.q = q.data_ptr()
+    p.q_dtype = dtype_code(q.dtype, "q", allow_fp8=False)
+    p.G = G
+    p.q_row_stride = q.stride(0)
+    p.gate = gate
+    p.mode = mode
+    p.threshold = float(threshold)
+    if scores is not None:
+        e_low, e_high = scores
+        for e in (e_low, e_high):
+            if (e.dtype != torch.float32 or e.dim() != 2 or e.shape[0] < kv.num_rows or e.shape[1] < kv.num_tiles
+                    or e.stride(1) != 1 or e.device != device or e.stride(0) != e_high.stride(0)):
+                raise ValueError(f"score_cache must hold float32 ({kv.num_rows}, >= {kv.num_tiles}) tensors on "
+                                 f"{device} with equal row strides")
+        p.score_e_low = _ptr(e_low)
+        p.score_e_high = _ptr(e_high)
+        p.score_row_stride = e_high.stride(0)
+    p.num_splits = P
+    p.out_dtype = dtype_code(out.dtype, "out", allow_fp8=False)
+    p.out = out.data_ptr()
+    p.out_row_stride = out.stride(0)
+    p.keep_out = _ptr(keep)
+    p.keep_row_stride = 0 if keep is None else keep.stride(0)
+    partials = None
+    if want_partials:
+        pm = torch.empty((rows_q, P), dtype=torch.float32, device=device)
+        pl = torch.empty((rows_q, P), dtype=torch.float32, device=device)
+        pacc = torch.empty((rows_q, P, d), dtype=torch.float32, device=device)
+        p.partial_m, p.partial_l, p.partial_acc = pm.data_ptr(), pl.data_ptr(), pacc.data_ptr()
+        partials = (pm, pl, pacc)
+    if kv.lengths is not None and kv.lengths.numel() * kv.rows_per_length < kv.num_rows:
+        raise ValueError("lengths has fewer entries than the kv rows need")
+    stream = current_stream(device)
+    lib = N.lib()
+    if not want_partials:
+        need = lib.oc_decode_workspace_size(ctypes.byref(p))
+        ws = workspace(device, stream, need)
+        p.workspace = ws.data_ptr()
+        p.workspace_bytes = ws.numel()
+    with torch.cuda.device(device):
+        N.check("oc_decode", lib.oc_decode(ctypes.byref(p), ctypes.c_void_p(stream)))
+    return DecodeResult(out=out, keep=keep, num_splits=P, partials=partials)
+
+
+def score_tiles(kv: KVLayout, zeta_max: float = 0.0, *, want_zeta: bool = True, want_keep: bool = True):
+    """oc_score_tiles: returns (e_low, e_high, zeta|None, keep|None), each (rows, T)."""
+    device = require_gpu(kv.k)
+    shape = (kv.num_rows, max(kv.num_tiles, 1))
+    e_low = torch.empty(shape, dtype=torch.float32, device=device)
+    e_high = torch.empty(shape, dtype=torch.float32, device=device)
+    zeta = torch.empty(shape, dtype=torch.float32, device=device) if want_zeta else None
+    keep = torch.empty(shape, dtype=torch.uint8, device=device) if want_keep else None
+    desc = kv.struct()
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_score_tiles", N.lib().oc_score_tiles(
+            ctypes.byref(desc), float(zeta_max), e_low.data_ptr(), e_high.data_ptr(), _ptr(zeta),
+            _ptr(keep), e_low.stride(0), ctypes.c_void_p(stream)))
+    return e_low, e_high, zeta, keep
+
+
+def fwht_tiles(kv: KVLayout) -> torch.Tensor:
+    """oc_fwht_tiles: (rows, T, 64, d) float32 spectra X = W64 @ K_tile."""
+    device = require_gpu(kv.k)
+    out = torch.empty((kv.num_rows, kv.num_tiles, TILE_SIZE, kv.head_dim), dtype=torch.float32, device=device)
+    desc = kv.struct()
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_fwht_tiles", N.lib().oc_fwht_tiles(ctypes.byref(desc), out.data_ptr(),
+                                                       ctypes.c_void_p(stream)))
+    return out
+
+
+def lse_merge(m: torch.Tensor, l: torch.Tensor, acc: torch.Tensor, out_dtype=torch.float32) -> torch.Tensor:
+    """oc_lse_merge of (rows, P) / (rows, P, d) float32 partials."""
+    device = require_gpu(m, l, acc)
+    rows, P = m.shape
+    d = acc.shape[-1]
+    m, l, acc = m.contiguous(), l.contiguous(), acc.contiguous()
+    out = torch.empty((rows, d), dtype=out_dtype, device=device)
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_lse_merge", N.lib().oc_lse_merge(
+            m.data_ptr(), l.data_ptr(), acc.data_ptr(), rows, P, d, out.data_ptr(),
+            dtype_code(out_dtype, "out", allow_fp8=False), out.stride(0), ctypes.c_void_p(stream)))
+    return out
+
+
+def counts_metadata(keep: torch.Tensor, tiles_total: int) -> dict:
+    retained = int(keep.sum().item())
+    evicted = tiles_total - retained
+    return {"tiles_retained": retained, "tiles_evicted": evicted,
+            "eviction_rate": evicted / max(1, tiles_total)}
+
+
+def kscale_mode(k_scale, num_rows: int, num_tiles: int, device) -> Tuple[int, float, Optional[torch.Tensor]]:
+    """Scalar k_scale != 1 folds into q (reference semantics); a tensor of
+    per-(row, tile) scales (extension) scales K elements."""
+    if isinstance(k_scale, torch.Tensor):
+        ks = k_scale.to(device=device, dtype=torch.float32).reshape(num_rows, -1)
+        if ks.shape[1] < num_tiles:
+            raise ValueError(f"k_scale has {ks.shape[1]} tiles per row, need {num_tiles}")
+        return N.OC_KSCALE_TILE, 1.0, ks.contiguous()
+    if k_scale != 1.0:
+        return N.OC_KSCALE_Q_FOLD, float(k_scale), None
+    return N.OC_KSCALE_NONE, 1.0, None
+
+
+def vscale_mode(v_scale, num_rows: int, num_tiles: int, device) -> Tuple[int, Optional[torch.Tensor]]:
+    if v_scale is None:
+        return N.OC_VSCALE_NONE, None
+    if not isinstance(v_scale, torch.Tensor):
+        raise TypeError("v_scale must be a tensor of per-(row, tile) float32 scales")
+    vs = v_scale.to(device=device, dtype=torch.float32).reshape(num_rows, -1)
+    if vs.shape[1] < num_tiles:
+        raise ValueError(f"v_scale has {vs.shape[1]} tiles per row, need {num_tiles}")
+    return N.OC_VSCALE_TILE, vs.contiguous()

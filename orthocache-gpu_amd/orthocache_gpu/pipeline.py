@@ -1,0 +1,254 @@
+"""orthocache_forward for MI355X (modes 'triton_fused' and 'dense').
+
+Drop-in for src/orthocache_gpu/pipeline.py of the reference for the decode
+path: same signature, BypassFlag / TelemetryLevel / GPUProfile types,
+crossover bypass and metadata.  'triton_fused' runs the zeta-gated split-K
+decode (fused_orthocache_attention_v2) on a strided (heads, seq, dim) view
+of the (seq, heads, dim) caches -- no permute().contiguous() copy
+(pipeline.py:437-439 copies all of K and V on every call).  'dense' runs the
+same decode kernel with the gate off.  The 512-token 'compact' mode and its
+spectral pipeline are not part of this build and raise NotImplementedError.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import enum
+import math
+import time
+
+import torch
+
+from . import _launch as X
+from . import _native as N
+
+
+class BypassFlag(enum.IntFlag):
+    """Bitmask flags for bypass/dispatch decisions (pipeline.py:62-72)."""
+    NONE = 0
+    CROSSOVER_BYPASS = 1 << 0
+    DENSE_EXPLICIT = 1 << 1
+    TRITON_FUSED = 1 << 2
+    SPECTRAL_EVICTION = 1 << 3
+    ZERO_ACTIVE = 1 << 4
+    TAU_AUTO = 1 << 5
+    PERFECT_EVICTION = 1 << 6
+    HW_AUTO_DETECTED = 1 << 7
+
+
+class TelemetryLevel(enum.IntEnum):
+    """Metadata verbosity (pipeline.py:75-84)."""
+    SILENT = 0
+    FLAGS = 1
+    VERBOSE = 2
+
+
+def format_bypass_reason(flags: BypassFlag, seq_len_k: int = 0, threshold: int = 0, profile=None) -> str:
+    """Human-readable form of a BypassFlag mask (pipeline.py:87-117)."""
+    parts = []
+    if flags & BypassFlag.CROSSOVER_BYPASS:
+        p = f"seq_len_k={seq_len_k} < crossover={threshold}"
+        if profile:
+            p += f" on {profile.name} ({profile.sm_count} CUs, {profile.mem_bandwidth_gbps:.0f} GB/s)"
+        parts.append(p)
+    if flags & BypassFlag.DENSE_EXPLICIT:
+        parts.append("mode=dense (explicit)")
+    if flags & BypassFlag.TRITON_FUSED:
+        parts.append("mode=triton_fused (gated split-K decode)")
+    if flags & BypassFlag.SPECTRAL_EVICTION:
+        parts.append("full spectral eviction path")
+    if flags & BypassFlag.ZERO_ACTIVE:
+        parts.append("all blocks evicted")
+    if flags & BypassFlag.TAU_AUTO:
+        parts.append("tau auto-computed (mean - 1σ)")
+    if flags & BypassFlag.HW_AUTO_DETECTED:
+        parts.append("GPU auto-detected via bandwidth-ratio model")
+    return "; ".join(parts) if parts else "no flags set"
+
+
+@dataclasses.dataclass(frozen=True)
+class GPUProfile:
+    """Hardware profile for the crossover threshold (pipeline.py:121-129)."""
+    name: str
+    sm_count: int
+    mem_bandwidth_gbps: float
+    sram_per_sm_kb: float
+    crossover_seq_len: int
+    compute_class: str
+
+
+# Known profiles.  The MI355X row is this build's own target; the others are
+# the reference's table (pipeline.py:139-203) kept for API compatibility.
+_GPU_PROFILES = {
+    "MI355X": GPUProfile("MI355X", 256, 8000.0, 160.0, 1024, "datacenter"),
+    "RTX 4060 Laptop": GPUProfile("RTX 4060 Laptop", 24, 256, 100, 4096, "consumer"),
+    "RTX 4060": GPUProfile("RTX 4060", 24, 272, 100, 4096, "consumer"),
+    "RTX 4070": GPUProfile("RTX 4070", 46, 504, 100, 3072, "consumer"),
+    "RTX 4080": GPUProfile("RTX 4080", 76, 717, 100, 2048, "consumer"),
+    "RTX 4090": GPUProfile("RTX 4090", 128, 1008, 100, 2048, "consumer"),
+    "A100": GPUProfile("A100", 108, 2039, 164, 2048, "datacenter"),
+    "H100": GPUProfile("H100", 132, 3350, 228, 1024, "datacenter"),
+    "H200": GPUProfile("H200", 132, 4800, 228, 1024, "datacenter"),
+    "B200": GPUProfile("B200", 192, 8000, 256, 512, "hpc"),
+    "GB200": GPUProfile("GB200", 192, 8000, 256, 512, "hpc"),
+}
+_REFERENCE_PROFILE = _GPU_PROFILES["RTX 4060 Laptop"]
+CROSSOVER_SEQ_LEN = _REFERENCE_PROFILE.crossover_seq_len
+
+
+def _detect_gpu_profile(device=None) -> GPUProfile:
+    """Profile of the current GPU (pipeline.py:209-280).  gfx950 parts map to
+    the MI355X row; unknown GPUs get the reference's bandwidth-ratio estimate,
+    read from `total_memory` (the reference reads a `total_mem` attribute
+    that torch does not have, pipeline.py:245)."""
+    if not torch.cuda.is_available():
+        return _REFERENCE_PROFILE
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    idx = device.index if device.index is not None else 0
+    props = torch.cuda.get_device_properties(idx)
+    name = props.name or ""
+    arch = getattr(props, "gcnArchName", "") or ""
+    if "gfx950" in arch or "MI355" in name or "MI350" in name:
+        base = _GPU_PROFILES["MI355X"]
+        return dataclasses.replace(base, sm_count=props.multi_processor_count)
+    for key, prof in _GPU_PROFILES.items():
+        if key in name:
+            return prof
+    total_mem_gb = props.total_memory / (1024 ** 3)
+    if total_mem_gb > 80:
+        est_bw = 4000.0
+    elif total_mem_gb > 48:
+        est_bw = 2500.0
+    elif total_mem_gb > 16:
+        est_bw = 700.0
+    else:
+        est_bw = 300.0
+    sm = props.multi_processor_count
+    raw = _REFERENCE_PROFILE.crossover_seq_len * (est_bw / _REFERENCE_PROFILE.mem_bandwidth_gbps) * (
+        _REFERENCE_PROFILE.sm_count / max(sm, 1))
+    clamped = max(512, min(8192, int(raw)))
+    crossover = 1 << int(math.log2(clamped) + 0.5)
+    return GPUProfile(f"{name} (auto-detected)", sm, est_bw, 100.0, crossover, "unknown")
+
+
+_cached_profile = None
+
+
+def get_hardware_profile(device=None) -> GPUProfile:
+    global _cached_profile
+    if _cached_profile is None:
+        _cached_profile = _detect_gpu_profile(device)
+    return _cached_profile
+
+
+def get_crossover_threshold(device=None) -> int:
+    return get_hardware_profile(device).crossover_seq_len
+
+
+def _dense_attention(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, head_dim: int) -> torch.Tensor:
+    """Dense softmax attention of every query token over every key
+    (pipeline.py:558-568), on the HIP decode kernel with the gate off.
+    q (Sq, H, d), keys/values (S, H, d) -> (Sq, H, d) in q.dtype."""
+    sq, h, d = q.shape
+    s_len = keys.shape[0]
+    k_rows = keys.permute(1, 0, 2)
+    v_rows = values.permute(1, 0, 2)
+    pad = (-s_len) % X.TILE_SIZE
+    kv = X.rows_layout(k_rows, v_rows)
+    kv.num_tiles = (s_len + pad) // X.TILE_SIZE
+    lengths = None
+    if pad:
+        # a partial last tile is masked by the per-row length; the kernel
+        # never reads tokens past the length for whole 4-token groups, the
+        # rest of the group stays inside the row's allocation when S % 4 == 0
+        if s_len % 4:
+            k_rows = torch.nn.functional.pad(k_rows, (0, 0, 0, pad))
+            v_rows = torch.nn.functional.pad(v_rows, (0, 0, 0, pad))
+            kv = X.rows_layout(k_rows, v_rows)
+        lengths = torch.full((h,), s_len, dtype=torch.int32, device=q.device)
+        kv.lengths = lengths
+        kv.num_tiles = (s_len + pad) // X.TILE_SIZE
+    outs = []
+    for s0 in range(0, sq, 64):
+        qq = q[s0:s0 + 64].permute(1, 0, 2).contiguous()  # (H, g, d)
+        g = qq.shape[1]
+        res = X.decode(kv, qq.reshape(h * g, d), g, gate=N.OC_GATE_NONE, threshold=0.0,
+                       out_dtype=q.dtype)
+        outs.append(res.out.view(h, g, d).permute(1, 0, 2))
+    return torch.cat(outs, dim=0)
+
+
+def orthocache_forward(
+    q: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    block_size: int = 512,
+    zeta_max: float = 5.0,
+    tau=None,
+    mode: str = "compact",
+    crossover_threshold: int = 0,
+    telemetry: TelemetryLevel = TelemetryLevel.FLAGS,
+):
+    """OrthoCache decode entry point (pipeline.py:312-456).
+
+    q (Sq, H, d), keys/values (S, H, d).  mode='triton_fused' decodes the
+    first query token with the zeta-gated split-K kernel and returns
+    (1, H, d); mode='dense' returns dense attention (Sq, H, d).
+    """
+    seq_len_k, num_heads, head_dim = keys.shape
+    seq_len_q = q.shape[0]
+    num_blocks = seq_len_k // block_size
+    crossover_fallback = False
+    original_mode = mode
+    if seq_len_k < crossover_threshold and mode in ("compact", "triton_fused"):
+        mode = "dense"
+        crossover_fallback = True
+    if telemetry == TelemetryLevel.SILENT:
+        metadata: dict = {}
+    else:
+        metadata = {
+            "mode": original_mode,
+            "actual_mode": mode,
+            "crossover_fallback": crossover_fallback,
+            "crossover_threshold": crossover_threshold,
+            "seq_len_q": seq_len_q,
+            "seq_len_k": seq_len_k,
+            "num_blocks": num_blocks,
+            "num_heads": num_heads,
+            "head_dim": head_dim,
+            "block_size": block_size,
+            "zeta_max": zeta_max,
+        }
+    if mode == "dense":
+        t0 = time.perf_counter()
+        output = _dense_attention(q, keys, values, head_dim)
+        torch.cuda.synchronize(q.device)
+        metadata["latency_ms"] = (time.perf_counter() - t0) * 1000
+        metadata["eviction_rate"] = 0.0
+        return output, metadata
+    hw_profile = get_hardware_profile(q.device)
+    if mode == "triton_fused":
+        from .triton_kernels.fused_eviction import fused_orthocache_attention_v2
+        t0 = time.perf_counter()
+        q_heads = q[0]
+        k_heads = keys.permute(1, 0, 2)
+        v_heads = values.permute(1, 0, 2)
+        output_heads, fused_meta = fused_orthocache_attention_v2(q_heads, k_heads, v_heads, zeta_max=zeta_max)
+        output = output_heads.unsqueeze(0)
+        tile_size = 64
+        metadata["latency_ms"] = (time.perf_counter() - t0) * 1000
+        metadata["eviction_rate"] = fused_meta.get("eviction_rate", 0.0)
+        metadata["tile_size_fused"] = tile_size
+        metadata["num_tiles_fused"] = seq_len_k // tile_size
+        metadata["num_splits"] = fused_meta.get("num_splits", 1)
+        metadata["tile_assignment"] = "interleaved"
+        if telemetry >= TelemetryLevel.FLAGS and telemetry != TelemetryLevel.SILENT:
+            metadata["bypass_flags"] = int(BypassFlag.TRITON_FUSED)
+            metadata["gpu_profile"] = hw_profile.name
+        return output, metadata
+    if mode == "compact":
+        raise NotImplementedError(
+            "orthocache_forward(mode='compact') (512-token spectral compaction) is not part of the "
+            "MI355X build; use mode='triton_fused' or mode='dense'")
+    raise ValueError(f"Unknown mode: {mode!r}. Use 'dense', 'compact', or 'triton_fused'.")

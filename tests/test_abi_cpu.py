@@ -1,0 +1,121 @@
+"""CPU tests of the boundary: the C-ABI library loads and exports every
+function include/orthocache_hip.h declares, the binding's struct layout
+matches, and the drop-in entry points raise the reference's assertion
+messages (these checks run before any GPU work).  No kernel is launched."""
+
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "orthocache_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(oc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_api():
+    names = _declared()
+    for n in ("oc_score_tiles", "oc_fwht_tiles", "oc_decode", "oc_decode_workspace_size", "oc_lse_merge",
+              "oc_device_cu_count", "oc_version", "oc_last_error", "oc_abi_sizes"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import ctypes
+    from orthocache_gpu import _native as N
+    lib = ctypes.CDLL(N.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in N.SIGNATURES, f"binding lacks {name}"
+
+
+def test_struct_layout_matches_library():
+    import ctypes
+    from orthocache_gpu import _native as N
+    N.lib()  # raises on a mismatch
+    kv, p = ctypes.c_size_t(), ctypes.c_size_t()
+    assert N.lib().oc_abi_sizes(ctypes.byref(kv), ctypes.byref(p)) == 0
+    assert kv.value == ctypes.sizeof(N.OcKvDesc)
+    assert p.value == ctypes.sizeof(N.OcDecodeParams)
+    assert "gfx950" in N.version()
+
+
+def test_invalid_arguments_return_status_and_message():
+    """Validation runs on the host; a bad call returns OC_ERR_* and a message."""
+    import ctypes
+    from orthocache_gpu import _native as N
+    p = N.OcDecodeParams()
+    p.kv.head_dim = 128
+    rc = N.lib().oc_decode(ctypes.byref(p), None)
+    assert rc == N.OC_ERR_INVALID
+    assert b"NULL" in N.lib().oc_last_error()
+    p.kv.dtype, p.kv.head_dim, p.kv.k = N.OC_BF16, 96, 256
+    assert N.lib().oc_decode(ctypes.byref(p), None) == N.OC_ERR_UNSUPPORTED
+    assert b"head_dim" in N.lib().oc_last_error()
+    with pytest.raises(N.OrthoCacheHIPError, match="oc_decode"):
+        N.check("oc_decode", N.lib().oc_decode(ctypes.byref(p), None))
+
+
+def test_reference_assertion_messages():
+    """test_fp8.py:128-158 and test_paged_eviction.py:139-159 of the reference."""
+    from orthocache_gpu import (fused_orthocache_attention, fused_orthocache_attention_paged,
+                                fused_orthocache_attention_v2, fused_orthocache_attention_v3_gqa)
+    q = torch.randn(1, 128)
+    keys = torch.randn(256, 128)
+    with pytest.raises(AssertionError, match="head_dim.*must be a power of 2"):
+        fused_orthocache_attention(torch.randn(1, 100), torch.randn(256, 100), torch.randn(256, 100), 5.0)
+    with pytest.raises(AssertionError, match="tile_size.*must be a power of 2"):
+        fused_orthocache_attention(q, keys, keys, zeta_max=5.0, tile_size=50)
+    with pytest.raises(AssertionError, match="not divisible by tile_size"):
+        fused_orthocache_attention(q, torch.randn(250, 128), torch.randn(250, 128), 5.0, tile_size=64)
+    with pytest.raises(AssertionError, match="num_splits.*greater than 0"):
+        fused_orthocache_attention_v2(torch.randn(2, 128), torch.randn(2, 256, 128), torch.randn(2, 256, 128),
+                                      5.0, num_splits=0)
+    with pytest.raises(AssertionError, match="num_query_heads"):
+        fused_orthocache_attention_v3_gqa(torch.randn(16, 128), torch.randn(4, 256, 128),
+                                          torch.randn(4, 256, 128), tau=1.0, num_query_groups=8)
+    bt = torch.tensor([[0, 1]], dtype=torch.int32)
+    with pytest.raises(AssertionError, match="head_dim.*power of 2"):
+        fused_orthocache_attention_paged(torch.randn(1, 2, 63), torch.randn(4, 2, 32, 63),
+                                         torch.randn(4, 2, 32, 63), bt, zeta_max=5.0)
+    with pytest.raises(AssertionError, match="block_size.*power of 2"):
+        fused_orthocache_attention_paged(torch.randn(1, 2, 64), torch.randn(4, 2, 31, 64),
+                                         torch.randn(4, 2, 31, 64), bt, zeta_max=5.0)
+
+
+def test_cpu_tensors_fail_loudly():
+    """No CPU fallback: the product path refuses host tensors."""
+    from orthocache_gpu import fused_orthocache_attention_v2, triton_fwht_eviction
+    with pytest.raises(RuntimeError, match="GPU"):
+        fused_orthocache_attention_v2(torch.randn(2, 128), torch.randn(2, 256, 128), torch.randn(2, 256, 128), 5.0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        triton_fwht_eviction(torch.randn(256, 128), 5.0)
+
+
+def test_pipeline_host_logic():
+    from orthocache_gpu import BypassFlag, TelemetryLevel, format_bypass_reason, get_hardware_profile
+    from orthocache_gpu.pipeline import _GPU_PROFILES, orthocache_forward
+    assert _GPU_PROFILES["MI355X"].sm_count == 256
+    if not torch.cuda.is_available():
+        assert get_hardware_profile().name == "RTX 4060 Laptop"
+    assert "crossover" in format_bypass_reason(BypassFlag.CROSSOVER_BYPASS, 100, 4096)
+    assert TelemetryLevel.SILENT < TelemetryLevel.FLAGS < TelemetryLevel.VERBOSE
+    q = torch.randn(1, 2, 64)
+    k = torch.randn(1024, 2, 64)
+    with pytest.raises(NotImplementedError, match="compact"):
+        orthocache_forward(q, k, k, mode="compact")
+    with pytest.raises(ValueError, match="Unknown mode"):
+        orthocache_forward(q, k, k, mode="bogus")
+
+
+def test_walsh_matrix_api():
+    from orthocache_gpu import generate_walsh_matrix
+    w = generate_walsh_matrix(64)
+    assert torch.allclose(w @ w.T, torch.eye(64), atol=1e-6)
+    assert torch.all(w[0] == 0.125)

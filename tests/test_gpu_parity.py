@@ -1,0 +1,459 @@
+"""GPU parity: the HIP path (through liborthocache_hip's C ABI) against the
+oracle and the reference's golden vectors.
+
+Bars: eviction masks, tile assignment and counts
+bit-exact; outputs within 1e-5 (fp32), 2e-3 (fp16/bf16 outputs, compared
+after rounding the oracle to the output dtype: one output ulp plus 2e-3
+absolute), 2e-2 (fp8 inputs) max-abs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import orthocache_oracle as O
+from tests import golden_io
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {"f32": 1e-5, "f16": 2e-3, "bf16": 2e-3, "fp8": 2e-2}
+TORCH_DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16, "fp8": torch.float8_e4m3fn}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import orthocache_gpu._native as N
+    N.lib()
+    yield
+
+
+def np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def out_tol(dtype_name, ref):
+    """tolerance for an output stored in `dtype_name`: bar + one ulp of the value"""
+    bar = TOL[dtype_name]
+    if dtype_name == "bf16":
+        return bar + np.abs(ref) * 2.0 ** -8
+    if dtype_name == "f16":
+        return bar + np.abs(ref) * 2.0 ** -11
+    return bar
+
+
+def assert_out(got, ref, dtype_name, what=""):
+    got = np32(got) if isinstance(got, torch.Tensor) else got
+    ref = np.asarray(ref, dtype=np.float32).reshape(got.shape)
+    err = np.abs(got - ref)
+    tol = out_tol(dtype_name, ref)
+    bad = err > tol
+    assert not bad.any(), f"{what}: max err {err.max():.3g} (tol {np.max(tol):.3g}) at {np.argwhere(bad)[:4]}"
+
+
+def to_dev(raw, dt):
+    """golden raw array -> device tensor of the stored dtype"""
+    if dt == "f32":
+        return torch.from_numpy(raw.astype(np.float32)).to(DEV)
+    if dt in ("f16", "bf16"):
+        return torch.from_numpy(raw.astype(np.uint16).view(np.int16)).view(TORCH_DT[dt]).to(DEV)
+    if dt == "fp8":
+        return torch.from_numpy(raw.astype(np.uint8)).view(torch.float8_e4m3fn).to(DEV)
+    if dt == "i32":
+        return torch.from_numpy(raw.astype(np.int32)).to(DEV)
+    raise ValueError(dt)
+
+
+# ---------------------------------------------------------------- library
+
+def test_library_and_device():
+    import orthocache_gpu._native as N
+    assert "gfx950" in N.version()
+    props = torch.cuda.get_device_properties(0)
+    assert N.device_cu_count() == props.multi_processor_count
+
+
+def test_fp8_decode_is_exact():
+    """fwht of a tile whose only non-zero token is token 0 gives k0/8 in every
+    spectral row, so row 0 of the transform reads back the decoded fp8 codes."""
+    from orthocache_gpu import fwht_tiles
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    k = torch.zeros((2 * 64, 128), dtype=torch.uint8)
+    k[0] = codes[:128]
+    k[64] = codes[128:]
+    x = fwht_tiles(k.view(torch.float8_e4m3fn).to(DEV))
+    got = np.concatenate([np32(x[0, 0]), np32(x[1, 0])]) * 8.0
+    ref = O.fp8_e4m3fn_table()
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+
+
+# ---------------------------------------------------------------- scores / FWHT
+
+def test_golden_scores_bit_exact_mask():
+    from orthocache_gpu import triton_fwht_eviction
+    raw, dec, dt, meta, params, _ = golden_io.load("fwht_scores")
+    keys = to_dev(raw["keys"], "f32")
+    mask, zeta = triton_fwht_eviction(keys, params["zeta_max"], return_zeta=True)
+    assert np.array_equal(mask.cpu().numpy(), dec["mask"].astype(bool))
+    np.testing.assert_allclose(np32(zeta), dec["zeta"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_integer_tiles_scores_exact(dtype, d):
+    """Integer tiles in [-4, 4]: exact in every summation order, so e_low,
+    e_high and zeta must equal the float64 closed forms bit for bit."""
+    from orthocache_gpu import score_tiles
+    rng = np.random.default_rng(d)
+    k = rng.integers(-4, 5, size=(3, 8 * 64, d)).astype(np.float32)
+    sc = score_tiles(torch.from_numpy(k).to(TORCH_DT[dtype]).to(DEV), zeta_max=1.0)
+    for r in range(3):
+        for t in range(8):
+            kt = k[r, t * 64:(t + 1) * 64].astype(np.float64)
+            eh = 0.5 * np.sum((kt[:32] - kt[32:]) ** 2)
+            s_r = np.stack([kt[i::8].sum(axis=0) for i in range(8)])
+            el = np.sum(s_r ** 2) / 8.0 - np.sum(kt.sum(axis=0) ** 2) / 64.0
+            assert float(sc.e_high[r, t]) == eh
+            assert float(sc.e_low[r, t]) == el
+            z = np.float32(np.float32(eh) / np.float32(np.float32(el) + np.float32(1e-6)))
+            assert float(sc.zeta[r, t]) == float(z)
+            assert bool(sc.keep[r, t]) == (not float(z) > 1.0)
+
+
+def test_fwht_full_transform():
+    from orthocache_gpu import fwht_tiles
+    rng = np.random.default_rng(4)
+    k = rng.standard_normal((5 * 64, 128)).astype(np.float32)
+    x = np32(fwht_tiles(torch.from_numpy(k).to(DEV)))
+    w = O.walsh_matrix().astype(np.float64)
+    for t in range(5):
+        ref = w @ k[t * 64:(t + 1) * 64].astype(np.float64)
+        np.testing.assert_allclose(x[t], ref, atol=2e-5)
+        np.testing.assert_allclose(x[t], O.fwht64_butterfly(k[t * 64:(t + 1) * 64]), atol=2e-5)
+
+
+# ---------------------------------------------------------------- golden cases
+
+@pytest.mark.parametrize("name", ["v1_f32", "v1_fp8k_bf16q"])
+def test_golden_v1(name):
+    from orthocache_gpu import fused_orthocache_attention
+    raw, dec, dt, meta, params, _ = golden_io.load(name)
+    out, m = fused_orthocache_attention(to_dev(raw["q"], dt["q"]), to_dev(raw["keys"], dt["keys"]),
+                                        to_dev(raw["values"], dt["values"]), params["zeta_max"],
+                                        return_mask=True, k_scale=params.get("k_scale", 1.0))
+    assert np.array_equal(m["eviction_mask"].cpu().numpy(), meta["eviction_mask"])
+    for k in ("tiles_retained", "tiles_evicted", "eviction_rate"):
+        assert m[k] == meta[k]
+    bar = "fp8" if dt["keys"] == "fp8" else dt["out"]
+    assert_out(out, dec["out"], bar, name)
+
+
+@pytest.mark.parametrize("name", ["v2_f32", "v2_f16", "v2_bf16"])
+def test_golden_v2(name):
+    from orthocache_gpu import fused_orthocache_attention_v2
+    raw, dec, dt, meta, params, _ = golden_io.load(name)
+    out, m = fused_orthocache_attention_v2(to_dev(raw["q"], dt["q"]), to_dev(raw["keys"], dt["keys"]),
+                                           to_dev(raw["values"], dt["values"]), params["zeta_max"])
+    for k, v in meta.items():
+        assert m[k] == v, k
+    assert m["tile_assignment"] == "interleaved"
+    assert_out(out, dec["out"], dt["out"], name)
+
+
+@pytest.mark.parametrize("name", ["v3_f32", "v3_bf16", "v3_fp8k"])
+def test_golden_v3(name):
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa
+    raw, dec, dt, meta, params, _ = golden_io.load(name)
+    out, m = fused_orthocache_attention_v3_gqa(
+        to_dev(raw["q"], dt["q"]), to_dev(raw["keys"], dt["keys"]), to_dev(raw["values"], dt["values"]),
+        params["tau"], params["G"], k_scale=params.get("k_scale", 1.0))
+    for k, v in meta.items():
+        assert m[k] == v, k
+    bar = "fp8" if dt["keys"] == "fp8" else dt["out"]
+    assert_out(out, dec["out"], bar, name)
+
+
+@pytest.mark.parametrize("name", ["paged_bs16", "paged_bs32", "paged_fp8k"])
+def test_golden_paged(name):
+    from orthocache_gpu import fused_orthocache_attention_paged
+    raw, dec, dt, meta, params, _ = golden_io.load(name)
+    out, m = fused_orthocache_attention_paged(
+        to_dev(raw["q"], dt["q"]), to_dev(raw["k_cache"], dt["k_cache"]), to_dev(raw["v_cache"], dt["v_cache"]),
+        to_dev(raw["block_tables"], "i32"), params["zeta_max"], k_scale=params.get("k_scale", 1.0))
+    assert m["layout"] == "paged"
+    bar = "fp8" if dt["k_cache"] == "fp8" else dt["out"]
+    assert_out(out, dec["out"], bar, name)
+
+
+# ---------------------------------------------------------------- random vs oracle
+
+def _mixed(rows, tiles, d, dtype, seed, noise_frac=0.5):
+    from orthocache_gpu.workloads import make_kv
+    return make_kv(rows, tiles * 64, d, noise_frac=noise_frac, dtype=TORCH_DT[dtype], seed=seed)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("num_splits", [None, 1, 3, 7, 40])
+def test_v2_random_vs_oracle(dtype, d, num_splits):
+    from orthocache_gpu import fused_orthocache_attention_v2
+    wl = _mixed(3, 21, d, dtype, seed=5)
+    q = torch.randn((3, d), generator=torch.Generator().manual_seed(2)).to(TORCH_DT[dtype])
+    out, m = fused_orthocache_attention_v2(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), 5.0,
+                                           num_splits=num_splits)
+    ref, rmeta, rmask = O.fused_v2(np32(q), np32(wl.keys), np32(wl.values), 5.0)
+    assert np.array_equal(m["eviction_mask"].cpu().numpy(), rmask)
+    assert np.array_equal(rmask, ~wl.noise.numpy())
+    for k in ("tiles_retained", "tiles_evicted", "eviction_rate"):
+        assert m[k] == rmeta[k]
+    assert_out(out, O.round_to(ref, dtype), dtype, "v2")
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 8, 12])
+@pytest.mark.parametrize("mode", ["single_pass", "cached"])
+def test_v3_random_vs_oracle(G, mode):
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa, score_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_q
+    wl = _mixed(2, 17, 128, "bf16", seed=G)
+    q = make_q(2, G, 128, dtype=torch.bfloat16, seed=G + 1, low_band_heads=min(2, G))
+    sc = score_tiles(wl.keys.to(DEV))
+    tau = calibrate_tau(sc.e_high, q.to(DEV), G)
+    out, m = fused_orthocache_attention_v3_gqa(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), tau, G,
+                                               mode=mode, score_cache=sc)
+    ref, rmeta, rmask = O.gqa_v3(np32(q), np32(wl.keys), np32(wl.values), tau, G)
+    assert np.array_equal(m["eviction_mask"].cpu().numpy(), rmask)
+    assert np.array_equal(rmask, wl.noise.numpy())  # CS keeps the noise tiles
+    for k in ("tiles_retained", "tiles_evicted", "eviction_rate", "num_kv_heads", "num_query_groups",
+              "gate_type"):
+        assert m[k] == rmeta[k]
+    assert_out(out, O.round_to(ref, "bf16"), "bf16", f"v3 G={G} {mode}")
+
+
+@pytest.mark.parametrize("gate", ["none", "zeta", "cs"])
+@pytest.mark.parametrize("P", [1, 2, 5, 16])
+def test_split_partials_and_assignment(gate, P):
+    """The partial state of split s covers exactly tiles {s + kP}: compare
+    every (m, l, acc) partial with the oracle's per-split online softmax."""
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa
+    G = 2
+    wl = _mixed(2, 13, 64, "f32", seed=P)
+    q = torch.randn((4, 64), generator=torch.Generator().manual_seed(P))
+    thr = {"none": 0.0, "zeta": 5.0, "cs": 150.0}[gate]
+    if gate == "cs":
+        out, m = fused_orthocache_attention_v3_gqa(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), thr, G,
+                                                   num_splits=P, return_partials=True)
+    else:
+        import orthocache_gpu._launch as X
+        import orthocache_gpu._native as N
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+        res = X.decode(kv, q.to(DEV), G, gate={"none": N.OC_GATE_NONE, "zeta": N.OC_GATE_ZETA}[gate],
+                       threshold=thr, num_splits=P, out_dtype=torch.float32, want_keep=True,
+                       want_partials=True)
+        torch.cuda.synchronize()
+        m = {"partials": res.partials}
+        out = res.out
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate=gate, threshold=thr, G=G,
+                        num_splits=P, want_partials=True)
+    pm, pl, pacc = (np32(x) for x in m["partials"])
+    assert np.array_equal(pm == np.float32(-1e9), ref["M"] == np.float32(-1e9))  # same empty splits
+    np.testing.assert_allclose(pm, ref["M"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(pl, ref["L"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(pacc, ref["ACC"], rtol=1e-5, atol=1e-5)
+    assert_out(out, ref["out"], "f32", "merged")
+
+
+def test_v1_matches_oracle_and_reference_edge_cases():
+    from orthocache_gpu import fused_orthocache_attention
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(1, 128, generator=g)
+    k = torch.randn(8 * 64, 128, generator=g)
+    v = torch.randn(8 * 64, 128, generator=g)
+    # zero eviction == dense (test_fused_integration.py:59-104)
+    out, m = fused_orthocache_attention(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=1e9, return_mask=True)
+    assert m["tiles_evicted"] == 0 and m["tiles_retained"] == 8
+    assert_out(out, O.dense_decode(np32(q), np32(k)[None], np32(v)[None]), "f32", "dense")
+    # total eviction -> zeros, no NaN (test_fused_integration.py:290-306)
+    out, m = fused_orthocache_attention(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=0.001, return_mask=True)
+    assert m["tiles_retained"] == 0 and torch.all(out == 0)
+    # large logits (x100), single tile
+    out, _ = fused_orthocache_attention((q * 100).to(DEV), (k[:256] * 100).to(DEV), v[:256].to(DEV), 1e9)
+    assert torch.isfinite(out).all()
+    ref = O.dense_decode(np32(q * 100), np32(k[:256] * 100)[None], np32(v[:256])[None])
+    assert_out(out, ref, "f32", "large logits")
+    out, _ = fused_orthocache_attention(q.to(DEV), k[:64].to(DEV), v[:64].to(DEV), 1e9)
+    assert torch.isfinite(out).all()
+
+
+def test_v2_zeta_max_zero_and_many_splits():
+    from orthocache_gpu import fused_orthocache_attention_v2
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(1, 128, generator=g)
+    k = torch.randn(1, 512, 128, generator=g)
+    v = torch.randn(1, 512, 128, generator=g)
+    out, m = fused_orthocache_attention_v2(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=0.0, num_splits=4)
+    assert out.shape == (1, 128) and torch.isfinite(out).all()
+    out1, _ = fused_orthocache_attention_v2(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=1e6, num_splits=1)
+    out16, m16 = fused_orthocache_attention_v2(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=1e6, num_splits=16)
+    assert m16["num_splits"] == 16
+    assert_out(out16, np32(out1), "f32", "1 vs 16 splits")
+    assert_out(out1, O.dense_decode(np32(q), np32(k), np32(v)), "f32", "dense")
+
+
+def test_auto_num_splits_on_device():
+    from orthocache_gpu import fused_orthocache_attention_v2
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for tiles, want in ((4, 1), (128, 32), (512, min(cus, 128)), (2048, min(cus, 512))):
+        q = torch.zeros(1, 64, device=DEV)
+        k = torch.zeros(1, tiles * 64, 64, device=DEV)
+        _, m = fused_orthocache_attention_v2(q, k, k, 5.0)
+        assert m["num_splits"] == want == O.auto_num_splits(tiles, cus)
+
+
+def test_context_lengths_vs_oracle():
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa
+    wl = _mixed(3, 6, 128, "f32", seed=9)
+    q = torch.randn((6, 128), generator=torch.Generator().manual_seed(3))
+    lens = torch.tensor([150, 384, 1], dtype=torch.int32)
+    out, m = fused_orthocache_attention_v3_gqa(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), 150.0, 2,
+                                               context_lens=lens.to(DEV), num_splits=3)
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate="cs", threshold=150.0, G=2,
+                        lengths=lens.tolist(), num_splits=3)
+    assert_out(out, ref["out"], "f32", "lengths")
+    assert m["tiles_retained"] == ref["retained"]
+    assert m["tiles_evicted"] == ref["evicted"]
+
+
+@pytest.mark.parametrize("block_size", [8, 16, 32, 64, 128])
+def test_paged_equals_contiguous(block_size):
+    """Shuffled physical pool == contiguous rows (test_paged_eviction.py:28-90)."""
+    from orthocache_gpu import fused_orthocache_attention_paged, fused_orthocache_attention_v2
+    from orthocache_gpu.workloads import paged_pool
+    B, H, d = 2, 4, 64
+    wl = _mixed(B * H, 4, d, "f32", seed=block_size)
+    q = torch.randn((B, H, d), generator=torch.Generator().manual_seed(1))
+    kc, vc, bt = paged_pool(wl.keys, wl.values, H, block_size, [256] * B, seed=3)
+    out, m = fused_orthocache_attention_paged(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), 5.0)
+    ref = torch.stack([fused_orthocache_attention_v2(q[b].to(DEV), wl.keys[b * H:(b + 1) * H].to(DEV),
+                                                     wl.values[b * H:(b + 1) * H].to(DEV), 5.0)[0]
+                       for b in range(B)])
+    torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+    oref, _, omask = O.paged(np32(q), np32(kc), np32(vc), bt.numpy(), 5.0)
+    assert_out(out, oref, "f32", "paged vs oracle")
+    assert m["tiles_retained"] == int(omask.sum())
+
+
+@pytest.mark.parametrize("mode", ["single_pass", "cached"])
+def test_paged_gqa_context_lens_cs(mode):
+    """Extension: GQA + per-sequence lengths + CS gate on a 16-token page pool
+    (config 3's recipe at small size)."""
+    from orthocache_gpu import fused_orthocache_attention_paged, score_paged_tiles
+    from orthocache_gpu.workloads import make_q, paged_pool
+    B, Hkv, G, d, tiles = 3, 2, 4, 128, 9
+    wl = _mixed(B * Hkv, tiles, d, "bf16", seed=21, noise_frac=0.4)
+    lens = [576, 300, 64 * 5]
+    kc, vc, bt = paged_pool(wl.keys, wl.values, Hkv, 16, lens, seed=4)
+    q = make_q(B * Hkv, G, d, seed=5)
+    sc = score_paged_tiles(kc.to(DEV), bt.to(DEV), context_lens=torch.tensor(lens).to(DEV))
+    out, m = fused_orthocache_attention_paged(q.view(B, Hkv * G, d).to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV),
+                                              5.0, num_query_groups=G, tau=150.0,
+                                              context_lens=torch.tensor(lens, dtype=torch.int32).to(DEV),
+                                              mode=mode, score_cache=sc)
+    row_lens = [lens[r // Hkv] for r in range(B * Hkv)]
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate="cs", threshold=150.0, G=G,
+                        lengths=row_lens)
+    assert_out(out.view(B * Hkv * G, d), O.round_to(ref["out"], "bf16"), "bf16", "paged gqa")
+    assert m["tiles_retained"] == ref["retained"] and m["tiles_evicted"] == ref["evicted"]
+
+
+@pytest.mark.parametrize("mode", ["single_pass", "cached"])
+def test_fp8_tile_scales_vs_oracle(mode):
+    """Extension (config 4's recipe at small size): fp8-e4m3fn K and V with
+    one fp32 scale per (row, tile), G=8, CS gate."""
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa, score_tiles
+    from orthocache_gpu.workloads import make_q
+    G = 8
+    wl = _mixed(2, 12, 128, "fp8", seed=8)
+    q = make_q(2, G, 128, seed=6)
+    sc = score_tiles(wl.keys.to(DEV), k_scale=wl.k_scales.to(DEV))
+    out, m = fused_orthocache_attention_v3_gqa(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), 150.0, G,
+                                               k_scale=wl.k_scales.to(DEV), v_scale=wl.v_scales.to(DEV),
+                                               mode=mode, score_cache=sc)
+    tab = O.fp8_e4m3fn_table()
+    kf = tab[wl.keys.view(torch.uint8).numpy()]
+    vf = tab[wl.values.view(torch.uint8).numpy()]
+    ref = O.decode_rows(np32(q), kf, vf, gate="cs", threshold=150.0, G=G,
+                        k_scales=wl.k_scales.numpy(), v_scales=wl.v_scales.numpy())
+    assert np.array_equal(m["eviction_mask"].cpu().numpy(), ref["keep"])
+    assert_out(out, O.round_to(ref["out"], "bf16"), "fp8", "fp8 tiles")
+
+
+def test_orthocache_forward_modes():
+    from orthocache_gpu import orthocache_forward
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 2, 128, generator=g)
+    k = torch.randn(512, 2, 128, generator=g)
+    v = torch.randn(512, 2, 128, generator=g)
+    out, meta = orthocache_forward(q.to(DEV), k.to(DEV), v.to(DEV), block_size=512, zeta_max=5.0,
+                                   mode="triton_fused")
+    assert out.shape == (1, 2, 128)
+    assert "num_splits" in meta and meta["tile_assignment"] == "interleaved" and "latency_ms" in meta
+    ref, _, _ = O.fused_v2(np32(q[0]), np32(k.permute(1, 0, 2)), np32(v.permute(1, 0, 2)), 5.0)
+    assert_out(out[0], ref, "f32", "triton_fused")
+    qd = torch.randn(3, 2, 128, generator=g)
+    out, meta = orthocache_forward(qd.to(DEV), k.to(DEV), v.to(DEV), mode="dense")
+    ref = np.stack([O.dense_decode(np32(qd[s]), np32(k.permute(1, 0, 2)), np32(v.permute(1, 0, 2)))
+                    for s in range(3)])
+    assert_out(out, ref, "f32", "dense")
+    out, meta = orthocache_forward(q.to(DEV), k[:100].to(DEV), v[:100].to(DEV), mode="triton_fused",
+                                   crossover_threshold=4096)
+    assert meta["crossover_fallback"] and meta["actual_mode"] == "dense"
+    ref = O.dense_decode(np32(q[0]), np32(k[:100].permute(1, 0, 2)), np32(v[:100].permute(1, 0, 2)))
+    assert_out(out[0], ref, "f32", "crossover dense")
+
+
+def test_paged_bad_block_id_rejected():
+    from orthocache_gpu import fused_orthocache_attention_paged
+    q = torch.randn(1, 2, 64, device=DEV)
+    kc = torch.randn(4, 2, 32, 64, device=DEV)
+    bt = torch.tensor([[0, 7]], dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError, match="block id"):
+        fused_orthocache_attention_paged(q, kc, kc, bt, 5.0)
+
+
+# ---------------------------------------------------------------- full size properties
+
+@pytest.mark.parametrize("gate", ["cs", "zeta"])
+def test_headline_size_properties(gate):
+    """At the headline shape (GQA 32/8, d=128, 32K tokens, bf16): the mask is
+    exactly the generator's tile labels, cached == single-pass, and the
+    output equals a float64 softmax over the retained tokens."""
+    from orthocache_gpu import fused_orthocache_attention_v3_gqa, fused_orthocache_attention_v2, score_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q
+    Hkv, G, S, d = 8, 4, 32768, 128
+    wl = make_kv(Hkv, S, d, dtype=torch.bfloat16, device=DEV, seed=0)
+    q = make_q(Hkv, G, d, device=DEV, seed=1)
+    sc = score_tiles(wl.keys)
+    if gate == "cs":
+        tau = calibrate_tau(sc.e_high, q, G)
+        o1, m1 = fused_orthocache_attention_v3_gqa(q, wl.keys, wl.values, tau, G)
+        o2, m2 = fused_orthocache_attention_v3_gqa(q, wl.keys, wl.values, tau, G, mode="cached", score_cache=sc)
+        want = wl.noise
+    else:
+        qq = q.view(Hkv, G, d)[:, 0].contiguous()
+        o1, m1 = fused_orthocache_attention_v2(qq, wl.keys, wl.values, 5.0)
+        o2, m2 = fused_orthocache_attention_v2(qq, wl.keys, wl.values, 5.0, mode="cached", score_cache=sc)
+        q, G, want = qq, 1, ~wl.noise
+    assert torch.equal(m1["eviction_mask"], want)
+    assert torch.equal(m2["eviction_mask"], want)
+    assert m1["eviction_rate"] == 0.5
+    assert (o1.float() - o2.float()).abs().max().item() <= 2e-3
+    keep_tok = want.repeat_interleave(64, dim=1)  # (Hkv, S)
+    k64, v64, q64 = wl.keys.double(), wl.values.double(), q.double().view(Hkv, G, d)
+    logits = torch.einsum("hgd,hsd->hgs", q64, k64) / d ** 0.5
+    logits = logits.masked_fill(~keep_tok[:, None, :], float("-inf"))
+    ref = torch.einsum("hgs,hsd->hgd", torch.softmax(logits, dim=-1), v64).reshape(Hkv * G, d)
+    err = (o1.double() - ref).abs() - ref.abs() * 2.0 ** -8
+    assert err.max().item() <= 2e-3
