@@ -61,6 +61,22 @@ def _kv_align(head_dim: int, es: int) -> int:
     return min(16, (head_dim // 16) * es)
 
 
+_WIDTH = {torch.float8_e4m3fn: 1, torch.float16: 2, torch.bfloat16: 2, torch.float32: 4}
+
+
+def harmonize_kv(k: torch.Tensor, v: Optional[torch.Tensor]):
+    """The kernels read K and V in one element type.  When they differ, the
+    narrower one is converted exactly to the wider one on the GPU (fp8-e4m3fn
+    values are exact in f16, bf16 and f32; f16 with bf16 go to f32), as the
+    reference's own fp8 paths mix an fp8 K with a wider V (test_fp8.py:43-57)."""
+    if v is None or v.dtype == k.dtype:
+        return k, v
+    wk, wv = _WIDTH.get(k.dtype, 4), _WIDTH.get(v.dtype, 4)
+    if wk == wv:
+        return k.to(torch.float32), v.to(torch.float32)
+    return (k.to(v.dtype), v) if wk < wv else (k, v.to(k.dtype))
+
+
 def last_dim_ready(t: torch.Tensor, head_dim: int) -> torch.Tensor:
     """Returns `t` if its last dimension is contiguous and every other stride
     and the base pointer keep the kernel's vector loads aligned; otherwise a
@@ -145,6 +161,7 @@ def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor]) -> KVLayout:
     rows, s_len, d = keys.shape
     if values is not None and values.shape != keys.shape:
         raise ValueError(f"keys {tuple(keys.shape)} and values {tuple(values.shape)} must have the same shape")
+    keys, values = harmonize_kv(keys, values)
     keys = last_dim_ready(keys, d)
     if values is not None:
         values = last_dim_ready(values, d)
@@ -163,6 +180,7 @@ def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: tor
         raise ValueError(f"k_cache {tuple(k_cache.shape)} and v_cache {tuple(v_cache.shape)} must have the same shape")
     if block_tables.dim() != 2:
         raise ValueError("block_tables must be 2-D (num_seqs, max_blocks)")
+    k_cache, v_cache = harmonize_kv(k_cache, v_cache)
     k_cache = last_dim_ready(k_cache, d)
     v_cache = last_dim_ready(v_cache, d)
     if block_tables.dtype != torch.int32:
