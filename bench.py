@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Decode benchmark on one MI355X: spectral-gated GQA decode at 32K context.
+
+Workload (the BASELINE.json metric): GQA 32 query / 8 kv heads, head_dim 128,
+32768-token context, bf16, 50% of the 64-token tiles evicted.  A "step" is
+one decode of every query head of the batch over its whole context.  The
+primary line is batch 1; batch 8 is reported alongside.
+
+Keys follow the reference benchmark recipe (half smooth / half noise tiles,
+orthocache_gpu/workloads.py); the Cauchy-Schwarz threshold is calibrated
+between the two tile clusters, which evicts exactly the smooth half.  Tile
+scores are computed once per buffer set (prefill, untimed) and the decode
+reads K and V of the retained tiles only (cached-score mode).  The
+single-pass mode (scores from K inside the decode) and this build's own
+dense decode are timed on the same buffers.
+
+Timing: W untimed warm-up steps, then K steps back to back between two HIP
+events on the launch stream, with synchronisation on both sides.  The KV
+buffers rotate over several sets whose total exceeds the 256 MB Infinity
+Cache, so every step streams from HBM.  The dominant kernel (the decode
+kernel) is also timed on its own (partials-only call) for the roofline.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "orthocache-gpu_amd"), ROOT]
+
+METRIC = "decode µs/step + HBM GB/s (% roofline), 32K ctx GQA 32/8 bf16, 50% evict"
+HBM_PEAK_GBPS = 8000.0
+HQ, HKV, D, S = 32, 8, 128, 32768
+G = HQ // HKV
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1, help="batch of the primary line")
+    ap.add_argument("--extra-batch", type=int, default=8, help="batch of the secondary line (0 = none)")
+    ap.add_argument("--cpu-rows", type=int, default=64,
+                    help="kv rows of the workload timed on the host for cpu_baseline (0 = skip)")
+    ap.add_argument("--spw", type=int, default=0, help="logical splits per workgroup (0 = library default)")
+    ap.add_argument("--only", choices=["cached", "single_pass", "dense", "copy"], default=None,
+                    help="time only this decode variant of the primary batch, or a plain 1 GiB device copy "
+                         "(the reference kernel for scaling the profiler's byte counters)")
+    return ap.parse_args()
+
+
+class Setup:
+    """Device buffers, cached scores and prebuilt C-ABI parameter blocks for
+    one batch size."""
+
+    def __init__(self, batch, seed=0, spw=0):
+        import torch
+        from orthocache_gpu import _launch as X
+        from orthocache_gpu import _native as N
+        from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
+        from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q
+
+        self.torch, self.X, self.N = torch, X, N
+        self.spw = spw
+        dev = torch.device("cuda", 0)
+        self.dev = dev
+        self.batch = batch
+        self.rows = batch * HKV
+        self.tiles = S // 64
+        set_bytes = self.rows * S * D * 2 * 2
+        self.nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
+        self.sets = []
+        for i in range(self.nsets):
+            wl = make_kv(self.rows, S, D, noise_frac=0.5, dtype=torch.bfloat16, device=dev, seed=seed + 17 * i)
+            q = make_q(self.rows, G, D, dtype=torch.bfloat16, device=dev, seed=seed + 17 * i + 1)
+            sc = score_tiles(wl.keys)
+            self.sets.append({"wl": wl, "q": q, "scores": sc})
+        # one tau for all sets (the clusters are the same by construction)
+        self.tau = calibrate_tau(self.sets[0]["scores"].e_high, self.sets[0]["q"], G)
+        self.P = X.auto_num_splits(self.tiles, dev)
+        self.out = torch.empty((self.rows * G, D), dtype=torch.bfloat16, device=dev)
+        self.pm = torch.empty((self.rows * G, self.P), dtype=torch.float32, device=dev)
+        self.pl = torch.empty_like(self.pm)
+        self.pacc = torch.empty((self.rows * G, self.P, D), dtype=torch.float32, device=dev)
+        self.keep = torch.zeros((self.rows, self.tiles), dtype=torch.uint8, device=dev)
+        self.stream = X.current_stream(dev)
+        self.lib = N.lib()
+        self.params = {}
+        for variant in ("cached", "single_pass", "dense", "cached_partials"):
+            self.params[variant] = [self._params(s, variant) for s in self.sets]
+
+    def _params(self, st, variant):
+        X, N = self.X, self.N
+        kv = X.rows_layout(st["wl"].keys, st["wl"].values)
+        p = N.OcDecodeParams()
+        p.kv = kv.struct()
+        p.q = st["q"].data_ptr()
+        p.q_dtype = N.OC_BF16
+        p.G = G
+        p.q_row_stride = st["q"].stride(0)
+        p.gate = N.OC_GATE_NONE if variant == "dense" else N.OC_GATE_CS
+        p.mode = N.OC_MODE_CACHED if variant.startswith("cached") else N.OC_MODE_SINGLE_PASS
+        p.threshold = self.tau
+        p.score_e_low = st["scores"].e_low.data_ptr()
+        p.score_e_high = st["scores"].e_high.data_ptr()
+        p.score_row_stride = st["scores"].e_high.stride(0)
+        p.num_splits = self.P
+        p.splits_per_group = self.spw
+        p.out_dtype = N.OC_BF16
+        p.out = None if variant == "cached_partials" else self.out.data_ptr()
+        p.out_row_stride = self.out.stride(0)
+        p.partial_m, p.partial_l, p.partial_acc = self.pm.data_ptr(), self.pl.data_ptr(), self.pacc.data_ptr()
+        st.setdefault("_keep", []).append((kv,))  # keep the layout (and its tensors) alive
+        return p
+
+    def run(self, variant, i):
+        rc = self.lib.oc_decode(ctypes.byref(self.params[variant][i % self.nsets]), ctypes.c_void_p(self.stream))
+        if rc:
+            self.N.check("oc_decode", rc)
+
+    def time(self, variant, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            self.run(variant, i)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            self.run(variant, i)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / steps  # us per step
+
+    def check(self):
+        """Eviction rate of the timed configuration (mask of set 0)."""
+        from orthocache_gpu import fused_orthocache_attention_v3_gqa
+        st = self.sets[0]
+        _, meta = fused_orthocache_attention_v3_gqa(st["q"], st["wl"].keys, st["wl"].values, self.tau, G,
+                                                    mode="cached", score_cache=st["scores"])
+        assert self.torch.equal(meta["eviction_mask"], st["wl"].noise), "mask differs from the tile labels"
+        return meta["eviction_rate"]
+
+    def bytes(self, variant, evict):
+        """Algorithmic HBM bytes of one decode-kernel launch."""
+        kv_tile = 64 * D * 2                     # one bf16 K (or V) tile
+        tiles = self.rows * self.tiles
+        kept = tiles * (1.0 - evict)
+        q_bytes = self.rows * G * D * 2
+        if variant == "dense":
+            return tiles * 2 * kv_tile + q_bytes
+        if variant == "single_pass":
+            return tiles * kv_tile + kept * kv_tile + q_bytes
+        return kept * 2 * kv_tile + q_bytes + tiles * 4  # + e_high score per tile
+
+
+def measure(setup, steps, warmup):
+    evict = setup.check()
+    r = {"batch": setup.batch, "eviction_rate": evict, "num_splits": setup.P, "tau": setup.tau,
+         "buffer_sets": setup.nsets}
+    for v in ("cached", "single_pass", "dense"):
+        r[v + "_us"] = setup.time(v, steps, warmup)
+    r["decode_kernel_us"] = setup.time("cached_partials", steps, warmup)
+    r["cached_bytes"] = setup.bytes("cached", evict)
+    r["dense_bytes"] = setup.bytes("dense", evict)
+    r["single_pass_bytes"] = setup.bytes("single_pass", evict)
+    r["speedup_vs_dense"] = r["dense_us"] / r["cached_us"]
+    r["kernel_gbps"] = r["cached_bytes"] / (r["decode_kernel_us"] * 1e-6) / 1e9
+    r["step_gbps"] = r["cached_bytes"] / (r["cached_us"] * 1e-6) / 1e9
+    r["dense_gbps"] = r["dense_bytes"] / (r["dense_us"] * 1e-6) / 1e9
+    r["single_pass_gbps"] = r["single_pass_bytes"] / (r["single_pass_us"] * 1e-6) / 1e9
+    return r
+
+
+def cpu_baseline(setup, rows):
+    """The oracle (numpy restatement of the reference CPU path: per-tile
+    W@K, CS gate, online softmax) on `rows` kv rows of the timed workload,
+    one BLAS thread.  Scaled to tokens/s of the primary batch."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import orthocache_oracle as O
+    st = setup.sets[0]
+    rows = min(rows, setup.rows)
+    k = st["wl"].keys[:rows].float().cpu().numpy()
+    v = st["wl"].values[:rows].float().cpu().numpy()
+    q = st["q"][:rows * G].float().cpu().numpy()
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        O.gqa_v3(q, k, v, setup.tau, G)
+        dt = time.perf_counter() - t0
+    sec_per_row = dt / rows
+    step_s = sec_per_row * setup.rows
+    return {"value": setup.batch / step_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{rows} kv rows x {setup.tiles} tiles (G={G}, CS gate) of the timed workload, "
+                      f"{dt:.1f} s; scaled to one batch-{setup.batch} step = {step_s * 1e3:.1f} ms",
+            "host_cpus": os.cpu_count()}
+
+
+def traffic_from_profiles():
+    """HBM bytes per decode launch measured with rocprofv3 counters, when a
+    summary has been committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no multi-GPU "
+              "path; see DESIGN.md for how the decode would shard.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs an AMD GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            dst.copy_(src)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / args.steps
+        print(json.dumps({"only": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "us_per_copy": us,
+                          "gbps_read_plus_write": 2 * (1 << 30) / (us * 1e-6) / 1e9}))
+        return
+    primary = Setup(args.batch, spw=args.spw)
+    if args.only:
+        v = "cached_partials" if args.only == "cached" else args.only
+        us = primary.time(v, args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "us_per_step": us}))
+        return
+    r1 = measure(primary, args.steps, args.warmup)
+    cpu = cpu_baseline(primary, args.cpu_rows) if args.cpu_rows else None
+    extra = None
+    if args.extra_batch:
+        del primary
+        torch.cuda.empty_cache()
+        sec = Setup(args.extra_batch, seed=100, spw=args.spw)
+        extra = measure(sec, max(20, args.steps // 4), max(5, args.warmup // 4))
+        del sec
+    ach = r1["kernel_gbps"]
+    traffic = traffic_from_profiles()
+    line = {
+        "metric": METRIC,
+        "value": args.batch / (r1["cached_us"] * 1e-6),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r1["cached_us"] / 1e3,
+        "us_per_step": r1["cached_us"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: reference benchmark tile recipe (50% smooth / 50% noise 64-token tiles), N(0,1) q and V",
+        "config": {"workload": f"GQA {HQ}q/{HKV}kv d{D} ctx {S} bf16 batch {args.batch}, 50% tiles evicted by the "
+                               "Cauchy-Schwarz gate (calibrated tau), cached-score decode",
+                   "batch": args.batch, "seq_len": S, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
+                   "gate": "cauchy_schwarz", "mode": "cached", "num_splits": r1["num_splits"]},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBPS, 4),
+                     "traffic": None if traffic is None else traffic.get("decode_cached_b%d" % args.batch)},
+        "cpu_baseline": cpu,
+        "decode_kernel_us": r1["decode_kernel_us"],
+        "algorithmic_bytes_per_step": r1["cached_bytes"],
+        "single_pass_us_per_step": r1["single_pass_us"],
+        "dense_us_per_step": r1["dense_us"],
+        "speedup_vs_dense": round(r1["speedup_vs_dense"], 3),
+        "kv_bytes_skipped_frac": round(1 - r1["cached_bytes"] / r1["dense_bytes"], 4),
+        "dense_gbps": round(r1["dense_gbps"], 1),
+        "single_pass_gbps": round(r1["single_pass_gbps"], 1),
+        "eviction_rate": r1["eviction_rate"],
+    }
+    if extra:
+        line["batch%d" % extra["batch"]] = {
+            "us_per_step": extra["cached_us"], "tokens_per_s": extra["batch"] / (extra["cached_us"] * 1e-6),
+            "decode_kernel_us": extra["decode_kernel_us"], "kernel_gbps": round(extra["kernel_gbps"], 1),
+            "roofline_frac": round(extra["kernel_gbps"] / HBM_PEAK_GBPS, 4),
+            "single_pass_us": extra["single_pass_us"], "dense_us": extra["dense_us"],
+            "speedup_vs_dense": round(extra["speedup_vs_dense"], 3), "dense_gbps": round(extra["dense_gbps"], 1)}
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

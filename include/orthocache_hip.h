@@ -64,8 +64,6 @@ extern "C" {
 #define OC_KSCALE_NONE 0     /* k = float(k_elem)                                   */
 #define OC_KSCALE_Q_FOLD 1   /* q := round_qdtype(float(q) * k_scale), k = float(k_elem)
                                 (fused_eviction.py:619-621, gqa_eviction.py:565-567) */
-#define OC_KSCALE_ELEM_QDTYPE 2 /* k = round_qdtype(float(k_elem) * k_scale), q unscaled
-                                (paged fp8 path, paged_eviction.py:354-357)          */
 #define OC_KSCALE_TILE 3     /* k = float(k_elem) * k_scales[row, tile]   (extension) */
 
 /* V dequantisation */
@@ -109,7 +107,7 @@ typedef struct oc_kv_desc {
   int64_t v_block_stride, v_head_stride;
   const int32_t* lengths;
   int32_t k_scale_mode;     /* OC_KSCALE_* */
-  float k_scale;            /* scalar for Q_FOLD / ELEM_QDTYPE */
+  float k_scale;            /* scalar for Q_FOLD */
   const float* k_scales;    /* (num_rows, >= num_tiles) for OC_KSCALE_TILE */
   int64_t k_scales_row_stride;
   int32_t v_scale_mode;     /* OC_VSCALE_* */
@@ -153,18 +151,26 @@ typedef struct oc_decode_params {
   const float* score_e_high;
   int64_t score_row_stride;
   int32_t num_splits;       /* P >= 1: split s owns tiles {s + kP} */
+  int32_t splits_per_group; /* logical splits per workgroup (0 = choose); the
+                               partial states are per group of splits */
   int32_t out_dtype;        /* OC_F32 / OC_F16 / OC_BF16 */
+  int32_t reserved1;
   void* out;                /* (num_rows * G, head_dim) */
   int64_t out_row_stride;
   uint8_t* keep_out;        /* optional (num_rows, num_tiles): 1 = retained */
   int64_t keep_row_stride;
-  int32_t* split_counts;    /* optional (num_rows, P): retained tiles per split */
-  float* partial_m;         /* optional (num_rows * G, P); NULL = workspace */
-  float* partial_l;         /* optional (num_rows * G, P) */
-  float* partial_acc;       /* optional (num_rows * G, P, head_dim) */
+  int32_t* split_counts;    /* optional (num_rows, Pg): retained tiles per group */
+  float* partial_m;         /* optional (num_rows * G, Pg); NULL = workspace */
+  float* partial_l;         /* optional (num_rows * G, Pg) */
+  float* partial_acc;       /* optional (num_rows * G, Pg, head_dim);
+                               Pg = oc_decode_num_groups(p) */
   void* workspace;          /* device memory, oc_decode_workspace_size() bytes */
   size_t workspace_bytes;
 } oc_decode_params;
+
+/* number of partial states per (row, query head): ceil(P / spw), with spw
+ * the effective splits_per_group of `p` */
+int32_t oc_decode_num_groups(const oc_decode_params* p);
 
 /* bytes of device workspace oc_decode needs for `p` (0 when partials are given) */
 size_t oc_decode_workspace_size(const oc_decode_params* p);
@@ -174,7 +180,13 @@ size_t oc_decode_workspace_size(const oc_decode_params* p);
  * For every row r and split s, the online-softmax state of each of its G
  * query heads over the retained tiles {s + kP} (fused_eviction.py:259) is
  * formed in float32 (m0 = -1e9), then the P states are merged and
- * out = acc / max(l, 1e-9) is written in out_dtype.
+ * out = acc / max(l, 1e-9) is written in out_dtype.  One workgroup handles
+ * splits_per_group consecutive splits and writes their merged state (the
+ * merge is associative); with splits_per_group = 1 the partials are exactly
+ * the per-split states.
+ * With out == NULL (and the three partial_* buffers given) only the
+ * partial states are written; the caller merges them with oc_lse_merge,
+ * e.g. after gathering the partials of a sequence split across devices.
  */
 int oc_decode(const oc_decode_params* p, void* stream);
 
@@ -185,6 +197,15 @@ int oc_decode(const oc_decode_params* p, void* stream);
 int oc_lse_merge(const float* m, const float* l, const float* acc, int32_t rows,
                  int32_t num_splits, int32_t head_dim, void* out, int32_t out_dtype,
                  int64_t out_row_stride, void* stream);
+
+/*
+ * oc_dequant_fp8 -- dst[i] = round_out(float(src[i]) * scale) for n
+ * fp8-e4m3fn elements, written as out_dtype (OC_F32 / OC_F16 / OC_BF16, ties
+ * to even).  This is the reference's paged fp8 key dequantisation,
+ * k_cache.to(q.dtype) * k_scale (paged_eviction.py:354-357); src and dst
+ * must be 16-byte aligned.
+ */
+int oc_dequant_fp8(const void* src, int64_t n, float scale, int32_t out_dtype, void* dst, void* stream);
 
 /* sizeof(oc_kv_desc) and sizeof(oc_decode_params) as compiled into the
  * library, so that a binding can check its own struct layout (no

@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 
@@ -63,6 +64,8 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
     return fail(OC_ERR_INVALID, "K/V base pointers must be %lld-byte aligned", (long long)al);
   int rc;
   if ((rc = chk(kv->k_token_stride, "K token"))) return rc;
+  if (kv->k_token_stride * es * 64 >= ((int64_t)1 << 31) || kv->v_token_stride * es * 64 >= ((int64_t)1 << 31))
+    return fail(OC_ERR_UNSUPPORTED, "token stride too large (64 tokens must span < 2 GiB)");
   if ((rc = chk(kv->v_token_stride, "V token"))) return rc;
   memset(&a, 0, sizeof a);
   a.k = (const char*)kv->k;
@@ -109,7 +112,7 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
   a.v_scales = kv->v_scales;
   a.vs_stride = kv->v_scales_row_stride;
   a.error_flag = kv->error_flag;
-  if (a.k_scale_mode < OC_KSCALE_NONE || a.k_scale_mode > OC_KSCALE_TILE)
+  if (a.k_scale_mode != OC_KSCALE_NONE && a.k_scale_mode != OC_KSCALE_Q_FOLD && a.k_scale_mode != OC_KSCALE_TILE)
     return fail(OC_ERR_INVALID, "k_scale_mode %d", a.k_scale_mode);
   if (a.k_scale_mode == OC_KSCALE_TILE && !a.k_scales) return fail(OC_ERR_INVALID, "k_scales is NULL");
   if (a.v_scale_mode == OC_VSCALE_TILE && !a.v_scales) return fail(OC_ERR_INVALID, "v_scales is NULL");
@@ -204,19 +207,85 @@ static int launch_merge(const float* m, const float* l, const float* acc, int ro
   return e == hipSuccess ? OC_OK : hip_fail(e, "merge launch");
 }
 
+// dst[i] = round_out(float(fp8 src[i]) * scale), 16 elements per thread
+__global__ __launch_bounds__(256) void dequant_fp8_kernel(const uint4* __restrict__ src, int64_t n16, float scale,
+                                                          int out_dtype, char* __restrict__ dst) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int es = out_dtype == OC_F32 ? 4 : 2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const uint4 w = src[i];
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    char* o = dst + i * 16 * es;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float x = elem<OC_FP8_E4M3FN>(ww, e) * scale;
+      store_scalar(o + e * es, out_dtype, x);
+    }
+  }
+}
+
 }  // namespace oc
 
 using namespace oc;
 
-static size_t partial_floats(const oc_decode_params* p) {
-  const size_t rq = (size_t)p->kv.num_rows * (size_t)p->G * (size_t)p->num_splits;
+extern "C" int oc_dequant_fp8(const void* src, int64_t n, float scale, int32_t out_dtype, void* dst, void* stream) {
+  if (!src || !dst) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (out_dtype != OC_F32 && out_dtype != OC_F16 && out_dtype != OC_BF16)
+    return fail(OC_ERR_INVALID, "out dtype %d", out_dtype);
+  if (n < 0 || n % 16) return fail(OC_ERR_INVALID, "element count %lld must be a multiple of 16", (long long)n);
+  if (!aligned(src, 16) || !aligned(dst, 16)) return fail(OC_ERR_INVALID, "src/dst must be 16-byte aligned");
+  if (n == 0) return OC_OK;
+  const int64_t n16 = n / 16;
+  const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 4096);
+  hipLaunchKernelGGL(dequant_fp8_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, (const uint4*)src, n16,
+                     scale, out_dtype, (char*)dst);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "dequant launch");
+}
+
+// CU count of the current device, cached per device index.
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Splits per workgroup: enough tiles per workgroup (about 16) to amortise
+// its prologue and epilogue, while keeping at least one workgroup per CU.
+static int choose_spw(const oc_decode_params* p) {
+  if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
+  const int P = p->num_splits;
+  const int T = std::max(1, p->kv.num_tiles);
+  const int tiles_per_split = std::max(1, (T + P - 1) / P);
+  int spw = std::max(1, 16 / tiles_per_split);
+  int cus = device_cus();
+  const int gchunks = (p->G + 7) / 8;
+  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < cus) spw >>= 1;
+  return std::min(spw, P);
+}
+
+static int num_groups(const oc_decode_params* p, int spw) { return (p->num_splits + spw - 1) / spw; }
+
+static size_t partial_floats(const oc_decode_params* p, int pg) {
+  const size_t rq = (size_t)p->kv.num_rows * (size_t)p->G * (size_t)pg;
   return rq * (2 + (size_t)p->kv.head_dim);
+}
+
+extern "C" int32_t oc_decode_num_groups(const oc_decode_params* p) {
+  if (!p || p->num_splits <= 0) return 0;
+  return num_groups(p, choose_spw(p));
 }
 
 extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   if (!p || p->num_splits <= 0 || p->G <= 0) return 0;
   if (p->partial_m && p->partial_l && p->partial_acc) return 0;
-  return partial_floats(p) * sizeof(float) + 256;
+  return partial_floats(p, num_groups(p, choose_spw(p))) * sizeof(float) + 256;
 }
 
 extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
@@ -232,14 +301,15 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
     return fail(OC_ERR_INVALID, "q dtype %d", p->q_dtype);
   if (p->out_dtype != OC_F32 && p->out_dtype != OC_F16 && p->out_dtype != OC_BF16)
     return fail(OC_ERR_INVALID, "out dtype %d", p->out_dtype);
-  if (!p->q || !p->out) return fail(OC_ERR_INVALID, "q/out pointer is NULL");
+  const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
+  if (!p->q) return fail(OC_ERR_INVALID, "q pointer is NULL");
+  if (!p->out && !partials_given) return fail(OC_ERR_INVALID, "out is NULL and no partial buffers are given");
   if (p->gate < OC_GATE_NONE || p->gate > OC_GATE_CS) return fail(OC_ERR_INVALID, "gate %d", p->gate);
   if (p->mode != OC_MODE_SINGLE_PASS && p->mode != OC_MODE_CACHED) return fail(OC_ERR_INVALID, "mode %d", p->mode);
   if (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE) {
     if (!p->score_e_high || (p->gate == OC_GATE_ZETA && !p->score_e_low))
       return fail(OC_ERR_INVALID, "cached mode needs score_e_high (and score_e_low for the zeta gate)");
   }
-  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) a.q_dtype = p->q_dtype;
   const int qes = p->q_dtype == OC_F32 ? 4 : 2;
   a.q = (const char*)p->q;
   a.q_row_stride = p->q_row_stride * qes;
@@ -252,11 +322,14 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   a.sc_eh = p->score_e_high;
   a.sc_stride = p->score_row_stride;
   a.P = p->num_splits;
+  if (p->splits_per_group < 0) return fail(OC_ERR_INVALID, "splits_per_group %d", p->splits_per_group);
+  a.spw = choose_spw(p);
+  a.Pg = num_groups(p, a.spw);
   a.keep_out = p->keep_out;
   a.keep_stride = p->keep_row_stride;
   a.split_counts = p->split_counts;
   a.scale = (float)(1.0 / std::sqrt((double)D));
-  if (p->partial_m && p->partial_l && p->partial_acc) {
+  if (partials_given) {
     a.pm = p->partial_m;
     a.pl = p->partial_l;
     a.pacc = p->partial_acc;
@@ -265,7 +338,7 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
     if (!p->workspace || p->workspace_bytes < need)
       return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
     char* w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
-    const size_t rq = (size_t)p->kv.num_rows * p->G * p->num_splits;
+    const size_t rq = (size_t)p->kv.num_rows * p->G * a.Pg;
     a.pacc = (float*)w;
     a.pm = a.pacc + rq * D;
     a.pl = a.pm + rq;
@@ -276,7 +349,8 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
   if (e != hipSuccess) return hip_fail(e, "decode launch");
-  return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, p->num_splits, D, p->out, p->out_dtype,
+  if (!p->out) return OC_OK;
+  return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, a.Pg, D, p->out, p->out_dtype,
                       p->out_row_stride, st);
 }
 
@@ -292,7 +366,6 @@ extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_lo
   a.o_keep = keep;
   a.o_stride = out_row_stride;
   a.q_dtype = OC_F32;
-  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) return fail(OC_ERR_INVALID, "ELEM_QDTYPE scaling needs a q dtype");
   if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
   const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
   return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
@@ -303,7 +376,6 @@ extern "C" int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream) {
   int rc = fill_kv(kv, a);
   if (rc) return rc;
   if (!out) return fail(OC_ERR_INVALID, "out is NULL");
-  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) return fail(OC_ERR_INVALID, "ELEM_QDTYPE scaling needs a q dtype");
   a.lengths = nullptr;
   a.o_fwht = out;
   if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;

@@ -52,7 +52,9 @@ struct DecodeArgs {
   const float* sc_el;
   const float* sc_eh;
   int64_t sc_stride;
-  int32_t P;
+  int32_t P;    // logical splits: split s owns tiles {s + kP}
+  int32_t spw;  // logical splits per workgroup (group g owns splits [g*spw, g*spw + spw))
+  int32_t Pg;   // workgroups (partial states) per row and query head: ceil(P / spw)
   float* pm;
   float* pl;
   float* pacc;
@@ -90,17 +92,48 @@ __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// Partner exchange inside a 16-lane DPP row: M=8 pairs lane k with 15-k
+// Cross-row exchange with the gfx950 lane swaps: with both operands x,
+// v_permlane16_swap returns the even 16-lane rows of x in [0] and the odd
+// rows in [1] (each duplicated over its row pair); v_permlane32_swap does
+// the same for the two 32-lane halves.
+template <int M>
+__device__ __forceinline__ void row_pair(float x, float& lo, float& hi) {
+  static_assert(M == 16 || M == 32, "cross-row exchange");
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  }
+}
+
+// Partner exchange: M=8 pairs lane k with 15-k inside its 16-lane DPP row
 // (row_mirror), M=4 with k^7 (row_half_mirror), M=2 and M=1 with k^2 and
-// k^1 (quad_perm).  Each pairing flips bit log2(M) of the lane index, which
-// is all a butterfly needs.  M >= 16 crosses DPP rows.
+// k^1 (quad_perm); each pairing flips bit log2(M) of the lane index, which
+// is all a butterfly needs.  M=16 and M=32 return the lane ^ M value.
 template <int M>
 __device__ __forceinline__ float xpair(float x) {
   if constexpr (M == 8) return dpp<0x140>(x);
   else if constexpr (M == 4) return dpp<0x141>(x);
   else if constexpr (M == 2) return dpp<0x4E>(x);
   else if constexpr (M == 1) return dpp<0xB1>(x);
-  else return __shfl_xor(x, M, kWave);
+  else {
+    float lo, hi;
+    row_pair<M>(x, lo, hi);
+    return (__lane_id() & M) ? lo : hi;
+  }
+}
+
+// Butterfly across lane bit log2(M) (16 or 32): the lower lane of each pair
+// gets x_lo + x_hi, the upper lane x_lo - x_hi.
+template <int M>
+__device__ __forceinline__ float butterfly_rows(float x) {
+  float lo, hi;
+  row_pair<M>(x, lo, hi);
+  return (__lane_id() & M) ? (lo - hi) : (lo + hi);
 }
 
 // value of lane 16*gamma + I for every lane of DPP row gamma (row_newbcast)
@@ -109,14 +142,22 @@ __device__ __forceinline__ float row_bcast(float x) {
   return dpp<0x150 + I>(x);
 }
 
-__device__ __forceinline__ float wave_sum(float x) {
+// Sum over the 16 lanes of each DPP row (identical bits in every lane).
+__device__ __forceinline__ float row16_sum(float x) {
   x += xpair<8>(x);
   x += xpair<4>(x);
   x += xpair<2>(x);
   x += xpair<1>(x);
-  x += xpair<16>(x);
-  x += xpair<32>(x);
   return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x = row16_sum(x);
+  float lo, hi;
+  row_pair<16>(x, lo, hi);
+  x = lo + hi;
+  row_pair<32>(x, lo, hi);
+  return lo + hi;
 }
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -124,9 +165,20 @@ __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, xpair<4>(x));
   x = fmaxf(x, xpair<2>(x));
   x = fmaxf(x, xpair<1>(x));
-  x = fmaxf(x, xpair<16>(x));
-  x = fmaxf(x, xpair<32>(x));
-  return x;
+  float lo, hi;
+  row_pair<16>(x, lo, hi);
+  x = fmaxf(lo, hi);
+  row_pair<32>(x, lo, hi);
+  return fmaxf(lo, hi);
+}
+
+// Sum over the four 16-lane rows for each lane position j.
+__device__ __forceinline__ float rows4_sum(float x) {
+  float lo, hi;
+  row_pair<16>(x, lo, hi);
+  x = lo + hi;
+  row_pair<32>(x, lo, hi);
+  return lo + hi;
 }
 
 // One transpose-reduce step: the lane keeps half of its n = 2M values (the
@@ -256,40 +308,67 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) {
   return ri;
 }
 
-// Loads one tile (K or V) of `row` into w[i][*] for this lane.  Register
-// rows whose first token is at or past n_tok are zero-filled without a
-// load; a paged block id outside the pool raises error_flag and reads zeros.
-template <int DT, int D>
+template <int LB>
+__device__ __forceinline__ void buffer_load_lane_row(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t* w) {
+  if constexpr (LB == 32) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto y = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+    w[4] = y[0]; w[5] = y[1]; w[6] = y[2]; w[7] = y[3];
+  } else if constexpr (LB == 16) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+  } else if constexpr (LB == 8) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    w[0] = x[0]; w[1] = x[1];
+  } else {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  }
+}
+
+// Loads one tile (K or V) of `row` into w[i][*] for this lane; tokens at or
+// past n_tok read as zero.
+// Contiguous rows (PAGED = false) use branch-free buffer loads: one SGPR
+// descriptor at the tile start whose size is the valid part of the tile
+// (the buffer unit returns zeros past it), one per-lane byte offset per
+// 4-token row.
+// Paged rows resolve a block id per 4-token group (block_size >= 4); rows at
+// or past n_tok are zero-filled without a load, and a block id outside the
+// pool raises error_flag and reads zeros.
+template <int DT, int D, bool PAGED>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, const RowInfo& ri, int row, int t,
                                           bool is_v, int lane, uint32_t (&w)[16][Lay<DT, D>::LW]) {
   using L = Lay<DT, D>;
   const int gamma = lane >> 4;
   const int j = lane & 15;
-  const int64_t lane_off = (int64_t)j * L::LB;
   const int tok0 = t * 64;
-  if (!a.paged) {
-    const char* base = (is_v ? a.v : a.k) + (int64_t)row * (is_v ? a.v_row_stride : a.k_row_stride);
+  const int valid = ri.n_tok - tok0;
+  if constexpr (!PAGED) {
     const int64_t ts = is_v ? a.v_tok_stride : a.k_tok_stride;
+    const char* base = (is_v ? a.v : a.k) + (int64_t)row * (is_v ? a.v_row_stride : a.k_row_stride) + tok0 * ts;
+    const int nbytes = (int)(min(valid, 64) * ts);
+    const int voff = gamma * (int)ts + j * L::LB;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      if (tok0 + 4 * i < ri.n_tok) {
-        load_lane_row<L::LB>(base + (int64_t)(tok0 + 4 * i + gamma) * ts + lane_off, w[i]);
-      } else {
-#pragma unroll
-        for (int x = 0; x < L::LW; ++x) w[i][x] = 0u;
-      }
+      // one descriptor per 4-token row keeps the lane offset in one VGPR; the
+      // range check (offset >= num_records) zero-fills tokens past n_tok
+      const int rb = 4 * i * (int)ts;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
+      buffer_load_lane_row<L::LB>(rs, voff, 0, w[i]);
     }
   } else {
     const char* base = is_v ? a.v : a.k;
     const int64_t bstride = is_v ? a.v_blk_stride : a.k_blk_stride;
     const int64_t hoff = (int64_t)ri.head * (is_v ? a.v_head_stride : a.k_head_stride);
     const int64_t ts = is_v ? a.v_tok_stride : a.k_tok_stride;
+    const int64_t lane_off = (int64_t)j * L::LB;
     const int32_t* btrow = a.bt + (int64_t)ri.seq * a.bt_stride;
     const int bmask = (1 << a.bs_log2) - 1;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int tok = tok0 + 4 * i;  // uniform; block_size >= 4 keeps tok..tok+3 in one block
-      bool ok = tok < ri.n_tok;
+      bool ok = 4 * i < valid;
       int64_t blk = 0;
       if (ok) {
         blk = btrow[tok >> a.bs_log2];
@@ -299,33 +378,35 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const RowInfo& ri
         }
       }
       if (ok) {
-        load_lane_row<L::LB>(base + blk * bstride + hoff + (int64_t)((tok & bmask) + gamma) * ts + lane_off,
-                             w[i]);
+        load_lane_row<L::LB>(base + blk * bstride + hoff + (int64_t)((tok & bmask) + gamma) * ts + lane_off, w[i]);
       } else {
 #pragma unroll
         for (int x = 0; x < L::LW; ++x) w[i][x] = 0u;
       }
     }
+    if (valid < 64) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (4 * i + gamma >= valid) {
+#pragma unroll
+          for (int x = 0; x < L::LW; ++x) w[i][x] = 0u;
+        }
+      }
+    }
   }
 }
 
-// Dequantisation of one tile: value = round_to(float(elem) * mul, rnd) when
-// `scaled`, float(elem) otherwise.
+// Per-tile dequantisation scale: value = float(elem) * mul when `scaled`.
 struct Deq {
   float mul;
-  int rnd;
   bool scaled;
 };
 
 // The CPL values of one register row of this lane as float32.
 template <int DT, int D>
-__device__ __forceinline__ void row_vals(const uint32_t* w, float (&f)[D / 16], const Deq& dq) {
+__device__ __forceinline__ void row_vals(const uint32_t* w, float (&f)[D / 16]) {
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) f[c] = elem<DT>(w, c);
-  if (dq.scaled) {
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) f[c] = round_to(f[c] * dq.mul, dq.rnd);
-  }
 }
 
 // Whole tile as float32 (used by the full-transform kernel).
@@ -333,7 +414,13 @@ template <int DT, int D>
 __device__ __forceinline__ void decode_tile(const uint32_t (&w)[16][Lay<DT, D>::LW],
                                             float (&f)[16][Lay<DT, D>::CPL], const Deq& dq) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) row_vals<DT, D>(w[i], f[i], dq);
+  for (int i = 0; i < 16; ++i) {
+    row_vals<DT, D>(w[i], f[i]);
+    if (dq.scaled) {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) f[i][c] *= dq.mul;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- tile score
@@ -352,11 +439,16 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&w)[16][Lay<DT, D>::
 //  * rows 0..7 only see the sum branches of stages t5, t4, t3, i.e. the
 //    residue sums S_r = sum_{t = r mod 8} k_t, followed by the full 8-point
 //    butterfly over t0..t2 (t2 in registers, t0 and t1 across lanes).
-// The summation order is fixed, so every kernel that calls this function
-// (scoring, single-pass decode) produces the same bits.
+// Elements are dequantised first (float(elem) * scale) as the reference
+// does before its W @ K.  The summation order is fixed, so every kernel that
+// calls this function (scoring, single-pass decode) produces the same bits.
+// `mul` is the tile's dequantisation scale (1 when unscaled: exact).  The
+// multiply is unconditional: a branch here lets the compiler hoist the
+// element conversions of both arms and keep the whole tile live as floats.
 template <int DT, int D>
-__device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D>::LW], const Deq& dq,
-                                              int lane, float& e_low, float& e_high) {
+__device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D>::LW], const Deq& dq, int lane,
+                                              float& e_low, float& e_high) {
+  const float mul = dq.mul;
   constexpr int CPL = D / 16;
   float h = 0.f;
   float s0[CPL], s1[CPL];  // residue sums for token parity t2 = 0 / 1
@@ -364,9 +456,15 @@ __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D
   for (int c = 0; c < CPL; ++c) s0[c] = s1[c] = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_barrier(0);
     float fa[CPL], fb[CPL];
-    row_vals<DT, D>(kw[i], fa, dq);
-    row_vals<DT, D>(kw[i + 8], fb, dq);
+    row_vals<DT, D>(kw[i], fa);
+    row_vals<DT, D>(kw[i + 8], fb);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      fa[c] *= mul;
+      fb[c] *= mul;
+    }
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const float d = fa[c] - fb[c];
@@ -387,18 +485,10 @@ __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D
     s0[c] = a0 + a1;
     s1[c] = a0 - a1;
     // butterflies on t0 (lane bit 4) and t1 (lane bit 5)
-    {
-      const float y0 = xpair<16>(s0[c]), y1 = xpair<16>(s1[c]);
-      const bool up = (lane & 16) != 0;
-      s0[c] = up ? (y0 - s0[c]) : (s0[c] + y0);
-      s1[c] = up ? (y1 - s1[c]) : (s1[c] + y1);
-    }
-    {
-      const float y0 = xpair<32>(s0[c]), y1 = xpair<32>(s1[c]);
-      const bool up = (lane & 32) != 0;
-      s0[c] = up ? (y0 - s0[c]) : (s0[c] + y0);
-      s1[c] = up ? (y1 - s1[c]) : (s1[c] + y1);
-    }
+    s0[c] = butterfly_rows<16>(s0[c]);
+    s1[c] = butterfly_rows<16>(s1[c]);
+    s0[c] = butterfly_rows<32>(s0[c]);
+    s1[c] = butterfly_rows<32>(s1[c]);
   }
   // lane holds X rows s = gamma (s0) and 4 + gamma (s1); skip the DC row
   float lo = 0.f;
@@ -413,6 +503,7 @@ __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D
   e_low = wave_sum(lo);
   e_high = wave_sum(h) * 0.5f;
 }
+
 
 // Gate decision from a tile's band energies; true = retain.
 //   zeta gate (fused_eviction.py:428-432): evict iff e_high/(e_low+1e-6) > zeta_max
@@ -435,85 +526,137 @@ __device__ __forceinline__ bool gate_keep(int gate, double thr, float e_low, flo
   return true;
 }
 
+__device__ __forceinline__ Deq tile_kdeq(const DecodeArgs& a, int row, int t) {
+  if (a.k_scale_mode == OC_KSCALE_TILE) return Deq{a.k_scales[(int64_t)row * a.ks_stride + t], true};
+  return Deq{1.f, false};
+}
+
+__device__ __forceinline__ float tile_vmul(const DecodeArgs& a, int row, int t) {
+  if (a.v_scale_mode == OC_VSCALE_TILE) return a.v_scales[(int64_t)row * a.vs_stride + t];
+  return 1.f;
+}
+
 // ---------------------------------------------------------------- decode
 
-template <int DT, int D, int GT>
+// q . k for the token rows of register row `w`, over this lane's CPL columns.
+// Two-element 16-bit dot products (v_dot2_f32_bf16 / v_dot2_f32_f16) when K
+// and q share a 16-bit type, float32 FMAs otherwise.
+template <int DT, int D, bool DOT2>
+__device__ __forceinline__ float row_dot(const uint32_t* w, const uint32_t (&qp)[D / 32 > 0 ? D / 32 : 1],
+                                         const float (&qf)[D / 16]) {
+  constexpr int CPL = D / 16;
+  if constexpr (DOT2 && DT == OC_BF16) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf2;
+    float s = 0.f;
+#pragma unroll
+    for (int x = 0; x < CPL / 2; ++x)
+      s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, w[x]), __builtin_bit_cast(bf2, qp[x]), s, false);
+    return s;
+  } else if constexpr (DOT2 && DT == OC_F16) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+    float s = 0.f;
+#pragma unroll
+    for (int x = 0; x < CPL / 2; ++x)
+      s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w[x]), __builtin_bit_cast(h2, qp[x]), s, false);
+    return s;
+  } else {
+    float f[CPL];
+    row_vals<DT, D>(w, f);
+    float s = f[0] * qf[0];
+#pragma unroll
+    for (int c = 1; c < CPL; ++c) s = __builtin_fmaf(f[c], qf[c], s);
+    return s;
+  }
+}
+
+template <int GT>
 struct WaveState {
-  static constexpr int CPL = Lay<DT, D>::CPL;
-  float q[GT][CPL];
   float m[GT];
-  float l[GT];      // per-lane partial sums
-  float acc[GT][CPL];
+  float l[GT];  // per-lane partial sums of p
 };
 
-// Online-softmax update of the wave's G states with one retained tile
-// (fused_eviction.py:280-299 per head; gqa_eviction.py:409-451 per g).
-// Token rows are processed in pairs (i, i+8) so that the first step of the
-// transpose-reduce happens before the next pair is decoded.
-template <int DT, int D, int GT>
-__device__ __forceinline__ void attend_tile(WaveState<DT, D, GT>& st,
-                                            const uint32_t (&kw)[16][Lay<DT, D>::LW], const Deq& kdq,
-                                            const uint32_t (&vw)[16][Lay<DT, D>::LW], const Deq& vdq,
-                                            int g_active, float scale, int valid, int lane) {
-  constexpr int CPL = D / 16;
-  float red[GT][8];
+// logits of query head g for the 64 tokens of a tile: lane 16*gamma + j
+// receives token 4j + gamma.  Token rows are taken in pairs (i, i+8) so the
+// first transpose-reduce step happens as soon as a pair is done.
+template <int DT, int D, bool DOT2>
+__device__ __forceinline__ float tile_logit(const uint32_t (&kw)[16][Lay<DT, D>::LW],
+                                            const uint32_t (&qp)[D / 32 > 0 ? D / 32 : 1],
+                                            const float (&qf)[D / 16], int lane) {
+  float v[8];
   const bool up8 = (lane & 8) != 0;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    float fa[CPL], fb[CPL];
-    row_vals<DT, D>(kw[k], fa, kdq);
-    row_vals<DT, D>(kw[k + 8], fb, kdq);
-#pragma unroll
-    for (int g = 0; g < GT; ++g) {
-      float da = fa[0] * st.q[g][0];
-      float db = fb[0] * st.q[g][0];
-#pragma unroll
-      for (int c = 1; c < CPL; ++c) {
-        da = __builtin_fmaf(fa[c], st.q[g][c], da);
-        db = __builtin_fmaf(fb[c], st.q[g][c], db);
-      }
-      const float keep = up8 ? db : da;
-      const float send = up8 ? da : db;
-      red[g][k] = keep + xpair<8>(send);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    const float da = row_dot<DT, D, DOT2>(kw[k], qp, qf);
+    const float db = row_dot<DT, D, DOT2>(kw[k + 8], qp, qf);
+    const float keep = up8 ? db : da;
+    const float send = up8 ? da : db;
+    v[k] = keep + xpair<8>(send);
   }
-  float p[GT];
+  tr_step<4>(v, lane);
+  tr_step<2>(v, lane);
+  tr_step<1>(v, lane);
+  return v[0];
+}
+
+// Online-softmax update of the wave's G states with one retained tile
+// (fused_eviction.py:280-299 per head; gqa_eviction.py:409-451 per g), in
+// two phases so that the next tile's K can be requested as soon as this
+// tile's K registers are free:
+//   tile_softmax: logits from K, new max, p = e^(logit - m), l and the acc
+//                 rescale;  lscale = 1/sqrt(d) * k_scale(tile) and
+//                 vmul = v_scale(tile) fold the per-tile dequantisation
+//                 scales into the logits and p;
+//   tile_pv:      acc[g][c] += sum_i p(token 4i+gamma) * v[i][c].
+template <int DT, int D, int GT, bool DOT2>
+__device__ __forceinline__ void tile_softmax(WaveState<GT>& st, float (&acc)[GT][D / 16], float (&p)[GT],
+                                             const uint32_t (&kw)[16][Lay<DT, D>::LW], const float* sh_qf,
+                                             const uint32_t* sh_qp, float lscale, float vmul, int valid, int lane) {
+  constexpr int CPL = D / 16;
+  constexpr int QW = D / 32 > 0 ? D / 32 : 1;
+  const int j = lane & 15;
+  const bool tok_ok = 4 * j + (lane >> 4) < valid;
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
-    tr_step<4>(red[g], lane);
-    tr_step<2>(red[g], lane);
-    tr_step<1>(red[g], lane);
-    // lane 16*gamma + j holds token 4j + gamma
-    float logit = red[g][0] * scale;
-    if (valid < 64) {
-      const int tok = 4 * (lane & 15) + (lane >> 4);
-      if (tok >= valid) logit = -__builtin_inff();
+    // heads past g_active run on zeroed q and are never written out
+    uint32_t qp[QW];
+    float qf[CPL];
+    if constexpr (DOT2) {
+#pragma unroll
+      for (int x = 0; x < QW; ++x) qp[x] = sh_qp[g * (D / 2) + j * QW + x];
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) qf[c] = sh_qf[g * D + j * CPL + c];
     }
-    if (g >= g_active) {
-      p[g] = 0.f;
-      continue;
-    }
+    // computed in every lane (the transpose-reduce reads all lanes), then masked
+    float logit = tile_logit<DT, D, DOT2>(kw, qp, qf, lane) * lscale;
+    logit = tok_ok ? logit : -__builtin_inff();
     const float mt = wave_max(logit);
     const float mn = fmaxf(st.m[g], mt);
     const float alpha = __expf(st.m[g] - mn);
     const float pg = __expf(logit - mn);
     st.l[g] = __builtin_fmaf(st.l[g], alpha, pg);
     st.m[g] = mn;
-    p[g] = pg;
+    p[g] = pg * vmul;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) st.acc[g][c] *= alpha;
+    for (int c = 0; c < CPL; ++c) acc[g][c] *= alpha;
   }
-  // acc[g][c] += sum_i p(token 4i+gamma) * v[i][c]; p of that token sits
-  // in lane 16*gamma + i of the same DPP row.
-#define OC_PV_STEP(I)                                                        \
-  {                                                                          \
-    float fv[CPL];                                                           \
-    row_vals<DT, D>(vw[I], fv, vdq);                                         \
-    _Pragma("unroll") for (int g = 0; g < GT; ++g) {                         \
-      const float pb = row_bcast<I>(p[g]);                                   \
-      _Pragma("unroll") for (int c = 0; c < CPL; ++c) st.acc[g][c] =         \
-          __builtin_fmaf(pb, fv[c], st.acc[g][c]);                           \
-    }                                                                        \
+}
+
+template <int DT, int D, int GT>
+__device__ __forceinline__ void tile_pv(float (&acc)[GT][D / 16], const float (&p)[GT],
+                                        const uint32_t (&vw)[16][Lay<DT, D>::LW]) {
+  constexpr int CPL = D / 16;
+  // p of token 4i+gamma sits in lane 16*gamma + i of the same DPP row
+#define OC_PV_STEP(I)                                                                       \
+  {                                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                      \
+    float fv[CPL];                                                                          \
+    row_vals<DT, D>(vw[I], fv);                                                             \
+    _Pragma("unroll") for (int g = 0; g < GT; ++g) {                                        \
+      const float pb = row_bcast<I>(p[g]);                                                  \
+      _Pragma("unroll") for (int c = 0; c < CPL; ++c) acc[g][c] = __builtin_fmaf(pb, fv[c], acc[g][c]); \
+    }                                                                                       \
   }
   OC_PV_STEP(0) OC_PV_STEP(1) OC_PV_STEP(2) OC_PV_STEP(3)
   OC_PV_STEP(4) OC_PV_STEP(5) OC_PV_STEP(6) OC_PV_STEP(7)
@@ -522,144 +665,114 @@ __device__ __forceinline__ void attend_tile(WaveState<DT, D, GT>& st,
 #undef OC_PV_STEP
 }
 
-__device__ __forceinline__ Deq tile_kdeq(const DecodeArgs& a, int row, int t) {
-  if (a.k_scale_mode == OC_KSCALE_ELEM_QDTYPE) return Deq{a.k_scale, a.q_dtype, true};
-  if (a.k_scale_mode == OC_KSCALE_TILE) return Deq{a.k_scales[(int64_t)row * a.ks_stride + t], OC_F32, true};
-  return Deq{1.f, OC_F32, false};
-}
-
-__device__ __forceinline__ Deq tile_vdeq(const DecodeArgs& a, int row, int t) {
-  if (a.v_scale_mode == OC_VSCALE_TILE) return Deq{a.v_scales[(int64_t)row * a.vs_stride + t], OC_F32, true};
-  return Deq{1.f, OC_F32, false};
-}
-
-// Retain decision for tile t of a row in cached mode (scores precomputed by
-// the scoring kernel).  A partial tail tile is always retained.
-__device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& ri, int row, int t,
+// Retain decision for tile t of a row in cached mode from its stored
+// energies; a partial tail tile is always retained.
+__device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& ri, int t, float el, float eh,
                                             float qmax, bool qnan) {
-  if ((t + 1) * 64 > ri.n_tok || a.gate == OC_GATE_NONE) return true;
-  const int64_t o = (int64_t)row * a.sc_stride + t;
-  const float el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
-  return gate_keep(a.gate, a.thr, el, a.sc_eh[o], qmax, qnan);
+  if ((t + 1) * 64 > ri.n_tok) return true;
+  return gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
 }
 
-// Main decode kernel.  grid = (P, num_rows, ceil(G / GT)); block = 4 waves.
-// Workgroup (s, row, chunk) forms the online-softmax state of query heads
-// [chunk*GT, chunk*GT + GT) over the retained tiles {s + kP} of the row:
-// the four waves take those tiles round-robin (single-pass) or take the
-// retained ones round-robin (cached), and their states are merged in LDS
-// into the split's partial (m, l, acc).
-template <int DT, int D, int GT>
-__global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
+// The tile loop, the wave merge and the partial-state write of one
+// workgroup (see decode_kernel).
+template <int DT, int D, int GT, bool DOT2, bool PAGED>
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, int s, int g0,
+                                            float qmax, bool qnan, const float* sh_qf,
+                                            const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
+                                            float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh) {
   constexpr int CPL = D / 16;
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int s = blockIdx.x;
-  const int row = blockIdx.y;
-  const int g0 = blockIdx.z * GT;
-  const int g_active = min(GT, a.G - g0);
-  const RowInfo ri = row_info(a, row);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15;
+  const bool cached = a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE;
+  // this workgroup's splits [s, s + w): list index x -> tile s + (x / w) * P + x % w
+  const int w = min(a.spw, a.P - s);
+  const int n_split = s < ri.n_tiles ? w * ((ri.n_tiles - s + a.P - 1) / a.P) : 0;
 
-  __shared__ float sh_m[kWaves][GT];
-  __shared__ float sh_l[kWaves][GT];
-  __shared__ float sh_acc[kWaves][GT][D];
-  __shared__ int sh_cnt[kWaves];
-
-  WaveState<DT, D, GT> st;
-  // q rows of this chunk (q := round(q * k_scale) for the Q_FOLD mode)
-  const float qmul = a.k_scale_mode == OC_KSCALE_Q_FOLD ? a.k_scale : 1.f;
+  WaveState<GT> st;
+  float acc[GT][CPL];
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
     st.m[g] = kM0;
     st.l[g] = 0.f;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      st.acc[g][c] = 0.f;
-      float x = 0.f;
-      if (g < g_active) {
-        const char* qp = a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride +
-                         (int64_t)(j * CPL + c) * (a.q_dtype == OC_F32 ? 4 : 2);
-        x = load_scalar(qp, a.q_dtype);
-        if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * qmul, a.q_dtype);
-      }
-      st.q[g][c] = x;
-    }
-  }
-  // max_g ||q_g|| over all G query heads of the row (CS gate)
-  float qmax = 0.f;
-  bool qnan = false;
-  if (a.gate == OC_GATE_CS) {
-    for (int g = 0; g < a.G; ++g) {
-      float ss = 0.f;
-      if (lane < 16) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const char* qp = a.q + (int64_t)(row * a.G + g) * a.q_row_stride +
-                           (int64_t)(j * CPL + c) * (a.q_dtype == OC_F32 ? 4 : 2);
-          float x = load_scalar(qp, a.q_dtype);
-          if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * qmul, a.q_dtype);
-          ss = __builtin_fmaf(x, x, ss);
-        }
-      }
-      float qn = __builtin_sqrtf(wave_sum(ss));
-      if ((double)qn < 1e-38) qn = 0.f;
-      if (__builtin_isnan(qn)) qnan = true;
-      qmax = fmaxf(qmax, qn);
-    }
+    for (int c = 0; c < CPL; ++c) acc[g][c] = 0.f;
   }
 
-  const int n_split = s < ri.n_tiles ? (ri.n_tiles - s + a.P - 1) / a.P : 0;
-  int kept = 0;
   uint32_t kw[16][L::LW];
   uint32_t vw[16][L::LW];
+  int kept = 0;
+  int kk = wave - kWaves;  // single-pass position in the group's tile list
+  uint64_t cmask = 0;      // cached: retained tiles of the current 64-entry chunk
+  int c0 = -64, rank = 0;
+  // next tile of this wave, or -1: every tile of the list round-robin
+  // (single-pass, dense) or every retained tile round-robin (cached)
+  auto next_tile = [&]() -> int {
+    int t = -1;
+    if (!cached) {
+      for (;;) {
+        kk += kWaves;
+        if (kk >= n_split) break;
+        t = s + (kk / w) * a.P + kk % w;
+        if (t < ri.n_tiles) break;
+        t = -1;
+      }
+    } else {
+      for (;;) {
+        if (cmask) {
+          const int bit = __ffsll((unsigned long long)cmask) - 1;
+          cmask &= cmask - 1;
+          if ((rank++ & (kWaves - 1)) == wave) {
+            const int x = c0 + bit;
+            t = s + (x / w) * a.P + x % w;
+            break;
+          }
+          continue;
+        }
+        c0 += 64;
+        if (c0 >= n_split) break;
+        const int kx = c0 + lane;
+        const int tx = s + (kx / w) * a.P + kx % w;
+        const bool in = kx < n_split && tx < ri.n_tiles;
+        float el = pre_el, eh = pre_eh;
+        if (c0 > 0 && in) {
+          const int64_t o = (int64_t)row * a.sc_stride + tx;
+          eh = a.sc_eh[o];
+          el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
+        }
+        const bool keep = in && cached_keep(a, ri, tx, el, eh, qmax, qnan);
+        if (a.keep_out && in && wave == 0 && blockIdx.z == 0)
+          a.keep_out[(int64_t)row * a.keep_stride + tx] = keep ? 1 : 0;
+        cmask = __ballot(keep);
+      }
+    }
+    return __builtin_amdgcn_readfirstlane(t);  // the tile index is wave-uniform
+  };
+  auto lscale_of = [&](int t) -> float {
+    return a.scale * (a.k_scale_mode == OC_KSCALE_TILE ? a.k_scales[(int64_t)row * a.ks_stride + t] : 1.f);
+  };
 
-  if (a.mode == OC_MODE_SINGLE_PASS || a.gate == OC_GATE_NONE) {
-    for (int kk = wave; kk < n_split; kk += kWaves) {
-      const int t = s + kk * a.P;
-      const int valid = min(64, ri.n_tok - t * 64);
-      load_tile<DT, D>(a, ri, row, t, false, lane, kw);
-      const Deq kdq = tile_kdeq(a, row, t);
-      bool keep = true;
-      if (a.gate != OC_GATE_NONE && valid == 64) {
+  float p[GT];
+  for (int t = next_tile(); t >= 0; t = next_tile()) {
+    const int valid = min(64, ri.n_tok - t * 64);
+    load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
+    bool keep = true;
+    if (!cached && a.gate != OC_GATE_NONE) {
+      // single pass: gate on the K tile just read; V is read only if kept
+      if (valid == 64) {
         float el, eh;
-        tile_energies<DT, D>(kw, kdq, lane, el, eh);
+        tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
         keep = gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
       }
       if (a.keep_out && lane == 0 && blockIdx.z == 0)
         a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
-      if (keep) {
-        ++kept;
-        load_tile<DT, D>(a, ri, row, t, true, lane, vw);
-        attend_tile<DT, D, GT>(st, kw, kdq, vw, tile_vdeq(a, row, t), g_active, a.scale, valid, lane);
-      }
     }
-  } else {
-    // cached scores: find the retained tiles of the split, 64 at a time
-    int base_rank = 0;
-    for (int c0 = 0; c0 < n_split; c0 += 64) {
-      const int kk = c0 + lane;
-      const int t = s + kk * a.P;
-      const bool in = kk < n_split;
-      const bool keep = in && cached_keep(a, ri, row, t, qmax, qnan);
-      if (a.keep_out && in && wave == 0 && blockIdx.z == 0)
-        a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
-      uint64_t mask = __ballot(keep);
-      int rank = base_rank;
-      base_rank += __popcll(mask);
-      while (mask) {
-        const int bit = __ffsll((unsigned long long)mask) - 1;
-        mask &= mask - 1;
-        if ((rank++ & (kWaves - 1)) != wave) continue;
-        const int tt = s + (c0 + bit) * a.P;
-        const int valid = min(64, ri.n_tok - tt * 64);
-        load_tile<DT, D>(a, ri, row, tt, false, lane, kw);
-        load_tile<DT, D>(a, ri, row, tt, true, lane, vw);
-        ++kept;
-        attend_tile<DT, D, GT>(st, kw, tile_kdeq(a, row, tt), vw, tile_vdeq(a, row, tt), g_active, a.scale,
-                               valid, lane);
-      }
+    if (keep) {
+      load_tile<DT, D, PAGED>(a, ri, row, t, true, lane, vw);
+      tile_softmax<DT, D, GT, DOT2>(st, acc, p, kw, sh_qf, sh_qp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+      tile_pv<DT, D, GT>(acc, p, vw);
+      ++kept;
     }
   }
 
@@ -669,9 +782,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     const float lt = wave_sum(st.l[g]);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      float x = st.acc[g][c];
-      x += xpair<16>(x);
-      x += xpair<32>(x);
+      const float x = rows4_sum(acc[g][c]);
       if (lane < 16) sh_acc[wave][g][j * CPL + c] = x;
     }
     if (lane == 0) {
@@ -680,6 +791,106 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
     }
   }
   if (lane == 0) sh_cnt[wave] = kept;
+}
+
+// Main decode kernel.  grid = (Pg, num_rows, ceil(G / GT)); block = 4 waves.
+// Workgroup (g, row, chunk) forms the online-softmax state of query heads
+// [chunk*GT, chunk*GT + GT) over the retained tiles of the logical splits
+// s = g*spw .. g*spw + spw - 1 of the row (split s owns tiles {s + kP}):
+// the four waves take those tiles round-robin (single-pass) or take the
+// retained ones round-robin (cached), and their states are merged in LDS
+// into the workgroup's partial (m, l, acc).  With spw = 1 every partial is
+// exactly one logical split's state.
+// Two waves per SIMD (<= 256 VGPRs) except for float32 K/V, whose raw K and
+// V tiles alone take 256 registers.
+template <int DT, int D, int GT, bool DOT2, bool PAGED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
+    const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int s = blockIdx.x * a.spw;  // first split of this workgroup
+  const int row = blockIdx.y;
+  const int g0 = blockIdx.z * GT;
+  const int g_active = min(GT, a.G - g0);
+  const RowInfo ri = row_info(a, row);
+
+  __shared__ float sh_qf[GT * D];
+  __shared__ uint32_t sh_qp[GT * D / 2];
+  __shared__ float sh_m[kWaves][GT];
+  __shared__ float sh_l[kWaves][GT];
+  __shared__ float sh_acc[kWaves][GT][D];
+  __shared__ int sh_cnt[kWaves];
+
+  // cached mode: fetch the first chunk's scores before anything else
+  float pre_el = 0.f, pre_eh = 0.f;
+  if (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) {
+    const int w = min(a.spw, a.P - s);
+    const int t = s + (lane / w) * a.P + lane % w;
+    if (s < ri.n_tiles && t < ri.n_tiles) {
+      const int64_t o = (int64_t)row * a.sc_stride + t;
+      pre_eh = a.sc_eh[o];
+      pre_el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
+    }
+  }
+
+  // stage q of this chunk in LDS (float and packed 16-bit); q := round(q *
+  // k_scale) in q's dtype for the Q_FOLD mode (fused_eviction.py:619-621)
+  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
+  for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
+    const int g = idx / D;
+    const int c = idx - g * D;
+    float x = 0.f;
+    if (g < g_active) {
+      x = load_scalar(a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride + (int64_t)c * qes, a.q_dtype);
+      if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * a.k_scale, a.q_dtype);
+    }
+    sh_qf[idx] = x;
+  }
+  __syncthreads();
+  if constexpr (DOT2) {
+    for (int idx = threadIdx.x; idx < GT * D / 2; idx += kThreads) {
+      const float x0 = sh_qf[2 * idx], x1 = sh_qf[2 * idx + 1];
+      uint32_t lo, hi;
+      if (DT == OC_BF16) {
+        lo = __float_as_uint(x0) >> 16;
+        hi = __float_as_uint(x1) >> 16;
+      } else {
+        lo = __builtin_bit_cast(uint16_t, (_Float16)x0);
+        hi = __builtin_bit_cast(uint16_t, (_Float16)x1);
+      }
+      sh_qp[idx] = lo | (hi << 16);
+    }
+  }
+  // max_g ||q_g|| over all G query heads of the row (CS gate)
+  float qmax = 0.f;
+  bool qnan = false;
+  if (a.gate == OC_GATE_CS) {
+    for (int g = 0; g < a.G; ++g) {
+      float ss = 0.f;
+      if (lane < 16) {
+        const int gl = g - g0;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const int col = (lane & 15) * (D / 16) + c;
+          float x;
+          if (gl >= 0 && gl < GT) {
+            x = sh_qf[gl * D + col];
+          } else {
+            x = load_scalar(a.q + (int64_t)(row * a.G + g) * a.q_row_stride + (int64_t)col * qes, a.q_dtype);
+            if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * a.k_scale, a.q_dtype);
+          }
+          ss = __builtin_fmaf(x, x, ss);
+        }
+      }
+      float qn = __builtin_sqrtf(wave_sum(ss));
+      if ((double)qn < 1e-38) qn = 0.f;
+      if (__builtin_isnan(qn)) qnan = true;
+      qmax = fmaxf(qmax, qn);
+    }
+  }
+  __syncthreads();
+
+  decode_body<DT, D, GT, DOT2, PAGED>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt, pre_el,
+                               pre_eh);
   __syncthreads();
 
   // merge the four wave states into the split's partial
@@ -697,23 +908,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(const DecodeArgs a) {
       l = __builtin_fmaf(sh_l[w][g], e, l);
     }
     const int64_t qh = (int64_t)row * a.G + g0 + g;
-    a.pacc[(qh * a.P + s) * D + c] = acc;
+    const int64_t pidx = qh * a.Pg + blockIdx.x;
+    a.pacc[pidx * D + c] = acc;
     if (c == 0) {
-      a.pm[qh * a.P + s] = mx;
-      a.pl[qh * a.P + s] = l;
+      a.pm[pidx] = mx;
+      a.pl[pidx] = l;
     }
   }
   if (a.split_counts && threadIdx.x == 0 && blockIdx.z == 0)
-    a.split_counts[(int64_t)row * a.P + s] = sh_cnt[0] + sh_cnt[1] + sh_cnt[2] + sh_cnt[3];
+    a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = sh_cnt[0] + sh_cnt[1] + sh_cnt[2] + sh_cnt[3];
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
-template <int DT, int D>
+template <int DT, int D, bool PAGED>
 __global__ __launch_bounds__(kThreads) void score_kernel(const DecodeArgs a) {
-  constexpr int CPL = D / 16;
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
-  const int64_t job = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t job = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (job >= (int64_t)a.num_rows * a.num_tiles) return;
   const int row = (int)(job / a.num_tiles);
   const int t = (int)(job - (int64_t)row * a.num_tiles);
@@ -723,7 +934,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(const DecodeArgs a) {
   uint8_t keep = 0;
   if ((t + 1) * 64 <= ri.n_tok) {
     uint32_t kw[16][L::LW];
-    load_tile<DT, D>(a, ri, row, t, false, lane, kw);
+    load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
     tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
     z = eh / (el + 1e-6f);
     keep = gate_keep(OC_GATE_ZETA, a.thr, el, eh, 0.f, false) ? 1 : 0;
@@ -740,12 +951,12 @@ __global__ __launch_bounds__(kThreads) void score_kernel(const DecodeArgs a) {
 
 // Full 64-point transform X = W64 @ K_tile of every tile (float32 out):
 // in-register butterflies over token bits t2..t5, cross-lane over t0, t1.
-template <int DT, int D>
+template <int DT, int D, bool PAGED>
 __global__ __launch_bounds__(kThreads) void fwht_kernel(const DecodeArgs a) {
   constexpr int CPL = D / 16;
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
-  const int64_t job = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int64_t job = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (job >= (int64_t)a.num_rows * a.num_tiles) return;
   const int row = (int)(job / a.num_tiles);
   const int t = (int)(job - (int64_t)row * a.num_tiles);
@@ -753,7 +964,7 @@ __global__ __launch_bounds__(kThreads) void fwht_kernel(const DecodeArgs a) {
   ri.n_tok = a.num_tiles * 64;  // the transform covers whole tiles
   uint32_t kw[16][L::LW];
   float f[16][CPL];
-  load_tile<DT, D>(a, ri, row, t, false, lane, kw);
+  load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
   decode_tile<DT, D>(kw, f, tile_kdeq(a, row, t));
 #pragma unroll
   for (int h = 1; h < 16; h <<= 1) {
@@ -772,11 +983,8 @@ __global__ __launch_bounds__(kThreads) void fwht_kernel(const DecodeArgs a) {
   for (int i = 0; i < 16; ++i) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      float x = f[i][c];
-      float y = xpair<16>(x);
-      x = (lane & 16) ? (y - x) : (x + y);
-      y = xpair<32>(x);
-      x = (lane & 32) ? (y - x) : (x + y);
+      float x = butterfly_rows<16>(f[i][c]);
+      x = butterfly_rows<32>(x);
       f[i][c] = x * 0.125f;
     }
   }
@@ -797,25 +1005,33 @@ hipError_t launch_score(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 
+#define OC_DECODE_GT(DT, HD, DOT2, PG)                                                               \
+  switch (gt) {                                                                                      \
+    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG>), grid, block, 0, st, a); break;  \
+    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG>), grid, block, 0, st, a); break;  \
+    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG>), grid, block, 0, st, a); break;  \
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG>), grid, block, 0, st, a); break; \
+  }
+#define OC_DECODE_CASES(DT, DOT2)                                                                    \
+  if (head_dim == 128) {                                                                             \
+    if (a.paged) { OC_DECODE_GT(DT, 128, DOT2, true) } else { OC_DECODE_GT(DT, 128, DOT2, false) }   \
+  } else {                                                                                           \
+    if (a.paged) { OC_DECODE_GT(DT, 64, DOT2, true) } else { OC_DECODE_GT(DT, 64, DOT2, false) }     \
+  }
+
+// q . k in 16-bit dot products when K and q share the 16-bit type
+template <int DT>
+constexpr bool kHasDot2 = DT == OC_BF16 || DT == OC_F16;
+
 #define OC_DEFINE_LAUNCHERS(DT)                                                                   \
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
-    const dim3 grid(a.P, a.num_rows, gchunks), block(kThreads);                                   \
-    if (head_dim == 128) {                                                                        \
-      switch (gt) {                                                                               \
-        case 1: hipLaunchKernelGGL((decode_kernel<DT, 128, 1>), grid, block, 0, st, a); break;    \
-        case 2: hipLaunchKernelGGL((decode_kernel<DT, 128, 2>), grid, block, 0, st, a); break;    \
-        case 4: hipLaunchKernelGGL((decode_kernel<DT, 128, 4>), grid, block, 0, st, a); break;    \
-        default: hipLaunchKernelGGL((decode_kernel<DT, 128, 8>), grid, block, 0, st, a); break;   \
-      }                                                                                           \
+    const dim3 grid(a.Pg, a.num_rows, gchunks), block(kThreads);                                  \
+    if (kHasDot2<DT> && a.q_dtype == DT) {                                                        \
+      OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \
-      switch (gt) {                                                                               \
-        case 1: hipLaunchKernelGGL((decode_kernel<DT, 64, 1>), grid, block, 0, st, a); break;     \
-        case 2: hipLaunchKernelGGL((decode_kernel<DT, 64, 2>), grid, block, 0, st, a); break;     \
-        case 4: hipLaunchKernelGGL((decode_kernel<DT, 64, 4>), grid, block, 0, st, a); break;     \
-        default: hipLaunchKernelGGL((decode_kernel<DT, 64, 8>), grid, block, 0, st, a); break;    \
-      }                                                                                           \
+      OC_DECODE_CASES(DT, false)                                                                  \
     }                                                                                             \
     return hipGetLastError();                                                                     \
   }                                                                                               \
@@ -823,16 +1039,26 @@ hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
   hipError_t launch_score<DT>(const DecodeArgs& a, int head_dim, hipStream_t st) {                \
     const int64_t jobs = (int64_t)a.num_rows * a.num_tiles;                                       \
     const dim3 grid((unsigned)((jobs + kWaves - 1) / kWaves)), block(kThreads);                   \
-    if (head_dim == 128) hipLaunchKernelGGL((score_kernel<DT, 128>), grid, block, 0, st, a);      \
-    else hipLaunchKernelGGL((score_kernel<DT, 64>), grid, block, 0, st, a);                       \
+    if (head_dim == 128) {                                                                        \
+      if (a.paged) hipLaunchKernelGGL((score_kernel<DT, 128, true>), grid, block, 0, st, a);      \
+      else hipLaunchKernelGGL((score_kernel<DT, 128, false>), grid, block, 0, st, a);             \
+    } else {                                                                                      \
+      if (a.paged) hipLaunchKernelGGL((score_kernel<DT, 64, true>), grid, block, 0, st, a);       \
+      else hipLaunchKernelGGL((score_kernel<DT, 64, false>), grid, block, 0, st, a);              \
+    }                                                                                             \
     return hipGetLastError();                                                                     \
   }                                                                                               \
   template <>                                                                                     \
   hipError_t launch_fwht<DT>(const DecodeArgs& a, int head_dim, hipStream_t st) {                 \
     const int64_t jobs = (int64_t)a.num_rows * a.num_tiles;                                       \
     const dim3 grid((unsigned)((jobs + kWaves - 1) / kWaves)), block(kThreads);                   \
-    if (head_dim == 128) hipLaunchKernelGGL((fwht_kernel<DT, 128>), grid, block, 0, st, a);       \
-    else hipLaunchKernelGGL((fwht_kernel<DT, 64>), grid, block, 0, st, a);                        \
+    if (head_dim == 128) {                                                                        \
+      if (a.paged) hipLaunchKernelGGL((fwht_kernel<DT, 128, true>), grid, block, 0, st, a);       \
+      else hipLaunchKernelGGL((fwht_kernel<DT, 128, false>), grid, block, 0, st, a);              \
+    } else {                                                                                      \
+      if (a.paged) hipLaunchKernelGGL((fwht_kernel<DT, 64, true>), grid, block, 0, st, a);        \
+      else hipLaunchKernelGGL((fwht_kernel<DT, 64, false>), grid, block, 0, st, a);               \
+    }                                                                                             \
     return hipGetLastError();                                                                     \
   }
 

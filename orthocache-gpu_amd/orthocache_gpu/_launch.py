@@ -249,8 +249,11 @@ class DecodeResult:
 def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float, mode: int = N.OC_MODE_SINGLE_PASS,
            scores: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_splits: Optional[int] = None,
            out_dtype: torch.dtype, want_keep: bool = False, want_partials: bool = False,
-           out: Optional[torch.Tensor] = None) -> DecodeResult:
-    """One oc_decode call.  q is (rows*G, d) with a contiguous last dimension."""
+           out: Optional[torch.Tensor] = None, splits_per_group: Optional[int] = None) -> DecodeResult:
+    """One oc_decode call.  q is (rows*G, d) with a contiguous last dimension.
+    With want_partials the per-split partial states (one workgroup per
+    logical split) are returned as (m, l, acc) of shapes (rows*G, P) and
+    (rows*G, P, d)."""
     device = require_gpu(q, kv.k, kv.v)
     d = kv.head_dim
     if q.stride(-1) != 1:
@@ -288,6 +291,7 @@ def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float
         p.score_e_high = _ptr(e_high)
         p.score_row_stride = e_high.stride(0)
     p.num_splits = P
+    p.splits_per_group = 1 if want_partials else (splits_per_group or 0)
     p.out_dtype = dtype_code(out.dtype, "out", allow_fp8=False)
     p.out = out.data_ptr()
     p.out_row_stride = out.stride(0)
@@ -355,6 +359,22 @@ def lse_merge(m: torch.Tensor, l: torch.Tensor, acc: torch.Tensor, out_dtype=tor
         N.check("oc_lse_merge", N.lib().oc_lse_merge(
             m.data_ptr(), l.data_ptr(), acc.data_ptr(), rows, P, d, out.data_ptr(),
             dtype_code(out_dtype, "out", allow_fp8=False), out.stride(0), ctypes.c_void_p(stream)))
+    return out
+
+
+def dequant_fp8(src: torch.Tensor, scale: float, out_dtype: torch.dtype) -> torch.Tensor:
+    """oc_dequant_fp8: round_out(float(src) * scale) as a new out_dtype tensor."""
+    device = require_gpu(src)
+    src = src.contiguous()
+    out = torch.empty(src.shape, dtype=out_dtype, device=device)
+    n = src.numel()
+    if n % 16:
+        raise ValueError("fp8 tensor size must be a multiple of 16 elements")
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_dequant_fp8", N.lib().oc_dequant_fp8(
+            src.data_ptr(), n, float(scale), dtype_code(out_dtype, "out", allow_fp8=False), out.data_ptr(),
+            ctypes.c_void_p(stream)))
     return out
 
 

@@ -26,7 +26,7 @@ OC_F32, OC_F16, OC_BF16, OC_FP8_E4M3FN = 0, 1, 2, 3
 # gates / modes / scale modes
 OC_GATE_NONE, OC_GATE_ZETA, OC_GATE_CS = 0, 1, 2
 OC_MODE_SINGLE_PASS, OC_MODE_CACHED = 0, 1
-OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_ELEM_QDTYPE, OC_KSCALE_TILE = 0, 1, 2, 3
+OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE = 0, 1, 3
 OC_VSCALE_NONE, OC_VSCALE_TILE = 0, 1
 
 _p = ctypes.c_void_p
@@ -59,7 +59,7 @@ class OcDecodeParams(ctypes.Structure):
         ("q", _p), ("q_dtype", _i32), ("G", _i32), ("q_row_stride", _i64),
         ("gate", _i32), ("mode", _i32), ("threshold", ctypes.c_double),
         ("score_e_low", _p), ("score_e_high", _p), ("score_row_stride", _i64),
-        ("num_splits", _i32), ("out_dtype", _i32),
+        ("num_splits", _i32), ("splits_per_group", _i32), ("out_dtype", _i32), ("reserved1", _i32),
         ("out", _p), ("out_row_stride", _i64),
         ("keep_out", _p), ("keep_row_stride", _i64),
         ("split_counts", _p),
@@ -73,8 +73,10 @@ SIGNATURES = {
     "oc_score_tiles": (_i32, [ctypes.POINTER(OcKvDesc), ctypes.c_double, _p, _p, _p, _p, _i64, _p]),
     "oc_fwht_tiles": (_i32, [ctypes.POINTER(OcKvDesc), _p, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
+    "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
     "oc_lse_merge": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i32, _i64, _p]),
+    "oc_dequant_fp8": (_i32, [_p, _i64, ctypes.c_float, _i32, _p, _p]),
     "oc_abi_sizes": (_i32, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "oc_device_cu_count": (_i32, [ctypes.POINTER(_i32)]),
     "oc_version": (ctypes.c_char_p, []),

@@ -85,12 +85,14 @@ def fused_orthocache_attention_paged(
     if num_splits is None:
         num_splits = _auto_num_splits(num_tiles, device)
 
-    kv = X.paged_layout(k_cache, v_cache, block_tables, num_tiles)
     rows = num_seqs * num_kv_heads
     if k_cache.dtype == torch.float8_e4m3fn and not isinstance(k_scale, torch.Tensor):
-        kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_ELEM_QDTYPE, float(k_scale)
-    else:
-        kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, device)
+        # reference semantics: k_cache.to(q.dtype) * k_scale in q's dtype, then
+        # no further scaling (paged_eviction.py:354-357)
+        k_cache = X.dequant_fp8(k_cache, float(k_scale), q.dtype)
+        k_scale = 1.0
+    kv = X.paged_layout(k_cache, v_cache, block_tables, num_tiles)
+    kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, device)
     kv.v_scale_mode, kv.v_scales = X.vscale_mode(v_scale, rows, num_tiles, device)
     if context_lens is not None:
         if context_lens.numel() != num_seqs:
