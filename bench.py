@@ -93,6 +93,7 @@ class Setup:
         self.keep = torch.zeros((self.rows, self.tiles), dtype=torch.uint8, device=dev)
         self.stream = X.current_stream(dev)
         self.lib = N.lib()
+        self.ws = None
         self.params = {}
         for variant in ("cached", "single_pass", "dense", "cached_partials"):
             self.params[variant] = [self._params(s, variant) for s in self.sets]
@@ -115,9 +116,19 @@ class Setup:
         p.num_splits = self.P
         p.splits_per_group = self.spw
         p.out_dtype = N.OC_BF16
-        p.out = None if variant == "cached_partials" else self.out.data_ptr()
         p.out_row_stride = self.out.stride(0)
-        p.partial_m, p.partial_l, p.partial_acc = self.pm.data_ptr(), self.pl.data_ptr(), self.pacc.data_ptr()
+        if variant == "cached_partials":
+            # partials only: the decode kernel alone, for the roofline
+            p.out = None
+            p.partial_m, p.partial_l, p.partial_acc = self.pm.data_ptr(), self.pl.data_ptr(), self.pacc.data_ptr()
+        else:
+            # the production call: partials and merge counters in the workspace
+            p.out = self.out.data_ptr()
+            need = self.lib.oc_decode_workspace_size(ctypes.byref(p))
+            if self.ws is None:
+                self.ws = self.torch.zeros(max(need, 1 << 20), dtype=self.torch.uint8, device=self.dev)
+            assert self.ws.numel() >= need, "workspace sizes differ between variants"
+            p.workspace, p.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
         st.setdefault("_keep", []).append((kv,))  # keep the layout (and its tensors) alive
         return p
 

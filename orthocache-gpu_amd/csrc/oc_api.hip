@@ -263,10 +263,13 @@ static int choose_spw(const oc_decode_params* p) {
   const int P = p->num_splits;
   const int T = std::max(1, p->kv.num_tiles);
   const int tiles_per_split = std::max(1, (T + P - 1) / P);
-  int spw = std::max(1, 16 / tiles_per_split);
-  int cus = device_cus();
+  // up to 64 tiles per workgroup, but at least two workgroups per CU (two
+  // 256-thread workgroups are resident per CU at the decode kernel's
+  // register budget), so that a small batch still fills the chip
+  int spw = std::max(1, 64 / tiles_per_split);
+  const int cus = device_cus();
   const int gchunks = (p->G + 7) / 8;
-  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < cus) spw >>= 1;
+  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < 2 * (int64_t)cus) spw >>= 1;
   return std::min(spw, P);
 }
 
@@ -282,10 +285,30 @@ extern "C" int32_t oc_decode_num_groups(const oc_decode_params* p) {
   return num_groups(p, choose_spw(p));
 }
 
+// query heads per decode workgroup for G heads per kv row
+static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G)); }
+
+// Workspace layout: [0, kCounterBytes) merge counters (zero before the first
+// call, left zero by every call), then the partial states unless the caller
+// gives its own.
+static constexpr size_t kCounterBytes = 64 << 10;
+
+// The split merge runs inside the decode kernel when the counters and the
+// merge weights (GT * Pg floats in the kernel's 4 * GT * D wave-merge LDS)
+// fit; otherwise merge_kernel runs after it.
+static bool fused_merge(const oc_decode_params* p, int pg) {
+  const int gchunks = (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
+  return p->out && (size_t)p->kv.num_rows * gchunks * sizeof(int32_t) <= kCounterBytes && pg <= 4 * p->kv.head_dim;
+}
+
 extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   if (!p || p->num_splits <= 0 || p->G <= 0) return 0;
-  if (p->partial_m && p->partial_l && p->partial_acc) return 0;
-  return partial_floats(p, num_groups(p, choose_spw(p))) * sizeof(float) + 256;
+  const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
+  if (partials_given && !p->out) return 0;
+  const int pg = num_groups(p, choose_spw(p));
+  size_t n = 256 + (p->out ? kCounterBytes : 0);
+  if (!partials_given) n += partial_floats(p, pg) * sizeof(float);
+  return n;
 }
 
 extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
@@ -329,27 +352,40 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   a.keep_stride = p->keep_row_stride;
   a.split_counts = p->split_counts;
   a.scale = (float)(1.0 / std::sqrt((double)D));
+  const size_t need = oc_decode_workspace_size(p);
+  char* w = nullptr;
+  if (need) {
+    if (!p->workspace || p->workspace_bytes < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+    w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
+  }
+  if (p->out) {
+    a.counters = (int32_t*)w;
+    w += kCounterBytes;
+  }
   if (partials_given) {
+    if (!aligned(p->partial_acc, 16)) return fail(OC_ERR_INVALID, "partial_acc must be 16-byte aligned");
     a.pm = p->partial_m;
     a.pl = p->partial_l;
     a.pacc = p->partial_acc;
   } else {
-    const size_t need = oc_decode_workspace_size(p);
-    if (!p->workspace || p->workspace_bytes < need)
-      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
-    char* w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
     const size_t rq = (size_t)p->kv.num_rows * p->G * a.Pg;
     a.pacc = (float*)w;
     a.pm = a.pacc + rq * D;
     a.pl = a.pm + rq;
   }
+  const int oes = p->out_dtype == OC_F32 ? 4 : 2;
+  a.fuse = fused_merge(p, a.Pg) ? 1 : 0;
+  a.out = (char*)p->out;
+  a.out_dtype = p->out_dtype;
+  a.out_stride = p->out_row_stride * oes;
   if (a.num_rows == 0) return OC_OK;
-  const int gt = p->G >= 8 ? 8 : (p->G >= 4 ? (p->G == 4 ? 4 : 8) : (p->G == 3 ? 4 : p->G));
+  const int gt = heads_per_group(p->G);
   const int gchunks = (p->G + gt - 1) / gt;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
   if (e != hipSuccess) return hip_fail(e, "decode launch");
-  if (!p->out) return OC_OK;
+  if (!p->out || a.fuse) return OC_OK;
   return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, a.Pg, D, p->out, p->out_dtype,
                       p->out_row_stride, st);
 }

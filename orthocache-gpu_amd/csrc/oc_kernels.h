@@ -62,6 +62,14 @@ struct DecodeArgs {
   int64_t keep_stride;
   int32_t* split_counts;
   float scale;
+  // fused merge: the last workgroup of each (row, head chunk) to finish
+  // merges the row's Pg partials into out (counters: one per (row, chunk),
+  // zero on entry and left zero)
+  int32_t fuse;
+  int32_t out_dtype;
+  int32_t* counters;
+  char* out;
+  int64_t out_stride;  // bytes between query-head rows of out
   // score kernel outputs
   float* o_el;
   float* o_eh;
@@ -793,6 +801,95 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   if (lane == 0) sh_cnt[wave] = kept;
 }
 
+// Fused split merge.  Every workgroup waits until its partial stores (agent
+// scope, written through to memory) are complete and takes a ticket on its
+// (row, chunk) counter; the workgroup that takes the last ticket resets the
+// counter, invalidates its L2 (agent-scope acquire) and forms
+//   out = sum_p e^(m_p - M) acc_p / max(sum_p e^(m_p - M) l_p, 1e-9)
+// for the chunk's query heads, the formula of the stand-alone merge kernel.
+// No full write-back fence is needed in the other workgroups.
+// sh_w (>= GT * Pg floats) and sh_inv (>= GT floats) reuse the wave-merge
+// LDS, which is dead by now.
+template <int D, int GT>
+__device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int g0, int g_active, float* sh_w,
+                                              float* sh_inv) {
+  __shared__ int sh_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are acknowledged
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int* ctr = a.counters + (int64_t)row * gridDim.z + blockIdx.z;
+    const int done = atomicAdd(ctr, 1) + 1;
+    sh_last = done == a.Pg;
+    if (done == a.Pg) atomicExch(ctr, 0);
+  }
+  __syncthreads();
+  if (!sh_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int Pg = a.Pg;
+  for (int g = wave; g < g_active; g += kWaves) {
+    const int64_t base = ((int64_t)row * a.G + g0 + g) * Pg;
+    float mx = -__builtin_inff();
+    for (int q = lane; q < Pg; q += 64) mx = fmaxf(mx, a.pm[base + q]);
+    mx = wave_max(mx);
+    float ls = 0.f;
+    for (int q = lane; q < Pg; q += 64) {
+      const float w = __expf(a.pm[base + q] - mx);
+      sh_w[g * Pg + q] = w;
+      ls = __builtin_fmaf(w, a.pl[base + q], ls);
+    }
+    ls = wave_sum(ls);
+    if (lane == 0) sh_inv[g] = fmaxf(ls, 1e-9f);
+  }
+  __syncthreads();
+  // weighted sum over the Pg partials: thread (slice, g, column quad) adds
+  // partials q = slice, slice + nslice, ... with all its loads independent;
+  // the slices are then added in a fixed order (deterministic result)
+  constexpr int CQ = D / 4;
+  constexpr int NPAIR = GT * CQ;
+  constexpr int NSLICE = kThreads / NPAIR;
+  __shared__ float4 sh_red[kThreads];
+  const int pair = threadIdx.x % NPAIR;
+  const int sl = threadIdx.x / NPAIR;
+  const int g = pair / CQ;
+  const int cq = pair - g * CQ;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (g < g_active) {
+    const int64_t qh = (int64_t)row * a.G + g0 + g;
+    const float4* ap = reinterpret_cast<const float4*>(a.pacc + qh * Pg * D) + cq;
+    const float* wg = sh_w + g * Pg;
+#pragma unroll 16
+    for (int q = sl; q < Pg; q += NSLICE) {
+      const float4 x = ap[(int64_t)q * CQ];
+      const float w = wg[q];
+      acc.x = __builtin_fmaf(x.x, w, acc.x);
+      acc.y = __builtin_fmaf(x.y, w, acc.y);
+      acc.z = __builtin_fmaf(x.z, w, acc.z);
+      acc.w = __builtin_fmaf(x.w, w, acc.w);
+    }
+  }
+  sh_red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x < NPAIR && g < g_active) {
+#pragma unroll
+    for (int k = 1; k < NSLICE; ++k) {
+      const float4 y = sh_red[k * NPAIR + threadIdx.x];
+      acc.x += y.x;
+      acc.y += y.y;
+      acc.z += y.z;
+      acc.w += y.w;
+    }
+    const float inv = sh_inv[g];
+    const int es = a.out_dtype == OC_F32 ? 4 : 2;
+    char* o = a.out + ((int64_t)row * a.G + g0 + g) * a.out_stride + (int64_t)(4 * cq) * es;
+    store_scalar(o, a.out_dtype, acc.x / inv);
+    store_scalar(o + es, a.out_dtype, acc.y / inv);
+    store_scalar(o + 2 * es, a.out_dtype, acc.z / inv);
+    store_scalar(o + 3 * es, a.out_dtype, acc.w / inv);
+  }
+}
+
 // Main decode kernel.  grid = (Pg, num_rows, ceil(G / GT)); block = 4 waves.
 // Workgroup (g, row, chunk) forms the online-softmax state of query heads
 // [chunk*GT, chunk*GT + GT) over the retained tiles of the logical splits
@@ -909,14 +1006,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == 
     }
     const int64_t qh = (int64_t)row * a.G + g0 + g;
     const int64_t pidx = qh * a.Pg + blockIdx.x;
-    a.pacc[pidx * D + c] = acc;
+    // agent-scope stores write through this XCD's L2, so the fused merge
+    // (possibly on another XCD) reads them without a cache write-back
+    __hip_atomic_store(a.pacc + pidx * D + c, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (c == 0) {
-      a.pm[pidx] = mx;
-      a.pl[pidx] = l;
+      __hip_atomic_store(a.pm + pidx, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.pl + pidx, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (a.split_counts && threadIdx.x == 0 && blockIdx.z == 0)
     a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = sh_cnt[0] + sh_cnt[1] + sh_cnt[2] + sh_cnt[3];
+  if (a.fuse) merge_if_last<D, GT>(a, row, g0, g_active, &sh_acc[0][0][0], &sh_l[0][0]);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.

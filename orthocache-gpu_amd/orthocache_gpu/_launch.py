@@ -203,11 +203,13 @@ _WORKSPACES: Dict[Tuple[int, int], torch.Tensor] = {}
 
 def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     """A reusable device buffer per (device, stream); calls on one stream are
-    ordered, so they can share it."""
+    ordered, so they can share it.  It is allocated zeroed: oc_decode keeps
+    its merge counters at the start of the workspace, needs them zero before
+    the first call and leaves them zero."""
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACES[key] = buf
     return buf
 
@@ -308,8 +310,8 @@ def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float
         raise ValueError("lengths has fewer entries than the kv rows need")
     stream = current_stream(device)
     lib = N.lib()
-    if not want_partials:
-        need = lib.oc_decode_workspace_size(ctypes.byref(p))
+    need = lib.oc_decode_workspace_size(ctypes.byref(p))
+    if need:
         ws = workspace(device, stream, need)
         p.workspace = ws.data_ptr()
         p.workspace_bytes = ws.numel()

@@ -265,6 +265,29 @@ def test_split_partials_and_assignment(gate, P):
     assert_out(out, ref["out"], "f32", "merged")
 
 
+def test_fused_merge_counters_and_fallback():
+    """The split merge runs in the last decode workgroup of each row (merge
+    counters in the workspace) unless Pg > 4 * head_dim, where the separate
+    merge kernel runs.  Calls of different shapes in a row, on both paths,
+    must all match the oracle and leave the counters zero."""
+    import orthocache_gpu._launch as X
+    import orthocache_gpu._native as N
+    cases = [(3, 40, 128, 40, 1), (2, 9, 128, None, 0), (1, 300, 64, 300, 1), (3, 40, 128, 7, 0),
+             (1, 300, 64, 300, 1), (2, 9, 128, 3, 2)]
+    for i, (rows, tiles, d, P, spw) in enumerate(cases):
+        wl = _mixed(rows, tiles, d, "f32", seed=30 + i)
+        q = torch.randn((rows * 2, d), generator=torch.Generator().manual_seed(i))
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+        res = X.decode(kv, q.to(DEV), 2, gate=N.OC_GATE_CS, threshold=150.0, num_splits=P,
+                       out_dtype=torch.float32, splits_per_group=spw)
+        torch.cuda.synchronize()
+        ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate="cs", threshold=150.0, G=2,
+                            num_splits=res.num_splits)
+        assert_out(res.out, ref["out"], "f32", f"case {i}")
+    for buf in X._WORKSPACES.values():
+        assert int(buf[: 64 << 10].count_nonzero()) == 0, "merge counters not left zero"
+
+
 def test_v1_matches_oracle_and_reference_edge_cases():
     from orthocache_gpu import fused_orthocache_attention
     g = torch.Generator().manual_seed(42)
