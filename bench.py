@@ -52,8 +52,10 @@ def parse():
     ap.add_argument("--extra-batch", type=int, default=8, help="batch of the secondary line (0 = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="host seconds spent on the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--read-probe", type=int, default=1, help="also time the streaming-read probe (0 = skip)")
     ap.add_argument("--spw", type=int, default=0, help="logical splits per workgroup (0 = library default)")
-    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy"], default=None,
+    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read"],
+                    default=None,
                     help="time only this decode variant of the primary batch, or a plain 1 GiB device copy "
                          "(the reference kernel for scaling the profiler's byte counters)")
     return ap.parse_args()
@@ -222,6 +224,38 @@ def cpu_baseline(setup, seconds):
             "host_cpus": os.cpu_count()}
 
 
+def read_probe(steps, warmup, nbytes=2 << 30):
+    """Achievable HBM read bandwidth: oc_hbm_read_probe (128-bit loads, four
+    in flight per thread) over a 2 GiB buffer, best grid size."""
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    lib, stream = N.lib(), X.current_stream(buf.device)
+    best = None
+    for blocks in (1024, 2048, 4096, 8192):
+        def run():
+            N.check("oc_hbm_read_probe", lib.oc_hbm_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes,
+                                                               ctypes.c_void_p(sink.data_ptr()), blocks,
+                                                               ctypes.c_void_p(stream)))
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            run()
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / steps
+        gbps = nbytes / (us * 1e-6) / 1e9
+        if best is None or gbps > best["gbps"]:
+            best = {"gbps": round(gbps, 1), "us": round(us, 1), "blocks": blocks, "bytes": nbytes}
+    del buf
+    return best
+
+
 def traffic_from_profiles():
     """HBM bytes per decode launch measured with rocprofv3 counters, when a
     summary has been committed under profiles/."""
@@ -259,6 +293,9 @@ def main():
         print(json.dumps({"only": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "us_per_copy": us,
                           "gbps_read_plus_write": 2 * (1 << 30) / (us * 1e-6) / 1e9}))
         return
+    if args.only == "read":
+        print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))
+        return
     primary = Setup(args.batch, spw=args.spw)
     if args.only:
         v = args.only
@@ -276,6 +313,7 @@ def main():
         del sec
     ach = r1["step_gbps"]
     traffic = traffic_from_profiles()
+    probe = read_probe(20, 3) if args.read_probe else None
     line = {
         "metric": METRIC,
         "value": args.batch / (r1["cached_us"] * 1e-6),
@@ -309,6 +347,8 @@ def main():
         "single_pass_gbps": round(r1["single_pass_gbps"], 1),
         "eviction_rate": r1["eviction_rate"],
     }
+    if probe:
+        line["hbm_read_probe"] = dict(probe, frac_of_peak=round(probe["gbps"] / HBM_PEAK_GBPS, 4))
     if extra:
         line["batch%d" % extra["batch"]] = {
             "us_per_step": extra["cached_us"], "tokens_per_s": extra["batch"] / (extra["cached_us"] * 1e-6),

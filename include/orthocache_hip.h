@@ -207,6 +207,14 @@ int oc_lse_merge(const float* m, const float* l, const float* acc, int32_t rows,
  */
 int oc_dequant_fp8(const void* src, int64_t n, float scale, int32_t out_dtype, void* dst, void* stream);
 
+/* oc_hbm_read_probe -- measurement aid with no counterpart in the
+ * reference: streams `bytes` (a multiple of 16, src 16-byte aligned) from
+ * device memory with 128-bit loads over `blocks` 256-thread workgroups and
+ * XOR-folds them per thread (sink[0..blocks) is written only when a
+ * thread's fold equals a fixed sentinel, which keeps the loads live).  Timed by bench.py to state the achievable read bandwidth
+ * next to the 8 TB/s peak. */
+int oc_hbm_read_probe(const void* src, size_t bytes, float* sink, int32_t blocks, void* stream);
+
 /* sizeof(oc_kv_desc) and sizeof(oc_decode_params) as compiled into the
  * library, so that a binding can check its own struct layout (no
  * counterpart in the reference, which has no native ABI) */
