@@ -287,18 +287,21 @@ static int device_cus() {
 
 // Splits per workgroup: enough tiles per workgroup (about 16) to amortise
 // its prologue and epilogue, while keeping at least one workgroup per CU.
+// query heads per decode workgroup for G heads per kv row
+static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G)); }
+
 static int choose_spw(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
   const int P = p->num_splits;
   const int T = std::max(1, p->kv.num_tiles);
   const int tiles_per_split = std::max(1, (T + P - 1) / P);
-  // up to 64 tiles per workgroup, but at least two workgroups per CU (two
-  // 256-thread workgroups are resident per CU at the decode kernel's
-  // register budget), so that a small batch still fills the chip
-  int spw = std::max(1, 64 / tiles_per_split);
+  // up to 128 tiles per workgroup, but at least one workgroup per CU (one
+  // 512-thread workgroup is resident per CU at the decode kernel's register
+  // budget), so that a small batch still fills the chip
+  int spw = std::max(1, 128 / tiles_per_split);
   const int cus = device_cus();
-  const int gchunks = (p->G + 7) / 8;
-  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < 2 * (int64_t)cus) spw >>= 1;
+  const int gchunks = (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
+  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < (int64_t)cus) spw >>= 1;
   return std::min(spw, P);
 }
 
@@ -314,8 +317,6 @@ extern "C" int32_t oc_decode_num_groups(const oc_decode_params* p) {
   return num_groups(p, choose_spw(p));
 }
 
-// query heads per decode workgroup for G heads per kv row
-static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G)); }
 
 // Workspace layout: [0, kCounterBytes) merge counters (zero before the first
 // call, left zero by every call), then the partial states unless the caller
@@ -405,6 +406,10 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   }
   const int oes = p->out_dtype == OC_F32 ? 4 : 2;
   a.fuse = fused_merge(p, a.Pg) ? 1 : 0;
+  // split the retained tiles of a row evenly over its workgroups (cached
+  // mode); with one split per workgroup each partial stays the state of
+  // exactly one logical split {s + kP}
+  a.bal = (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && a.spw > 1 && p->kv.num_tiles <= kMaxBalTiles) ? 1 : 0;
   a.out = (char*)p->out;
   a.out_dtype = p->out_dtype;
   a.out_stride = p->out_row_stride * oes;

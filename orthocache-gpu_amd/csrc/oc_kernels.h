@@ -21,9 +21,16 @@
 namespace oc {
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // scoring / transform kernels: one tile per wave
 constexpr int kThreads = kWave * kWaves;
+// Decode kernel workgroup: 8 waves (one workgroup per CU at two waves per
+// SIMD) except float32 K/V at head_dim 128, which runs one wave per SIMD.
+template <int DT, int D>
+struct DecWaves {
+  static constexpr int value = (DT == OC_F32 && D == 128) ? 4 : 8;
+};
 constexpr float kM0 = -1e9f;
+constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
 
 // Kernel arguments (byte strides).  Built by oc_api.hip from oc_decode_params.
 struct DecodeArgs {
@@ -67,6 +74,10 @@ struct DecodeArgs {
   // zero on entry and left zero)
   int32_t fuse;
   int32_t out_dtype;
+  // balanced cached decode: the workgroups of a row split the row's retained
+  // tiles evenly by rank (set when cached, spw > 1 and T <= kMaxBalTiles)
+  int32_t bal;
+  int32_t reserved_bal;
   int32_t* counters;
   char* out;
   int64_t out_stride;  // bytes between query-head rows of out
@@ -187,6 +198,20 @@ __device__ __forceinline__ float rows4_sum(float x) {
   x = lo + hi;
   row_pair<32>(x, lo, hi);
   return lo + hi;
+}
+
+// Inclusive prefix sum over the 64 lanes: row_shr 1, 2, 4, 8 inside each
+// 16-lane row, then lane 15 added to row 1 and row 3 (row_bcast:15) and
+// lane 31 to rows 2 and 3 (row_bcast:31).  Lanes whose DPP source does not
+// exist add 0.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return x;
 }
 
 // One transpose-reduce step: the lane keeps half of its n = 2M values (the
@@ -687,8 +712,10 @@ template <int DT, int D, int GT, bool DOT2, bool PAGED>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, int s, int g0,
                                             float qmax, bool qnan, const float* sh_qf,
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
-                                            float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh) {
+                                            float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh,
+                                            const uint64_t* sh_bits, int wpre, int r0, int r1) {
   constexpr int CPL = D / 16;
+  constexpr int kDW = DecWaves<DT, D>::value;
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -711,16 +738,39 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   uint32_t kw[16][L::LW];
   uint32_t vw[16][L::LW];
   int kept = 0;
-  int kk = wave - kWaves;  // single-pass position in the group's tile list
+  int kk = wave - kDW;  // single-pass position in the group's tile list
   uint64_t cmask = 0;      // cached: retained tiles of the current 64-entry chunk
   int c0 = -64, rank = 0;
+  int rb = r0 + wave - kDW, wc = 0;  // balanced: retained rank, bitmask word
   // next tile of this wave, or -1: every tile of the list round-robin
-  // (single-pass, dense) or every retained tile round-robin (cached)
+  // (single-pass, dense), every retained tile round-robin (cached), or the
+  // retained tiles of ranks r0 + wave, r0 + wave + 4, ... < r1 (balanced)
   auto next_tile = [&]() -> int {
     int t = -1;
-    if (!cached) {
+    if (a.bal) {
+      rb += kDW;
+      if (rb < r1) {
+        // lane group holding rank rb: the first lane whose inclusive prefix
+        // exceeds rb; then the word inside its four
+        const int lg = __popcll((unsigned long long)__ballot(wpre <= rb));
+        int base = __builtin_amdgcn_readlane(wpre, lg);
+        wc = 4 * lg + 3;
+        uint64_t bits = sh_bits[wc];
+        base -= __popcll((unsigned long long)bits);
+        for (int q = 2; q >= 0 && base > rb; --q) {
+          bits = sh_bits[4 * lg + q];
+          wc = 4 * lg + q;
+          base -= __popcll((unsigned long long)bits);
+        }
+        const int k = rb - base;
+        // the k-th set bit of bits: the lane whose bit is set with k set bits below it
+        const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+        const bool hit = ((bits >> lane) & 1ull) && below == k;
+        t = wc * 64 + __ffsll((unsigned long long)__ballot(hit)) - 1;
+      }
+    } else if (!cached) {
       for (;;) {
-        kk += kWaves;
+        kk += kDW;
         if (kk >= n_split) break;
         t = s + (kk / w) * a.P + kk % w;
         if (t < ri.n_tiles) break;
@@ -731,7 +781,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
         if (cmask) {
           const int bit = __ffsll((unsigned long long)cmask) - 1;
           cmask &= cmask - 1;
-          if ((rank++ & (kWaves - 1)) == wave) {
+          if ((rank++ & (kDW - 1)) == wave) {
             const int x = c0 + bit;
             t = s + (x / w) * a.P + x % w;
             break;
@@ -810,7 +860,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // No full write-back fence is needed in the other workgroups.
 // sh_w (>= GT * Pg floats) and sh_inv (>= GT floats) reuse the wave-merge
 // LDS, which is dead by now.
-template <int D, int GT>
+template <int D, int GT, int kDW>
 __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int g0, int g_active, float* sh_w,
                                               float* sh_inv) {
   __shared__ int sh_last;
@@ -824,20 +874,65 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   }
   __syncthreads();
   if (!sh_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // the other workgroups' partials are read with agent-scope (sc1) loads,
+  // which are coherent across the XCDs' L2s without an L2 invalidate.  All
+  // first-round loads (m, l of partials 0..63 and the first PF accumulator
+  // quads of every thread) are issued before any of them is used.
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int Pg = a.Pg;
-  for (int g = wave; g < g_active; g += kWaves) {
+  constexpr int CQ = D / 4;
+  constexpr int NPAIR = GT * CQ;
+  constexpr int kDT = kDW * kWave;
+  constexpr int NSLICE = kDT / NPAIR;
+  constexpr int PF = D >= 128 ? 32 : 8;  // the D = 64 kernels keep more waves per SIMD
+  const int pair = threadIdx.x % NPAIR;
+  const int sl = threadIdx.x / NPAIR;
+  const int gp = pair / CQ;
+  const int cq = pair - gp * CQ;
+  // one buffer descriptor over this head's Pg x D partial accumulators
+  const float* hp = a.pacc + ((int64_t)row * a.G + g0 + min(gp, g_active - 1)) * Pg * D;
+  const __amdgpu_buffer_rsrc_t pr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)hp, (short)0, Pg * D * (int)sizeof(float), 0x00020000);
+  auto ld4 = [&](int q) -> float4 {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, (q * D + 4 * cq) * (int)sizeof(float), 0, 16 /* sc1 */);
+    return make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+  };
+  auto ldc = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  static_assert(GT <= 2 * kDW, "a wave merges at most two heads");
+  float m0[2], l0[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int g = wave + k * kDW;
     const int64_t base = ((int64_t)row * a.G + g0 + g) * Pg;
-    float mx = -__builtin_inff();
-    for (int q = lane; q < Pg; q += 64) mx = fmaxf(mx, a.pm[base + q]);
+    const bool ok = g < g_active && lane < Pg;
+    m0[k] = ok ? ldc(a.pm + base + lane) : -__builtin_inff();
+    l0[k] = ok ? ldc(a.pl + base + lane) : 0.f;
+  }
+  float4 pf[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    const int q = sl + i * NSLICE;
+    pf[i] = (gp < g_active && q < Pg) ? ld4(q) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int g = wave + k * kDW;
+    if (g >= g_active) break;
+    const int64_t base = ((int64_t)row * a.G + g0 + g) * Pg;
+    float mx = m0[k];
+    for (int q = lane + 64; q < Pg; q += 64) mx = fmaxf(mx, ldc(a.pm + base + q));
     mx = wave_max(mx);
     float ls = 0.f;
-    for (int q = lane; q < Pg; q += 64) {
-      const float w = __expf(a.pm[base + q] - mx);
+    if (lane < Pg) {
+      const float w = __expf(m0[k] - mx);
+      sh_w[g * Pg + lane] = w;
+      ls = w * l0[k];
+    }
+    for (int q = lane + 64; q < Pg; q += 64) {
+      const float w = __expf(ldc(a.pm + base + q) - mx);
       sh_w[g * Pg + q] = w;
-      ls = __builtin_fmaf(w, a.pl[base + q], ls);
+      ls = __builtin_fmaf(w, ldc(a.pl + base + q), ls);
     }
     ls = wave_sum(ls);
     if (lane == 0) sh_inv[g] = fmaxf(ls, 1e-9f);
@@ -846,22 +941,23 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   // weighted sum over the Pg partials: thread (slice, g, column quad) adds
   // partials q = slice, slice + nslice, ... with all its loads independent;
   // the slices are then added in a fixed order (deterministic result)
-  constexpr int CQ = D / 4;
-  constexpr int NPAIR = GT * CQ;
-  constexpr int NSLICE = kThreads / NPAIR;
-  __shared__ float4 sh_red[kThreads];
-  const int pair = threadIdx.x % NPAIR;
-  const int sl = threadIdx.x / NPAIR;
-  const int g = pair / CQ;
-  const int cq = pair - g * CQ;
+  __shared__ float4 sh_red[kDT];
+  const int g = gp;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (g < g_active) {
-    const int64_t qh = (int64_t)row * a.G + g0 + g;
-    const float4* ap = reinterpret_cast<const float4*>(a.pacc + qh * Pg * D) + cq;
     const float* wg = sh_w + g * Pg;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int q = sl + i * NSLICE;
+      const float w = q < Pg ? wg[q] : 0.f;
+      acc.x = __builtin_fmaf(pf[i].x, w, acc.x);
+      acc.y = __builtin_fmaf(pf[i].y, w, acc.y);
+      acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
+      acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
+    }
 #pragma unroll 16
-    for (int q = sl; q < Pg; q += NSLICE) {
-      const float4 x = ap[(int64_t)q * CQ];
+    for (int q = sl + PF * NSLICE; q < Pg; q += NSLICE) {
+      const float4 x = ld4(q);
       const float w = wg[q];
       acc.x = __builtin_fmaf(x.x, w, acc.x);
       acc.y = __builtin_fmaf(x.y, w, acc.y);
@@ -890,19 +986,21 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   }
 }
 
-// Main decode kernel.  grid = (Pg, num_rows, ceil(G / GT)); block = 4 waves.
+// Main decode kernel.  grid = (Pg, num_rows, ceil(G / GT)); block = 8 waves.
 // Workgroup (g, row, chunk) forms the online-softmax state of query heads
 // [chunk*GT, chunk*GT + GT) over the retained tiles of the logical splits
 // s = g*spw .. g*spw + spw - 1 of the row (split s owns tiles {s + kP}):
-// the four waves take those tiles round-robin (single-pass) or take the
+// the eight waves take those tiles round-robin (single-pass) or take the
 // retained ones round-robin (cached), and their states are merged in LDS
 // into the workgroup's partial (m, l, acc).  With spw = 1 every partial is
 // exactly one logical split's state.
 // Two waves per SIMD (<= 256 VGPRs) except for float32 K/V, whose raw K and
 // V tiles alone take 256 registers.
 template <int DT, int D, int GT, bool DOT2, bool PAGED>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
+__global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
     const DecodeArgs a) {
+  constexpr int kDW = DecWaves<DT, D>::value;
+  constexpr int kDT = kDW * kWave;
   const int lane = threadIdx.x & 63;
   const int s = blockIdx.x * a.spw;  // first split of this workgroup
   const int row = blockIdx.y;
@@ -912,40 +1010,61 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == 
 
   __shared__ float sh_qf[GT * D];
   __shared__ uint32_t sh_qp[GT * D / 2];
-  __shared__ float sh_m[kWaves][GT];
-  __shared__ float sh_l[kWaves][GT];
-  __shared__ float sh_acc[kWaves][GT][D];
-  __shared__ int sh_cnt[kWaves];
+  __shared__ float sh_m[kDW][GT];
+  __shared__ float sh_l[kDW][GT];
+  __shared__ float sh_acc[kDW][GT][D];
+  __shared__ int sh_cnt[kDW];
+  __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row
 
-  // cached mode: fetch the first chunk's scores before anything else
-  float pre_el = 0.f, pre_eh = 0.f;
+  // cached mode: fetch the scores before anything else (balanced: tiles
+  // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
+  // entry of the first chunk of the split list)
+  constexpr int kPreChunks = 4;
+  float pre_el[kPreChunks], pre_eh[kPreChunks];
+#pragma unroll
+  for (int k = 0; k < kPreChunks; ++k) pre_el[k] = pre_eh[k] = 0.f;
   if (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) {
-    const int w = min(a.spw, a.P - s);
-    const int t = s + (lane / w) * a.P + lane % w;
-    if (s < ri.n_tiles && t < ri.n_tiles) {
-      const int64_t o = (int64_t)row * a.sc_stride + t;
-      pre_eh = a.sc_eh[o];
-      pre_el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kPreChunks; ++k) {
+      int t;
+      bool in;
+      if (a.bal) {
+        t = k * kDT + threadIdx.x;
+        in = t < ri.n_tiles;
+      } else {
+        const int w = min(a.spw, a.P - s);
+        t = s + (lane / w) * a.P + lane % w;
+        in = k == 0 && s < ri.n_tiles && t < ri.n_tiles;
+      }
+      if (in) {
+        const int64_t o = (int64_t)row * a.sc_stride + t;
+        pre_eh[k] = a.sc_eh[o];
+        pre_el[k] = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
+      }
     }
   }
 
   // stage q of this chunk in LDS (float and packed 16-bit); q := round(q *
   // k_scale) in q's dtype for the Q_FOLD mode (fused_eviction.py:619-621)
   const int qes = a.q_dtype == OC_F32 ? 4 : 2;
-  for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
-    const int g = idx / D;
-    const int c = idx - g * D;
-    float x = 0.f;
+  for (int idx = threadIdx.x; idx < GT * D / 2; idx += kDT) {
+    const int e0 = 2 * idx;
+    const int g = e0 / D;
+    const int c = e0 - g * D;
+    float x0 = 0.f, x1 = 0.f;
     if (g < g_active) {
-      x = load_scalar(a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride + (int64_t)c * qes, a.q_dtype);
-      if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * a.k_scale, a.q_dtype);
+      const char* qp = a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride + (int64_t)c * qes;
+      x0 = load_scalar(qp, a.q_dtype);
+      x1 = load_scalar(qp + qes, a.q_dtype);
+      if (a.k_scale_mode == OC_KSCALE_Q_FOLD) {
+        x0 = round_to(x0 * a.k_scale, a.q_dtype);
+        x1 = round_to(x1 * a.k_scale, a.q_dtype);
+      }
     }
-    sh_qf[idx] = x;
-  }
-  __syncthreads();
-  if constexpr (DOT2) {
-    for (int idx = threadIdx.x; idx < GT * D / 2; idx += kThreads) {
-      const float x0 = sh_qf[2 * idx], x1 = sh_qf[2 * idx + 1];
+    sh_qf[e0] = x0;
+    sh_qf[e0 + 1] = x1;
+    if constexpr (DOT2) {
+      // x0, x1 are exact in the 16-bit q dtype, so the narrowing is exact
       uint32_t lo, hi;
       if (DT == OC_BF16) {
         lo = __float_as_uint(x0) >> 16;
@@ -957,11 +1076,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == 
       sh_qp[idx] = lo | (hi << 16);
     }
   }
-  // max_g ||q_g|| over all G query heads of the row (CS gate)
+  __syncthreads();
+  // max_g ||q_g|| over all G query heads of the row (CS gate): wave w forms
+  // the norms of heads w, w + 8, ... (lane j sums its D/16 columns, then the
+  // 16 lanes are added), the wave maxima are combined after the barrier
+  __shared__ float sh_qn[kDW];
+  __shared__ int sh_qnan[kDW];
   float qmax = 0.f;
   bool qnan = false;
   if (a.gate == OC_GATE_CS) {
-    for (int g = 0; g < a.G; ++g) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float wmax = 0.f;
+    bool wnan = false;
+    for (int g = wave; g < a.G; g += kDW) {
       float ss = 0.f;
       if (lane < 16) {
         const int gl = g - g0;
@@ -980,26 +1107,88 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == 
       }
       float qn = __builtin_sqrtf(wave_sum(ss));
       if ((double)qn < 1e-38) qn = 0.f;
-      if (__builtin_isnan(qn)) qnan = true;
-      qmax = fmaxf(qmax, qn);
+      if (__builtin_isnan(qn)) wnan = true;
+      wmax = fmaxf(wmax, qn);
+    }
+    if (lane == 0) {
+      sh_qn[wave] = wmax;
+      sh_qnan[wave] = wnan ? 1 : 0;
     }
   }
   __syncthreads();
+  if (a.gate == OC_GATE_CS) {
+#pragma unroll
+    for (int w = 0; w < kDW; ++w) {
+      qmax = fmaxf(qmax, sh_qn[w]);
+      qnan = qnan || sh_qnan[w] != 0;
+    }
+  }
 
-  decode_body<DT, D, GT, DOT2, PAGED>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt, pre_el,
-                               pre_eh);
+  // balanced cached decode: retained-tile bitmask of the whole row and its
+  // prefix counts, then this workgroup's even share [r0, r1) of the ranks
+  int r0 = 0, r1 = 0, wpre = 0;
+  if (a.bal) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = (ri.n_tiles + 63) / 64;
+#pragma unroll
+    for (int c = 0; c < kPreChunks * kDT; c += kDT) {
+      if (c < ri.n_tiles) {
+        const int t = c + threadIdx.x;
+        const bool keep = t < ri.n_tiles && cached_keep(a, ri, t, pre_el[c / kDT], pre_eh[c / kDT], qmax, qnan);
+        if (a.keep_out && t < ri.n_tiles && blockIdx.x == 0 && blockIdx.z == 0)
+          a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+        const uint64_t m = __ballot(keep);
+        const int wi = (c >> 6) + wave;
+        if (lane == 0 && wi < nw) sh_bits[wi] = m;
+      }
+    }
+    for (int c = kPreChunks * kDT; c < ri.n_tiles; c += kDT) {
+      const int t = c + threadIdx.x;
+      const bool in = t < ri.n_tiles;
+      float el = 0.f, eh = 0.f;
+      if (in) {
+        const int64_t o = (int64_t)row * a.sc_stride + t;
+        eh = a.sc_eh[o];
+        el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
+      }
+      const bool keep = in && cached_keep(a, ri, t, el, eh, qmax, qnan);
+      if (a.keep_out && in && blockIdx.x == 0 && blockIdx.z == 0)
+        a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+      const uint64_t m = __ballot(keep);
+      const int wi = (c >> 6) + wave;
+      if (lane == 0 && wi < nw) sh_bits[wi] = m;
+    }
+    // words nw .. (nw rounded up to 4) read as empty in the lookups below
+    if (threadIdx.x < 4 && nw + (int)threadIdx.x < ((nw + 3) & ~3)) sh_bits[nw + threadIdx.x] = 0;
+    __syncthreads();
+    // every wave: lane l counts the retained tiles of bitmask words
+    // 4l .. 4l+3; wpre = inclusive prefix of those counts over the lanes
+    int x = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int wi = 4 * lane + k;
+      x += wi < nw ? __popcll((unsigned long long)sh_bits[wi]) : 0;
+    }
+    wpre = wave_incl_scan(x);
+    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(wpre, 63);
+    r0 = (int)(total * blockIdx.x / (uint32_t)a.Pg);
+    r1 = (int)(total * (blockIdx.x + 1) / (uint32_t)a.Pg);
+  }
+
+  decode_body<DT, D, GT, DOT2, PAGED>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
+                                      pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1);
   __syncthreads();
 
-  // merge the four wave states into the split's partial
-  for (int idx = threadIdx.x; idx < g_active * D; idx += kThreads) {
+  // merge the eight wave states into the split's partial
+  for (int idx = threadIdx.x; idx < g_active * D; idx += kDT) {
     const int g = idx / D;
     const int c = idx - g * D;
     float mx = sh_m[0][g];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, sh_m[w][g]);
+    for (int w = 1; w < kDW; ++w) mx = fmaxf(mx, sh_m[w][g]);
     float acc = 0.f, l = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kDW; ++w) {
       const float e = __expf(sh_m[w][g] - mx);
       acc = __builtin_fmaf(sh_acc[w][g][c], e, acc);
       l = __builtin_fmaf(sh_l[w][g], e, l);
@@ -1015,8 +1204,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DT == 
     }
   }
   if (a.split_counts && threadIdx.x == 0 && blockIdx.z == 0)
-    a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = sh_cnt[0] + sh_cnt[1] + sh_cnt[2] + sh_cnt[3];
-  if (a.fuse) merge_if_last<D, GT>(a, row, g0, g_active, &sh_acc[0][0][0], &sh_l[0][0]);
+  {
+    int n = 0;
+#pragma unroll
+    for (int w = 0; w < kDW; ++w) n += sh_cnt[w];
+    a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = n;
+  }
+  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, &sh_acc[0][0][0], &sh_l[0][0]);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
@@ -1107,10 +1301,10 @@ hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 
 #define OC_DECODE_GT(DT, HD, DOT2, PG)                                                               \
   switch (gt) {                                                                                      \
-    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG>), grid, block, 0, st, a); break;  \
-    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG>), grid, block, 0, st, a); break;  \
-    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG>), grid, block, 0, st, a); break;  \
-    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG>), grid, block, 0, st, a); break; \
+    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
+    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
+    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break; \
   }
 #define OC_DECODE_CASES(DT, DOT2)                                                                    \
   if (head_dim == 128) {                                                                             \
@@ -1127,7 +1321,7 @@ constexpr bool kHasDot2 = DT == OC_BF16 || DT == OC_F16;
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
-    const dim3 grid(a.Pg, a.num_rows, gchunks), block(kThreads);                                  \
+    const dim3 grid(a.Pg, a.num_rows, gchunks);                                  \
     if (kHasDot2<DT> && a.q_dtype == DT) {                                                        \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \

@@ -284,8 +284,58 @@ def test_fused_merge_counters_and_fallback():
         ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate="cs", threshold=150.0, G=2,
                             num_splits=res.num_splits)
         assert_out(res.out, ref["out"], "f32", f"case {i}")
+    # same shape, new data each call: the merge must read this call's partials
+    for i in range(4):
+        wl = _mixed(2, 24, 128, "bf16", seed=50 + i)
+        q = torch.randn((8, 128), generator=torch.Generator().manual_seed(60 + i)).to(torch.bfloat16)
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+        res = X.decode(kv, q.to(DEV), 4, gate=N.OC_GATE_CS, threshold=150.0, num_splits=24,
+                       out_dtype=torch.float32, splits_per_group=2)
+        torch.cuda.synchronize()
+        ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate="cs", threshold=150.0, G=4,
+                            num_splits=24)
+        assert_out(res.out, ref["out"], "f32", f"repeat {i}")
     for buf in X._WORKSPACES.values():
         assert int(buf[: 64 << 10].count_nonzero()) == 0, "merge counters not left zero"
+
+
+@pytest.mark.parametrize("tiles", [45, 160])
+@pytest.mark.parametrize("spw", [2, 3, 8, 64])
+@pytest.mark.parametrize("gate", ["cs", "zeta"])
+def test_balanced_cached_decode(spw, gate, tiles):
+    """Cached mode with several splits per workgroup: the workgroups of a row
+    take equal shares of the row's retained tiles by rank, or (with at least
+    32 tiles per workgroup) take ranks from a shared counter.  The output, the
+    keep mask and the retained counts must match the oracle, with context
+    lengths that cut tiles (partial tail tiles are always retained)."""
+    import orthocache_gpu._launch as X
+    import orthocache_gpu._native as N
+    from orthocache_gpu.workloads import calibrate_tau, make_q
+    G = 4
+    wl = _mixed(3, tiles, 128, "bf16", seed=40 + spw)
+    q = make_q(3, G, 128, dtype=torch.bfloat16, seed=spw, low_band_heads=2)
+    lens = torch.tensor([tiles * 64, 1000, 64 * 7], dtype=torch.int32)
+    kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+    kv.lengths = lens.to(DEV)
+    el, eh, _, _ = X.score_tiles(kv, want_zeta=False, want_keep=False)
+    if gate == "cs":
+        thr = calibrate_tau(eh, q.to(DEV), G)
+        gcode = N.OC_GATE_CS
+    else:
+        thr, gcode = 5.0, N.OC_GATE_ZETA
+    for P in (None, 9):
+        res = X.decode(kv, q.to(DEV), G, gate=gcode, threshold=thr, mode=N.OC_MODE_CACHED, scores=(el, eh),
+                       num_splits=P, out_dtype=torch.float32, want_keep=True, splits_per_group=spw)
+        torch.cuda.synchronize()
+        ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate=gate, threshold=thr, G=G,
+                            lengths=lens.tolist(), num_splits=res.num_splits)
+        got_keep = res.keep.cpu().numpy().astype(bool)
+        for r, n in enumerate(lens.tolist()):
+            nt = (n + 63) // 64
+            assert np.array_equal(got_keep[r, :nt], ref["keep"][r, :nt]), f"row {r}"
+        assert_out(res.out, ref["out"], "f32", f"balanced spw={spw} P={P}")
+    for buf in X._WORKSPACES.values():
+        assert int(buf[: 64 << 10].count_nonzero()) == 0, "counters not left zero"
 
 
 def test_v1_matches_oracle_and_reference_edge_cases():
