@@ -698,6 +698,174 @@ __device__ __forceinline__ void tile_pv(float (&acc)[GT][D / 16], const float (&
 #undef OC_PV_STEP
 }
 
+// ------------------------------------------------- q.k on the matrix cores
+//
+// Cached and dense decode with 16-bit K and q of the same type form the
+// logits of a 64-token tile with v_mfma_f32_16x16x32_{bf16,f16}:
+// D[m][n] = sum_k A[m][k] B[k][n] with A = q (m = query head, zero rows past
+// GT), B = K^T of one 16-token block (n = token) and k = 32 head-dim columns
+// per instruction, fp32 accumulation (the same products and accumulation
+// type as v_dot2_f32).  Lane layouts (lane = 16*kg + x):
+//   A: q[head x][32*dc + 8*kg .. +8]        B: K[token 16*tb + x][32*dc + 8*kg .. +8]
+//   D: lane 16*r + x, register i -> head 4*r + i, token 16*tb + x
+// so the K tile is read as 16-byte row pieces (tb, dc) of one token per lane.
+// The probabilities go to the wave's LDS slot as p[token][head] and p.V
+// runs on the VALU in the tile layout above (V is not transposed).
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_qk(const uint32_t (&aq)[4], const uint32_t (&bk)[4], f32x4 c) {
+  const u32x4 av = {aq[0], aq[1], aq[2], aq[3]};
+  const u32x4 bv = {bk[0], bk[1], bk[2], bk[3]};
+  if constexpr (DT == OC_BF16) {
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv),
+                                                   c, 0, 0, 0);
+  } else {
+    typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv), c,
+                                                  0, 0, 0);
+  }
+}
+
+// A operand: q of head (lane & 15) from the packed LDS copy (zero past GT).
+template <int D, int GT>
+__device__ __forceinline__ void load_q_mfma(const uint32_t* sh_qp, int lane, uint32_t (&aq)[D / 32][4]) {
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int dc = 0; dc < D / 32; ++dc)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) aq[dc][w] = x < GT ? sh_qp[x * (D / 2) + 16 * dc + 4 * kg + w] : 0u;
+}
+
+// B operand pieces of one K tile (contiguous rows, 16-bit elements): lane
+// 16*kg + x reads token 16*tb + x, columns 32*dc + 8*kg .. +8.  One buffer
+// descriptor per 16-token block whose size is the valid part of the block,
+// so tokens at or past n_tok read as zero.
+template <int D>
+__device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
+                                            uint32_t (&kb)[4][D / 32][4]) {
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+  const int tok0 = t * 64;
+  const int64_t ts = a.k_tok_stride;
+  const char* base = a.k + (int64_t)row * a.k_row_stride + tok0 * ts;
+  const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
+  const int voff = x * (int)ts + 16 * kg;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int rb = 16 * tb * (int)ts;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * dc, 0, 0);
+      kb[tb][dc][0] = v[0];
+      kb[tb][dc][1] = v[1];
+      kb[tb][dc][2] = v[2];
+      kb[tb][dc][3] = v[3];
+    }
+  }
+}
+
+// Online-softmax state in the MFMA output layout: lane 16*r + x keeps heads
+// 4*r + i (i = 0..3); l is the lane's partial sum over its tokens.
+struct MState {
+  float m[4];
+  float l[4];
+};
+
+// Logits of one tile on the matrix cores, the online-softmax update of the
+// heads' states, p (times vmul) to the wave's LDS slot sp[token * 8 + head],
+// and the rescale of the p.V accumulators by e^(m_old - m_new).
+template <int DT, int D, int GT>
+__device__ __forceinline__ void tile_softmax_mfma(MState& ms, float (&acc)[GT][D / 16], const uint32_t (&aq)[D / 32][4],
+                                                  const uint32_t (&kb)[4][D / 32][4], float* sp, float lscale,
+                                                  float vmul, int valid, int lane) {
+  constexpr int CPL = D / 16;
+  const int x = lane & 15;
+  const int r = lane >> 4;
+  float v[4][4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) c = mfma_qk<DT>(aq[dc], kb[tb][dc], c);
+    const bool tok_ok = 16 * tb + x < valid;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[i] * lscale : -__builtin_inff();
+  }
+  float alpha[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float mt = fmaxf(fmaxf(v[0][i], v[1][i]), fmaxf(v[2][i], v[3][i]));
+    mt = fmaxf(mt, xpair<8>(mt));
+    mt = fmaxf(mt, xpair<4>(mt));
+    mt = fmaxf(mt, xpair<2>(mt));
+    mt = fmaxf(mt, xpair<1>(mt));
+    const float mn = fmaxf(ms.m[i], mt);
+    alpha[i] = __expf(ms.m[i] - mn);
+    ms.m[i] = mn;
+    float ls = 0.f;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const float pp = __expf(v[tb][i] - mn);
+      ls += pp;
+      v[tb][i] = pp * vmul;
+    }
+    ms.l[i] = __builtin_fmaf(ms.l[i], alpha[i], ls);
+  }
+  if (r < (GT + 3) / 4) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      float4 pv = make_float4(v[tb][0], v[tb][1], v[tb][2], v[tb][3]);
+      *reinterpret_cast<float4*>(sp + (16 * tb + x) * 8 + 4 * r) = pv;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    // head g's factor lives in the lanes of row g / 4, register g % 4
+    const float al = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha[g & 3]), 16 * (g >> 2)));
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[g][c] *= al;
+  }
+}
+
+// acc[g][c] += sum_i p(token 4i+gamma, head g) * v[i][c], p read from the
+// wave's LDS slot (all 16 lanes of a row read the same token).
+template <int DT, int D, int GT>
+__device__ __forceinline__ void tile_pv_lds(float (&acc)[GT][D / 16], const float* sp,
+                                            const uint32_t (&vw)[16][Lay<DT, D>::LW], int lane) {
+  constexpr int CPL = D / 16;
+  const int gamma = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float* pt = sp + (4 * i + gamma) * 8;
+    float pg[8];
+    const float4 p0 = *reinterpret_cast<const float4*>(pt);
+    pg[0] = p0.x;
+    pg[1] = p0.y;
+    pg[2] = p0.z;
+    pg[3] = p0.w;
+    if constexpr (GT > 4) {
+      const float4 p1 = *reinterpret_cast<const float4*>(pt + 4);
+      pg[4] = p1.x;
+      pg[5] = p1.y;
+      pg[6] = p1.z;
+      pg[7] = p1.w;
+    }
+    float fv[CPL];
+    row_vals<DT, D>(vw[i], fv);
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[g][c] = __builtin_fmaf(pg[g], fv[c], acc[g][c]);
+  }
+}
+
 // Retain decision for tile t of a row in cached mode from its stored
 // energies; a partial tail tile is always retained.
 __device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& ri, int t, float el, float eh,
@@ -708,12 +876,12 @@ __device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& 
 
 // The tile loop, the wave merge and the partial-state write of one
 // workgroup (see decode_kernel).
-template <int DT, int D, int GT, bool DOT2, bool PAGED>
+template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, int s, int g0,
                                             float qmax, bool qnan, const float* sh_qf,
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
                                             float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh,
-                                            const uint64_t* sh_bits, int wpre, int r0, int r1) {
+                                            const uint64_t* sh_bits, int wpre, int r0, int r1, float* sh_p) {
   constexpr int CPL = D / 16;
   constexpr int kDW = DecWaves<DT, D>::value;
   using L = Lay<DT, D>;
@@ -735,7 +903,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     for (int c = 0; c < CPL; ++c) acc[g][c] = 0.f;
   }
 
-  uint32_t kw[16][L::LW];
+  MState ms;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ms.m[i] = kM0;
+    ms.l[i] = 0.f;
+  }
+  uint32_t aq[MQK ? D / 32 : 1][4];
+  if constexpr (MQK) load_q_mfma<D, GT>(sh_qp, lane, aq);
+  float* sp = sh_p + wave * 512;  // this wave's p[token][head] slot (MQK)
+
   uint32_t vw[16][L::LW];
   int kept = 0;
   int kk = wave - kDW;  // single-pass position in the group's tile list
@@ -811,40 +988,62 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     return a.scale * (a.k_scale_mode == OC_KSCALE_TILE ? a.k_scales[(int64_t)row * a.ks_stride + t] : 1.f);
   };
 
-  float p[GT];
-  for (int t = next_tile(); t >= 0; t = next_tile()) {
-    const int valid = min(64, ri.n_tok - t * 64);
-    load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
-    bool keep = true;
-    if (!cached && a.gate != OC_GATE_NONE) {
-      // single pass: gate on the K tile just read; V is read only if kept
-      if (valid == 64) {
-        float el, eh;
-        tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
-        keep = gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
-      }
-      if (a.keep_out && lane == 0 && blockIdx.z == 0)
-        a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
-    }
-    if (keep) {
+  if constexpr (MQK) {
+    // cached or dense decode: every listed tile is attended
+    uint32_t kb[4][D / 32][4];
+    for (int t = next_tile(); t >= 0; t = next_tile()) {
+      const int valid = min(64, ri.n_tok - t * 64);
+      load_k_mfma<D>(a, ri, row, t, lane, kb);
       load_tile<DT, D, PAGED>(a, ri, row, t, true, lane, vw);
-      tile_softmax<DT, D, GT, DOT2>(st, acc, p, kw, sh_qf, sh_qp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
-      tile_pv<DT, D, GT>(acc, p, vw);
+      tile_softmax_mfma<DT, D, GT>(ms, acc, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+      tile_pv_lds<DT, D, GT>(acc, sp, vw, lane);
       ++kept;
+    }
+  } else {
+    uint32_t kw[16][L::LW];
+    float p[GT];
+    for (int t = next_tile(); t >= 0; t = next_tile()) {
+      const int valid = min(64, ri.n_tok - t * 64);
+      load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
+      bool keep = true;
+      if (!cached && a.gate != OC_GATE_NONE) {
+        // single pass: gate on the K tile just read; V is read only if kept
+        if (valid == 64) {
+          float el, eh;
+          tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
+          keep = gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
+        }
+        if (a.keep_out && lane == 0 && blockIdx.z == 0)
+          a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+      }
+      if (keep) {
+        load_tile<DT, D, PAGED>(a, ri, row, t, true, lane, vw);
+        tile_softmax<DT, D, GT, DOT2>(st, acc, p, kw, sh_qf, sh_qp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+        tile_pv<DT, D, GT>(acc, p, vw);
+        ++kept;
+      }
     }
   }
 
   // wave -> LDS: l summed over lanes, acc summed over the 4 token groups
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
-    const float lt = wave_sum(st.l[g]);
+    float mg, lt;
+    if constexpr (MQK) {
+      // head g: register g % 4 of the lanes of row g / 4
+      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g & 3]), 16 * (g >> 2)));
+      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g & 3])), 16 * (g >> 2)));
+    } else {
+      mg = st.m[g];
+      lt = wave_sum(st.l[g]);
+    }
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const float x = rows4_sum(acc[g][c]);
       if (lane < 16) sh_acc[wave][g][j * CPL + c] = x;
     }
     if (lane == 0) {
-      sh_m[wave][g] = st.m[g];
+      sh_m[wave][g] = mg;
       sh_l[wave][g] = lt;
     }
   }
@@ -996,7 +1195,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
 // exactly one logical split's state.
 // Two waves per SIMD (<= 256 VGPRs) except for float32 K/V, whose raw K and
 // V tiles alone take 256 registers.
-template <int DT, int D, int GT, bool DOT2, bool PAGED>
+template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK>
 __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
     const DecodeArgs a) {
   constexpr int kDW = DecWaves<DT, D>::value;
@@ -1015,6 +1214,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_acc[kDW][GT][D];
   __shared__ int sh_cnt[kDW];
   __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row
+  __shared__ float sh_p[MQK ? kDW * 512 : 1];       // per wave p[token][head] of the current tile (MQK)
 
   // cached mode: fetch the scores before anything else (balanced: tiles
   // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
@@ -1175,8 +1375,8 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     r1 = (int)(total * (blockIdx.x + 1) / (uint32_t)a.Pg);
   }
 
-  decode_body<DT, D, GT, DOT2, PAGED>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
-                                      pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1);
+  decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
+                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p);
   __syncthreads();
 
   // merge the eight wave states into the split's partial
@@ -1299,19 +1499,38 @@ hipError_t launch_score(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 
-#define OC_DECODE_GT(DT, HD, DOT2, PG)                                                               \
-  switch (gt) {                                                                                      \
-    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
-    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
-    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break;  \
-    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG>), grid, dim3(DecWaves<DT, HD>::value * kWave), 0, st, a); break; \
+template <int DT, int HD, bool DOT2, bool PG, bool MQ>
+inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  const dim3 block(DecWaves<DT, HD>::value * kWave);
+  switch (gt) {
+    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a); break;
   }
-#define OC_DECODE_CASES(DT, DOT2)                                                                    \
-  if (head_dim == 128) {                                                                             \
-    if (a.paged) { OC_DECODE_GT(DT, 128, DOT2, true) } else { OC_DECODE_GT(DT, 128, DOT2, false) }   \
-  } else {                                                                                           \
-    if (a.paged) { OC_DECODE_GT(DT, 64, DOT2, true) } else { OC_DECODE_GT(DT, 64, DOT2, false) }     \
+}
+
+// q . k on the matrix cores for contiguous 16-bit K (q of the same type)
+// whenever every listed tile is attended (cached scores or no gate)
+template <int DT, int HD, bool DOT2>
+inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  if (a.paged) {
+    launch_decode_gt<DT, HD, DOT2, true, false>(a, gt, grid, st);
+    return;
   }
+  if constexpr (DOT2) {
+    // up to four heads per workgroup (eight spill in this variant)
+    if ((a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE) && gt <= 4) {
+      launch_decode_gt<DT, HD, DOT2, false, true>(a, gt, grid, st);
+      return;
+    }
+  }
+  launch_decode_gt<DT, HD, DOT2, false, false>(a, gt, grid, st);
+}
+
+#define OC_DECODE_CASES(DT, DOT2)                                 \
+  if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
+  else launch_decode_hd<DT, 64, DOT2>(a, gt, grid, st);
 
 // q . k in 16-bit dot products when K and q share the 16-bit type
 template <int DT>
