@@ -778,14 +778,35 @@ struct MState {
   float l[4];
 };
 
-// Logits of one tile on the matrix cores, the online-softmax update of the
-// heads' states, p (times vmul) to the wave's LDS slot sp[token * 8 + head],
-// and the rescale of the p.V accumulators by e^(m_old - m_new).
+// V tile of one 64-token tile into the wave's LDS slot, row-major
+// [token][D] 16-bit, by direct-to-LDS buffer loads (16 bytes per lane, one
+// 1 KiB instruction per 1024 / (2 D) tokens); tokens at or past n_tok read
+// as zero through the descriptor's range check.
+template <int D>
+__device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
+                                           uint16_t* sv) {
+  constexpr int TPI = 1024 / (2 * D);  // tokens per instruction
+  constexpr int LPT = 64 / TPI;        // lanes per token
+  const int64_t ts = a.v_tok_stride;
+  const int tok0 = t * 64;
+  const char* base = a.v + (int64_t)row * a.v_row_stride + tok0 * ts;
+  const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
+  const int voff = (lane / LPT) * (int)ts + 16 * (lane % LPT);
+#pragma unroll
+  for (int i = 0; i < 64 / TPI; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 512),
+                                             16, voff + i * TPI * (int)ts, 0, 0, 0);
+}
+
+// Logits of one tile on the matrix cores and the online-softmax update of
+// the heads' states; p (times vmul) goes to the wave's LDS slot as
+// sp[head * 64 + token] and the p.V accumulators are rescaled by
+// e^(m_old - m_new) (same lane layout as the state).
 template <int DT, int D, int GT>
-__device__ __forceinline__ void tile_softmax_mfma(MState& ms, float (&acc)[GT][D / 16], const uint32_t (&aq)[D / 32][4],
+__device__ __forceinline__ void tile_softmax_mfma(MState& ms, f32x4 (&accp)[D / 16], const uint32_t (&aq)[D / 32][4],
                                                   const uint32_t (&kb)[4][D / 32][4], float* sp, float lscale,
                                                   float vmul, int valid, int lane) {
-  constexpr int CPL = D / 16;
   const int x = lane & 15;
   const int r = lane >> 4;
   float v[4][4];
@@ -798,7 +819,6 @@ __device__ __forceinline__ void tile_softmax_mfma(MState& ms, float (&acc)[GT][D
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[i] * lscale : -__builtin_inff();
   }
-  float alpha[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float mt = fmaxf(fmaxf(v[0][i], v[1][i]), fmaxf(v[2][i], v[3][i]));
@@ -807,7 +827,7 @@ __device__ __forceinline__ void tile_softmax_mfma(MState& ms, float (&acc)[GT][D
     mt = fmaxf(mt, xpair<2>(mt));
     mt = fmaxf(mt, xpair<1>(mt));
     const float mn = fmaxf(ms.m[i], mt);
-    alpha[i] = __expf(ms.m[i] - mn);
+    const float alpha = __expf(ms.m[i] - mn);
     ms.m[i] = mn;
     float ls = 0.f;
 #pragma unroll
@@ -816,53 +836,73 @@ __device__ __forceinline__ void tile_softmax_mfma(MState& ms, float (&acc)[GT][D
       ls += pp;
       v[tb][i] = pp * vmul;
     }
-    ms.l[i] = __builtin_fmaf(ms.l[i], alpha[i], ls);
+    ms.l[i] = __builtin_fmaf(ms.l[i], alpha, ls);
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha;
   }
-  if (r < (GT + 3) / 4) {
+  if (r == 0) {
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      float4 pv = make_float4(v[tb][0], v[tb][1], v[tb][2], v[tb][3]);
-      *reinterpret_cast<float4*>(sp + (16 * tb + x) * 8 + 4 * r) = pv;
-    }
-  }
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-  for (int g = 0; g < GT; ++g) {
-    // head g's factor lives in the lanes of row g / 4, register g % 4
-    const float al = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha[g & 3]), 16 * (g >> 2)));
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) acc[g][c] *= al;
+      for (int tb = 0; tb < 4; ++tb) sp[i * 64 + 16 * tb + x] = v[tb][i];
   }
 }
 
-// acc[g][c] += sum_i p(token 4i+gamma, head g) * v[i][c], p read from the
-// wave's LDS slot (all 16 lanes of a row read the same token).
+// p.V on the matrix cores: D[head][d] += sum_token P[head][token] V[token][d]
+// per 32-token block and 16-column chunk.  A = P of head (lane & 15), tokens
+// 8*kg .. +8 of the block, as a 16-bit high part plus the 16-bit rounding
+// of the remainder (two instructions, so the products keep about 16
+// mantissa bits of p; V is exact); B = V read from the LDS tile with the
+// transposing ds_read_b64_tr_b16 (lane x of group kg gets V[8kg + e][16nc + x]
+// from the four lanes that address rows 8kg + e, columns 16nc + 4(x%4) ..).
 template <int DT, int D, int GT>
-__device__ __forceinline__ void tile_pv_lds(float (&acc)[GT][D / 16], const float* sp,
-                                            const uint32_t (&vw)[16][Lay<DT, D>::LW], int lane) {
-  constexpr int CPL = D / 16;
-  const int gamma = lane >> 4;
+__device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float* sp, const uint16_t* sv, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int x = lane & 15;
+  const int kg = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float* pt = sp + (4 * i + gamma) * 8;
-    float pg[8];
-    const float4 p0 = *reinterpret_cast<const float4*>(pt);
-    pg[0] = p0.x;
-    pg[1] = p0.y;
-    pg[2] = p0.z;
-    pg[3] = p0.w;
-    if constexpr (GT > 4) {
-      const float4 p1 = *reinterpret_cast<const float4*>(pt + 4);
-      pg[4] = p1.x;
-      pg[5] = p1.y;
-      pg[6] = p1.z;
-      pg[7] = p1.w;
+  for (int tb2 = 0; tb2 < 2; ++tb2) {
+    float pv[8];
+    if (x < GT) {
+      const float4 p0 = *reinterpret_cast<const float4*>(sp + x * 64 + 32 * tb2 + 8 * kg);
+      const float4 p1 = *reinterpret_cast<const float4*>(sp + x * 64 + 32 * tb2 + 8 * kg + 4);
+      pv[0] = p0.x; pv[1] = p0.y; pv[2] = p0.z; pv[3] = p0.w;
+      pv[4] = p1.x; pv[5] = p1.y; pv[6] = p1.z; pv[7] = p1.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = 0.f;
     }
-    float fv[CPL];
-    row_vals<DT, D>(vw[i], fv);
+    uint32_t ahi[4], alo[4];
 #pragma unroll
-    for (int g = 0; g < GT; ++g)
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == OC_BF16) {
+        const __bf16 h0 = (__bf16)pv[2 * e], h1 = (__bf16)pv[2 * e + 1];
+        const __bf16 l0 = (__bf16)(pv[2 * e] - (float)h0), l1 = (__bf16)(pv[2 * e + 1] - (float)h1);
+        ahi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        alo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+      } else {
+        const _Float16 h0 = (_Float16)pv[2 * e], h1 = (_Float16)pv[2 * e + 1];
+        const _Float16 l0 = (_Float16)(pv[2 * e] - (float)h0), l1 = (_Float16)(pv[2 * e + 1] - (float)h1);
+        ahi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        alo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+      }
+    }
+    // rows of this lane's transposing reads: 32*tb2 + 8*kg + 4*h + x/4
+    const uint16_t* rowp = sv + (32 * tb2 + 8 * kg + (x >> 2)) * D + 4 * (x & 3);
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) acc[g][c] = __builtin_fmaf(pg[g], fv[c], acc[g][c]);
+    for (int nc = 0; nc < D / 16; ++nc) {
+      const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
+      const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
+      uint32_t bk[4];
+      bk[0] = (uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16);
+      bk[1] = (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16);
+      bk[2] = (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16);
+      bk[3] = (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16);
+      accp[nc] = mfma_qk<DT>(ahi, bk, accp[nc]);
+      accp[nc] = mfma_qk<DT>(alo, bk, accp[nc]);
+    }
   }
 }
 
@@ -881,7 +921,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
                                             float qmax, bool qnan, const float* sh_qf,
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
                                             float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh,
-                                            const uint64_t* sh_bits, int wpre, int r0, int r1, float* sh_p) {
+                                            const uint64_t* sh_bits, int wpre, int r0, int r1, float* sh_p,
+                                            uint16_t* sh_v) {
   constexpr int CPL = D / 16;
   constexpr int kDW = DecWaves<DT, D>::value;
   using L = Lay<DT, D>;
@@ -911,7 +952,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   }
   uint32_t aq[MQK ? D / 32 : 1][4];
   if constexpr (MQK) load_q_mfma<D, GT>(sh_qp, lane, aq);
-  float* sp = sh_p + wave * 512;  // this wave's p[token][head] slot (MQK)
+  float* sp = sh_p + wave * 256;          // this wave's p[head][token] slot (MQK)
+  uint16_t* sv = sh_v + wave * 64 * D;    // this wave's V tile slot (MQK)
+  f32x4 accp[MQK ? D / 16 : 1];
+#pragma unroll
+  for (int nc = 0; nc < (MQK ? D / 16 : 1); ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   uint32_t vw[16][L::LW];
   int kept = 0;
@@ -989,14 +1034,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   };
 
   if constexpr (MQK) {
+    static_assert(GT <= 4, "the matrix-core path keeps all heads in lane row 0");
     // cached or dense decode: every listed tile is attended
     uint32_t kb[4][D / 32][4];
     for (int t = next_tile(); t >= 0; t = next_tile()) {
       const int valid = min(64, ri.n_tok - t * 64);
       load_k_mfma<D>(a, ri, row, t, lane, kb);
-      load_tile<DT, D, PAGED>(a, ri, row, t, true, lane, vw);
-      tile_softmax_mfma<DT, D, GT>(ms, acc, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
-      tile_pv_lds<DT, D, GT>(acc, sp, vw, lane);
+      load_v_lds<D>(a, ri, row, t, lane, sv);
+      tile_softmax_mfma<DT, D, GT>(ms, accp, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+      // the V tile's direct-to-LDS loads (issued after K) have landed
+      __builtin_amdgcn_s_waitcnt(0);
+      tile_pv_mfma<DT, D, GT>(accp, sp, sv, lane);
       ++kept;
     }
   } else {
@@ -1030,17 +1078,23 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   for (int g = 0; g < GT; ++g) {
     float mg, lt;
     if constexpr (MQK) {
-      // head g: register g % 4 of the lanes of row g / 4
-      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g & 3]), 16 * (g >> 2)));
-      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g & 3])), 16 * (g >> 2)));
+      // head g: register g of the lanes of row 0 (GT <= 4); the p.V result
+      // of head g, column 16nc + x sits in lane x, register g of accp[nc].
+      // It goes to the wave's (now idle) V slot.
+      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g]), 0));
+      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g])), 0));
+      float* ao = reinterpret_cast<float*>(sv);
+#pragma unroll
+      for (int nc = 0; nc < D / 16; ++nc)
+        if (lane < 16) ao[g * D + 16 * nc + lane] = accp[nc][g];
     } else {
       mg = st.m[g];
       lt = wave_sum(st.l[g]);
-    }
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const float x = rows4_sum(acc[g][c]);
-      if (lane < 16) sh_acc[wave][g][j * CPL + c] = x;
+      for (int c = 0; c < CPL; ++c) {
+        const float x = rows4_sum(acc[g][c]);
+        if (lane < 16) sh_acc[wave][g][j * CPL + c] = x;
+      }
     }
     if (lane == 0) {
       sh_m[wave][g] = mg;
@@ -1211,10 +1265,11 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ uint32_t sh_qp[GT * D / 2];
   __shared__ float sh_m[kDW][GT];
   __shared__ float sh_l[kDW][GT];
-  __shared__ float sh_acc[kDW][GT][D];
+  __shared__ float sh_acc[MQK ? 1 : kDW][GT][D];  // MQK: the wave states go to the V slots
   __shared__ int sh_cnt[kDW];
   __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row
-  __shared__ float sh_p[MQK ? kDW * 512 : 1];       // per wave p[token][head] of the current tile (MQK)
+  __shared__ float sh_p[MQK ? kDW * 256 : 1];       // per wave p[head][token] of the current tile (MQK)
+  __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
   // cached mode: fetch the scores before anything else (balanced: tiles
   // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
@@ -1376,7 +1431,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   }
 
   decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
-                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p);
+                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v);
   __syncthreads();
 
   // merge the eight wave states into the split's partial
@@ -1390,7 +1445,8 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
 #pragma unroll
     for (int w = 0; w < kDW; ++w) {
       const float e = __expf(sh_m[w][g] - mx);
-      acc = __builtin_fmaf(sh_acc[w][g][c], e, acc);
+      const float aw = MQK ? reinterpret_cast<const float*>(sh_v + w * 64 * D)[g * D + c] : sh_acc[MQK ? 0 : w][g][c];
+      acc = __builtin_fmaf(aw, e, acc);
       l = __builtin_fmaf(sh_l[w][g], e, l);
     }
     const int64_t qh = (int64_t)row * a.G + g0 + g;
@@ -1410,7 +1466,9 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     for (int w = 0; w < kDW; ++w) n += sh_cnt[w];
     a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = n;
   }
-  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, &sh_acc[0][0][0], &sh_l[0][0]);
+  // merge scratch (GT * Pg floats): the wave-state area, idle by now
+  float* sh_w = MQK ? reinterpret_cast<float*>(sh_v) : &sh_acc[0][0][0];
+  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0]);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
@@ -1506,7 +1564,9 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
     case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ>), grid, block, 0, st, a); break;
     case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a); break;
+    default:
+      if constexpr (!MQ) hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a);
+      break;
   }
 }
 
