@@ -1302,6 +1302,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   // stage q of this chunk in LDS (float and packed 16-bit); q := round(q *
   // k_scale) in q's dtype for the Q_FOLD mode (fused_eviction.py:619-621)
   const int qes = a.q_dtype == OC_F32 ? 4 : 2;
+  float qss = 0.f;  // x0^2 + x1^2 of this thread's pair (head norms below)
   for (int idx = threadIdx.x; idx < GT * D / 2; idx += kDT) {
     const int e0 = 2 * idx;
     const int g = e0 / D;
@@ -1318,6 +1319,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     }
     sh_qf[e0] = x0;
     sh_qf[e0 + 1] = x1;
+    qss = __builtin_fmaf(x1, x1, x0 * x0);
     if constexpr (DOT2) {
       // x0, x1 are exact in the 16-bit q dtype, so the narrowing is exact
       uint32_t lo, hi;
@@ -1331,15 +1333,48 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       sh_qp[idx] = lo | (hi << 16);
     }
   }
-  __syncthreads();
-  // max_g ||q_g|| over all G query heads of the row (CS gate): wave w forms
-  // the norms of heads w, w + 8, ... (lane j sums its D/16 columns, then the
-  // 16 lanes are added), the wave maxima are combined after the barrier
+  // max_g ||q_g|| over all G query heads of the row (CS gate).  When all G
+  // heads are in this workgroup (and GT * D / 2 <= threads), the D / 2
+  // threads of a head (one wave at D = 128, half a wave at D = 64) add their
+  // pairs' squares right away; otherwise wave w forms the norms of heads w,
+  // w + 8, ... from LDS and global memory after the barrier.  The wave
+  // maxima are combined after the next barrier.
   __shared__ float sh_qn[kDW];
   __shared__ int sh_qnan[kDW];
+  const bool fast_norms = a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
+  if (fast_norms) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float ss;
+    if constexpr (D == 128) {
+      ss = wave_sum(qss);
+    } else {
+      float lo, hi;
+      row_pair<16>(row16_sum(qss), lo, hi);
+      ss = lo + hi;  // the 32-lane half of this lane
+    }
+    float qn = __builtin_sqrtf(ss);
+    if ((double)qn < 1e-38) qn = 0.f;
+    const int hpw = 128 / D;  // heads per wave
+    float wmax = 0.f;
+    bool wnan = false;
+#pragma unroll
+    for (int h = 0; h < 128 / D; ++h) {
+      const int g = wave * hpw + h;
+      const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qn), h * (64 / hpw)));
+      if (g < a.G) {
+        if (__builtin_isnan(x)) wnan = true;
+        wmax = fmaxf(wmax, x);
+      }
+    }
+    if (lane == 0) {
+      sh_qn[wave] = wmax;
+      sh_qnan[wave] = wnan ? 1 : 0;
+    }
+  }
+  __syncthreads();
   float qmax = 0.f;
   bool qnan = false;
-  if (a.gate == OC_GATE_CS) {
+  if (a.gate == OC_GATE_CS && !fast_norms) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float wmax = 0.f;
     bool wnan = false;
@@ -1369,8 +1404,8 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       sh_qn[wave] = wmax;
       sh_qnan[wave] = wnan ? 1 : 0;
     }
+    __syncthreads();
   }
-  __syncthreads();
   if (a.gate == OC_GATE_CS) {
 #pragma unroll
     for (int w = 0; w < kDW; ++w) {
