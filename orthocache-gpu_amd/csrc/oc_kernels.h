@@ -840,11 +840,11 @@ __device__ __forceinline__ void tile_softmax_mfma(MState& ms, f32x4 (&accp)[D / 
 #pragma unroll
     for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha;
   }
-  if (r == 0) {
+  if (r < (GT + 3) / 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) sp[i * 64 + 16 * tb + x] = v[tb][i];
+      for (int tb = 0; tb < 4; ++tb) sp[(4 * r + i) * 64 + 16 * tb + x] = v[tb][i];
   }
 }
 
@@ -925,6 +925,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
                                             uint16_t* sh_v) {
   constexpr int CPL = D / 16;
   constexpr int kDW = DecWaves<DT, D>::value;
+  constexpr int kPH = GT > 4 ? 8 : 4;  // heads per P slot row block (MQK)
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -952,7 +953,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   }
   uint32_t aq[MQK ? D / 32 : 1][4];
   if constexpr (MQK) load_q_mfma<D, GT>(sh_qp, lane, aq);
-  float* sp = sh_p + wave * 256;          // this wave's p[head][token] slot (MQK)
+  float* sp = sh_p + wave * 64 * kPH;     // this wave's p[head][token] slot (MQK)
   uint16_t* sv = sh_v + wave * 64 * D;    // this wave's V tile slot (MQK)
   f32x4 accp[MQK ? D / 16 : 1];
 #pragma unroll
@@ -1034,7 +1035,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   };
 
   if constexpr (MQK) {
-    static_assert(GT <= 4, "the matrix-core path keeps all heads in lane row 0");
+    static_assert(GT <= 8, "the matrix-core path keeps the heads in lane rows 0 and 1");
     // cached or dense decode: every listed tile is attended
     uint32_t kb[4][D / 32][4];
     for (int t = next_tile(); t >= 0; t = next_tile()) {
@@ -1078,15 +1079,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   for (int g = 0; g < GT; ++g) {
     float mg, lt;
     if constexpr (MQK) {
-      // head g: register g of the lanes of row 0 (GT <= 4); the p.V result
-      // of head g, column 16nc + x sits in lane x, register g of accp[nc].
-      // It goes to the wave's (now idle) V slot.
-      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g]), 0));
-      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g])), 0));
+      // head g: register g % 4 of the lanes of row g / 4; the p.V result of
+      // head g, column 16nc + x sits in lane 16 (g / 4) + x, register g % 4 of
+      // accp[nc].  It goes to the wave's (now idle) V slot.
+      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g & 3]), 16 * (g >> 2)));
+      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g & 3])), 16 * (g >> 2)));
       float* ao = reinterpret_cast<float*>(sv);
 #pragma unroll
       for (int nc = 0; nc < D / 16; ++nc)
-        if (lane < 16) ao[g * D + 16 * nc + lane] = accp[nc][g];
+        if ((lane >> 4) == (g >> 2)) ao[g * D + 16 * nc + (lane & 15)] = accp[nc][g & 3];
     } else {
       mg = st.m[g];
       lt = wave_sum(st.l[g]);
@@ -1115,7 +1116,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // LDS, which is dead by now.
 template <int D, int GT, int kDW>
 __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int g0, int g_active, float* sh_w,
-                                              float* sh_inv) {
+                                              float* sh_inv, float4* sh_red) {
   __shared__ int sh_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are acknowledged
   __syncthreads();
@@ -1194,7 +1195,6 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   // weighted sum over the Pg partials: thread (slice, g, column quad) adds
   // partials q = slice, slice + nslice, ... with all its loads independent;
   // the slices are then added in a fixed order (deterministic result)
-  __shared__ float4 sh_red[kDT];
   const int g = gp;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (g < g_active) {
@@ -1266,9 +1266,10 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_m[kDW][GT];
   __shared__ float sh_l[kDW][GT];
   __shared__ float sh_acc[MQK ? 1 : kDW][GT][D];  // MQK: the wave states go to the V slots
+  __shared__ float4 sh_red_own[MQK ? 1 : kDT];     // merge reduction (MQK: inside the V slots)
   __shared__ int sh_cnt[kDW];
   __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row
-  __shared__ float sh_p[MQK ? kDW * 256 : 1];       // per wave p[head][token] of the current tile (MQK)
+  __shared__ float sh_p[MQK ? kDW * 64 * (GT > 4 ? 8 : 4) : 1];  // per wave p[head][token] of the current tile (MQK)
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
   // cached mode: fetch the scores before anything else (balanced: tiles
@@ -1501,9 +1502,11 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     for (int w = 0; w < kDW; ++w) n += sh_cnt[w];
     a.split_counts[(int64_t)row * a.Pg + blockIdx.x] = n;
   }
-  // merge scratch (GT * Pg floats): the wave-state area, idle by now
+  // merge scratch: GT * Pg weights in the wave-state area, idle by now, and
+  // one float4 per thread (MQK: both inside the V slots)
   float* sh_w = MQK ? reinterpret_cast<float*>(sh_v) : &sh_acc[0][0][0];
-  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0]);
+  float4* sh_red = MQK ? reinterpret_cast<float4*>(sh_v + kDW * 64 * D / 2) : sh_red_own;
+  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0], sh_red);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
@@ -1599,9 +1602,7 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
     case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ>), grid, block, 0, st, a); break;
     case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ>), grid, block, 0, st, a); break;
-    default:
-      if constexpr (!MQ) hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a);
-      break;
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a); break;
   }
 }
 
@@ -1615,7 +1616,7 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
   }
   if constexpr (DOT2) {
     // up to four heads per workgroup (eight spill in this variant)
-    if ((a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE) && gt <= 4) {
+    if (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE) {
       launch_decode_gt<DT, HD, DOT2, false, true>(a, gt, grid, st);
       return;
     }
