@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "orthocache_hip.h"
 
 namespace oc {
@@ -31,6 +33,7 @@ struct DecWaves {
 };
 constexpr float kM0 = -1e9f;
 constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
+constexpr int kKeepLds = kMaxBalTiles / 8;  // keep flags staged in LDS (bytes of the bitmask array)
 
 // Kernel arguments (byte strides).  Built by oc_api.hip from oc_decode_params.
 struct DecodeArgs {
@@ -709,8 +712,8 @@ __device__ __forceinline__ void tile_pv(float (&acc)[GT][D / 16], const float (&
 //   A: q[head x][32*dc + 8*kg .. +8]        B: K[token 16*tb + x][32*dc + 8*kg .. +8]
 //   D: lane 16*r + x, register i -> head 4*r + i, token 16*tb + x
 // so the K tile is read as 16-byte row pieces (tb, dc) of one token per lane.
-// The probabilities go to the wave's LDS slot as p[token][head] and p.V
-// runs on the VALU in the tile layout above (V is not transposed).
+// The probabilities go to the wave's LDS slot as p[head][token] and p.V runs
+// on the matrix cores too, with V staged in LDS (tile_pv_mfma).
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -799,25 +802,34 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
                                              16, voff + i * TPI * (int)ts, 0, 0, 0);
 }
 
-// Logits of one tile on the matrix cores and the online-softmax update of
-// the heads' states; p (times vmul) goes to the wave's LDS slot as
-// sp[head * 64 + token] and the p.V accumulators are rescaled by
-// e^(m_old - m_new) (same lane layout as the state).
+// Raw logits q.k of one tile on the matrix cores: c[tb] in the D layout
+// above (head 4r + i, token 16 tb + x in lane 16r + x, register i).
+template <int DT, int D>
+__device__ __forceinline__ void tile_logits_mfma(const uint32_t (&aq)[D / 32][4], const uint32_t (&kb)[4][D / 32][4],
+                                                 f32x4 (&c)[4]) {
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) c[tb] = mfma_qk<DT>(aq[dc], kb[tb][dc], c[tb]);
+  }
+}
+
+// Online-softmax update of the heads' states from a tile's raw logits; p
+// (times vmul) goes to the wave's LDS slot as sp[head * 64 + token] and the
+// p.V accumulators are rescaled by e^(m_old - m_new) (same lane layout as
+// the state).
 template <int DT, int D, int GT>
-__device__ __forceinline__ void tile_softmax_mfma(MState& ms, f32x4 (&accp)[D / 16], const uint32_t (&aq)[D / 32][4],
-                                                  const uint32_t (&kb)[4][D / 32][4], float* sp, float lscale,
-                                                  float vmul, int valid, int lane) {
+__device__ __forceinline__ void tile_softmax_regs(MState& ms, f32x4 (&accp)[D / 16], const f32x4 (&c)[4], float* sp,
+                                                  float lscale, float vmul, int valid, int lane) {
   const int x = lane & 15;
   const int r = lane >> 4;
   float v[4][4];
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int dc = 0; dc < D / 32; ++dc) c = mfma_qk<DT>(aq[dc], kb[tb][dc], c);
     const bool tok_ok = 16 * tb + x < valid;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[i] * lscale : -__builtin_inff();
+    for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[tb][i] * lscale : -__builtin_inff();
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -847,6 +859,87 @@ __device__ __forceinline__ void tile_softmax_mfma(MState& ms, f32x4 (&accp)[D / 
       for (int tb = 0; tb < 4; ++tb) sp[(4 * r + i) * 64 + 16 * tb + x] = v[tb][i];
   }
 }
+
+template <int DT, int D, int GT>
+__device__ __forceinline__ void tile_softmax_mfma(MState& ms, f32x4 (&accp)[D / 16], const uint32_t (&aq)[D / 32][4],
+                                                  const uint32_t (&kb)[4][D / 32][4], float* sp, float lscale,
+                                                  float vmul, int valid, int lane) {
+  f32x4 c[4];
+  tile_logits_mfma<DT, D>(aq, kb, c);
+  tile_softmax_regs<DT, D, GT>(ms, accp, c, sp, lscale, vmul, valid, lane);
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack16x2(uint32_t u, float& lo, float& hi) {
+  if constexpr (DT == OC_BF16) {
+    lo = __uint_as_float(u << 16);
+    hi = __uint_as_float(u & 0xffff0000u);
+  } else {
+    lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+    hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+  }
+}
+
+// Band energies of a 16-bit K tile held in the matrix-core layout (lane
+// 16*kg + x: tokens 16*tb + x, columns 32*dc + 8*kg .. +8), for the
+// single-pass gate of the matrix-core decode:
+//   E_high = 1/2 sum_{u<32} ||k_u - k_{u+32}||^2 (W64 rows 32..63, as in
+//     tile_energies); the pairs (tb, tb + 2) sit in the same lane.
+//   E_low = sum_{i=1..7} ||X_i||^2, X_i = 1/8 sum_r h8_i(r) S_r over the
+//     residue sums S_r = sum_{t = r mod 8} k_t.  A lane sums its four tokens
+//     (residue r = x & 7), adds lane x ^ 8 (row_ror:8; lanes x and x ^ 8 then
+//     hold identical copies) and runs an 8-point butterfly over lane bits 0
+//     and 1 (quad_perm) and 2 (row_ror:4, which reaches residue r ^ 4 in
+//     either direction thanks to the copies).  A stage is y += s * partner
+//     with s = -1 where the lane's bit is set, so the upper lane of a pair
+//     holds -(lo - hi): the transform is exact up to per-lane signs, which
+//     the squares drop.  The lane with r = 0 holds the DC row (no sign
+//     flips), which E_low leaves out; lanes x >= 8 are the copies.
+// The summation order is not that of tile_energies, so the two can differ
+// in the last bits.
+template <int DT, int D, bool LOW>
+__device__ __forceinline__ void tile_energies_mfma(const uint32_t (&kb)[4][D / 32][4], int lane, float& e_low,
+                                                   float& e_high) {
+  const int x = lane & 15;
+  const float s0 = (x & 1) ? -1.f : 1.f;
+  const float s1 = (x & 2) ? -1.f : 1.f;
+  const float s2 = (x & 4) ? -1.f : 1.f;
+  const bool low_lane = (x & 7) != 0 && x < 8;
+  float h = 0.f, lo = 0.f;
+#pragma unroll
+  for (int dc = 0; dc < D / 32; ++dc) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      // one packed column pair at a time: keeps the unpacked floats of the
+      // whole tile from being live at once
+      __builtin_amdgcn_sched_barrier(0);
+      float f[4][2];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) unpack16x2<DT>(kb[tb][dc][w], f[tb][0], f[tb][1]);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float d0 = f[0][e] - f[2][e];
+        const float d1 = f[1][e] - f[3][e];
+        h = __builtin_fmaf(d0, d0, h);
+        h = __builtin_fmaf(d1, d1, h);
+        if constexpr (LOW) {
+          float y = (f[0][e] + f[1][e]) + (f[2][e] + f[3][e]);
+          y += dpp<0x128>(y);                         // row_ror:8
+          y = __builtin_fmaf(dpp<0xB1>(y), s0, y);    // quad_perm [1,0,3,2]
+          y = __builtin_fmaf(dpp<0x4E>(y), s1, y);    // quad_perm [2,3,0,1]
+          y = __builtin_fmaf(dpp<0x124>(y), s2, y);   // row_ror:4
+          lo = low_lane ? __builtin_fmaf(y, y, lo) : lo;
+        }
+      }
+    }
+  }
+  e_high = wave_sum(h) * 0.5f;
+  e_low = LOW ? wave_sum(lo) * (1.f / 64.f) : 0.f;
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding; export and LDS counts left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 
 // p.V on the matrix cores: D[head][d] += sum_token P[head][token] V[token][d]
 // per 32-token block and 16-column chunk.  A = P of head (lane & 15), tokens
@@ -922,7 +1015,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
                                             float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh,
                                             const uint64_t* sh_bits, int wpre, int r0, int r1, float* sh_p,
-                                            uint16_t* sh_v) {
+                                            uint16_t* sh_v, uint8_t* sh_keep) {
   constexpr int CPL = D / 16;
   constexpr int kDW = DecWaves<DT, D>::value;
   constexpr int kPH = GT > 4 ? 8 : 4;  // heads per P slot row block (MQK)
@@ -1036,17 +1129,75 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 
   if constexpr (MQK) {
     static_assert(GT <= 8, "the matrix-core path keeps the heads in lane rows 0 and 1");
-    // cached or dense decode: every listed tile is attended
     uint32_t kb[4][D / 32][4];
-    for (int t = next_tile(); t >= 0; t = next_tile()) {
-      const int valid = min(64, ri.n_tok - t * 64);
-      load_k_mfma<D>(a, ri, row, t, lane, kb);
-      load_v_lds<D>(a, ri, row, t, lane, sv);
-      tile_softmax_mfma<DT, D, GT>(ms, accp, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
-      // the V tile's direct-to-LDS loads (issued after K) have landed
-      __builtin_amdgcn_s_waitcnt(0);
-      tile_pv_mfma<DT, D, GT>(accp, sp, sv, lane);
-      ++kept;
+    if (cached || a.gate == OC_GATE_NONE) {
+      // cached or dense decode: every listed tile is attended
+      for (int t = next_tile(); t >= 0; t = next_tile()) {
+        const int valid = min(64, ri.n_tok - t * 64);
+        load_k_mfma<D>(a, ri, row, t, lane, kb);
+        load_v_lds<D>(a, ri, row, t, lane, sv);
+        tile_softmax_mfma<DT, D, GT>(ms, accp, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+        // the V tile's direct-to-LDS loads (issued after K) have landed
+        __builtin_amdgcn_s_waitcnt(0);
+        tile_pv_mfma<DT, D, GT>(accp, sp, sv, lane);
+        ++kept;
+      }
+    } else {
+      // single pass: gate every K tile of the list; V only for retained
+      // tiles.  The next K tile is requested as soon as the current one has
+      // been consumed (logits and energies), so it streams in while this
+      // tile's V lands and p.V runs.  Keep flags go to LDS (sh_keep, list
+      // order) and are written out after the loop: a global store pending
+      // among the loads would make every wait a full one.
+      constexpr int kNK = 4 * (D / 32);  // K loads per tile
+      const bool keep_lds = n_split <= kKeepLds;
+      // one copy of the loop per gate (E_low only for the zeta gate): the
+      // two in one loop body overflow the register budget
+      auto single_pass = [&](auto low_tag) {
+        constexpr bool LOW = decltype(low_tag)::value;
+        int t = next_tile();
+        if (t >= 0) load_k_mfma<D>(a, ri, row, t, lane, kb);
+        while (t >= 0) {
+          const int valid = min(64, ri.n_tok - t * 64);
+          // per-tile scales first: a load issued after the V and K requests
+          // below would make its wait a wait for all of them
+          const float lsc = lscale_of(t);
+          const float vmul = tile_vmul(a, row, t);
+          f32x4 lg[4];
+          tile_logits_mfma<DT, D>(aq, kb, lg);
+          bool keep = true;
+          if (valid == 64) {
+            float el, eh;
+            tile_energies_mfma<DT, D, LOW>(kb, lane, el, eh);
+            keep = gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
+          }
+          keep = __builtin_amdgcn_readfirstlane(keep ? 1 : 0) != 0;
+          if (a.keep_out && blockIdx.z == 0) {
+            if (keep_lds) {
+              if (lane == 0) sh_keep[kk] = keep ? 1 : 0;
+            } else if (lane == 0) {
+              a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+            }
+          }
+          if (keep) load_v_lds<D>(a, ri, row, t, lane, sv);
+          __builtin_amdgcn_sched_barrier(0);
+          const int tn = next_tile();
+          if (tn >= 0) load_k_mfma<D>(a, ri, row, tn, lane, kb);
+          __builtin_amdgcn_sched_barrier(0);
+          if (keep) {
+            tile_softmax_regs<DT, D, GT>(ms, accp, lg, sp, lsc, vmul, valid, lane);
+            // the V tile has landed once at most the next tile's K loads
+            // (issued after it) are outstanding
+            if (tn >= 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(kNK));
+            else __builtin_amdgcn_s_waitcnt(0);
+            tile_pv_mfma<DT, D, GT>(accp, sp, sv, lane);
+            ++kept;
+          }
+          t = tn;
+        }
+      };
+      if (a.gate == OC_GATE_ZETA) single_pass(std::true_type{});
+      else single_pass(std::false_type{});
     }
   } else {
     uint32_t kw[16][L::LW];
@@ -1268,7 +1419,8 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_acc[MQK ? 1 : kDW][GT][D];  // MQK: the wave states go to the V slots
   __shared__ float4 sh_red_own[MQK ? 1 : kDT];     // merge reduction (MQK: inside the V slots)
   __shared__ int sh_cnt[kDW];
-  __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row
+  __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row;
+                                                   // matrix-core single pass: keep flags
   __shared__ float sh_p[MQK ? kDW * 64 * (GT > 4 ? 8 : 4) : 1];  // per wave p[head][token] of the current tile (MQK)
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
@@ -1467,8 +1619,21 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   }
 
   decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
-                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v);
+                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v,
+                                           reinterpret_cast<uint8_t*>(sh_bits));
   __syncthreads();
+  // matrix-core single pass: the keep flags staged in LDS in list order
+  if (MQK && a.mode != OC_MODE_CACHED && a.gate != OC_GATE_NONE && a.keep_out && blockIdx.z == 0) {
+    const int w = min(a.spw, a.P - s);
+    const int n_split = s < ri.n_tiles ? w * ((ri.n_tiles - s + a.P - 1) / a.P) : 0;
+    if (n_split <= kKeepLds) {
+      const uint8_t* sh_keep = reinterpret_cast<const uint8_t*>(sh_bits);
+      for (int x = threadIdx.x; x < n_split; x += kDT) {
+        const int t = s + (x / w) * a.P + x % w;
+        if (t < ri.n_tiles) a.keep_out[(int64_t)row * a.keep_stride + t] = sh_keep[x];
+      }
+    }
+  }
 
   // merge the eight wave states into the split's partial
   for (int idx = threadIdx.x; idx < g_active * D; idx += kDT) {
@@ -1607,7 +1772,6 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 }
 
 // q . k on the matrix cores for contiguous 16-bit K (q of the same type)
-// whenever every listed tile is attended (cached scores or no gate)
 template <int DT, int HD, bool DOT2>
 inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if (a.paged) {
@@ -1615,8 +1779,9 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
     return;
   }
   if constexpr (DOT2) {
-    // up to four heads per workgroup (eight spill in this variant)
-    if (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE) {
+    // single pass with per-tile K scales stays on the VALU path, which
+    // scores the dequantised elements
+    if (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE || a.k_scale_mode != OC_KSCALE_TILE) {
       launch_decode_gt<DT, HD, DOT2, false, true>(a, gt, grid, st);
       return;
     }

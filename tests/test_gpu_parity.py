@@ -380,6 +380,33 @@ def test_v2_zeta_max_zero_and_many_splits():
     assert_out(out1, O.dense_decode(np32(q), np32(k), np32(v)), "f32", "dense")
 
 
+@pytest.mark.parametrize("gate", ["cs", "zeta"])
+def test_single_pass_long_split_list(gate):
+    """One split of 2100 tiles: more keep flags than the matrix-core single
+    pass stages in LDS (2048), so they are stored from inside the tile loop.
+    Mask = generator labels = oracle; output against the oracle."""
+    from orthocache_gpu import fused_orthocache_attention_v2, fused_orthocache_attention_v3_gqa, score_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_q
+    wl = _mixed(1, 2100, 128, "bf16", seed=31)
+    if gate == "cs":
+        G = 4
+        q = make_q(1, G, 128, dtype=torch.bfloat16, seed=32)
+        tau = calibrate_tau(score_tiles(wl.keys.to(DEV)).e_high, q.to(DEV), G)
+        out, m = fused_orthocache_attention_v3_gqa(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), tau, G,
+                                                   num_splits=1)
+        ref, rmeta, rmask = O.gqa_v3(np32(q), np32(wl.keys), np32(wl.values), tau, G)
+        want = wl.noise.numpy()
+    else:
+        q = torch.randn((1, 128), generator=torch.Generator().manual_seed(33)).to(torch.bfloat16)
+        out, m = fused_orthocache_attention_v2(q.to(DEV), wl.keys.to(DEV), wl.values.to(DEV), 5.0, num_splits=1)
+        ref, rmeta, rmask = O.fused_v2(np32(q), np32(wl.keys), np32(wl.values), 5.0)
+        want = ~wl.noise.numpy()
+    assert np.array_equal(m["eviction_mask"].cpu().numpy(), rmask)
+    assert np.array_equal(rmask, want)
+    assert m["tiles_retained"] == rmeta["tiles_retained"]
+    assert_out(out, O.round_to(ref, "bf16"), "bf16", f"single split {gate}")
+
+
 def test_auto_num_splits_on_device():
     from orthocache_gpu import fused_orthocache_attention_v2
     cus = torch.cuda.get_device_properties(0).multi_processor_count
