@@ -1086,7 +1086,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
       }
     } else if (!cached) {
       for (;;) {
-        kk += kDW;
+        if (MQK && a.gate != OC_GATE_NONE && kk >= 0) {
+          // matrix-core single pass: after the wave's first tile (position
+          // `wave`), list positions are handed out in LDS, so a wave that
+          // drew evicted (cheaper) tiles takes more of them
+          int x = 0;
+          if (lane == 0) x = atomicAdd(&sh_cnt[kDW], 1);
+          kk = __builtin_amdgcn_readfirstlane(x);
+        } else {
+          kk += kDW;
+        }
         if (kk >= n_split) break;
         t = s + (kk / w) * a.P + kk % w;
         if (t < ri.n_tiles) break;
@@ -1418,7 +1427,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_l[kDW][GT];
   __shared__ float sh_acc[MQK ? 1 : kDW][GT][D];  // MQK: the wave states go to the V slots
   __shared__ float4 sh_red_own[MQK ? 1 : kDT];     // merge reduction (MQK: inside the V slots)
-  __shared__ int sh_cnt[kDW];
+  __shared__ int sh_cnt[kDW + 1];  // per-wave retained counts; [kDW]: single-pass list position
   __shared__ uint64_t sh_bits[kMaxBalTiles / 64];  // balanced: retained-tile bitmask of the row;
                                                    // matrix-core single pass: keep flags
   __shared__ float sh_p[MQK ? kDW * 64 * (GT > 4 ? 8 : 4) : 1];  // per wave p[head][token] of the current tile (MQK)
@@ -1494,6 +1503,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   // maxima are combined after the next barrier.
   __shared__ float sh_qn[kDW];
   __shared__ int sh_qnan[kDW];
+  if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
   const bool fast_norms = a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
   if (fast_norms) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
