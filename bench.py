@@ -55,7 +55,10 @@ def parse():
                     help="host seconds spent on the cpu_baseline sample (0 = skip)")
     ap.add_argument("--read-probe", type=int, default=1, help="also time the streaming-read probe (0 = skip)")
     ap.add_argument("--spw", type=int, default=0, help="logical splits per workgroup (0 = library default)")
-    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read"],
+    ap.add_argument("--extra-configs", type=int, default=1,
+                    help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
+    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read",
+                                       "paged", "fp8"],
                     default=None,
                     help="time only this decode variant of the primary batch, or a plain 1 GiB device copy "
                          "(the reference kernel for scaling the profiler's byte counters)")
@@ -178,6 +181,137 @@ class Setup:
         return kept * 2 * kv_tile + q_bytes + tiles * 4  # + e_high score per tile
 
 
+def _decode_params(lib, N, kv, q, G, gate, mode, tau, scores, P, out, ws):
+    """OcDecodeParams of one production oc_decode call (merge fused, partials
+    and counters in the workspace `ws`, a zeroed device buffer)."""
+    p = N.OcDecodeParams()
+    p.kv = kv.struct()
+    p.q = q.data_ptr()
+    p.q_dtype = N.OC_BF16
+    p.G = G
+    p.q_row_stride = q.stride(0)
+    p.gate = gate
+    p.mode = mode
+    p.threshold = tau
+    if scores is not None:
+        p.score_e_low = scores.e_low.data_ptr()
+        p.score_e_high = scores.e_high.data_ptr()
+        p.score_row_stride = scores.e_high.stride(0)
+    p.num_splits = P
+    p.out_dtype = N.OC_BF16
+    p.out = out.data_ptr()
+    p.out_row_stride = out.stride(0)
+    need = lib.oc_decode_workspace_size(ctypes.byref(p))
+    assert ws.numel() >= need, "workspace too small"
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    return p
+
+
+class ExtraConfig:
+    """BASELINE.json configs 3 (paged GQA, 16 sequences of 4K..128K tokens,
+    16-token pages in a shuffled pool, 40% noise tiles) and 4 (fp8-e4m3 K/V
+    with one scale per (row, tile), G = 8, batch 4, 128K tokens) at full
+    size, each with the Cauchy-Schwarz gate at a calibrated tau: cached,
+    single-pass and dense decode, one oc_decode call per step."""
+
+    def __init__(self, which, seed=300):
+        import torch
+        from orthocache_gpu import _launch as X
+        from orthocache_gpu import _native as N
+        from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
+        from orthocache_gpu.triton_kernels.paged_eviction import score_paged_tiles
+        from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q, paged_pool
+        self.torch, self.N, self.which = torch, N, which
+        dev = torch.device("cuda", 0)
+        self.lib = N.lib()
+        self.stream = X.current_stream(dev)
+        d = 128
+        if which == "paged":
+            B, hkv, self.G, bs, s_max = 16, 8, 4, 16, 131072
+            g = torch.Generator().manual_seed(seed)
+            lens = (torch.randint(4096, s_max + 1, (B,), generator=g) // 64 * 64).tolist()
+            wl = make_kv(B * hkv, s_max, d, noise_frac=0.4, dtype=torch.bfloat16, device=dev, seed=seed)
+            kc, vc, bt = paged_pool(wl.keys, wl.values, hkv, bs, lens, seed=seed + 1)
+            del wl
+            torch.cuda.empty_cache()
+            lens_t = torch.tensor(lens, dtype=torch.int32, device=dev)
+            self.scores = score_paged_tiles(kc, bt, context_lens=lens_t)
+            kv = X.paged_layout(kc, vc, bt, s_max // 64)
+            kv.lengths = lens_t
+            self.rows = B * hkv
+            self.row_tiles = torch.tensor([n // 64 for n in lens for _ in range(hkv)], device=dev)
+            self.es, self.scale_bytes = 2, 0
+            self.table_bytes = sum(-(-n // bs) for n in lens) * 4 * hkv
+            self.tokens = sum(lens)
+            self.desc = (f"config 3: {B} sequences x {hkv} kv heads, context {min(lens)}..{max(lens)} "
+                         f"(sum {self.tokens}), page {bs}, G={self.G}, bf16, 40% noise tiles")
+        else:
+            B, hkv, self.G, s = 4, 8, 8, 131072
+            wl = make_kv(B * hkv, s, d, noise_frac=0.5, dtype=torch.float8_e4m3fn, device=dev, seed=seed)
+            kv = X.rows_layout(wl.keys, wl.values)
+            kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(wl.k_scales, kv.num_rows, kv.num_tiles, dev)
+            kv.v_scale_mode, kv.v_scales = X.vscale_mode(wl.v_scales, kv.num_rows, kv.num_tiles, dev)
+            self.scores = score_tiles(wl.keys, k_scale=wl.k_scales)
+            self.rows = B * hkv
+            self.row_tiles = torch.full((self.rows,), s // 64, device=dev)
+            self.es, self.scale_bytes, self.table_bytes = 1, 8, 0
+            self.tokens = B * s
+            self.desc = f"config 4: batch {B} x {hkv} kv heads, {s} tokens, G={self.G}, fp8-e4m3 K/V + per-tile scales"
+            self._wl = wl
+        self.kv = kv
+        self.q = make_q(self.rows, self.G, d, dtype=torch.bfloat16, device=dev, seed=seed + 2)
+        t_idx = torch.arange(self.scores.e_high.shape[1], device=dev)[None, :]
+        live = t_idx < self.row_tiles[:, None]
+        self.tau = calibrate_tau(self.scores.e_high, self.q, self.G, live=live)
+        self.P = X.auto_num_splits(kv.num_tiles, dev)
+        self.out = torch.empty((self.rows * self.G, d), dtype=torch.bfloat16, device=dev)
+        self.ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+        self.params = {}
+        for v, gate, mode in (("cached", N.OC_GATE_CS, N.OC_MODE_CACHED), ("single_pass", N.OC_GATE_CS, N.OC_MODE_SINGLE_PASS),
+                              ("dense", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS)):
+            self.params[v] = _decode_params(self.lib, N, kv, self.q, self.G, gate, mode, self.tau, self.scores,
+                                            self.P, self.out, self.ws)
+        # retained tiles from the cached scores (what the gate keeps)
+        qn = self.q.float().view(self.rows, self.G, -1).norm(dim=2).amax(dim=1)
+        cs = qn[:, None] * self.scores.e_high.sqrt()
+        self.kept = int(((cs > self.tau) & live).sum())
+        self.tiles = int(self.row_tiles.sum())
+
+    def time(self, variant, steps, warmup):
+        torch = self.torch
+        p = self.params[variant]
+        run = lambda: self.N.check("oc_decode", self.lib.oc_decode(ctypes.byref(p), ctypes.c_void_p(self.stream)))
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            run()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / steps
+
+    def bytes(self, variant):
+        tile = 64 * 128 * self.es + self.scale_bytes // 2   # one K (or V) tile and its scale
+        q = self.rows * self.G * 128 * 2
+        if variant == "dense":
+            return self.tiles * 2 * tile + q + self.table_bytes
+        if variant == "single_pass":
+            return self.tiles * tile + self.kept * tile + q + self.table_bytes
+        return self.kept * 2 * tile + self.tiles * 4 + q + self.table_bytes
+
+    def measure(self, steps, warmup):
+        r = {"workload": self.desc, "eviction_rate": round(1 - self.kept / self.tiles, 4), "num_splits": self.P}
+        for v in ("cached", "single_pass", "dense"):
+            us = self.time(v, steps, warmup)
+            r[v + "_us"] = round(us, 2)
+            r[v + "_gbps"] = round(self.bytes(v) / (us * 1e-6) / 1e9, 1)
+        r["tokens_per_s"] = round(self.rows // 8 * 1.0 / (r["cached_us"] * 1e-6), 1)
+        r["speedup_vs_dense"] = round(r["dense_us"] / r["cached_us"], 3)
+        return r
+
+
 def measure(setup, steps, warmup):
     evict = setup.check()
     r = {"batch": setup.batch, "eviction_rate": evict, "num_splits": setup.P, "tau": setup.tau,
@@ -297,6 +431,9 @@ def main():
     if args.only == "read":
         print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))
         return
+    if args.only in ("paged", "fp8"):
+        print(json.dumps(dict(only=args.only, **ExtraConfig(args.only).measure(args.steps, args.warmup))))
+        return
     primary = Setup(args.batch, spw=args.spw)
     if args.only:
         v = args.only
@@ -312,6 +449,13 @@ def main():
         sec = Setup(args.extra_batch, seed=100, spw=args.spw)
         extra = measure(sec, args.steps, args.warmup)
         del sec
+    extras = {}
+    if args.extra_configs:
+        for which in ("paged", "fp8"):
+            torch.cuda.empty_cache()
+            cfg = ExtraConfig(which)
+            extras[which] = cfg.measure(args.steps, args.warmup)
+            del cfg
     ach = r1["step_gbps"]
     traffic = traffic_from_profiles()
     probe = read_probe(20, 3) if args.read_probe else None
@@ -357,6 +501,9 @@ def main():
             "partials_only_us": extra["partials_only_us"], "partials_only_gbps": round(extra["partials_only_gbps"], 1),
             "single_pass_us": extra["single_pass_us"], "dense_us": extra["dense_us"],
             "speedup_vs_dense": round(extra["speedup_vs_dense"], 3), "dense_gbps": round(extra["dense_gbps"], 1)}
+    if extras:
+        line["config3_paged"] = extras["paged"]
+        line["config4_fp8"] = extras["fp8"]
     print(json.dumps(line))
 
 

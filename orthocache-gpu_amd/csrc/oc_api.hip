@@ -331,12 +331,34 @@ static bool fused_merge(const oc_decode_params* p, int pg) {
   return p->out && (size_t)p->kv.num_rows * gchunks * sizeof(int32_t) <= kCounterBytes && pg <= 4 * p->kv.head_dim;
 }
 
+// Rows of different lengths (a lengths array) are laid out flat: row r gets
+// workgroups in proportion to its tiles, about kFlatPerCU per CU in all
+// (flat_map in the kernel), with the merge fused.  Not with partials
+// requested (their layout is the per-split one), per-split counts, or a
+// cached decode too long for the in-LDS retained-tile bitmask.
+static constexpr int kFlatPerCU = 4;
+
+static bool flat_layout(const oc_decode_params* p) {
+  const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
+  const bool cached = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
+  return p->kv.lengths && p->out && !partials_given && !p->split_counts && p->splits_per_group != 1 &&
+         (!cached || p->kv.num_tiles <= kMaxBalTiles) && (int64_t)p->kv.num_rows * p->kv.num_tiles < (1 << 30) &&
+         fused_merge(p, 1);
+}
+
+static int flat_target() { return kFlatPerCU * device_cus(); }
+
 extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   if (!p || p->num_splits <= 0 || p->G <= 0) return 0;
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
   if (partials_given && !p->out) return 0;
-  const int pg = num_groups(p, choose_spw(p));
   size_t n = 256 + (p->out ? kCounterBytes : 0);
+  if (flat_layout(p)) {
+    // one partial per (slot, query head); slots = target + rows
+    const size_t slots = (size_t)flat_target() + (size_t)p->kv.num_rows;
+    return n + slots * (size_t)p->G * (2 + (size_t)p->kv.head_dim) * sizeof(float);
+  }
+  const int pg = num_groups(p, choose_spw(p));
   if (!partials_given) n += partial_floats(p, pg) * sizeof(float);
   return n;
 }
@@ -378,6 +400,8 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   if (p->splits_per_group < 0) return fail(OC_ERR_INVALID, "splits_per_group %d", p->splits_per_group);
   a.spw = choose_spw(p);
   a.Pg = num_groups(p, a.spw);
+  a.flat = flat_layout(p) ? 1 : 0;
+  a.flat_target = flat_target();
   a.keep_out = p->keep_out;
   a.keep_stride = p->keep_row_stride;
   a.split_counts = p->split_counts;
@@ -399,17 +423,18 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
     a.pl = p->partial_l;
     a.pacc = p->partial_acc;
   } else {
-    const size_t rq = (size_t)p->kv.num_rows * p->G * a.Pg;
+    const size_t rq = a.flat ? ((size_t)a.flat_target + p->kv.num_rows) * p->G : (size_t)p->kv.num_rows * p->G * a.Pg;
     a.pacc = (float*)w;
     a.pm = a.pacc + rq * D;
     a.pl = a.pm + rq;
   }
   const int oes = p->out_dtype == OC_F32 ? 4 : 2;
-  a.fuse = fused_merge(p, a.Pg) ? 1 : 0;
+  a.fuse = (a.flat || fused_merge(p, a.Pg)) ? 1 : 0;
   // split the retained tiles of a row evenly over its workgroups (cached
   // mode); with one split per workgroup each partial stays the state of
   // exactly one logical split {s + kP}
-  a.bal = (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && a.spw > 1 && p->kv.num_tiles <= kMaxBalTiles) ? 1 : 0;
+  a.bal = (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && (a.spw > 1 || a.flat) &&
+           p->kv.num_tiles <= kMaxBalTiles) ? 1 : 0;
   a.out = (char*)p->out;
   a.out_dtype = p->out_dtype;
   a.out_stride = p->out_row_stride * oes;

@@ -80,7 +80,11 @@ struct DecodeArgs {
   // balanced cached decode: the workgroups of a row split the row's retained
   // tiles evenly by rank (set when cached, spw > 1 and T <= kMaxBalTiles)
   int32_t bal;
-  int32_t reserved_bal;
+  // variable-length rows (lengths given, merge fused): blockIdx.x is a flat
+  // workgroup slot; row r gets q_r workgroups in proportion to its tiles
+  // (flat_map) and its partials live at slots [first slot of r, + q_r)
+  int32_t flat;
+  int32_t flat_target;  // workgroups the flat layout aims at (slots = flat_target + num_rows)
   int32_t* counters;
   char* out;
   int64_t out_stride;  // bytes between query-head rows of out
@@ -744,13 +748,52 @@ __device__ __forceinline__ void load_q_mfma(const uint32_t* sh_qp, int lane, uin
     for (int w = 0; w < 4; ++w) aq[dc][w] = x < GT ? sh_qp[x * (D / 2) + 16 * dc + 4 * kg + w] : 0u;
 }
 
-// B operand pieces of one K tile (contiguous rows, 16-bit elements): lane
-// 16*kg + x reads token 16*tb + x, columns 32*dc + 8*kg .. +8.  One buffer
-// descriptor per 16-token block whose size is the valid part of the block,
-// so tokens at or past n_tok read as zero.
-template <int D>
+// Pages of the four 16-token blocks of a tile (paged K/V on the matrix-core
+// path, block_size >= 16, so each block lies in one page): the block id
+// (-1: no valid token, or an id outside the pool, which sets `bad` and
+// reads as zeros) and the block's valid tokens.  Wave-uniform.
+struct TilePages {
+  int id[4];
+  int n[4];
+};
+
+__device__ __forceinline__ TilePages tile_pages(const DecodeArgs& a, const RowInfo& ri, int t, bool& bad) {
+  TilePages pg;
+  const int32_t* btrow = a.bt + (int64_t)ri.seq * a.bt_stride;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int tok = t * 64 + 16 * tb;
+    int n = min(max(ri.n_tok - tok, 0), 16);
+    int id = -1;
+    if (n > 0) {
+      id = btrow[tok >> a.bs_log2];
+      if (id < 0 || id >= a.num_blocks) {
+        bad = true;
+        id = -1;
+        n = 0;
+      }
+    }
+    pg.id[tb] = id;
+    pg.n[tb] = n;
+  }
+  return pg;
+}
+
+// Byte address of token `tok` of block id `id` (paged pool, kv head of the
+// row; the pool start for id -1, whose descriptor then covers no bytes).
+__device__ __forceinline__ const char* page_row(const char* pool, int64_t blk_stride, int64_t head_off, int64_t ts,
+                                                int id, int tok, int bmask) {
+  return pool + (id >= 0 ? (int64_t)id * blk_stride + head_off + (int64_t)(tok & bmask) * ts : 0);
+}
+
+// B operand pieces of one K tile (16-bit elements): lane 16*kg + x reads
+// token 16*tb + x, columns 32*dc + 8*kg .. +8.  One buffer descriptor per
+// 16-token block (contiguous rows: at the block; paged: at the block's
+// place in its page) whose size is the valid part of the block, so tokens
+// at or past n_tok read as zero.
+template <int D, bool PAGED>
 __device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
-                                            uint32_t (&kb)[4][D / 32][4]) {
+                                            uint32_t (&kb)[4][D / 32][4], const TilePages& pg) {
   const int x = lane & 15;
   const int kg = lane >> 4;
   const int tok0 = t * 64;
@@ -761,8 +804,14 @@ __device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& 
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int rb = 16 * tb * (int)ts;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
+    __amdgpu_buffer_rsrc_t rs;
+    if constexpr (PAGED) {
+      const char* pb = page_row(a.k, a.k_blk_stride, (int64_t)ri.head * a.k_head_stride, ts, pg.id[tb],
+                                tok0 + 16 * tb, (1 << a.bs_log2) - 1);
+      rs = __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, pg.n[tb] * (int)ts, 0x00020000);
+    } else {
+      rs = __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
+    }
 #pragma unroll
     for (int dc = 0; dc < D / 32; ++dc) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * dc, 0, 0);
@@ -785,21 +834,37 @@ struct MState {
 // [token][D] 16-bit, by direct-to-LDS buffer loads (16 bytes per lane, one
 // 1 KiB instruction per 1024 / (2 D) tokens); tokens at or past n_tok read
 // as zero through the descriptor's range check.
-template <int D>
+template <int D, bool PAGED>
 __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
-                                           uint16_t* sv) {
+                                           uint16_t* sv, const TilePages& pg) {
   constexpr int TPI = 1024 / (2 * D);  // tokens per instruction
   constexpr int LPT = 64 / TPI;        // lanes per token
   const int64_t ts = a.v_tok_stride;
   const int tok0 = t * 64;
-  const char* base = a.v + (int64_t)row * a.v_row_stride + tok0 * ts;
-  const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
   const int voff = (lane / LPT) * (int)ts + 16 * (lane % LPT);
+  if constexpr (PAGED) {
+    // one descriptor per 16-token block (in one page), 16 / TPI instructions each
 #pragma unroll
-  for (int i = 0; i < 64 / TPI; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 512),
-                                             16, voff + i * TPI * (int)ts, 0, 0, 0);
+    for (int tb = 0; tb < 4; ++tb) {
+      const char* pb = page_row(a.v, a.v_blk_stride, (int64_t)ri.head * a.v_head_stride, ts, pg.id[tb],
+                                tok0 + 16 * tb, (1 << a.bs_log2) - 1);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, pg.n[tb] * (int)ts, 0x00020000);
+#pragma unroll
+      for (int j = 0; j < 16 / TPI; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(sv + (tb * (16 / TPI) + j) * 512), 16,
+            voff + j * TPI * (int)ts, 0, 0, 0);
+    }
+  } else {
+    const char* base = a.v + (int64_t)row * a.v_row_stride + tok0 * ts;
+    const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 64 / TPI; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 512),
+                                               16, voff + i * TPI * (int)ts, 0, 0, 0);
+  }
 }
 
 // Raw logits q.k of one tile on the matrix cores: c[tb] in the D layout
@@ -1007,10 +1072,101 @@ __device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& 
   return gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
 }
 
+// A workgroup's tile list: index x < n -> tile s + (x / w) * P + x % w
+// (logical splits s .. s + w - 1 of P; or, with P = w = 1, the tile range
+// [s, s + n)).
+struct TileList {
+  int s, w, P, n;
+};
+
+__device__ __forceinline__ TileList split_list(const DecodeArgs& a, const RowInfo& ri, int s) {
+  TileList tl;
+  tl.s = s;
+  tl.P = a.P;
+  tl.w = min(a.spw, a.P - s);
+  tl.n = s < ri.n_tiles ? tl.w * ((ri.n_tiles - s + a.P - 1) / a.P) : 0;
+  return tl;
+}
+
+__device__ __forceinline__ int row_tiles(const DecodeArgs& a, int r) {
+  int n = a.num_tiles * 64;
+  if (a.lengths) {
+    const int len = a.lengths[r / a.rows_per_length];
+    n = len < 0 ? 0 : (len < n ? len : n);
+  }
+  return (n + 63) >> 6;
+}
+
+// Flat workgroup layout for rows of different lengths.  With N tiles in all
+// and n_max in the longest row, U = max(ceil(N / flat_target),
+// ceil(n_max / qcap), 1) and row r gets q_r = max(1, ceil(n_r / U))
+// workgroups; the rows' workgroups are numbered row after row over
+// blockIdx.x.  Every workgroup recomputes the table (two passes over the
+// rows' lengths) and finds its row, its index g among the row's q_r
+// workgroups and the row's first slot.  Returns false for the slots past
+// the last row's.  sh_i: 2 kDW + 8 ints of LDS.
+template <int kDW>
+__device__ __forceinline__ bool flat_map(const DecodeArgs& a, int qcap, int* sh_i, int& row, int& g, int& q,
+                                         int& slot0) {
+  constexpr int kDT = kDW * kWave;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int bid = blockIdx.x;
+  int sum = 0, mx = 0;
+  for (int r = threadIdx.x; r < a.num_rows; r += kDT) {
+    const int n = row_tiles(a, r);
+    sum += n;
+    mx = max(mx, n);
+  }
+  sum = wave_incl_scan(sum);
+  mx = (int)wave_max((float)mx);  // exact: a row has < 2^24 tiles
+  if (threadIdx.x == 0) sh_i[2 * kDW + 4] = -1;
+  if (lane == 63) sh_i[wave] = sum;
+  if (lane == 0) sh_i[kDW + wave] = mx;
+  __syncthreads();
+  int total = 0, nmax = 0;
+#pragma unroll
+  for (int w = 0; w < kDW; ++w) {
+    total += sh_i[w];
+    nmax = max(nmax, sh_i[kDW + w]);
+  }
+  const int U = max(1, max((total + a.flat_target - 1) / a.flat_target, (nmax + qcap - 1) / qcap));
+  int carry = 0;
+  for (int c = 0; c < a.num_rows; c += kDT) {
+    __syncthreads();  // sh_i[0 .. kDW) is reused
+    const int r = c + threadIdx.x;
+    const int qr = r < a.num_rows ? max(1, (row_tiles(a, r) + U - 1) / U) : 0;
+    const int incl = wave_incl_scan(qr);
+    if (lane == 63) sh_i[wave] = incl;
+    __syncthreads();
+    int before = carry, all = 0;
+#pragma unroll
+    for (int w = 0; w < kDW; ++w) {
+      const int x = sh_i[w];
+      before += w < wave ? x : 0;
+      all += x;
+    }
+    const int first = before + incl - qr;
+    if (qr > 0 && first <= bid && bid < first + qr) {
+      sh_i[2 * kDW + 4] = r;
+      sh_i[2 * kDW + 5] = bid - first;
+      sh_i[2 * kDW + 6] = qr;
+      sh_i[2 * kDW + 7] = first;
+    }
+    carry += all;
+  }
+  __syncthreads();
+  row = sh_i[2 * kDW + 4];
+  g = sh_i[2 * kDW + 5];
+  q = sh_i[2 * kDW + 6];
+  slot0 = sh_i[2 * kDW + 7];
+  return row >= 0;
+}
+
 // The tile loop, the wave merge and the partial-state write of one
 // workgroup (see decode_kernel).
 template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, int s, int g0,
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, const TileList& tl, int g0,
                                             float qmax, bool qnan, const float* sh_qf,
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
                                             float (*sh_acc)[GT][D], int* sh_cnt, float pre_el, float pre_eh,
@@ -1024,9 +1180,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int j = lane & 15;
   const bool cached = a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE;
-  // this workgroup's splits [s, s + w): list index x -> tile s + (x / w) * P + x % w
-  const int w = min(a.spw, a.P - s);
-  const int n_split = s < ri.n_tiles ? w * ((ri.n_tiles - s + a.P - 1) / a.P) : 0;
+  // this workgroup's tile list: index x < n -> tile s + (x / w) * P + x % w
+  const int s = tl.s, w = tl.w, n_split = tl.n;
 
   WaveState<GT> st;
   float acc[GT][CPL];
@@ -1097,7 +1252,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
           kk += kDW;
         }
         if (kk >= n_split) break;
-        t = s + (kk / w) * a.P + kk % w;
+        t = s + (kk / w) * tl.P + kk % w;
         if (t < ri.n_tiles) break;
         t = -1;
       }
@@ -1108,7 +1263,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
           cmask &= cmask - 1;
           if ((rank++ & (kDW - 1)) == wave) {
             const int x = c0 + bit;
-            t = s + (x / w) * a.P + x % w;
+            t = s + (x / w) * tl.P + x % w;
             break;
           }
           continue;
@@ -1116,7 +1271,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
         c0 += 64;
         if (c0 >= n_split) break;
         const int kx = c0 + lane;
-        const int tx = s + (kx / w) * a.P + kx % w;
+        const int tx = s + (kx / w) * tl.P + kx % w;
         const bool in = kx < n_split && tx < ri.n_tiles;
         float el = pre_el, eh = pre_eh;
         if (c0 > 0 && in) {
@@ -1139,12 +1294,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   if constexpr (MQK) {
     static_assert(GT <= 8, "the matrix-core path keeps the heads in lane rows 0 and 1");
     uint32_t kb[4][D / 32][4];
+    // a block id outside the pool (paged): raised once after the loop, so no
+    // global atomic sits among the tile loads
+    bool bad_page = false;
     if (cached || a.gate == OC_GATE_NONE) {
       // cached or dense decode: every listed tile is attended
       for (int t = next_tile(); t >= 0; t = next_tile()) {
         const int valid = min(64, ri.n_tok - t * 64);
-        load_k_mfma<D>(a, ri, row, t, lane, kb);
-        load_v_lds<D>(a, ri, row, t, lane, sv);
+        TilePages pg{};
+        if constexpr (PAGED) pg = tile_pages(a, ri, t, bad_page);
+        load_k_mfma<D, PAGED>(a, ri, row, t, lane, kb, pg);
+        load_v_lds<D, PAGED>(a, ri, row, t, lane, sv, pg);
         tile_softmax_mfma<DT, D, GT>(ms, accp, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
         // the V tile's direct-to-LDS loads (issued after K) have landed
         __builtin_amdgcn_s_waitcnt(0);
@@ -1165,7 +1325,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
       auto single_pass = [&](auto low_tag) {
         constexpr bool LOW = decltype(low_tag)::value;
         int t = next_tile();
-        if (t >= 0) load_k_mfma<D>(a, ri, row, t, lane, kb);
+        TilePages pg{};
+        if (t >= 0) {
+          if constexpr (PAGED) pg = tile_pages(a, ri, t, bad_page);
+          load_k_mfma<D, PAGED>(a, ri, row, t, lane, kb, pg);
+        }
         while (t >= 0) {
           const int valid = min(64, ri.n_tok - t * 64);
           // per-tile scales first: a load issued after the V and K requests
@@ -1188,10 +1352,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
               a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
             }
           }
-          if (keep) load_v_lds<D>(a, ri, row, t, lane, sv);
+          if (keep) load_v_lds<D, PAGED>(a, ri, row, t, lane, sv, pg);
           __builtin_amdgcn_sched_barrier(0);
           const int tn = next_tile();
-          if (tn >= 0) load_k_mfma<D>(a, ri, row, tn, lane, kb);
+          if (tn >= 0) {
+            if constexpr (PAGED) pg = tile_pages(a, ri, tn, bad_page);
+            load_k_mfma<D, PAGED>(a, ri, row, tn, lane, kb, pg);
+          }
           __builtin_amdgcn_sched_barrier(0);
           if (keep) {
             tile_softmax_regs<DT, D, GT>(ms, accp, lg, sp, lsc, vmul, valid, lane);
@@ -1208,6 +1375,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
       if (a.gate == OC_GATE_ZETA) single_pass(std::true_type{});
       else single_pass(std::false_type{});
     }
+    if (PAGED && bad_page && a.error_flag && lane == 0) atomicOr(a.error_flag, 1);
   } else {
     uint32_t kw[16][L::LW];
     float p[GT];
@@ -1276,15 +1444,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // LDS, which is dead by now.
 template <int D, int GT, int kDW>
 __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int g0, int g_active, float* sh_w,
-                                              float* sh_inv, float4* sh_red) {
+                                              float* sh_inv, float4* sh_red, int Pg, int64_t pbase, int hstride,
+                                              int qstride) {
   __shared__ int sh_last;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
     int* ctr = a.counters + (int64_t)row * gridDim.z + blockIdx.z;
     const int done = atomicAdd(ctr, 1) + 1;
-    sh_last = done == a.Pg;
-    if (done == a.Pg) atomicExch(ctr, 0);
+    sh_last = done == Pg;
+    if (done == Pg) atomicExch(ctr, 0);
   }
   __syncthreads();
   if (!sh_last) return;
@@ -1294,7 +1463,6 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   // quads of every thread) are issued before any of them is used.
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int Pg = a.Pg;
   constexpr int CQ = D / 4;
   constexpr int NPAIR = GT * CQ;
   constexpr int kDT = kDW * kWave;
@@ -1304,12 +1472,14 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   const int sl = threadIdx.x / NPAIR;
   const int gp = pair / CQ;
   const int cq = pair - gp * CQ;
-  // one buffer descriptor over this head's Pg x D partial accumulators
-  const float* hp = a.pacc + ((int64_t)row * a.G + g0 + min(gp, g_active - 1)) * Pg * D;
-  const __amdgpu_buffer_rsrc_t pr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)hp, (short)0, Pg * D * (int)sizeof(float), 0x00020000);
+  // one buffer descriptor over this head's Pg partial accumulators (D
+  // floats each, qstride * D floats apart)
+  const float* hp = a.pacc + (pbase + (int64_t)(g0 + min(gp, g_active - 1)) * hstride) * D;
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)hp, (short)0, ((Pg - 1) * qstride + 1) * D * (int)sizeof(float), 0x00020000);
   auto ld4 = [&](int q) -> float4 {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, (q * D + 4 * cq) * (int)sizeof(float), 0, 16 /* sc1 */);
+    const auto x =
+        __builtin_amdgcn_raw_buffer_load_b128(pr, (q * qstride * D + 4 * cq) * (int)sizeof(float), 0, 16 /* sc1 */);
     return make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
   };
   auto ldc = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
@@ -1318,10 +1488,10 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int g = wave + k * kDW;
-    const int64_t base = ((int64_t)row * a.G + g0 + g) * Pg;
+    const int64_t base = pbase + (int64_t)(g0 + g) * hstride;
     const bool ok = g < g_active && lane < Pg;
-    m0[k] = ok ? ldc(a.pm + base + lane) : -__builtin_inff();
-    l0[k] = ok ? ldc(a.pl + base + lane) : 0.f;
+    m0[k] = ok ? ldc(a.pm + base + lane * qstride) : -__builtin_inff();
+    l0[k] = ok ? ldc(a.pl + base + lane * qstride) : 0.f;
   }
   float4 pf[PF];
 #pragma unroll
@@ -1333,9 +1503,9 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   for (int k = 0; k < 2; ++k) {
     const int g = wave + k * kDW;
     if (g >= g_active) break;
-    const int64_t base = ((int64_t)row * a.G + g0 + g) * Pg;
+    const int64_t base = pbase + (int64_t)(g0 + g) * hstride;
     float mx = m0[k];
-    for (int q = lane + 64; q < Pg; q += 64) mx = fmaxf(mx, ldc(a.pm + base + q));
+    for (int q = lane + 64; q < Pg; q += 64) mx = fmaxf(mx, ldc(a.pm + base + q * qstride));
     mx = wave_max(mx);
     float ls = 0.f;
     if (lane < Pg) {
@@ -1344,9 +1514,9 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
       ls = w * l0[k];
     }
     for (int q = lane + 64; q < Pg; q += 64) {
-      const float w = __expf(ldc(a.pm + base + q) - mx);
+      const float w = __expf(ldc(a.pm + base + q * qstride) - mx);
       sh_w[g * Pg + q] = w;
-      ls = __builtin_fmaf(w, ldc(a.pl + base + q), ls);
+      ls = __builtin_fmaf(w, ldc(a.pl + base + q * qstride), ls);
     }
     ls = wave_sum(ls);
     if (lane == 0) sh_inv[g] = fmaxf(ls, 1e-9f);
@@ -1415,11 +1585,26 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   constexpr int kDW = DecWaves<DT, D>::value;
   constexpr int kDT = kDW * kWave;
   const int lane = threadIdx.x & 63;
-  const int s = blockIdx.x * a.spw;  // first split of this workgroup
-  const int row = blockIdx.y;
   const int g0 = blockIdx.z * GT;
   const int g_active = min(GT, a.G - g0);
+  // the row, this workgroup's index among the row's workgroups, their
+  // number and (flat layout) the row's first partial slot
+  int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0;
+  if (a.flat) {
+    __shared__ int sh_fm[2 * kDW + 8];
+    if (!flat_map<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0)) return;
+  }
   const RowInfo ri = row_info(a, row);
+  TileList tl;
+  if (a.flat) {
+    // a contiguous share of the row's tiles (single pass, dense); cached
+    // mode splits the retained ranks instead (a.bal)
+    tl.s = (int)((int64_t)ri.n_tiles * gidx / npg);
+    tl.n = (int)((int64_t)ri.n_tiles * (gidx + 1) / npg) - tl.s;
+    tl.w = tl.P = 1;
+  } else {
+    tl = split_list(a, ri, blockIdx.x * a.spw);
+  }
 
   __shared__ float sh_qf[GT * D];
   __shared__ uint32_t sh_qp[GT * D / 2];
@@ -1449,9 +1634,8 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
         t = k * kDT + threadIdx.x;
         in = t < ri.n_tiles;
       } else {
-        const int w = min(a.spw, a.P - s);
-        t = s + (lane / w) * a.P + lane % w;
-        in = k == 0 && s < ri.n_tiles && t < ri.n_tiles;
+        t = tl.s + (lane / tl.w) * tl.P + lane % tl.w;
+        in = k == 0 && lane < tl.n && t < ri.n_tiles;
       }
       if (in) {
         const int64_t o = (int64_t)row * a.sc_stride + t;
@@ -1588,7 +1772,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       if (c < ri.n_tiles) {
         const int t = c + threadIdx.x;
         const bool keep = t < ri.n_tiles && cached_keep(a, ri, t, pre_el[c / kDT], pre_eh[c / kDT], qmax, qnan);
-        if (a.keep_out && t < ri.n_tiles && blockIdx.x == 0 && blockIdx.z == 0)
+        if (a.keep_out && t < ri.n_tiles && gidx == 0 && blockIdx.z == 0)
           a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
         const uint64_t m = __ballot(keep);
         const int wi = (c >> 6) + wave;
@@ -1605,7 +1789,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
         el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
       }
       const bool keep = in && cached_keep(a, ri, t, el, eh, qmax, qnan);
-      if (a.keep_out && in && blockIdx.x == 0 && blockIdx.z == 0)
+      if (a.keep_out && in && gidx == 0 && blockIdx.z == 0)
         a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
       const uint64_t m = __ballot(keep);
       const int wi = (c >> 6) + wave;
@@ -1624,28 +1808,31 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     }
     wpre = wave_incl_scan(x);
     const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(wpre, 63);
-    r0 = (int)(total * blockIdx.x / (uint32_t)a.Pg);
-    r1 = (int)(total * (blockIdx.x + 1) / (uint32_t)a.Pg);
+    r0 = (int)((uint64_t)total * gidx / (uint32_t)npg);
+    r1 = (int)((uint64_t)total * (gidx + 1) / (uint32_t)npg);
   }
 
-  decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, s, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
+  decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, tl, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
                                            pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v,
                                            reinterpret_cast<uint8_t*>(sh_bits));
   __syncthreads();
   // matrix-core single pass: the keep flags staged in LDS in list order
   if (MQK && a.mode != OC_MODE_CACHED && a.gate != OC_GATE_NONE && a.keep_out && blockIdx.z == 0) {
-    const int w = min(a.spw, a.P - s);
-    const int n_split = s < ri.n_tiles ? w * ((ri.n_tiles - s + a.P - 1) / a.P) : 0;
-    if (n_split <= kKeepLds) {
+    if (tl.n <= kKeepLds) {
       const uint8_t* sh_keep = reinterpret_cast<const uint8_t*>(sh_bits);
-      for (int x = threadIdx.x; x < n_split; x += kDT) {
-        const int t = s + (x / w) * a.P + x % w;
+      for (int x = threadIdx.x; x < tl.n; x += kDT) {
+        const int t = tl.s + (x / tl.w) * tl.P + x % tl.w;
         if (t < ri.n_tiles) a.keep_out[(int64_t)row * a.keep_stride + t] = sh_keep[x];
       }
     }
   }
 
-  // merge the eight wave states into the split's partial
+  // merge the eight wave states into the split's partial.  Partial index of
+  // query head h in slot p of the row: (row * G + h) * Pg + p, or with the
+  // flat layout (slot0 + p) * G + h
+  const int64_t pbase = a.flat ? (int64_t)slot0 * a.G : (int64_t)row * a.G * a.Pg;
+  const int hstride = a.flat ? 1 : a.Pg;
+  const int qstride = a.flat ? a.G : 1;
   for (int idx = threadIdx.x; idx < g_active * D; idx += kDT) {
     const int g = idx / D;
     const int c = idx - g * D;
@@ -1661,7 +1848,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       l = __builtin_fmaf(sh_l[w][g], e, l);
     }
     const int64_t qh = (int64_t)row * a.G + g0 + g;
-    const int64_t pidx = qh * a.Pg + blockIdx.x;
+    const int64_t pidx = pbase + (int64_t)(g0 + g) * hstride + (int64_t)gidx * qstride;
     // agent-scope stores write through this XCD's L2, so the fused merge
     // (possibly on another XCD) reads them without a cache write-back
     __hip_atomic_store(a.pacc + pidx * D + c, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1681,7 +1868,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   // one float4 per thread (MQK: both inside the V slots)
   float* sh_w = MQK ? reinterpret_cast<float*>(sh_v) : &sh_acc[0][0][0];
   float4* sh_red = MQK ? reinterpret_cast<float4*>(sh_v + kDW * 64 * D / 2) : sh_red_own;
-  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0], sh_red);
+  if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0], sh_red, npg, pbase, hstride, qstride);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
@@ -1785,7 +1972,11 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 template <int DT, int HD, bool DOT2>
 inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if (a.paged) {
-    launch_decode_gt<DT, HD, DOT2, true, false>(a, gt, grid, st);
+    // matrix cores for pages of >= 16 tokens (a 16-token block in one page)
+    if (DOT2 && a.bs_log2 >= 4 && (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE || a.k_scale_mode != OC_KSCALE_TILE))
+      launch_decode_gt<DT, HD, DOT2, true, DOT2>(a, gt, grid, st);
+    else
+      launch_decode_gt<DT, HD, DOT2, true, false>(a, gt, grid, st);
     return;
   }
   if constexpr (DOT2) {
@@ -1811,7 +2002,7 @@ constexpr bool kHasDot2 = DT == OC_BF16 || DT == OC_F16;
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
-    const dim3 grid(a.Pg, a.num_rows, gchunks);                                  \
+    const dim3 grid = a.flat ? dim3(a.flat_target + a.num_rows, 1, gchunks) : dim3(a.Pg, a.num_rows, gchunks); \
     if (kHasDot2<DT> && a.q_dtype == DT) {                                                        \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \

@@ -117,16 +117,18 @@ def make_q(rows: int, G: int, head_dim: int, *, dtype=torch.bfloat16, device="cp
     return q.reshape(rows * G, head_dim).to(dtype)
 
 
-def calibrate_tau(e_high: torch.Tensor, q: torch.Tensor, G: int) -> float:
+def calibrate_tau(e_high: torch.Tensor, q: torch.Tensor, G: int, live: Optional[torch.Tensor] = None) -> float:
     """A CS threshold halfway (geometrically) between the largest bound of a
     row's smooth tiles and the smallest of its noise tiles, pooled over rows
     (the reference calibrates zeta_max from sorted scores,
-    profile_multihead.py:108-118)."""
+    profile_multihead.py:108-118).  `live` (rows, T) bool: the tiles inside
+    each row's length (rows of different lengths)."""
     rows = e_high.shape[0]
     qn = q.float().view(rows, G, -1).norm(dim=2).amax(dim=1)
     cs = qn[:, None] * e_high.float().sqrt()
+    cs = cs.flatten() if live is None else cs[live]
     # split the two clusters at the largest multiplicative gap
-    v = cs.flatten().sort().values.clamp(min=1e-30)
+    v = cs.sort().values.clamp(min=1e-30)
     gaps = v[1:] / v[:-1]
     k = int(gaps.argmax())
     return float(math.sqrt(float(v[k]) * float(v[k + 1])))

@@ -431,22 +431,65 @@ def test_context_lengths_vs_oracle():
     assert m["tiles_evicted"] == ref["evicted"]
 
 
+FLAT_CASES = [("cs", "cached", "bf16", 4, False), ("cs", "single_pass", "bf16", 4, False),
+              ("zeta", "single_pass", "bf16", 1, False), ("zeta", "cached", "f32", 1, False),
+              ("none", "single_pass", "bf16", 4, False), ("cs", "cached", "bf16", 12, False),
+              ("cs", "single_pass", "f32", 2, False), ("cs", "cached", "bf16", 4, True),
+              ("cs", "single_pass", "bf16", 4, True)]
+
+
+@pytest.mark.parametrize("gate,mode,dtype,G,paged", FLAT_CASES)
+def test_variable_lengths_flat_layout(gate, mode, dtype, G, paged):
+    """Rows of very different lengths (one 700-tile row with a partial tail,
+    a 3-tile row, a partial single tile, an empty row): the flat workgroup
+    layout gives the long row many workgroups (up to the 512-per-row cap) and
+    each short row one; outputs and masks against the oracle."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import calibrate_tau, make_q, paged_pool
+    lens = [700 * 64 + 17, 3 * 64, 37, 0]
+    rows, T, d = len(lens), 701, 128
+    wl = _mixed(rows, T, d, dtype, seed=41)
+    q = make_q(rows, G, d, dtype=TORCH_DT[dtype], seed=42)
+    el, eh, _, _ = X.score_tiles(X.rows_layout(wl.keys.to(DEV), None))
+    if paged:
+        kc, vc, bt = paged_pool(wl.keys, wl.values, 1, 16, lens, seed=43)
+        kv = X.paged_layout(kc.to(DEV), vc.to(DEV), bt.to(DEV), T)
+    else:
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    gcode = {"none": N.OC_GATE_NONE, "zeta": N.OC_GATE_ZETA, "cs": N.OC_GATE_CS}[gate]
+    thr = {"cs": calibrate_tau(eh, q.to(DEV), G) if gate == "cs" else 0.0, "zeta": 5.0, "none": 0.0}[gate]
+    res = X.decode(kv, q.to(DEV), G, gate=gcode, threshold=thr,
+                   mode=N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS, scores=(el, eh),
+                   out_dtype=TORCH_DT[dtype], want_keep=True)
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate=gate, threshold=thr, G=G, lengths=lens)
+    if gate != "none":
+        assert np.array_equal(res.keep[:, :T].cpu().numpy().astype(bool), ref["keep"])
+    assert_out(res.out, O.round_to(ref["out"], dtype), dtype, f"flat {gate} {mode} {dtype} G={G} paged={paged}")
+
+
 @pytest.mark.parametrize("block_size", [8, 16, 32, 64, 128])
-def test_paged_equals_contiguous(block_size):
-    """Shuffled physical pool == contiguous rows (test_paged_eviction.py:28-90)."""
+@pytest.mark.parametrize("dtype,d", [("f32", 64), ("bf16", 128)])
+def test_paged_equals_contiguous(block_size, dtype, d):
+    """Shuffled physical pool == contiguous rows (test_paged_eviction.py:28-90).
+    bf16 with pages of >= 16 tokens runs on the matrix-core path."""
     from orthocache_gpu import fused_orthocache_attention_paged, fused_orthocache_attention_v2
     from orthocache_gpu.workloads import paged_pool
-    B, H, d = 2, 4, 64
-    wl = _mixed(B * H, 4, d, "f32", seed=block_size)
-    q = torch.randn((B, H, d), generator=torch.Generator().manual_seed(1))
+    B, H = 2, 4
+    wl = _mixed(B * H, 4, d, dtype, seed=block_size)
+    q = torch.randn((B, H, d), generator=torch.Generator().manual_seed(1)).to(TORCH_DT[dtype])
     kc, vc, bt = paged_pool(wl.keys, wl.values, H, block_size, [256] * B, seed=3)
     out, m = fused_orthocache_attention_paged(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), 5.0)
     ref = torch.stack([fused_orthocache_attention_v2(q[b].to(DEV), wl.keys[b * H:(b + 1) * H].to(DEV),
                                                      wl.values[b * H:(b + 1) * H].to(DEV), 5.0)[0]
                        for b in range(B)])
-    torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+    if dtype == "f32":
+        torch.testing.assert_close(out, ref, atol=1e-5, rtol=1e-5)
+    else:
+        assert_out(out, np32(ref), dtype, "paged vs contiguous")
     oref, _, omask = O.paged(np32(q), np32(kc), np32(vc), bt.numpy(), 5.0)
-    assert_out(out, oref, "f32", "paged vs oracle")
+    assert_out(out, O.round_to(oref, dtype), dtype, "paged vs oracle")
     assert m["tiles_retained"] == int(omask.sum())
 
 
@@ -519,10 +562,12 @@ def test_orthocache_forward_modes():
     assert_out(out[0], ref, "f32", "crossover dense")
 
 
-def test_paged_bad_block_id_rejected():
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_paged_bad_block_id_rejected(dtype):
     from orthocache_gpu import fused_orthocache_attention_paged
-    q = torch.randn(1, 2, 64, device=DEV)
-    kc = torch.randn(4, 2, 32, 64, device=DEV)
+    dt = TORCH_DT[dtype]
+    q = torch.randn(1, 2, 64, device=DEV).to(dt)
+    kc = torch.randn(4, 2, 32, 64, device=DEV).to(dt)
     bt = torch.tensor([[0, 7]], dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError, match="block id"):
         fused_orthocache_attention_paged(q, kc, kc, bt, 5.0)
