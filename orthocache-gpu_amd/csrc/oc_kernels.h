@@ -722,6 +722,22 @@ __device__ __forceinline__ void tile_pv(float (&acc)[GT][D / 16], const float (&
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// 16-bit type the matrix cores run in for K of type DT: the type itself, or
+// bf16 for fp8-e4m3 K, whose values bf16 holds exactly (widened with
+// v_cvt_scalef32_pk_bf16_fp8 at scale 1; all 256 codes checked on the GPU
+// against the float32 decode).
+template <int DT>
+struct MfmaT {
+  static constexpr int value = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
+};
+
+// four fp8 values (one word) -> two words of bf16 pairs
+__device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+}
+
 template <int DT>
 __device__ __forceinline__ f32x4 mfma_qk(const uint32_t (&aq)[4], const uint32_t (&bk)[4], f32x4 c) {
   const u32x4 av = {aq[0], aq[1], aq[2], aq[3]};
@@ -738,14 +754,34 @@ __device__ __forceinline__ f32x4 mfma_qk(const uint32_t (&aq)[4], const uint32_t
 }
 
 // A operand: q of head (lane & 15) from the packed LDS copy (zero past GT).
-template <int D, int GT>
+// Instruction dc takes head-dim columns 32*dc + 8*kg .. +8 from lane group
+// kg; for fp8 K, whose lanes hold D/4 consecutive columns (kg*D/4 ..),
+// columns kg*D/4 + 8*dc .. +8 (any column order works if q and K agree).
+template <int DT, int D, int GT>
 __device__ __forceinline__ void load_q_mfma(const uint32_t* sh_qp, int lane, uint32_t (&aq)[D / 32][4]) {
   const int x = lane & 15;
   const int kg = lane >> 4;
 #pragma unroll
   for (int dc = 0; dc < D / 32; ++dc)
 #pragma unroll
-    for (int w = 0; w < 4; ++w) aq[dc][w] = x < GT ? sh_qp[x * (D / 2) + 16 * dc + 4 * kg + w] : 0u;
+    for (int w = 0; w < 4; ++w) {
+      const int pair = DT == OC_FP8_E4M3FN ? kg * (D / 8) + 4 * dc + w : 16 * dc + 4 * kg + w;
+      aq[dc][w] = x < GT ? sh_qp[x * (D / 2) + pair] : 0u;
+    }
+}
+
+// B operand (eight 16-bit values) of instruction (tb, dc) from the K
+// registers: kb[tb][dc] for 16-bit K; for fp8 K the lane's bytes 8*dc .. +8
+// of its D/4-byte row piece (words 2dc, 2dc + 1), widened to bf16.
+template <int DT, int D>
+__device__ __forceinline__ void k_operand(const uint32_t (&kb)[4][D / 32][4], int tb, int dc, uint32_t (&b)[4]) {
+  if constexpr (DT == OC_FP8_E4M3FN) {
+    fp8x4_to_bf16(kb[tb][(2 * dc) >> 2][(2 * dc) & 3], b[0], b[1]);
+    fp8x4_to_bf16(kb[tb][(2 * dc + 1) >> 2][(2 * dc + 1) & 3], b[2], b[3]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) b[w] = kb[tb][dc][w];
+  }
 }
 
 // Pages of the four 16-token blocks of a tile (paged K/V on the matrix-core
@@ -791,16 +827,20 @@ __device__ __forceinline__ const char* page_row(const char* pool, int64_t blk_st
 // 16-token block (contiguous rows: at the block; paged: at the block's
 // place in its page) whose size is the valid part of the block, so tokens
 // at or past n_tok read as zero.
-template <int D, bool PAGED>
+//
+// fp8 K: lane 16*kg + x reads the D/4 bytes kg*D/4 .. of token 16*tb + x
+// (D/64 128-bit loads per block) into kb[tb][0..D/64).
+template <int DT, int D, bool PAGED>
 __device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
                                             uint32_t (&kb)[4][D / 32][4], const TilePages& pg) {
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
   const int x = lane & 15;
   const int kg = lane >> 4;
   const int tok0 = t * 64;
   const int64_t ts = a.k_tok_stride;
   const char* base = a.k + (int64_t)row * a.k_row_stride + tok0 * ts;
   const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
-  const int voff = x * (int)ts + 16 * kg;
+  const int voff = x * (int)ts + (F8 ? kg * (D / 4) : 16 * kg);
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     const int rb = 16 * tb * (int)ts;
@@ -813,8 +853,8 @@ __device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& 
       rs = __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
     }
 #pragma unroll
-    for (int dc = 0; dc < D / 32; ++dc) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * dc, 0, 0);
+    for (int dc = 0; dc < (F8 ? D / 64 : D / 32); ++dc) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (F8 ? 16 : 64) * dc, 0, 0);
       kb[tb][dc][0] = v[0];
       kb[tb][dc][1] = v[1];
       kb[tb][dc][2] = v[2];
@@ -834,10 +874,10 @@ struct MState {
 // [token][D] 16-bit, by direct-to-LDS buffer loads (16 bytes per lane, one
 // 1 KiB instruction per 1024 / (2 D) tokens); tokens at or past n_tok read
 // as zero through the descriptor's range check.
-template <int D, bool PAGED>
+template <int DT, int D, bool PAGED>
 __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
                                            uint16_t* sv, const TilePages& pg) {
-  constexpr int TPI = 1024 / (2 * D);  // tokens per instruction
+  constexpr int TPI = 1024 / (Elem<DT>::size * D);  // tokens per instruction
   constexpr int LPT = 64 / TPI;        // lanes per token
   const int64_t ts = a.v_tok_stride;
   const int tok0 = t * 64;
@@ -876,7 +916,11 @@ __device__ __forceinline__ void tile_logits_mfma(const uint32_t (&aq)[D / 32][4]
   for (int tb = 0; tb < 4; ++tb) {
     c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dc = 0; dc < D / 32; ++dc) c[tb] = mfma_qk<DT>(aq[dc], kb[tb][dc], c[tb]);
+    for (int dc = 0; dc < D / 32; ++dc) {
+      uint32_t b[4];
+      k_operand<DT, D>(kb, tb, dc, b);
+      c[tb] = mfma_qk<MfmaT<DT>::value>(aq[dc], b, c[tb]);
+    }
   }
 }
 
@@ -962,9 +1006,16 @@ __device__ __forceinline__ void unpack16x2(uint32_t u, float& lo, float& hi) {
 //     flips), which E_low leaves out; lanes x >= 8 are the copies.
 // The summation order is not that of tile_energies, so the two can differ
 // in the last bits.
+//
+// fp8 K (a lane holds D/4 columns per token, kb[tb][0..D/64)) with a
+// per-tile scale s: the energies of the stored values times s^2 (the
+// energies of the dequantised tile s*k up to float rounding).
 template <int DT, int D, bool LOW>
-__device__ __forceinline__ void tile_energies_mfma(const uint32_t (&kb)[4][D / 32][4], int lane, float& e_low,
-                                                   float& e_high) {
+__device__ __forceinline__ void tile_energies_mfma(const uint32_t (&kb)[4][D / 32][4], int lane, float mul,
+                                                   float& e_low, float& e_high) {
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
+  constexpr int NW = F8 ? D / 16 : D / 8;  // words of one token's row piece
+  constexpr int EPW = F8 ? 4 : 2;          // values per word
   const int x = lane & 15;
   const float s0 = (x & 1) ? -1.f : 1.f;
   const float s1 = (x & 2) ? -1.f : 1.f;
@@ -972,34 +1023,44 @@ __device__ __forceinline__ void tile_energies_mfma(const uint32_t (&kb)[4][D / 3
   const bool low_lane = (x & 7) != 0 && x < 8;
   float h = 0.f, lo = 0.f;
 #pragma unroll
-  for (int dc = 0; dc < D / 32; ++dc) {
+  for (int i = 0; i < NW; ++i) {
+    // one word per token at a time: keeps the unpacked floats of the whole
+    // tile from being live at once
+    __builtin_amdgcn_sched_barrier(0);
+    float f[4][EPW];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      // one packed column pair at a time: keeps the unpacked floats of the
-      // whole tile from being live at once
-      __builtin_amdgcn_sched_barrier(0);
-      float f[4][2];
+    for (int tb = 0; tb < 4; ++tb) {
+      const uint32_t u = kb[tb][i >> 2][i & 3];
+      if constexpr (F8) {
+        const auto p0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)u, false);
+        const auto p1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)u, true);
+        f[tb][0] = p0[0];
+        f[tb][1] = p0[1];
+        f[tb][2] = p1[0];
+        f[tb][3] = p1[1];
+      } else {
+        unpack16x2<DT>(u, f[tb][0], f[tb][1]);
+      }
+    }
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) unpack16x2<DT>(kb[tb][dc][w], f[tb][0], f[tb][1]);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float d0 = f[0][e] - f[2][e];
-        const float d1 = f[1][e] - f[3][e];
-        h = __builtin_fmaf(d0, d0, h);
-        h = __builtin_fmaf(d1, d1, h);
-        if constexpr (LOW) {
-          float y = (f[0][e] + f[1][e]) + (f[2][e] + f[3][e]);
-          y += dpp<0x128>(y);                         // row_ror:8
-          y = __builtin_fmaf(dpp<0xB1>(y), s0, y);    // quad_perm [1,0,3,2]
-          y = __builtin_fmaf(dpp<0x4E>(y), s1, y);    // quad_perm [2,3,0,1]
-          y = __builtin_fmaf(dpp<0x124>(y), s2, y);   // row_ror:4
-          lo = low_lane ? __builtin_fmaf(y, y, lo) : lo;
-        }
+    for (int e = 0; e < EPW; ++e) {
+      const float d0 = f[0][e] - f[2][e];
+      const float d1 = f[1][e] - f[3][e];
+      h = __builtin_fmaf(d0, d0, h);
+      h = __builtin_fmaf(d1, d1, h);
+      if constexpr (LOW) {
+        float y = (f[0][e] + f[1][e]) + (f[2][e] + f[3][e]);
+        y += dpp<0x128>(y);                         // row_ror:8
+        y = __builtin_fmaf(dpp<0xB1>(y), s0, y);    // quad_perm [1,0,3,2]
+        y = __builtin_fmaf(dpp<0x4E>(y), s1, y);    // quad_perm [2,3,0,1]
+        y = __builtin_fmaf(dpp<0x124>(y), s2, y);   // row_ror:4
+        lo = low_lane ? __builtin_fmaf(y, y, lo) : lo;
       }
     }
   }
-  e_high = wave_sum(h) * 0.5f;
-  e_low = LOW ? wave_sum(lo) * (1.f / 64.f) : 0.f;
+  const float m2 = mul * mul;
+  e_high = wave_sum(h) * 0.5f * m2;
+  e_low = LOW ? wave_sum(lo) * (1.f / 64.f) * m2 : 0.f;
 }
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
@@ -1033,7 +1094,7 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
     uint32_t ahi[4], alo[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      if constexpr (DT == OC_BF16) {
+      if constexpr (MfmaT<DT>::value == OC_BF16) {
         const __bf16 h0 = (__bf16)pv[2 * e], h1 = (__bf16)pv[2 * e + 1];
         const __bf16 l0 = (__bf16)(pv[2 * e] - (float)h0), l1 = (__bf16)(pv[2 * e + 1] - (float)h1);
         ahi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
@@ -1047,19 +1108,31 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
     }
     // rows of this lane's transposing reads: 32*tb2 + 8*kg + 4*h + x/4
     const uint16_t* rowp = sv + (32 * tb2 + 8 * kg + (x >> 2)) * D + 4 * (x & 3);
+    // fp8 V: ds_read_b64_tr_b8 with lane x addressing row 32*tb2 + 8*kg +
+    // x/2, bytes 16*nc + 8*(x%2) .. +8 returns V[32*tb2 + 8*kg + e][16*nc + x]
+    // in byte e (e = 0..7; checked on the GPU with an in-bounds probe)
+    const uint8_t* rowp8 = reinterpret_cast<const uint8_t*>(sv) + (32 * tb2 + 8 * kg + (x >> 1)) * D + 8 * (x & 1);
 #pragma unroll
     for (int nc = 0; nc < D / 16; ++nc) {
-      const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
-      const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
       uint32_t bk[4];
-      bk[0] = (uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16);
-      bk[1] = (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16);
-      bk[2] = (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16);
-      bk[3] = (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16);
-      accp[nc] = mfma_qk<DT>(ahi, bk, accp[nc]);
-      accp[nc] = mfma_qk<DT>(alo, bk, accp[nc]);
+      if constexpr (DT == OC_FP8_E4M3FN) {
+        typedef int i32x2 __attribute__((ext_vector_type(2)));
+        const i32x2 b8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * nc));
+        fp8x4_to_bf16((uint32_t)b8[0], bk[0], bk[1]);
+        fp8x4_to_bf16((uint32_t)b8[1], bk[2], bk[3]);
+      } else {
+        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
+        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
+        bk[0] = (uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16);
+        bk[1] = (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16);
+        bk[2] = (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16);
+        bk[3] = (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16);
+      }
+      accp[nc] = mfma_qk<MfmaT<DT>::value>(ahi, bk, accp[nc]);
+      accp[nc] = mfma_qk<MfmaT<DT>::value>(alo, bk, accp[nc]);
     }
   }
 }
@@ -1200,7 +1273,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     ms.l[i] = 0.f;
   }
   uint32_t aq[MQK ? D / 32 : 1][4];
-  if constexpr (MQK) load_q_mfma<D, GT>(sh_qp, lane, aq);
+  if constexpr (MQK) load_q_mfma<DT, D, GT>(sh_qp, lane, aq);
   float* sp = sh_p + wave * 64 * kPH;     // this wave's p[head][token] slot (MQK)
   uint16_t* sv = sh_v + wave * 64 * D;    // this wave's V tile slot (MQK)
   f32x4 accp[MQK ? D / 16 : 1];
@@ -1303,8 +1376,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
         const int valid = min(64, ri.n_tok - t * 64);
         TilePages pg{};
         if constexpr (PAGED) pg = tile_pages(a, ri, t, bad_page);
-        load_k_mfma<D, PAGED>(a, ri, row, t, lane, kb, pg);
-        load_v_lds<D, PAGED>(a, ri, row, t, lane, sv, pg);
+        load_k_mfma<DT, D, PAGED>(a, ri, row, t, lane, kb, pg);
+        load_v_lds<DT, D, PAGED>(a, ri, row, t, lane, sv, pg);
         tile_softmax_mfma<DT, D, GT>(ms, accp, aq, kb, sp, lscale_of(t), tile_vmul(a, row, t), valid, lane);
         // the V tile's direct-to-LDS loads (issued after K) have landed
         __builtin_amdgcn_s_waitcnt(0);
@@ -1328,20 +1401,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
         TilePages pg{};
         if (t >= 0) {
           if constexpr (PAGED) pg = tile_pages(a, ri, t, bad_page);
-          load_k_mfma<D, PAGED>(a, ri, row, t, lane, kb, pg);
+          load_k_mfma<DT, D, PAGED>(a, ri, row, t, lane, kb, pg);
         }
         while (t >= 0) {
           const int valid = min(64, ri.n_tok - t * 64);
           // per-tile scales first: a load issued after the V and K requests
           // below would make its wait a wait for all of them
-          const float lsc = lscale_of(t);
+          const float kmul = tile_kdeq(a, row, t).mul;
+          const float lsc = a.scale * kmul;  // = lscale_of(t)
           const float vmul = tile_vmul(a, row, t);
           f32x4 lg[4];
           tile_logits_mfma<DT, D>(aq, kb, lg);
           bool keep = true;
           if (valid == 64) {
             float el, eh;
-            tile_energies_mfma<DT, D, LOW>(kb, lane, el, eh);
+            tile_energies_mfma<DT, D, LOW>(kb, lane, kmul, el, eh);
             keep = gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
           }
           keep = __builtin_amdgcn_readfirstlane(keep ? 1 : 0) != 0;
@@ -1352,12 +1426,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
               a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
             }
           }
-          if (keep) load_v_lds<D, PAGED>(a, ri, row, t, lane, sv, pg);
+          if (keep) load_v_lds<DT, D, PAGED>(a, ri, row, t, lane, sv, pg);
           __builtin_amdgcn_sched_barrier(0);
           const int tn = next_tile();
           if (tn >= 0) {
             if constexpr (PAGED) pg = tile_pages(a, ri, tn, bad_page);
-            load_k_mfma<D, PAGED>(a, ri, row, tn, lane, kb, pg);
+            load_k_mfma<DT, D, PAGED>(a, ri, row, tn, lane, kb, pg);
           }
           __builtin_amdgcn_sched_barrier(0);
           if (keep) {
@@ -1669,7 +1743,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     if constexpr (DOT2) {
       // x0, x1 are exact in the 16-bit q dtype, so the narrowing is exact
       uint32_t lo, hi;
-      if (DT == OC_BF16) {
+      if (MfmaT<DT>::value == OC_BF16) {
         lo = __float_as_uint(x0) >> 16;
         hi = __float_as_uint(x1) >> 16;
       } else {
@@ -1971,39 +2045,42 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 // q . k on the matrix cores for contiguous 16-bit K (q of the same type)
 template <int DT, int HD, bool DOT2>
 inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
-  if (a.paged) {
-    // matrix cores for pages of >= 16 tokens (a 16-token block in one page)
-    if (DOT2 && a.bs_log2 >= 4 && (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE || a.k_scale_mode != OC_KSCALE_TILE))
-      launch_decode_gt<DT, HD, DOT2, true, DOT2>(a, gt, grid, st);
-    else
-      launch_decode_gt<DT, HD, DOT2, true, false>(a, gt, grid, st);
-    return;
-  }
+  // matrix cores whenever q has the 16-bit type K runs in (bf16 q for fp8
+  // K, which is widened exactly): contiguous K/V, or pages of >= 16 tokens
+  // (a 16-token block inside one page)
   if constexpr (DOT2) {
-    // single pass with per-tile K scales stays on the VALU path, which
-    // scores the dequantised elements
-    if (a.mode == OC_MODE_CACHED || a.gate == OC_GATE_NONE || a.k_scale_mode != OC_KSCALE_TILE) {
-      launch_decode_gt<DT, HD, DOT2, false, true>(a, gt, grid, st);
+    if (!a.paged) {
+      launch_decode_gt<DT, HD, true, false, true>(a, gt, grid, st);
+      return;
+    }
+    if (a.bs_log2 >= 4) {
+      launch_decode_gt<DT, HD, true, true, true>(a, gt, grid, st);
       return;
     }
   }
-  launch_decode_gt<DT, HD, DOT2, false, false>(a, gt, grid, st);
+  // VALU path (v_dot2 q.k for 16-bit K and q of the same type)
+  constexpr bool VDOT2 = DOT2 && DT != OC_FP8_E4M3FN;
+  if (a.paged) launch_decode_gt<DT, HD, VDOT2, true, false>(a, gt, grid, st);
+  else launch_decode_gt<DT, HD, VDOT2, false, false>(a, gt, grid, st);
 }
 
 #define OC_DECODE_CASES(DT, DOT2)                                 \
   if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
   else launch_decode_hd<DT, 64, DOT2>(a, gt, grid, st);
 
-// q . k in 16-bit dot products when K and q share the 16-bit type
+// q . k on 16-bit operands (matrix cores, or v_dot2 on the VALU path) when
+// q has K's 16-bit type; for fp8 K when q is bf16
 template <int DT>
-constexpr bool kHasDot2 = DT == OC_BF16 || DT == OC_F16;
+constexpr bool kHasDot2 = DT == OC_BF16 || DT == OC_F16 || DT == OC_FP8_E4M3FN;
+template <int DT>
+constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
 
 #define OC_DEFINE_LAUNCHERS(DT)                                                                   \
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
     const dim3 grid = a.flat ? dim3(a.flat_target + a.num_rows, 1, gchunks) : dim3(a.Pg, a.num_rows, gchunks); \
-    if (kHasDot2<DT> && a.q_dtype == DT) {                                                        \
+    if (kHasDot2<DT> && a.q_dtype == kDot2Q<DT>) {                                               \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \
       OC_DECODE_CASES(DT, false)                                                                  \

@@ -538,6 +538,54 @@ def test_fp8_tile_scales_vs_oracle(mode):
     assert_out(out, O.round_to(ref["out"], "bf16"), "fp8", "fp8 tiles")
 
 
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("gate,mode", [("cs", "single_pass"), ("cs", "cached"), ("zeta", "single_pass"),
+                                       ("none", "single_pass")])
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp8_tile_scales_grid(d, gate, mode, paged):
+    """fp8-e4m3fn K and V with per-(row, tile) scales and bf16 q (the
+    matrix-core path, K and V widened to bf16 exactly), contiguous and on a
+    16-token page pool, with a partial tail tile; masks and outputs against
+    the oracle on the decoded values."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import calibrate_tau, make_q, paged_pool
+    G, rows, T = 4, 3, 13
+    wl = _mixed(rows, T, d, "fp8", seed=50 + d)
+    q = make_q(rows, G, d, seed=51)
+    lens = [T * 64, T * 64 - 20, 5 * 64]
+    tab = O.fp8_e4m3fn_table()
+    kf = tab[wl.keys.view(torch.uint8).numpy()]
+    vf = tab[wl.values.view(torch.uint8).numpy()]
+    ks, vs = wl.k_scales.to(DEV), wl.v_scales.to(DEV)
+    el, eh, _, _ = X.score_tiles(_with_kscales(X.rows_layout(wl.keys.to(DEV), None), ks))
+    if paged:
+        kc, vc, bt = paged_pool(wl.keys.view(torch.uint8), wl.values.view(torch.uint8), 1, 16, lens, seed=52)
+        kv = X.paged_layout(kc.view(torch.float8_e4m3fn).to(DEV), vc.view(torch.float8_e4m3fn).to(DEV),
+                            bt.to(DEV), T)
+    else:
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    _with_kscales(kv, ks)
+    kv.v_scale_mode, kv.v_scales = X.vscale_mode(vs, kv.num_rows, kv.num_tiles, DEV)
+    gcode = {"none": N.OC_GATE_NONE, "zeta": N.OC_GATE_ZETA, "cs": N.OC_GATE_CS}[gate]
+    thr = {"cs": calibrate_tau(eh, q.to(DEV), G) if gate == "cs" else 0.0, "zeta": 5.0, "none": 0.0}[gate]
+    res = X.decode(kv, q.to(DEV), G, gate=gcode, threshold=thr,
+                   mode=N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS, scores=(el, eh),
+                   out_dtype=torch.bfloat16, want_keep=True)
+    ref = O.decode_rows(np32(q), kf, vf, gate=gate, threshold=thr, G=G, lengths=lens,
+                        k_scales=wl.k_scales.numpy(), v_scales=wl.v_scales.numpy())
+    if gate != "none":
+        assert np.array_equal(res.keep[:, :T].cpu().numpy().astype(bool), ref["keep"])
+    assert_out(res.out, O.round_to(ref["out"], "bf16"), "fp8", f"fp8 d={d} {gate} {mode} paged={paged}")
+
+
+def _with_kscales(kv, ks):
+    from orthocache_gpu import _launch as X
+    kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(ks, kv.num_rows, kv.num_tiles, ks.device)
+    return kv
+
+
 def test_orthocache_forward_modes():
     from orthocache_gpu import orthocache_forward
     g = torch.Generator().manual_seed(0)
