@@ -24,6 +24,16 @@
  *                      _paged_splitk_reduce_kernel (paged_eviction.py:195-237)
  *   oc_device_cu_count <- torch.cuda.get_device_properties(...).multi_processor_count
  *                      as read by _auto_num_splits (fused_eviction.py:556-570)
+ *   oc_band_norms   <- SpectralNormCache.update_prefill / populate_from_keys
+ *                      (src/orthocache_gpu/norm_cache.py:58-117)
+ *   oc_decode_gate  <- _decode_gate_kernel + decode_gate (decode_gate.py:108-245);
+ *                      with the Walsh-subspace q norm, _pytorch_decode_gate
+ *                      (decode_gate.py:248-295)
+ *   oc_q_high_norms <- compute_q_high_norm_exact (decode_gate.py:54-100)
+ *   oc_apply_tile_mask <- apply_decode_mask / apply_decode_mask_vectorized
+ *                      (decode_gate.py:302-374)
+ *   oc_score_tile_range: no reference counterpart (the append path of the
+ *                      score cache: rescore the tiles a decode step completed)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -136,6 +146,66 @@ int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e
  * Replaces the W @ K products (fwht_fused_prototype.py:160-162).
  */
 int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream);
+
+/*
+ * oc_score_tile_range -- oc_score_tiles for tiles [first_tile, first_tile +
+ * count) of every row only, written at those columns of the outputs.  The
+ * append path of a score cache: after a decode step completes a tile, only
+ * that tile is rescored.  No reference counterpart.
+ */
+int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int32_t count, double zeta_max,
+                        float* e_low, float* e_high, float* zeta, uint8_t* keep,
+                        int64_t out_row_stride, void* stream);
+
+/*
+ * oc_band_norms -- ||(W64 @ K_t)[band_lo:band_hi]||_F (float32, 0 when below
+ * 1e-38) of tiles [first_tile, first_tile + count) of every row, written to
+ * out[r * out_row_stride + t]; tiles not wholly inside a row's length are
+ * skipped.  valid_tiles (optional, int32 per row) is raised to t + 1 for
+ * every tile written.  Replaces SpectralNormCache.update_prefill and
+ * populate_from_keys (norm_cache.py:58-117; their band is [48, 64)).
+ */
+int oc_band_norms(const oc_kv_desc* kv, int32_t first_tile, int32_t count, int32_t band_lo,
+                  int32_t band_hi, float* out, int64_t out_row_stride, int32_t* valid_tiles,
+                  void* stream);
+
+/* q-norm of the decode gate */
+#define OC_QNORM_SPATIAL 0     /* ||q||_2 (the GPU path of decode_gate) */
+#define OC_QNORM_WALSH_HIGH 1  /* Walsh-subspace ||q_high||_2 (compute_q_high_norm_exact) */
+
+/*
+ * oc_decode_gate -- the O(1) decode gate from cached K band norms.  For kv
+ * head h: qn = max over its G query heads of the q norm (`q_norm_mode`;
+ * q rows h*G .. h*G+G-1 of (num_kv_heads*G, head_dim), q_dtype F32/F16/BF16),
+ * q_norms[h] = qn, and for t < num_tiles
+ *   mask[h, t] = (qn * norm_cache[h, t] <= (float)tau_norm)   (1 = evict),
+ * mask[h, t] = 0 for num_tiles <= t < max_tiles.  tau_norm = tau * tile_size
+ * * head_dim, as decode_gate pre-multiplies it (decode_gate.py:210-212).
+ * Replaces _decode_gate_kernel and its launch (decode_gate.py:108-245).
+ */
+int oc_decode_gate(const void* q, int32_t q_dtype, int64_t q_row_stride, int32_t num_kv_heads, int32_t G,
+                   int32_t head_dim, const float* norm_cache, int64_t norm_row_stride, int32_t num_tiles,
+                   int32_t max_tiles, double tau_norm, int32_t q_norm_mode, int32_t low_band,
+                   uint8_t* mask, int64_t mask_row_stride, float* q_norms, void* stream);
+
+/*
+ * oc_q_high_norms -- out[r] = sqrt(max(||q_r||^2 - sum_i S_i^2 / bs, 0)),
+ * S_i the sums of the low_band blocks of bs = head_dim / low_band elements
+ * (float32).  Replaces compute_q_high_norm_exact (decode_gate.py:54-100).
+ */
+int oc_q_high_norms(const void* q, int32_t q_dtype, int64_t rows, int32_t head_dim, int64_t q_row_stride,
+                    int32_t low_band, float* out, void* stream);
+
+/*
+ * oc_apply_tile_mask -- in place, logits[h, s] = -inf for every query head
+ * h < num_q_heads and token s < seq_len whose tile t = s / tile_size is
+ * below num_tiles with mask[h / G, t] != 0.  logits dtype F32/F16/BF16,
+ * rows `logits_row_stride` elements apart, tokens contiguous.  Replaces
+ * apply_decode_mask and apply_decode_mask_vectorized (decode_gate.py:302-374).
+ */
+int oc_apply_tile_mask(void* logits, int32_t dtype, int32_t num_q_heads, int64_t seq_len,
+                       int64_t logits_row_stride, const uint8_t* mask, int64_t mask_row_stride, int32_t G,
+                       int32_t tile_size, int32_t num_tiles, void* stream);
 
 /* decode parameters; see oc_decode */
 typedef struct oc_decode_params {

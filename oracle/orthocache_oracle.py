@@ -17,6 +17,13 @@ paths with the same per-head, per-tile loop structure:
 * ``paged``                   <- paged_eviction.py:244-316 (+ wrapper :323-368)
 * ``auto_num_splits``         <- fused_eviction.py:556-570
 * ``dense_decode``            <- pipeline.py:558-568 (fp32 form)
+* ``band_norm`` / ``band_norms`` <- SpectralNormCache.update_prefill /
+                                 populate_from_keys (norm_cache.py:58-117)
+* ``q_high_norm_exact``       <- compute_q_high_norm_exact (decode_gate.py:54-100)
+* ``decode_gate``             <- decode_gate / _decode_gate_kernel
+                                 (decode_gate.py:108-245); tight=True:
+                                 _pytorch_decode_gate (decode_gate.py:248-295)
+* ``apply_decode_mask``       <- apply_decode_mask(_vectorized) (decode_gate.py:302-374)
 
 (all paths relative to ``src/orthocache_gpu/triton_kernels/`` or
 ``src/orthocache_gpu/`` of the reference tree).
@@ -40,6 +47,13 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   zero-eviction == dense, total eviction == 0.
 * split partials: the LSE merge of the per-split partials equals the
   single-split result (float64), and the tile sets are {s + kP}.
+* ``band_norm``: the closed forms of the [32,64) and [48,64) bands
+  (1/2 sum ||k_u - k_{u+32}||^2 and 1/4 sum ||k_t - k_{t+16} - k_{t+32} +
+  k_{t+48}||^2) in float64, integer tiles exact.
+* ``q_high_norm_exact``: the residual of a least-squares projection onto
+  block-constant vectors (float64), and its two special cases.
+* ``decode_gate`` / ``apply_decode_mask``: explicit per-(head, tile) loops,
+  special thresholds, and the max-over-G rule.
 """
 
 from __future__ import annotations
@@ -533,3 +547,93 @@ def fwht64_butterfly(x: np.ndarray) -> np.ndarray:
         x = y.reshape(x.shape)
         h *= 2
     return x / math.sqrt(n)
+
+
+# ---------------------------------------------------------------------------
+# Score-cache maintenance and the O(1) decode gate
+# ---------------------------------------------------------------------------
+
+def band_norm(k_tile: np.ndarray, band_lo: int = 48, band_hi: int = 64) -> F32:
+    """||(W @ k_tile)[band_lo:band_hi]||_F of one 64xd tile in float32, 0
+    below 1e-38 (SpectralNormCache.update_prefill, norm_cache.py:78-86)."""
+    x = (walsh_matrix() @ _as_f32(k_tile)).astype(F32)
+    n = F32(np.sqrt(np.sum(x[band_lo:band_hi] * x[band_lo:band_hi], dtype=F32)))
+    return F32(0.0) if float(n) < _CS_CLAMP else n
+
+
+def band_norms(keys: np.ndarray, band_lo: int = 48, band_hi: int = 64) -> np.ndarray:
+    """band_norm of every complete tile of (rows, S, d) keys, (rows, S // 64)
+    (populate_from_keys, norm_cache.py:90-117)."""
+    keys = _as_f32(keys)
+    rows, s_len, _ = keys.shape
+    t_count = s_len // TILE_SIZE
+    out = np.zeros((rows, t_count), dtype=F32)
+    for r in range(rows):
+        for t in range(t_count):
+            out[r, t] = band_norm(keys[r, t * TILE_SIZE:(t + 1) * TILE_SIZE], band_lo, band_hi)
+    return out
+
+
+def q_high_norm_exact(q: np.ndarray, low_band: int = 8) -> np.ndarray:
+    """sqrt(max(||q||^2 - sum_i S_i^2 / bs, 0)) over the last axis, float32,
+    S_i the sums of low_band blocks of bs = d / low_band elements
+    (compute_q_high_norm_exact, decode_gate.py:86-100)."""
+    q = _as_f32(q)
+    d = q.shape[-1]
+    bs = d // low_band
+    assert d % low_band == 0
+    sq = np.sum(q * q, axis=-1, dtype=F32)
+    sums = np.sum(q.reshape(*q.shape[:-1], low_band, bs), axis=-1, dtype=F32)
+    lo = (np.sum(sums * sums, axis=-1, dtype=F32) / F32(bs)).astype(F32)
+    hi = (sq - lo).astype(F32)
+    hi = np.where(hi < 0, F32(0.0), hi)
+    return np.sqrt(hi).astype(F32)
+
+
+def decode_gate(q: np.ndarray, norm_cache: np.ndarray, tau: float, num_tiles: int, G: int,
+                tile_size: int = TILE_SIZE, tight: bool = False, low_band: int = 8):
+    """(mask (Hkv, max_tiles) bool True = evict, q_norms (Hkv,)).
+
+    tight=False follows the GPU path (_decode_gate_kernel,
+    decode_gate.py:140-181): the largest ||q_g||^2 of the group, then its
+    square root.  tight=True follows _pytorch_decode_gate (:248-295): the
+    largest Walsh-subspace ||q_high||.  Evict tile t < num_tiles of kv head h
+    iff qn[h] * norm_cache[h, t] <= tau * tile_size * head_dim (float32)."""
+    q = _as_f32(q)
+    hq, d = q.shape
+    hkv = hq // G
+    nc = _as_f32(norm_cache)
+    max_tiles = nc.shape[1]
+    tau_norm = F32(tau * float(tile_size * d))
+    qn = np.zeros(hkv, dtype=F32)
+    for h in range(hkv):
+        group = q[h * G:(h + 1) * G]
+        if tight:
+            qn[h] = np.max(q_high_norm_exact(group, low_band))
+        else:
+            best = F32(0.0)
+            for g in range(G):
+                sq = np.sum(group[g] * group[g], dtype=F32)
+                if sq > best:
+                    best = sq
+            qn[h] = np.sqrt(best)
+    mask = np.zeros((hkv, max_tiles), dtype=bool)
+    for h in range(hkv):
+        for t in range(num_tiles):
+            mask[h, t] = bool(F32(qn[h] * nc[h, t]) <= tau_norm)
+    return mask, qn
+
+
+def apply_decode_mask(logits: np.ndarray, mask: np.ndarray, G: int, tile_size: int = TILE_SIZE,
+                      num_tiles: Optional[int] = None) -> np.ndarray:
+    """logits (Hq, 1, S): -inf over every evicted tile (decode_gate.py:302-331),
+    on a copy."""
+    out = np.array(logits, copy=True)
+    s_len = out.shape[2]
+    if num_tiles is None:
+        num_tiles = s_len // tile_size
+    for kv_h in range(mask.shape[0]):
+        for t in range(num_tiles):
+            if mask[kv_h, t]:
+                out[kv_h * G:(kv_h + 1) * G, :, t * tile_size:min((t + 1) * tile_size, s_len)] = -np.inf
+    return out

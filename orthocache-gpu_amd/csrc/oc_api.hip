@@ -11,26 +11,14 @@
 #include <string>
 
 #include "oc_kernels.h"
+#include "oc_status.h"
 #include "orthocache_hip.h"
 
 namespace oc {
 
 static thread_local std::string g_last_error;
 
-static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-static int fail(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return code;
-}
-
-static int hip_fail(hipError_t e, const char* what) {
-  return fail(OC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-}
+void set_last_error(const char* msg) { g_last_error = msg; }
 
 static int elem_size(int dt) {
   switch (dt) {
@@ -143,6 +131,15 @@ static hipError_t dispatch_score(int dt, const DecodeArgs& a, int hd, hipStream_
     case OC_F16: return launch_score<OC_F16>(a, hd, st);
     case OC_BF16: return launch_score<OC_BF16>(a, hd, st);
     default: return launch_score<OC_FP8_E4M3FN>(a, hd, st);
+  }
+}
+
+static hipError_t dispatch_band(int dt, const DecodeArgs& a, int hd, hipStream_t st) {
+  switch (dt) {
+    case OC_F32: return launch_band<OC_F32>(a, hd, st);
+    case OC_F16: return launch_band<OC_F16>(a, hd, st);
+    case OC_BF16: return launch_band<OC_BF16>(a, hd, st);
+    default: return launch_band<OC_FP8_E4M3FN>(a, hd, st);
   }
 }
 
@@ -461,9 +458,56 @@ extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_lo
   a.o_keep = keep;
   a.o_stride = out_row_stride;
   a.q_dtype = OC_F32;
+  a.t0 = 0;
+  a.tcnt = kv->num_tiles;
   if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
   const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
   return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
+}
+
+extern "C" int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int32_t count, double zeta_max,
+                                   float* e_low, float* e_high, float* zeta, uint8_t* keep, int64_t out_row_stride,
+                                   void* stream) {
+  DecodeArgs a;
+  int rc = fill_kv(kv, a);
+  if (rc) return rc;
+  if (first_tile < 0 || count < 0 || (int64_t)first_tile + count > kv->num_tiles)
+    return fail(OC_ERR_INVALID, "tile range [%d, %d) outside 0..%d", first_tile, first_tile + count, kv->num_tiles);
+  a.thr = zeta_max;
+  a.o_el = e_low;
+  a.o_eh = e_high;
+  a.o_z = zeta;
+  a.o_keep = keep;
+  a.o_stride = out_row_stride;
+  a.q_dtype = OC_F32;
+  a.t0 = first_tile;
+  a.tcnt = count;
+  if ((int64_t)kv->num_rows * count == 0) return OC_OK;
+  const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
+}
+
+extern "C" int oc_band_norms(const oc_kv_desc* kv, int32_t first_tile, int32_t count, int32_t band_lo,
+                             int32_t band_hi, float* out, int64_t out_row_stride, int32_t* valid_tiles,
+                             void* stream) {
+  DecodeArgs a;
+  int rc = fill_kv(kv, a);
+  if (rc) return rc;
+  if (!out) return fail(OC_ERR_INVALID, "out is NULL");
+  if (first_tile < 0 || count < 0 || (int64_t)first_tile + count > kv->num_tiles)
+    return fail(OC_ERR_INVALID, "tile range [%d, %d) outside 0..%d", first_tile, first_tile + count, kv->num_tiles);
+  if (band_lo < 0 || band_hi > 64 || band_lo > band_hi)
+    return fail(OC_ERR_INVALID, "band [%d, %d) outside the 64 Walsh rows", band_lo, band_hi);
+  a.t0 = first_tile;
+  a.tcnt = count;
+  a.band_lo = band_lo;
+  a.band_hi = band_hi;
+  a.o_norm = out;
+  a.o_stride = out_row_stride;
+  a.o_valid = valid_tiles;
+  if ((int64_t)kv->num_rows * count == 0) return OC_OK;
+  const hipError_t e = dispatch_band(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  return e == hipSuccess ? OC_OK : hip_fail(e, "band-norm launch");
 }
 
 extern "C" int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream) {

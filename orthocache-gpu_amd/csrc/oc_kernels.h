@@ -95,6 +95,14 @@ struct DecodeArgs {
   uint8_t* o_keep;
   int64_t o_stride;
   float* o_fwht;
+  // tile range of the scoring / band-norm kernels: tiles [t0, t0 + tcnt) of
+  // every row
+  int32_t t0, tcnt;
+  // band-norm kernel: ||(W64 K)[band_lo, band_hi)||_F per tile, and the
+  // per-row count of scored tiles raised to t + 1 (atomic max), if given
+  int32_t band_lo, band_hi;
+  float* o_norm;
+  int32_t* o_valid;
 };
 
 template <int DT>
@@ -1951,9 +1959,9 @@ __global__ __launch_bounds__(kThreads) void score_kernel(const DecodeArgs a) {
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
   const int64_t job = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (job >= (int64_t)a.num_rows * a.num_tiles) return;
-  const int row = (int)(job / a.num_tiles);
-  const int t = (int)(job - (int64_t)row * a.num_tiles);
+  if (job >= (int64_t)a.num_rows * a.tcnt) return;
+  const int row = (int)(job / a.tcnt);
+  const int t = a.t0 + (int)(job - (int64_t)row * a.tcnt);
   const RowInfo ri = row_info(a, row);
   const int64_t o = (int64_t)row * a.o_stride + t;
   float el = 0.f, eh = 0.f, z = 0.f;
@@ -2023,6 +2031,60 @@ __global__ __launch_bounds__(kThreads) void fwht_kernel(const DecodeArgs a) {
   }
 }
 
+// Band norms ||(W64 K_t)[band_lo, band_hi)||_F of tiles [t0, t0 + tcnt) of
+// every row (norm_cache.py:58-117), float32, clamped to 0 below 1e-38 as
+// the reference does; the full 64-point transform in registers as in
+// fwht_kernel, then the squares of the band's rows.  Tiles not wholly
+// inside the row's length are not written.
+template <int DT, int D, bool PAGED>
+__global__ __launch_bounds__(kThreads) void band_norm_kernel(const DecodeArgs a) {
+  constexpr int CPL = D / 16;
+  using L = Lay<DT, D>;
+  const int lane = threadIdx.x & 63;
+  const int64_t job = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (job >= (int64_t)a.num_rows * a.tcnt) return;
+  const int row = (int)(job / a.tcnt);
+  const int t = a.t0 + (int)(job - (int64_t)row * a.tcnt);
+  const RowInfo ri = row_info(a, row);
+  if ((t + 1) * 64 > ri.n_tok) return;
+  uint32_t kw[16][L::LW];
+  float f[16][CPL];
+  load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
+  decode_tile<DT, D>(kw, f, tile_kdeq(a, row, t));
+#pragma unroll
+  for (int h = 1; h < 16; h <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i & h) continue;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const float x = f[i][c], y = f[i + h][c];
+        f[i][c] = x + y;
+        f[i + h][c] = x - y;
+      }
+    }
+  }
+  // lane (gamma, j) holds spectral rows 4i + gamma, columns j*CPL ..
+  const int gamma = lane >> 4;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const bool in = 4 * i + gamma >= a.band_lo && 4 * i + gamma < a.band_hi;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      float x = butterfly_rows<16>(f[i][c]);
+      x = butterfly_rows<32>(x) * 0.125f;
+      ss = in ? __builtin_fmaf(x, x, ss) : ss;
+    }
+  }
+  float n = __builtin_sqrtf(wave_sum(ss));
+  if ((double)n < 1e-38) n = 0.f;
+  if (lane == 0) {
+    a.o_norm[(int64_t)row * a.o_stride + t] = n;
+    if (a.o_valid) atomicMax(a.o_valid + row, t + 1);
+  }
+}
+
 // Launchers instantiated per element type (oc_kernels_<dtype>.hip).
 template <int DT>
 hipError_t launch_decode(const DecodeArgs& a, int head_dim, int gt, int gchunks, hipStream_t st);
@@ -2030,6 +2092,8 @@ template <int DT>
 hipError_t launch_score(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
+template <int DT>
+hipError_t launch_band(const DecodeArgs& a, int head_dim, hipStream_t st);
 
 template <int DT, int HD, bool DOT2, bool PG, bool MQ>
 inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
@@ -2089,7 +2153,7 @@ constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
   }                                                                                               \
   template <>                                                                                     \
   hipError_t launch_score<DT>(const DecodeArgs& a, int head_dim, hipStream_t st) {                \
-    const int64_t jobs = (int64_t)a.num_rows * a.num_tiles;                                       \
+    const int64_t jobs = (int64_t)a.num_rows * a.tcnt;                                            \
     const dim3 grid((unsigned)((jobs + kWaves - 1) / kWaves)), block(kThreads);                   \
     if (head_dim == 128) {                                                                        \
       if (a.paged) hipLaunchKernelGGL((score_kernel<DT, 128, true>), grid, block, 0, st, a);      \
@@ -2110,6 +2174,19 @@ constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
     } else {                                                                                      \
       if (a.paged) hipLaunchKernelGGL((fwht_kernel<DT, 64, true>), grid, block, 0, st, a);        \
       else hipLaunchKernelGGL((fwht_kernel<DT, 64, false>), grid, block, 0, st, a);               \
+    }                                                                                             \
+    return hipGetLastError();                                                                     \
+  }                                                                                               \
+  template <>                                                                                     \
+  hipError_t launch_band<DT>(const DecodeArgs& a, int head_dim, hipStream_t st) {                 \
+    const int64_t jobs = (int64_t)a.num_rows * a.tcnt;                                            \
+    const dim3 grid((unsigned)((jobs + kWaves - 1) / kWaves)), block(kThreads);                   \
+    if (head_dim == 128) {                                                                        \
+      if (a.paged) hipLaunchKernelGGL((band_norm_kernel<DT, 128, true>), grid, block, 0, st, a);  \
+      else hipLaunchKernelGGL((band_norm_kernel<DT, 128, false>), grid, block, 0, st, a);         \
+    } else {                                                                                      \
+      if (a.paged) hipLaunchKernelGGL((band_norm_kernel<DT, 64, true>), grid, block, 0, st, a);   \
+      else hipLaunchKernelGGL((band_norm_kernel<DT, 64, false>), grid, block, 0, st, a);          \
     }                                                                                             \
     return hipGetLastError();                                                                     \
   }

@@ -337,6 +337,53 @@ def score_tiles(kv: KVLayout, zeta_max: float = 0.0, *, want_zeta: bool = True, 
     return e_low, e_high, zeta, keep
 
 
+def score_tile_range(kv: KVLayout, first_tile: int, count: int, e_low: torch.Tensor, e_high: torch.Tensor,
+                     zeta: Optional[torch.Tensor] = None, keep: Optional[torch.Tensor] = None,
+                     zeta_max: float = 0.0) -> None:
+    """oc_score_tile_range: rescore tiles [first_tile, first_tile + count) of
+    every row into columns of existing (rows, >= T) score tensors."""
+    device = require_gpu(kv.k, e_low, e_high)
+    for t in (e_low, e_high, zeta, keep):
+        if t is not None and (t.dim() != 2 or t.shape[0] < kv.num_rows or t.shape[1] < first_tile + count
+                              or t.stride(1) != 1 or t.stride(0) != e_high.stride(0) or t.device != device):
+            raise ValueError(f"score tensors must be ({kv.num_rows}, >= {first_tile + count}) with equal row "
+                             f"strides on {device}")
+    desc = kv.struct()
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_score_tile_range", N.lib().oc_score_tile_range(
+            ctypes.byref(desc), int(first_tile), int(count), float(zeta_max), e_low.data_ptr(), e_high.data_ptr(),
+            _ptr(zeta), _ptr(keep), e_high.stride(0), ctypes.c_void_p(stream)))
+
+
+def band_norms(kv: KVLayout, first_tile: int, count: int, band: Tuple[int, int], out: torch.Tensor,
+               valid_tiles: Optional[torch.Tensor] = None, tile_offset: int = 0) -> None:
+    """oc_band_norms: ||(W64 K_t)[band]||_F of tiles [first_tile, first_tile +
+    count) of every row into out (rows, >= T) float32.  With tile_offset
+    > 0 the layout's tile 0 is numbered tile_offset (the descriptor's rows
+    start tile_offset tiles before kv.k, which is never read): a single
+    tile scored into column tile_offset of the outputs."""
+    device = require_gpu(kv.k, out)
+    if out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1 or out.shape[0] < kv.num_rows \
+            or out.shape[1] < tile_offset + first_tile + count:
+        raise ValueError(f"out must be float32 ({kv.num_rows}, >= {first_tile + count}) with contiguous rows")
+    if valid_tiles is not None and (valid_tiles.dtype != torch.int32 or valid_tiles.numel() < kv.num_rows
+                                    or not valid_tiles.is_contiguous()):
+        raise ValueError("valid_tiles must be a contiguous int32 tensor with one entry per row")
+    desc = kv.struct()
+    if tile_offset:
+        if kv.paged:
+            raise ValueError("tile_offset applies to contiguous rows only")
+        desc.k -= tile_offset * TILE_SIZE * kv.k_token_stride * kv.k.element_size()
+        desc.num_tiles += tile_offset
+        first_tile += tile_offset
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_band_norms", N.lib().oc_band_norms(
+            ctypes.byref(desc), int(first_tile), int(count), int(band[0]), int(band[1]), out.data_ptr(),
+            out.stride(0), _ptr(valid_tiles), ctypes.c_void_p(stream)))
+
+
 def fwht_tiles(kv: KVLayout) -> torch.Tensor:
     """oc_fwht_tiles: (rows, T, 64, d) float32 spectra X = W64 @ K_tile."""
     device = require_gpu(kv.k)
@@ -378,6 +425,72 @@ def dequant_fp8(src: torch.Tensor, scale: float, out_dtype: torch.dtype) -> torc
             src.data_ptr(), n, float(scale), dtype_code(out_dtype, "out", allow_fp8=False), out.data_ptr(),
             ctypes.c_void_p(stream)))
     return out
+
+
+def decode_gate(q: torch.Tensor, norm_cache: torch.Tensor, tau_norm: float, num_tiles: int, G: int,
+                q_norm_mode: int, low_band: int = 8) -> Tuple[torch.Tensor, torch.Tensor]:
+    """oc_decode_gate: (mask (Hkv, max_tiles) bool, True = evict; q_norms (Hkv,))."""
+    device = require_gpu(q, norm_cache)
+    if q.dim() != 2 or q.shape[0] % G:
+        raise ValueError(f"q must be (num_kv_heads * G, head_dim), got {tuple(q.shape)} for G={G}")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    hkv = q.shape[0] // G
+    if norm_cache.dtype != torch.float32:
+        norm_cache = norm_cache.float()
+    if norm_cache.dim() != 2 or norm_cache.shape[0] < hkv or norm_cache.stride(1) != 1:
+        raise ValueError(f"norm_cache must be ({hkv}, max_tiles) float32 with contiguous rows")
+    max_tiles = norm_cache.shape[1]
+    if not 0 <= num_tiles <= max_tiles:
+        raise ValueError(f"num_tiles {num_tiles} outside 0..{max_tiles}")
+    mask = torch.empty((hkv, max_tiles), dtype=torch.bool, device=device)
+    q_norms = torch.empty((hkv,), dtype=torch.float32, device=device)
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_decode_gate", N.lib().oc_decode_gate(
+            q.data_ptr(), dtype_code(q.dtype, "q", allow_fp8=False), q.stride(0), hkv, G, q.shape[1],
+            norm_cache.data_ptr(), norm_cache.stride(0), int(num_tiles), max_tiles, float(tau_norm), q_norm_mode,
+            int(low_band), mask.data_ptr(), mask.stride(0), q_norms.data_ptr(), ctypes.c_void_p(stream)))
+    return mask, q_norms
+
+
+def q_high_norms(q: torch.Tensor, low_band: int) -> torch.Tensor:
+    """oc_q_high_norms over the last dimension of q; returns q.shape[:-1] float32."""
+    device = require_gpu(q)
+    d = q.shape[-1]
+    q2 = q.reshape(-1, d)
+    if q2.stride(-1) != 1:
+        q2 = q2.contiguous()
+    out = torch.empty((q2.shape[0],), dtype=torch.float32, device=device)
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_q_high_norms", N.lib().oc_q_high_norms(
+            q2.data_ptr(), dtype_code(q2.dtype, "q", allow_fp8=False), q2.shape[0], d, q2.stride(0), int(low_band),
+            out.data_ptr(), ctypes.c_void_p(stream)))
+    return out.view(q.shape[:-1])
+
+
+def apply_tile_mask(logits: torch.Tensor, mask: torch.Tensor, G: int, tile_size: int, num_tiles: int) -> None:
+    """oc_apply_tile_mask on (num_q_heads, 1, seq_len) or (num_q_heads, seq_len) logits, in place."""
+    device = require_gpu(logits, mask)
+    if logits.dim() == 3:
+        if logits.shape[1] != 1:
+            raise ValueError(f"logits must be (num_q_heads, 1, seq_len), got {tuple(logits.shape)}")
+        rows = logits[:, 0, :]
+    else:
+        rows = logits
+    if rows.stride(-1) != 1:
+        raise ValueError("logits must be contiguous along the sequence")
+    if mask.dtype not in (torch.bool, torch.uint8) or mask.dim() != 2 or mask.stride(1) != 1:
+        raise ValueError("mask must be a (num_kv_heads, max_tiles) bool tensor with contiguous rows")
+    if rows.shape[0] > mask.shape[0] * G or num_tiles > mask.shape[1]:
+        raise ValueError("mask does not cover the logits' heads or tiles")
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_apply_tile_mask", N.lib().oc_apply_tile_mask(
+            rows.data_ptr(), dtype_code(rows.dtype, "logits", allow_fp8=False), rows.shape[0], rows.shape[1],
+            rows.stride(0), mask.data_ptr(), mask.stride(0), G, int(tile_size), int(num_tiles),
+            ctypes.c_void_p(stream)))
 
 
 def counts_metadata(keep: torch.Tensor, tiles_total: int) -> dict:

@@ -28,6 +28,8 @@ OC_GATE_NONE, OC_GATE_ZETA, OC_GATE_CS = 0, 1, 2
 OC_MODE_SINGLE_PASS, OC_MODE_CACHED = 0, 1
 OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE = 0, 1, 3
 OC_VSCALE_NONE, OC_VSCALE_TILE = 0, 1
+# q norm of the decode gate
+OC_QNORM_SPATIAL, OC_QNORM_WALSH_HIGH = 0, 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -72,6 +74,13 @@ class OcDecodeParams(ctypes.Structure):
 SIGNATURES = {
     "oc_score_tiles": (_i32, [ctypes.POINTER(OcKvDesc), ctypes.c_double, _p, _p, _p, _p, _i64, _p]),
     "oc_fwht_tiles": (_i32, [ctypes.POINTER(OcKvDesc), _p, _p]),
+    "oc_score_tile_range": (_i32, [ctypes.POINTER(OcKvDesc), _i32, _i32, ctypes.c_double, _p, _p, _p, _p, _i64,
+                                   _p]),
+    "oc_band_norms": (_i32, [ctypes.POINTER(OcKvDesc), _i32, _i32, _i32, _i32, _p, _i64, _p, _p]),
+    "oc_decode_gate": (_i32, [_p, _i32, _i64, _i32, _i32, _i32, _p, _i64, _i32, _i32, ctypes.c_double, _i32, _i32,
+                              _p, _i64, _p, _p]),
+    "oc_q_high_norms": (_i32, [_p, _i32, _i64, _i32, _i64, _i32, _p, _p]),
+    "oc_apply_tile_mask": (_i32, [_p, _i32, _i32, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),

@@ -90,17 +90,62 @@ def score_tiles(keys: torch.Tensor, zeta_max: float = 0.0, k_scale=None):
             kv.k_scale_mode, kv.k_scale = X.N.OC_KSCALE_NONE, 1.0
     e_low, e_high, zeta, keep = X.score_tiles(kv, zeta_max)
     return TileScores(e_low[:, :kv.num_tiles], e_high[:, :kv.num_tiles], zeta[:, :kv.num_tiles],
-                      keep[:, :kv.num_tiles].bool())
+                      keep[:, :kv.num_tiles].bool(), zeta_max=zeta_max)
 
 
 class TileScores:
-    """Cached per-(row, tile) spectral scores (see score_tiles)."""
+    """Cached per-(row, tile) spectral scores (see score_tiles).
 
-    def __init__(self, e_low, e_high, zeta=None, keep=None):
+    The append path: `TileScores.allocate` sizes a cache for the longest
+    context, the prefill scores its complete tiles with `update`, and each
+    decode step that completes a tile rescores only that tile with
+    `update(keys, t)` (one small launch), so no step re-reads a whole K
+    cache to keep its scores current."""
+
+    def __init__(self, e_low, e_high, zeta=None, keep=None, zeta_max: float = 0.0):
         self.e_low, self.e_high, self.zeta, self.keep = e_low, e_high, zeta, keep
+        self.zeta_max = zeta_max
 
     def as_pair(self):
         return self.e_low, self.e_high
+
+    @classmethod
+    def allocate(cls, rows: int, max_tiles: int, device, zeta_max: float = 0.0) -> "TileScores":
+        """Zeroed (rows, max_tiles) score tensors to fill with `update`."""
+        z = lambda dt: torch.zeros((rows, max_tiles), dtype=dt, device=device)
+        return cls(z(torch.float32), z(torch.float32), z(torch.float32), z(torch.bool), zeta_max=zeta_max)
+
+    def update(self, keys: torch.Tensor, first_tile: int, count: int = 1, *, block_tables=None,
+               context_lens=None, k_scale=None) -> "TileScores":
+        """Rescore tiles [first_tile, first_tile + count) of every row in
+        place.  `keys` is the (rows, S, d) K cache, or with `block_tables`
+        the paged (num_blocks, Hkv, block_size, d) cache (rows = b*Hkv + h);
+        `k_scale`: optional (rows, T) per-tile scales.  Tiles not wholly
+        inside a row's length (context_lens) score as partial tails."""
+        T = self.e_high.shape[1]
+        if not 0 <= first_tile and first_tile + count <= T:
+            raise ValueError(f"tiles [{first_tile}, {first_tile + count}) outside the cache's {T} tiles")
+        if block_tables is not None:
+            X.require_gpu(keys, block_tables)
+            nb, hkv, bs, d = keys.shape
+            kv = X.paged_layout(keys, keys, block_tables, -(-(block_tables.shape[1] * bs) // TILE_SIZE))
+        else:
+            squeeze = keys.ndim == 2
+            keys = keys.unsqueeze(0) if squeeze else keys
+            X.require_gpu(keys)
+            kv = X.rows_layout(keys, None)
+        if first_tile + count > kv.num_tiles:
+            raise ValueError(f"keys hold {kv.num_tiles} tiles, tiles up to {first_tile + count} requested")
+        if kv.num_rows > self.e_high.shape[0]:
+            raise ValueError(f"keys have {kv.num_rows} rows, the cache {self.e_high.shape[0]}")
+        if context_lens is not None:
+            kv.lengths = context_lens.to(device=keys.device, dtype=torch.int32).contiguous()
+        if isinstance(k_scale, torch.Tensor):
+            kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, kv.num_rows, kv.num_tiles,
+                                                                     keys.device)
+        X.score_tile_range(kv, first_tile, count, self.e_low, self.e_high, self.zeta,
+                           None if self.keep is None else self.keep.view(torch.uint8), self.zeta_max)
+        return self
 
 
 def fwht_tiles(keys: torch.Tensor) -> torch.Tensor:
