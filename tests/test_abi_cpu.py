@@ -62,6 +62,29 @@ def test_invalid_arguments_return_status_and_message():
         N.check("oc_decode", N.lib().oc_decode(ctypes.byref(p), None))
 
 
+def test_gate_and_norm_cache_argument_checks():
+    """The score-cache and decode-gate entry points validate on the host
+    (no launch happens for these calls)."""
+    import ctypes
+    from orthocache_gpu import _native as N
+    L = N.lib()
+    kv = N.OcKvDesc()
+    kv.k, kv.dtype, kv.head_dim, kv.num_rows, kv.num_tiles = 256, N.OC_BF16, 128, 2, 4
+    kv.k_token_stride = 128
+    assert L.oc_band_norms(ctypes.byref(kv), 0, 4, 40, 70, 256, 4, None, None) == N.OC_ERR_INVALID
+    assert b"band" in L.oc_last_error()
+    assert L.oc_band_norms(ctypes.byref(kv), 2, 3, 48, 64, 256, 4, None, None) == N.OC_ERR_INVALID
+    assert b"tile range" in L.oc_last_error()
+    assert L.oc_score_tile_range(ctypes.byref(kv), -1, 1, 0.0, 256, 256, None, None, 4, None) == N.OC_ERR_INVALID
+    assert L.oc_decode_gate(None, N.OC_F32, 64, 2, 4, 64, 256, 8, 8, 8, 1.0, 0, 8, 256, 8, None,
+                            None) == N.OC_ERR_INVALID
+    assert L.oc_decode_gate(256, N.OC_F32, 64, 2, 4, 60, 256, 8, 8, 8, 1.0, N.OC_QNORM_WALSH_HIGH, 8, 256, 8,
+                            None, None) == N.OC_ERR_INVALID
+    assert b"low_band" in L.oc_last_error()
+    assert L.oc_q_high_norms(256, N.OC_FP8_E4M3FN, 4, 64, 64, 8, 256, None) == N.OC_ERR_INVALID
+    assert L.oc_apply_tile_mask(256, N.OC_F32, 4, 100, 100, None, 4, 2, 64, 1, None) == N.OC_ERR_INVALID
+
+
 def test_reference_assertion_messages():
     """test_fp8.py:128-158 and test_paged_eviction.py:139-159 of the reference."""
     from orthocache_gpu import (fused_orthocache_attention, fused_orthocache_attention_paged,
