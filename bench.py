@@ -55,6 +55,8 @@ def parse():
                     help="host seconds spent on the cpu_baseline sample (0 = skip)")
     ap.add_argument("--read-probe", type=int, default=1, help="also time the streaming-read probe (0 = skip)")
     ap.add_argument("--spw", type=int, default=0, help="logical splits per workgroup (0 = library default)")
+    ap.add_argument("--variants", default="",
+                    help="with --only paged/fp8: comma-separated subset of cached,single_pass,dense")
     ap.add_argument("--extra-configs", type=int, default=1,
                     help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
     ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read",
@@ -301,14 +303,16 @@ class ExtraConfig:
             return self.tiles * tile + self.kept * tile + q + self.table_bytes
         return self.kept * 2 * tile + self.tiles * 4 + q + self.table_bytes
 
-    def measure(self, steps, warmup):
+    def measure(self, steps, warmup, variants=("cached", "single_pass", "dense")):
         r = {"workload": self.desc, "eviction_rate": round(1 - self.kept / self.tiles, 4), "num_splits": self.P}
-        for v in ("cached", "single_pass", "dense"):
+        for v in variants:
             us = self.time(v, steps, warmup)
             r[v + "_us"] = round(us, 2)
             r[v + "_gbps"] = round(self.bytes(v) / (us * 1e-6) / 1e9, 1)
-        r["tokens_per_s"] = round(self.rows // 8 * 1.0 / (r["cached_us"] * 1e-6), 1)
-        r["speedup_vs_dense"] = round(r["dense_us"] / r["cached_us"], 3)
+        if "cached_us" in r:
+            r["tokens_per_s"] = round(self.rows // 8 * 1.0 / (r["cached_us"] * 1e-6), 1)
+        if "cached_us" in r and "dense_us" in r:
+            r["speedup_vs_dense"] = round(r["dense_us"] / r["cached_us"], 3)
         return r
 
 
@@ -432,7 +436,8 @@ def main():
         print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))
         return
     if args.only in ("paged", "fp8"):
-        print(json.dumps(dict(only=args.only, **ExtraConfig(args.only).measure(args.steps, args.warmup))))
+        variants = tuple(args.variants.split(",")) if args.variants else ("cached", "single_pass", "dense")
+        print(json.dumps(dict(only=args.only, **ExtraConfig(args.only).measure(args.steps, args.warmup, variants))))
         return
     primary = Setup(args.batch, spw=args.spw)
     if args.only:

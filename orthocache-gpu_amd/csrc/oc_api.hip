@@ -282,24 +282,23 @@ static int device_cus() {
   return cache[dev];
 }
 
-// Splits per workgroup: enough tiles per workgroup (about 16) to amortise
-// its prologue and epilogue, while keeping at least one workgroup per CU.
 // query heads per decode workgroup for G heads per kv row
 static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G)); }
 
+// Splits per workgroup: as many as keep the workgroup count at or below the
+// CU count, so that the decode runs as one round of workgroups (one
+// 512-thread workgroup is resident per CU at the decode kernel's register
+// budget).  A second round would pay the prologue (q, scores, retained-tile
+// bitmask) and the merge tail twice and leave its own imbalance (config 4,
+// 32 rows of 2048 tiles: 512 workgroups took 121 us cached and 162 us single
+// pass, 256 take 115 and 147).
 static int choose_spw(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
   const int P = p->num_splits;
-  const int T = std::max(1, p->kv.num_tiles);
-  const int tiles_per_split = std::max(1, (T + P - 1) / P);
-  // up to 128 tiles per workgroup, but at least one workgroup per CU (one
-  // 512-thread workgroup is resident per CU at the decode kernel's register
-  // budget), so that a small batch still fills the chip
-  int spw = std::max(1, 128 / tiles_per_split);
-  const int cus = device_cus();
-  const int gchunks = (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
-  while (spw > 1 && (int64_t)p->kv.num_rows * gchunks * ((P + spw - 1) / spw) < (int64_t)cus) spw >>= 1;
-  return std::min(spw, P);
+  const int64_t cus = device_cus();
+  const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G));
+  const int64_t spw = (P * groups + cus - 1) / cus;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(spw, P));
 }
 
 static int num_groups(const oc_decode_params* p, int spw) { return (p->num_splits + spw - 1) / spw; }
