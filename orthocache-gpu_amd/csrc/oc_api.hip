@@ -223,17 +223,20 @@ __global__ __launch_bounds__(256) void dequant_fp8_kernel(const uint4* __restric
 
 // Streaming read: each thread keeps four 128-bit loads in flight per step.
 __global__ __launch_bounds__(256) void read_probe_kernel(const uint4* __restrict__ src, int64_t n16, float* sink) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u* p = reinterpret_cast<const v4u*>(src);
   uint32_t s = 0u;
   const int64_t stride = (int64_t)gridDim.x * 256 * 4;
   for (int64_t base = (int64_t)blockIdx.x * 256 * 4 + threadIdx.x; base < n16; base += stride) {
-    uint4 v[4];
+    v4u v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      // non-temporal, the cache policy of the decode's K/V loads
       const int64_t i = base + (int64_t)u * 256;
-      v[u] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+      v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : v4u{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) s ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < 4; ++u) s ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
   }
   // a data-dependent store the compiler cannot remove keeps the loads live
   if (s == 0x9E3779B9u) sink[blockIdx.x] = 1.0f;

@@ -256,21 +256,25 @@ __device__ __forceinline__ float transpose_reduce16(float (&v)[16], int lane) {
 
 // ---------------------------------------------------------------- elements
 
+// Non-temporal loads of one lane's row piece (paged VALU path; the K/V
+// tiles are streamed once, as with kStreamAux on the buffer loads).
 template <int LB>
 __device__ __forceinline__ void load_lane_row(const char* p, uint32_t* w) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  typedef uint32_t v2u __attribute__((ext_vector_type(2)));
   if constexpr (LB == 32) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint4 b = *reinterpret_cast<const uint4*>(p + 16);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    const v4u a = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    const v4u b = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p + 16));
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
   } else if constexpr (LB == 16) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    const v4u a = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
   } else if constexpr (LB == 8) {
-    const uint2 a = *reinterpret_cast<const uint2*>(p);
-    w[0] = a.x; w[1] = a.y;
+    const v2u a = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+    w[0] = a[0]; w[1] = a[1];
   } else {
-    w[0] = *reinterpret_cast<const uint32_t*>(p);
+    w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
   }
 }
 
@@ -356,21 +360,27 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) {
   return ri;
 }
 
+// Cache policy of the K/V tile loads: non-temporal (the buffer instructions'
+// nt bit).  K and V are streamed once per decode step; on MI355X nt loads
+// of the decode's 16 KiB K/V chunk pattern reach 6.86 TB/s against 6.0 for
+// the default policy (7.15 against 6.33 for a plain stream).
+constexpr int kStreamAux = 2;
+
 template <int LB>
 __device__ __forceinline__ void buffer_load_lane_row(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t* w) {
   if constexpr (LB == 32) {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-    const auto y = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, 0);
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kStreamAux);
+    const auto y = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, soff, kStreamAux);
     w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
     w[4] = y[0]; w[5] = y[1]; w[6] = y[2]; w[7] = y[3];
   } else if constexpr (LB == 16) {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kStreamAux);
     w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
   } else if constexpr (LB == 8) {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kStreamAux);
     w[0] = x[0]; w[1] = x[1];
   } else {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kStreamAux);
   }
 }
 
@@ -862,7 +872,7 @@ __device__ __forceinline__ void load_k_mfma(const DecodeArgs& a, const RowInfo& 
     }
 #pragma unroll
     for (int dc = 0; dc < (F8 ? D / 64 : D / 32); ++dc) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (F8 ? 16 : 64) * dc, 0, 0);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (F8 ? 16 : 64) * dc, 0, kStreamAux);
       kb[tb][dc][0] = v[0];
       kb[tb][dc][1] = v[1];
       kb[tb][dc][2] = v[2];
@@ -902,7 +912,7 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
       for (int j = 0; j < 16 / TPI; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (__attribute__((address_space(3))) void*)(sv + (tb * (16 / TPI) + j) * 512), 16,
-            voff + j * TPI * (int)ts, 0, 0, 0);
+            voff + j * TPI * (int)ts, 0, 0, kStreamAux);
     }
   } else {
     const char* base = a.v + (int64_t)row * a.v_row_stride + tok0 * ts;
@@ -911,7 +921,7 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
 #pragma unroll
     for (int i = 0; i < 64 / TPI; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 512),
-                                               16, voff + i * TPI * (int)ts, 0, 0, 0);
+                                               16, voff + i * TPI * (int)ts, 0, 0, kStreamAux);
   }
 }
 
