@@ -16,7 +16,9 @@ single-pass mode (scores from K inside the decode) and this build's own
 dense decode are timed on the same buffers.
 
 Timing: W untimed warm-up steps, then K steps back to back between two HIP
-events on the launch stream, with synchronisation on both sides.  The KV
+events on the launch stream, with synchronisation on both sides (the
+reported mean); a second pass with an event pair around every step gives
+the p5 / p50 / p95 of single steps.  The KV
 buffers rotate over several sets whose total exceeds the 256 MB Infinity
 Cache, so every step streams from HBM.  A step is one oc_decode call, which
 is one launch of the decode kernel (the split merge runs inside it), so the
@@ -160,6 +162,21 @@ class Setup:
         end.record()
         torch.cuda.synchronize()
         return start.elapsed_time(end) * 1e3 / steps  # us per step
+
+    def step_percentiles(self, variant, steps):
+        """p5 / p50 / p95 of single-step durations: a HIP event pair around
+        every step (back to back, same stream), µs."""
+        torch = self.torch
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        for i, (e0, e1) in enumerate(ev):
+            e0.record()
+            self.run(variant, i)
+            e1.record()
+        torch.cuda.synchronize()
+        us = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
+        pick = lambda q: us[min(len(us) - 1, int(round(q * (len(us) - 1))))]
+        return {"p5": round(pick(0.05), 2), "p50": round(pick(0.5), 2), "p95": round(pick(0.95), 2)}
 
     def check(self):
         """Eviction rate of the timed configuration (mask of set 0)."""
@@ -323,6 +340,7 @@ def measure(setup, steps, warmup):
     for v in ("cached", "single_pass", "dense"):
         r[v + "_us"] = setup.time(v, steps, warmup)
     r["partials_only_us"] = setup.time("cached_partials", steps, warmup)
+    r["cached_step_us_percentiles"] = setup.step_percentiles("cached", steps)
     r["cached_bytes"] = setup.bytes("cached", evict)
     r["dense_bytes"] = setup.bytes("dense", evict)
     r["single_pass_bytes"] = setup.bytes("single_pass", evict)
@@ -486,6 +504,7 @@ def main():
                      "frac": round(ach / HBM_PEAK_GBPS, 4),
                      "traffic": None if traffic is None else traffic.get("decode_cached_b%d" % args.batch)},
         "cpu_baseline": cpu,
+        "step_us_percentiles": r1["cached_step_us_percentiles"],
         "partials_only_us": r1["partials_only_us"],
         "partials_only_gbps": round(r1["partials_only_gbps"], 1),
         "algorithmic_bytes_per_step": r1["cached_bytes"],
@@ -502,6 +521,7 @@ def main():
     if extra:
         line["batch%d" % extra["batch"]] = {
             "us_per_step": extra["cached_us"], "tokens_per_s": extra["batch"] / (extra["cached_us"] * 1e-6),
+            "step_us_percentiles": extra["cached_step_us_percentiles"],
             "step_gbps": round(extra["step_gbps"], 1), "roofline_frac": round(extra["step_gbps"] / HBM_PEAK_GBPS, 4),
             "partials_only_us": extra["partials_only_us"], "partials_only_gbps": round(extra["partials_only_gbps"], 1),
             "single_pass_us": extra["single_pass_us"], "dense_us": extra["dense_us"],
