@@ -34,6 +34,9 @@
  *                      (decode_gate.py:302-374)
  *   oc_score_tile_range: no reference counterpart (the append path of the
  *                      score cache: rescore the tiles a decode step completed)
+ *   oc_tile_mask_from_blocks + oc_decode(OC_GATE_MASK) <- the kernels of
+ *                      triton_block_sparse_attention (sparse_attention.py:208-279)
+ *                      and triton_indirect_attention (indirect_attention.py:200-286)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -64,6 +67,7 @@ extern "C" {
 #define OC_GATE_NONE 0  /* dense decode: every tile retained                    */
 #define OC_GATE_ZETA 1  /* retain iff !(e_high/(e_low+1e-6) > threshold)        */
 #define OC_GATE_CS 2    /* retain iff !(max_g ||q_g|| * sqrt(e_high) <= threshold) */
+#define OC_GATE_MASK 3  /* retain iff tile_mask[row, tile] != 0 (cached mode)      */
 
 /* where tile scores come from */
 #define OC_MODE_SINGLE_PASS 0 /* scores computed from K inside the decode kernel  */
@@ -203,6 +207,19 @@ int oc_q_high_norms(const void* q, int32_t q_dtype, int64_t rows, int32_t head_d
  * rows `logits_row_stride` elements apart, tokens contiguous.  Replaces
  * apply_decode_mask and apply_decode_mask_vectorized (decode_gate.py:302-374).
  */
+/*
+ * oc_tile_mask_from_blocks -- the 64-token tile mask (count = num_blocks *
+ * tiles_per_block bytes) of a block mask or an index list: with block_mask,
+ * tile_mask[t] = block_mask[t / tiles_per_block]; with indices (count
+ * int32), tile_mask = 1 exactly on the tiles of the listed blocks, and an
+ * index outside [0, num_blocks) is skipped and sets *error_flag (if given).
+ * For the block-sparse and indirect attention wrappers
+ * (sparse_attention.py:208-279, indirect_attention.py:200-286), which run
+ * oc_decode with OC_GATE_MASK on the result.
+ */
+int oc_tile_mask_from_blocks(const uint8_t* block_mask, const int32_t* indices, int32_t count, int32_t num_blocks,
+                             int32_t tiles_per_block, uint8_t* tile_mask, int32_t* error_flag, void* stream);
+
 int oc_apply_tile_mask(void* logits, int32_t dtype, int32_t num_q_heads, int64_t seq_len,
                        int64_t logits_row_stride, const uint8_t* mask, int64_t mask_row_stride, int32_t G,
                        int32_t tile_size, int32_t num_tiles, void* stream);
@@ -236,6 +253,8 @@ typedef struct oc_decode_params {
                                Pg = oc_decode_num_groups(p) */
   void* workspace;          /* device memory, oc_decode_workspace_size() bytes */
   size_t workspace_bytes;
+  const uint8_t* tile_mask; /* OC_GATE_MASK: (num_rows, num_tiles), 1 = attend */
+  int64_t tile_mask_row_stride;
 } oc_decode_params;
 
 /* number of partial states per (row, query head): ceil(P / spw), with spw

@@ -24,6 +24,8 @@ paths with the same per-head, per-tile loop structure:
                                  (decode_gate.py:108-245); tight=True:
                                  _pytorch_decode_gate (decode_gate.py:248-295)
 * ``apply_decode_mask``       <- apply_decode_mask(_vectorized) (decode_gate.py:302-374)
+* ``block_sparse_attention``  <- _pytorch_block_sparse_attention (sparse_attention.py:144-203)
+* ``indirect_attention``      <- _pytorch_indirect_attention (indirect_attention.py:136-197)
 
 (all paths relative to ``src/orthocache_gpu/triton_kernels/`` or
 ``src/orthocache_gpu/`` of the reference tree).
@@ -54,6 +56,8 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   block-constant vectors (float64), and its two special cases.
 * ``decode_gate`` / ``apply_decode_mask``: explicit per-(head, tile) loops,
   special thresholds, and the max-over-G rule.
+* ``block_sparse_attention`` / ``indirect_attention``: float64 softmax over
+  the retained tokens, all blocks == dense, no block == zeros.
 """
 
 from __future__ import annotations
@@ -637,3 +641,42 @@ def apply_decode_mask(logits: np.ndarray, mask: np.ndarray, G: int, tile_size: i
             if mask[kv_h, t]:
                 out[kv_h * G:(kv_h + 1) * G, :, t * tile_size:min((t + 1) * tile_size, s_len)] = -np.inf
     return out
+
+
+# ---------------------------------------------------------------------------
+# Mask-given single-query attention
+# ---------------------------------------------------------------------------
+
+def _block_online_softmax(q, keys, values, blocks, block_size):
+    """The per-block online softmax of the reference's CPU paths, float32."""
+    q = _as_f32(q).reshape(1, -1)
+    keys, values = _as_f32(keys), _as_f32(values)
+    d = q.shape[1]
+    scale = F32(1.0 / (d ** 0.5))
+    m = _M0
+    l = F32(0.0)
+    acc = np.zeros((1, d), dtype=F32)
+    for b in blocks:
+        k = keys[b * block_size:(b + 1) * block_size]
+        v = values[b * block_size:(b + 1) * block_size]
+        logits = ((q @ k.T) * scale).astype(F32)
+        new_m = F32(max(m, logits.max()))
+        p = np.exp(logits - new_m).astype(F32)
+        a = F32(np.exp(F32(m - new_m)))
+        l = F32(l * a + p.sum(dtype=F32))
+        acc = (acc * a + p @ v).astype(F32)
+        m = new_m
+    return (acc / max(l, _L_MIN)).astype(F32)
+
+
+def block_sparse_attention(q, keys, values, block_mask, block_size: int = 512) -> np.ndarray:
+    """Blocks b with block_mask[b], in order (sparse_attention.py:144-203); (1, d)."""
+    n_blocks = keys.shape[0] // block_size
+    return _block_online_softmax(q, keys, values, [b for b in range(n_blocks) if block_mask[b]], block_size)
+
+
+def indirect_attention(q, keys, values, active_indices, num_active: int, block_size: int = 512) -> np.ndarray:
+    """Blocks active_indices[:num_active], in list order (indirect_attention.py:136-197); (1, d)."""
+    if num_active == 0:
+        return np.zeros((1, np.asarray(q).shape[-1]), dtype=F32)
+    return _block_online_softmax(q, keys, values, [int(b) for b in active_indices[:num_active]], block_size)

@@ -378,9 +378,11 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
   if (!p->q) return fail(OC_ERR_INVALID, "q pointer is NULL");
   if (!p->out && !partials_given) return fail(OC_ERR_INVALID, "out is NULL and no partial buffers are given");
-  if (p->gate < OC_GATE_NONE || p->gate > OC_GATE_CS) return fail(OC_ERR_INVALID, "gate %d", p->gate);
+  if (p->gate < OC_GATE_NONE || p->gate > OC_GATE_MASK) return fail(OC_ERR_INVALID, "gate %d", p->gate);
+  if (p->gate == OC_GATE_MASK && (p->mode != OC_MODE_CACHED || !p->tile_mask))
+    return fail(OC_ERR_INVALID, "the mask gate needs cached mode and a tile_mask");
   if (p->mode != OC_MODE_SINGLE_PASS && p->mode != OC_MODE_CACHED) return fail(OC_ERR_INVALID, "mode %d", p->mode);
-  if (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE) {
+  if (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && p->gate != OC_GATE_MASK) {
     if (!p->score_e_high || (p->gate == OC_GATE_ZETA && !p->score_e_low))
       return fail(OC_ERR_INVALID, "cached mode needs score_e_high (and score_e_low for the zeta gate)");
   }
@@ -394,6 +396,8 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   a.thr = p->threshold;
   a.sc_el = p->score_e_low;
   a.sc_eh = p->score_e_high;
+  a.tmask = p->tile_mask;
+  a.tmask_stride = p->tile_mask_row_stride;
   a.sc_stride = p->score_row_stride;
   a.P = p->num_splits;
   if (p->splits_per_group < 0) return fail(OC_ERR_INVALID, "splits_per_group %d", p->splits_per_group);

@@ -135,6 +135,28 @@ __global__ __launch_bounds__(kGateThreads) void apply_mask_kernel(char* logits, 
   else reinterpret_cast<uint16_t*>(logits)[i] = 0xFC00u;
 }
 
+// tile mask of a block mask (block_mask given) or zeros (indices given)
+__global__ __launch_bounds__(kGateThreads) void block_tile_mask_kernel(const uint8_t* block_mask, int64_t n_tiles,
+                                                                       int tpb, uint8_t* tile_mask) {
+  const int64_t t = (int64_t)blockIdx.x * kGateThreads + threadIdx.x;
+  if (t >= n_tiles) return;
+  tile_mask[t] = block_mask ? (block_mask[t / tpb] ? 1 : 0) : 0;
+}
+
+// set the tiles of every listed block; indices outside the range raise the flag
+__global__ __launch_bounds__(kGateThreads) void index_tile_mask_kernel(const int32_t* indices, int count,
+                                                                       int num_blocks, int tpb, uint8_t* tile_mask,
+                                                                       int32_t* error_flag) {
+  const int i = blockIdx.x * kGateThreads + threadIdx.x;
+  if (i >= count) return;
+  const int b = indices[i];
+  if (b < 0 || b >= num_blocks) {
+    if (error_flag) atomicOr(error_flag, 1);
+    return;
+  }
+  for (int k = 0; k < tpb; ++k) tile_mask[(int64_t)b * tpb + k] = 1;
+}
+
 bool float_dtype(int dt) { return dt == OC_F32 || dt == OC_F16 || dt == OC_BF16; }
 
 }  // namespace
@@ -196,4 +218,24 @@ extern "C" int oc_apply_tile_mask(void* logits, int32_t dtype, int32_t num_q_hea
                      tile_size, num_tiles);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "mask launch");
+}
+
+extern "C" int oc_tile_mask_from_blocks(const uint8_t* block_mask, const int32_t* indices, int32_t count,
+                                        int32_t num_blocks, int32_t tiles_per_block, uint8_t* tile_mask,
+                                        int32_t* error_flag, void* stream) {
+  if (!tile_mask || (!block_mask && !indices) || (block_mask && indices))
+    return fail(OC_ERR_INVALID, "give exactly one of block_mask and indices, and tile_mask");
+  if (num_blocks < 0 || tiles_per_block < 1 || count < 0) return fail(OC_ERR_INVALID, "bad sizes");
+  const int64_t n_tiles = (int64_t)num_blocks * tiles_per_block;
+  if (n_tiles == 0) return OC_OK;
+  const int64_t blocks = (n_tiles + kGateThreads - 1) / kGateThreads;
+  if (blocks > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many tiles");
+  hipLaunchKernelGGL(block_tile_mask_kernel, dim3((unsigned)blocks), dim3(kGateThreads), 0, (hipStream_t)stream,
+                     block_mask, n_tiles, tiles_per_block, tile_mask);
+  if (indices && count > 0)
+    hipLaunchKernelGGL(index_tile_mask_kernel, dim3((unsigned)((count + kGateThreads - 1) / kGateThreads)),
+                       dim3(kGateThreads), 0, (hipStream_t)stream, indices, count, num_blocks, tiles_per_block,
+                       tile_mask, error_flag);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "tile-mask launch");
 }

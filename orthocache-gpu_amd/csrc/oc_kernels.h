@@ -61,6 +61,8 @@ struct DecodeArgs {
   double thr;
   const float* sc_el;
   const float* sc_eh;
+  const uint8_t* tmask;  // OC_GATE_MASK: given (rows, T) tile mask
+  int64_t tmask_stride;
   int64_t sc_stride;
   int32_t P;    // logical splits: split s owns tiles {s + kP}
   int32_t spw;  // logical splits per workgroup (group g owns splits [g*spw, g*spw + spw))
@@ -570,6 +572,7 @@ __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D
 //   monotone in q for k >= 0, so max_g fl(q_g*k) = fl(qmax*k)).
 __device__ __forceinline__ bool gate_keep(int gate, double thr, float e_low, float e_high,
                                           float qmax, bool qnan) {
+  if (gate == OC_GATE_MASK) return e_high != 0.f;  // the given mask, read as 0 / 1
   if (gate == OC_GATE_ZETA) {
     const float z = e_high / (e_low + 1e-6f);
     return !((double)z > thr);
@@ -1159,8 +1162,21 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
 // energies; a partial tail tile is always retained.
 __device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& ri, int t, float el, float eh,
                                             float qmax, bool qnan) {
-  if ((t + 1) * 64 > ri.n_tok) return true;
+  if ((t + 1) * 64 > ri.n_tok && a.gate != OC_GATE_MASK) return true;
   return gate_keep(a.gate, a.thr, el, eh, qmax, qnan);
+}
+
+// The cached scores of tile t of a row (cached mode): (e_low, e_high) from
+// the score cache, or for OC_GATE_MASK the given mask byte as e_high = 0 / 1.
+__device__ __forceinline__ void cached_scores(const DecodeArgs& a, int row, int t, float& el, float& eh) {
+  if (a.gate == OC_GATE_MASK) {
+    eh = a.tmask[(int64_t)row * a.tmask_stride + t] ? 1.f : 0.f;
+    el = 0.f;
+    return;
+  }
+  const int64_t o = (int64_t)row * a.sc_stride + t;
+  eh = a.sc_eh[o];
+  el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
 }
 
 // A workgroup's tile list: index x < n -> tile s + (x / w) * P + x % w
@@ -1365,11 +1381,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
         const int tx = s + (kx / w) * tl.P + kx % w;
         const bool in = kx < n_split && tx < ri.n_tiles;
         float el = pre_el, eh = pre_eh;
-        if (c0 > 0 && in) {
-          const int64_t o = (int64_t)row * a.sc_stride + tx;
-          eh = a.sc_eh[o];
-          el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
-        }
+        if (c0 > 0 && in) cached_scores(a, row, tx, el, eh);
         const bool keep = in && cached_keep(a, ri, tx, el, eh, qmax, qnan);
         if (a.keep_out && in && wave == 0 && blockIdx.z == 0)
           a.keep_out[(int64_t)row * a.keep_stride + tx] = keep ? 1 : 0;
@@ -1729,11 +1741,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
         t = tl.s + (lane / tl.w) * tl.P + lane % tl.w;
         in = k == 0 && lane < tl.n && t < ri.n_tiles;
       }
-      if (in) {
-        const int64_t o = (int64_t)row * a.sc_stride + t;
-        pre_eh[k] = a.sc_eh[o];
-        pre_el[k] = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
-      }
+      if (in) cached_scores(a, row, t, pre_el[k], pre_eh[k]);
     }
   }
 
@@ -1875,11 +1883,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       const int t = c + threadIdx.x;
       const bool in = t < ri.n_tiles;
       float el = 0.f, eh = 0.f;
-      if (in) {
-        const int64_t o = (int64_t)row * a.sc_stride + t;
-        eh = a.sc_eh[o];
-        el = a.gate == OC_GATE_ZETA ? a.sc_el[o] : 0.f;
-      }
+      if (in) cached_scores(a, row, t, el, eh);
       const bool keep = in && cached_keep(a, ri, t, el, eh, qmax, qnan);
       if (a.keep_out && in && gidx == 0 && blockIdx.z == 0)
         a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;

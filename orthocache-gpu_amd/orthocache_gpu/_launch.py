@@ -493,6 +493,58 @@ def apply_tile_mask(logits: torch.Tensor, mask: torch.Tensor, G: int, tile_size:
             ctypes.c_void_p(stream)))
 
 
+def tile_mask_from_blocks(num_blocks: int, tiles_per_block: int, device, *, block_mask=None,
+                          indices=None) -> torch.Tensor:
+    """oc_tile_mask_from_blocks: (1, num_blocks * tiles_per_block) uint8 tile
+    mask of a bool block mask or of an int32 block-index list (indices outside
+    [0, num_blocks) raise ValueError after a device sync)."""
+    tile_mask = torch.empty((1, max(1, num_blocks * tiles_per_block)), dtype=torch.uint8, device=device)
+    err = None
+    bm = ix = None
+    count = 0
+    if block_mask is not None:
+        bm = block_mask.to(device=device, dtype=torch.uint8).contiguous()
+    else:
+        ix = indices.to(device=device, dtype=torch.int32).contiguous()
+        count = ix.numel()
+        err = torch.zeros(1, dtype=torch.int32, device=device)
+    stream = current_stream(device)
+    with torch.cuda.device(device):
+        N.check("oc_tile_mask_from_blocks", N.lib().oc_tile_mask_from_blocks(
+            _ptr(bm), _ptr(ix), count, num_blocks, tiles_per_block, tile_mask.data_ptr(), _ptr(err),
+            ctypes.c_void_p(stream)))
+    if err is not None and int(err.item()):
+        raise ValueError(f"active_indices holds a block index outside [0, {num_blocks})")
+    return tile_mask
+
+
+def masked_decode(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, tile_mask: torch.Tensor) -> torch.Tensor:
+    """One query row over (S, d) keys/values attending exactly the tiles whose
+    tile_mask byte is set (oc_decode with OC_GATE_MASK); returns (1, d) in
+    q's dtype."""
+    kv = rows_layout(keys.unsqueeze(0), values.unsqueeze(0))
+    p = N.OcDecodeParams()
+    device = require_gpu(q, keys, values)
+    qq = q.contiguous()
+    out = torch.empty((1, kv.head_dim), dtype=q.dtype, device=device)
+    p.kv = kv.struct()
+    p.q, p.q_dtype, p.G, p.q_row_stride = qq.data_ptr(), dtype_code(qq.dtype, "q", allow_fp8=False), 1, qq.stride(0)
+    p.gate, p.mode = N.OC_GATE_MASK, N.OC_MODE_CACHED
+    p.tile_mask, p.tile_mask_row_stride = tile_mask.data_ptr(), tile_mask.stride(0)
+    p.num_splits = auto_num_splits(kv.num_tiles, device)
+    p.out_dtype = dtype_code(out.dtype, "out", allow_fp8=False)
+    p.out, p.out_row_stride = out.data_ptr(), out.stride(0)
+    stream = current_stream(device)
+    lib = N.lib()
+    need = lib.oc_decode_workspace_size(ctypes.byref(p))
+    if need:
+        ws = workspace(device, stream, need)
+        p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    with torch.cuda.device(device):
+        N.check("oc_decode", lib.oc_decode(ctypes.byref(p), ctypes.c_void_p(stream)))
+    return out
+
+
 def counts_metadata(keep: torch.Tensor, tiles_total: int) -> dict:
     retained = int(keep.sum().item())
     evicted = tiles_total - retained

@@ -24,7 +24,7 @@ OC_ERR_WORKSPACE = 4
 # element types
 OC_F32, OC_F16, OC_BF16, OC_FP8_E4M3FN = 0, 1, 2, 3
 # gates / modes / scale modes
-OC_GATE_NONE, OC_GATE_ZETA, OC_GATE_CS = 0, 1, 2
+OC_GATE_NONE, OC_GATE_ZETA, OC_GATE_CS, OC_GATE_MASK = 0, 1, 2, 3
 OC_MODE_SINGLE_PASS, OC_MODE_CACHED = 0, 1
 OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE = 0, 1, 3
 OC_VSCALE_NONE, OC_VSCALE_TILE = 0, 1
@@ -67,6 +67,7 @@ class OcDecodeParams(ctypes.Structure):
         ("split_counts", _p),
         ("partial_m", _p), ("partial_l", _p), ("partial_acc", _p),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("tile_mask", _p), ("tile_mask_row_stride", _i64),
     ]
 
 
@@ -81,6 +82,7 @@ SIGNATURES = {
                               _p, _i64, _p, _p]),
     "oc_q_high_norms": (_i32, [_p, _i32, _i64, _i32, _i64, _i32, _p, _p]),
     "oc_apply_tile_mask": (_i32, [_p, _i32, _i32, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p]),
+    "oc_tile_mask_from_blocks": (_i32, [_p, _p, _i32, _i32, _i32, _p, _p, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),

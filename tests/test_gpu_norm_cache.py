@@ -1,6 +1,8 @@
-"""GPU parity of the score-cache maintenance and the O(1) decode gate:
-oc_band_norms (SpectralNormCache), oc_score_tile_range (TileScores.update),
-oc_decode_gate, oc_q_high_norms and oc_apply_tile_mask against the oracle.
+"""GPU parity of the score-cache maintenance, the O(1) decode gate and the
+mask-given attention: oc_band_norms (SpectralNormCache), oc_score_tile_range
+(TileScores.update), oc_decode_gate, oc_q_high_norms, oc_apply_tile_mask and
+oc_decode with OC_GATE_MASK (block-sparse / indirect attention) against the
+oracle.
 
 Bars: band norms and q norms within 4 float32 ulp of the oracle (the
 summation order differs); masks bit-exact on data whose gate products are
@@ -146,3 +148,41 @@ def test_apply_decode_mask_exact(dtype):
     for fn in (apply_decode_mask, apply_decode_mask_vectorized):
         got = fn(logits.clone().to(DEV), mask.to(DEV), G)
         assert np.array_equal(np32(got), ref)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("block_size", [512, 128, 64])
+def test_block_sparse_attention_vs_oracle(dtype, block_size):
+    from orthocache_gpu.triton_kernels import triton_block_sparse_attention
+    g = torch.Generator().manual_seed(block_size)
+    n_blocks, d = 24, 128
+    q = torch.randn((1, d), generator=g).to(TORCH_DT[dtype])
+    k = torch.randn((n_blocks * block_size, d), generator=g).to(TORCH_DT[dtype])
+    v = torch.randn((n_blocks * block_size, d), generator=g).to(TORCH_DT[dtype])
+    for mask in (torch.rand(n_blocks, generator=g) < 0.4, torch.ones(n_blocks, dtype=torch.bool),
+                 torch.zeros(n_blocks, dtype=torch.bool)):
+        out = triton_block_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV), block_size)
+        assert out.dtype == q.dtype and out.shape == (1, d)
+        ref = O.round_to(O.block_sparse_attention(np32(q), np32(k), np32(v), mask.numpy(), block_size), dtype)
+        tol = 1e-5 if dtype == "f32" else 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == "bf16" else 2.0 ** -11)
+        assert (np.abs(np32(out) - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_indirect_attention_vs_oracle(dtype):
+    from orthocache_gpu.triton_kernels import triton_indirect_attention
+    g = torch.Generator().manual_seed(7)
+    n_blocks, d, bs = 20, 128, 512
+    q = torch.randn((1, d), generator=g).to(TORCH_DT[dtype])
+    k = torch.randn((n_blocks * bs + 100, d), generator=g).to(TORCH_DT[dtype])  # a partial block at the end
+    v = torch.randn((n_blocks * bs + 100, d), generator=g).to(TORCH_DT[dtype])
+    idx = torch.randperm(n_blocks, generator=g)[:9].to(torch.int32)
+    out = triton_indirect_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), 7, bs)
+    ref = O.round_to(O.indirect_attention(np32(q), np32(k), np32(v), idx.numpy(), 7, bs), dtype)
+    tol = 1e-5 if dtype == "f32" else 2e-3 + np.abs(ref) * 2.0 ** -8
+    assert (np.abs(np32(out) - ref) <= tol).all()
+    zero = triton_indirect_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), 0, bs)
+    assert not zero.any()
+    with pytest.raises(ValueError, match="block index"):
+        triton_indirect_attention(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor([3, 99], dtype=torch.int32,
+                                                                                 device=DEV), 2, bs)

@@ -113,3 +113,25 @@ def test_apply_decode_mask_rules():
             assert (out[h, 0, s] == -np.inf) == evicted
             if not evicted:
                 assert out[h, 0, s] == logits[h, 0, s]
+
+
+@pytest.mark.parametrize("block_size", [64, 512])
+def test_block_sparse_and_indirect_oracle(block_size):
+    rng = np.random.default_rng(block_size)
+    n_blocks, d = 6, 64
+    q = rng.standard_normal((1, d)).astype(np.float32)
+    k = rng.standard_normal((n_blocks * block_size, d)).astype(np.float32)
+    v = rng.standard_normal((n_blocks * block_size, d)).astype(np.float32)
+    mask = np.array([True, False, True, True, False, True])
+    got = O.block_sparse_attention(q, k, v, mask, block_size)
+    keep = np.repeat(mask, block_size)
+    lg = (q.astype(np.float64) @ k[keep].T.astype(np.float64)) / np.sqrt(d)
+    p = np.exp(lg - lg.max())
+    want = (p / p.sum()) @ v[keep].astype(np.float64)
+    np.testing.assert_allclose(got, want, atol=2e-6)
+    np.testing.assert_allclose(O.block_sparse_attention(q, k, v, np.ones(n_blocks, bool), block_size),
+                               O.dense_decode(q, k[None], v[None]), atol=2e-6)
+    assert not O.block_sparse_attention(q, k, v, np.zeros(n_blocks, bool), block_size).any()
+    idx = np.array([5, 0, 2, 3, 4], dtype=np.int32)
+    np.testing.assert_allclose(O.indirect_attention(q, k, v, idx, 4, block_size), got, atol=2e-6)
+    assert not O.indirect_attention(q, k, v, idx, 0, block_size).any()
