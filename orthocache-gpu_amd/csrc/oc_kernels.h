@@ -1326,7 +1326,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   auto next_tile = [&]() -> int {
     int t = -1;
     if (a.bal) {
-      rb += kDW;
+      if (rb < r0) {
+        rb += kDW;  // the wave's first rank: r0 + wave
+      } else {
+        // later ranks from the workgroup's LDS counter, so that waves whose
+        // tiles arrived sooner take more of them
+        int x = 0;
+        if (lane == 0) x = atomicAdd(&sh_cnt[kDW], 1);
+        rb = r0 + __builtin_amdgcn_readfirstlane(x);
+      }
       if (rb < r1) {
         // lane group holding rank rb: the first lane whose inclusive prefix
         // exceeds rb; then the word inside its four
