@@ -1356,10 +1356,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
       }
     } else if (!cached) {
       for (;;) {
-        if (MQK && a.gate != OC_GATE_NONE && kk >= 0) {
-          // matrix-core single pass: after the wave's first tile (position
-          // `wave`), list positions are handed out in LDS, so a wave that
-          // drew evicted (cheaper) tiles takes more of them
+        if (MQK && kk >= 0) {
+          // matrix-core single pass and dense: after the wave's first tile
+          // (position `wave`), list positions are handed out in LDS, so a
+          // wave whose tiles arrived sooner (or were evicted, cheaper) takes
+          // more of them
           int x = 0;
           if (lane == 0) x = atomicAdd(&sh_cnt[kDW], 1);
           kk = __builtin_amdgcn_readfirstlane(x);
