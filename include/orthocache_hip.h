@@ -37,6 +37,18 @@
  *   oc_tile_mask_from_blocks + oc_decode(OC_GATE_MASK) <- the kernels of
  *                      triton_block_sparse_attention (sparse_attention.py:208-279)
  *                      and triton_indirect_attention (indirect_attention.py:200-286)
+ * Model-side attention hook (eval/perplexity_eval.py of the reference tree):
+ *   oc_prefill_attention <- the prefill branch of
+ *                      OrthoCache_GQA_Attention.orthocache_attention (logits,
+ *                      causal mask, tile eviction, softmax, entropy, P @ V;
+ *                      perplexity_eval.py:399-545) and _dense_attention
+ *                      (perplexity_eval.py:675-689)
+ *   oc_row_norms + oc_kth_smallest <- torch.norm(q_group, dim=-1) and its
+ *                      .median(dim=1) (perplexity_eval.py:454-456);
+ *                      _compute_q_high_norm (perplexity_eval.py:547-573)
+ *   oc_group_gate   <- the per-(kv head, tile) Cauchy-Schwarz compares of the
+ *                      prefill and decode branches (perplexity_eval.py:476-491,
+ *                      :639-657)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -223,6 +235,87 @@ int oc_tile_mask_from_blocks(const uint8_t* block_mask, const int32_t* indices, 
 int oc_apply_tile_mask(void* logits, int32_t dtype, int32_t num_q_heads, int64_t seq_len,
                        int64_t logits_row_stride, const uint8_t* mask, int64_t mask_row_stride, int32_t G,
                        int32_t tile_size, int32_t num_tiles, void* stream);
+
+/* group reductions of oc_group_gate */
+#define OC_GROUP_MAX 0     /* largest of the G per-head norms (NaN propagates) */
+#define OC_GROUP_MEDIAN 1  /* element of rank G/2 (0-based) of their ascending order */
+
+/*
+ * oc_row_norms -- out[(i0 * n1 + i1) * n2 + i2] = ||x[i0, i1, i2, :]||_2 over
+ * head_dim elements (dtype F32/F16/BF16, element strides stride0..2, the
+ * last dimension contiguous), accumulated in float32; with low_band > 0 the
+ * Walsh-subspace high part sqrt(max(||x||^2 - sum_i S_i^2 / bs, 0)) as in
+ * oc_q_high_norms.  Replaces torch.norm(q_group, p=2, dim=-1) of the hook's
+ * prefill gate (perplexity_eval.py:454) and _compute_q_high_norm
+ * (perplexity_eval.py:547-573).
+ */
+int oc_row_norms(const void* x, int32_t dtype, int64_t n0, int64_t n1, int64_t n2, int64_t stride0,
+                 int64_t stride1, int64_t stride2, int32_t head_dim, int32_t low_band, float* out, void* stream);
+
+/*
+ * oc_kth_smallest -- out[r] = the k-th smallest (0-based) of the n floats
+ * x[r * row_stride .. + n), for non-negative inputs (norms; NaN sorts
+ * last).  Exact (radix select over the bit patterns).  k = (n - 1) / 2 is
+ * torch.median's lower median (perplexity_eval.py:456).
+ */
+int oc_kth_smallest(const float* x, int64_t rows, int64_t n, int64_t row_stride, int64_t k, float* out,
+                    void* stream);
+
+/*
+ * oc_group_gate -- for every (batch b, kv head h): qn = reduce over the G
+ * per-head norms q_norms[(b * num_kv_heads + h) * G + g] (OC_GROUP_MAX or
+ * OC_GROUP_MEDIAN), group_norms[b * num_kv_heads + h] = qn (if given), and
+ * for t < mask_cols
+ *   evict(t) = t < num_tiles && qn * k_norms[b * k_norms_stride_b + h * k_norms_stride_h + t]
+ *              <= (float)tau_norm
+ *   mask[b * mask_stride_b + h * mask_stride_h + t] = keep_polarity ? !evict(t) : evict(t)
+ * (keep_polarity 0: 1 = evict, the prefill kernel's convention; 1: 1 =
+ * attend, oc_decode's OC_GATE_MASK convention).  tau_norm = tau * 64 *
+ * head_dim: the hook compares qn * ||K_high|| / (64 * head_dim) with tau
+ * (perplexity_eval.py:476-491 with the max of the per-head medians,
+ * :639-657 with the median of the Walsh-subspace norms).
+ */
+int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv_heads, int32_t G, int32_t reduce,
+                  const float* k_norms, int64_t k_norms_stride_b, int64_t k_norms_stride_h, int32_t num_tiles,
+                  int32_t mask_cols, double tau_norm, int32_t keep_polarity, uint8_t* mask, int64_t mask_stride_b,
+                  int64_t mask_stride_h, float* group_norms, void* stream);
+
+/*
+ * oc_prefill_attention -- causal GQA attention of q_len queries over kv_len
+ * keys (query s sees keys j <= s + kv_len - q_len), skipping the 64-token
+ * tiles t < kv_len / 64 whose tile_mask byte is set (1 = evict, for every
+ * query of the kv head's G query heads):
+ *   out[b, h, s] = sum_j softmax_j(q[b, h, s] . k[b, h / G, j] * scale) v[b, h / G, j]
+ * over the visible, retained j; a query with none gets zeros (the hook's
+ * nan_to_num).  float32 accumulation; out in dtype (round to nearest even).
+ * With entropy given, entropy[(b * num_q_heads + h) * q_len + s] =
+ * -sum_j p_j ln max(p_j, 1e-10) over all kv_len keys (evicted and masked
+ * keys count as p = 0), the attention entropy the hook's EntropyGovernor
+ * reads (perplexity_eval.py:522-531).  dtype F32/F16/BF16, head_dim 64 or
+ * 128; q/k/v rows 16-byte aligned.
+ */
+typedef struct oc_prefill_params {
+  const void* q;                  /* (batch, num_q_heads, q_len, head_dim) */
+  int64_t q_stride_b, q_stride_h, q_stride_s;  /* elements; head_dim contiguous */
+  const void* k;                  /* (batch, num_kv_heads, kv_len, head_dim) */
+  int64_t k_stride_b, k_stride_h, k_stride_s;
+  const void* v;
+  int64_t v_stride_b, v_stride_h, v_stride_s;
+  void* out;                      /* (batch, num_q_heads, q_len, head_dim) */
+  int64_t out_stride_b, out_stride_h, out_stride_s;
+  int32_t dtype;                  /* of q, k, v and out */
+  int32_t batch, num_q_heads, num_kv_heads, q_len, kv_len, head_dim;
+  const uint8_t* tile_mask;       /* (batch, num_kv_heads, tile_mask_cols) or NULL */
+  int64_t tile_mask_stride_b, tile_mask_stride_h;
+  int32_t tile_mask_cols;         /* >= kv_len / 64 */
+  float scale;                    /* logit scale, 1/sqrt(head_dim) in the hook */
+  float* entropy;                 /* (batch, num_q_heads, q_len) or NULL */
+} oc_prefill_params;
+
+int oc_prefill_attention(const oc_prefill_params* p, void* stream);
+
+/* sizeof(oc_prefill_params) as compiled, for binding checks */
+size_t oc_prefill_params_bytes(void);
 
 /* decode parameters; see oc_decode */
 typedef struct oc_decode_params {

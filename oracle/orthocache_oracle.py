@@ -26,6 +26,11 @@ paths with the same per-head, per-tile loop structure:
 * ``apply_decode_mask``       <- apply_decode_mask(_vectorized) (decode_gate.py:302-374)
 * ``block_sparse_attention``  <- _pytorch_block_sparse_attention (sparse_attention.py:144-203)
 * ``indirect_attention``      <- _pytorch_indirect_attention (indirect_attention.py:136-197)
+* ``hook_causal_attention``, ``hook_prefill``, ``hook_decode`` <- the
+  model-side hook OrthoCache_GQA_Attention (eval/perplexity_eval.py:366-689
+  of the reference tree: prefill branch :399-545, decode branch :575-673,
+  dense fallback :675-689); ``torch_lower_median`` <- torch.median(dim)
+  (:456); ``residual_tau`` / ``entropy_tau`` <- the governors (:236-318)
 
 (all paths relative to ``src/orthocache_gpu/triton_kernels/`` or
 ``src/orthocache_gpu/`` of the reference tree).
@@ -58,6 +63,11 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   special thresholds, and the max-over-G rule.
 * ``block_sparse_attention`` / ``indirect_attention``: float64 softmax over
   the retained tokens, all blocks == dense, no block == zeros.
+* hook functions: causal attention == per-query dense decode over the
+  visible keys (float64), no eviction == causal softmax, entropy of uniform
+  attention == ln n, the median rank rules on explicit lists, and the
+  gate's decisions by an explicit per-(kv head, tile) loop
+  (tests/test_oracle_hook.py).
 """
 
 from __future__ import annotations
@@ -680,3 +690,142 @@ def indirect_attention(q, keys, values, active_indices, num_active: int, block_s
     if num_active == 0:
         return np.zeros((1, np.asarray(q).shape[-1]), dtype=F32)
     return _block_online_softmax(q, keys, values, [int(b) for b in active_indices[:num_active]], block_size)
+
+
+# ---------------------------------------------------------------- model hook
+# eval/perplexity_eval.py of the reference tree
+
+HOOK_HIGH_BAND = (48, 64)  # (tile_size * 3) // 4 .. tile_size (perplexity_eval.py:441-442)
+_P_CLAMP = 1e-10           # attn_weights.clamp(min=1e-10) before the log (:526)
+
+
+def torch_lower_median(x: np.ndarray) -> np.ndarray:
+    """torch.median(dim=-1): the lower of the two middle values, rank
+    (n - 1) // 2 of the sorted order (perplexity_eval.py:456)."""
+    n = x.shape[-1]
+    return np.sort(x, axis=-1)[..., (n - 1) // 2]
+
+
+def residual_tau(tau: float, alpha: float, rates) -> float:
+    """ResidualGovernor.get_tau_effective after the layers' rates were
+    reported (perplexity_eval.py:270-276)."""
+    return tau * max(0.0, 1.0 - alpha * float(sum(rates)))
+
+
+def entropy_tau(tau: float, alpha: float, rates, beta: float, h_median: float, entropy) -> float:
+    """EntropyGovernor.get_tau_effective (perplexity_eval.py:304-318)."""
+    t = residual_tau(tau, alpha, rates)
+    if entropy is not None:
+        t *= 2.0 * (1.0 / (1.0 + np.exp(-beta * (entropy - h_median))))
+    return t
+
+
+def hook_tile_norms(keys: np.ndarray) -> np.ndarray:
+    """||(W64 K_t)[48:64]||_F of every complete tile of (B, Hkv, S, d) keys,
+    float32 (B, Hkv, S // 64) (perplexity_eval.py:466-470)."""
+    B, H, S, _ = keys.shape
+    T = S // TILE_SIZE
+    out = np.zeros((B, H, T), dtype=F32)
+    w = walsh_matrix()
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                x = (w @ _as_f32(keys[b, h, t * TILE_SIZE:(t + 1) * TILE_SIZE])).astype(F32)
+                hi = x[HOOK_HIGH_BAND[0]:HOOK_HIGH_BAND[1]]
+                out[b, h, t] = np.sqrt(np.sum(hi * hi, dtype=F32))
+    return out
+
+
+def hook_causal_attention(q, k, v, G: int, evict: Optional[np.ndarray] = None):
+    """Causal GQA softmax attention in float64 with evicted tiles masked for
+    every query of the group (perplexity_eval.py:418-430, :483-500, :533):
+    query s of q (B, Hq, Sq, d) sees keys j <= s + Skv - Sq of k, v
+    (B, Hkv, Skv, d); evict (B, Hkv, >= Skv // 64) bool covers the complete
+    tiles.  A query with no key left gets zeros (nan_to_num).  Returns
+    (out float64 (B, Hq, Sq, d), entropy float64 (B, Hq, Sq) of the
+    1e-10-clamped probabilities over all Skv keys)."""
+    q, k, v = (np.asarray(a, dtype=np.float64) for a in (q, k, v))
+    B, Hq, Sq, d = q.shape
+    Skv = k.shape[2]
+    T = Skv // TILE_SIZE
+    scale = 1.0 / np.sqrt(d)
+    out = np.zeros((B, Hq, Sq, d))
+    ent = np.zeros((B, Hq, Sq))
+    j = np.arange(Skv)
+    for b in range(B):
+        for h in range(Hq):
+            logits = (q[b, h] @ k[b, h // G].T) * scale
+            allowed = j[None, :] <= (np.arange(Sq)[:, None] + Skv - Sq)
+            if evict is not None:
+                tile_ok = np.ones(Skv, dtype=bool)
+                for t in range(T):
+                    if evict[b, h // G, t]:
+                        tile_ok[t * TILE_SIZE:(t + 1) * TILE_SIZE] = False
+                allowed = allowed & tile_ok[None, :]
+            lg = np.where(allowed, logits, -np.inf)
+            m = lg.max(axis=1, keepdims=True)
+            m = np.where(np.isfinite(m), m, 0.0)
+            p = np.where(allowed, np.exp(lg - m), 0.0)
+            z = p.sum(axis=1, keepdims=True)
+            p = np.where(z > 0, p / np.where(z > 0, z, 1.0), 0.0)
+            out[b, h] = p @ v[b, h // G]
+            pc = np.maximum(p, _P_CLAMP)
+            ent[b, h] = -(pc * np.log(pc)).sum(axis=1)
+    return out, ent
+
+
+def hook_prefill(q, k, v, G: int, tau: float):
+    """The prefill branch of OrthoCache_GQA_Attention.orthocache_attention
+    for one call (perplexity_eval.py:399-545): per batch element and kv
+    head, qn = max over the group of the lower median over positions of
+    ||q||_2 (float32), k_norm = hook_tile_norms, and a complete tile is
+    evicted when qn * k_norm / (64 d) <= tau (float64 compare).  Returns a
+    dict: out (float64), evict (B, Hkv, T) bool, k_norms, qn (B, Hkv),
+    per batch element `evicted`, `max_q`, `max_k`, `h_score`, `entropy`
+    (the mean over heads and positions)."""
+    q32 = _as_f32(q)
+    B, Hq, Sq, d = q32.shape
+    Hkv = k.shape[1]
+    kn = hook_tile_norms(k)
+    T = kn.shape[2]
+    qnorm = np.sqrt(np.sum(q32.astype(np.float64) ** 2, axis=-1)).astype(F32)  # (B, Hq, Sq)
+    med = torch_lower_median(qnorm)                                          # (B, Hq)
+    qn = med.reshape(B, Hkv, G).max(axis=2)
+    nf = float(TILE_SIZE * d)
+    evict = np.zeros((B, Hkv, T), dtype=bool)
+    for b in range(B):
+        for h in range(Hkv):
+            for t in range(T):
+                evict[b, h, t] = (float(qn[b, h]) * float(kn[b, h, t])) / nf <= tau
+    out, ent = hook_causal_attention(q, k, v, G, evict)
+    max_q = np.maximum(qn.max(axis=1).astype(np.float64), 0.0)
+    max_k = np.maximum(kn.reshape(B, -1).max(axis=1).astype(np.float64), 0.0) if T else np.zeros(B)
+    return {"out": out, "evict": evict, "k_norms": kn, "qn": qn, "evicted": evict.reshape(B, -1).sum(axis=1),
+            "max_q": max_q, "max_k": max_k, "h_score": max_q / (max_k + 1e-10),
+            "entropy": ent.reshape(B, -1).mean(axis=1)}
+
+
+def hook_decode(q, k, v, norm_cache: np.ndarray, G: int, tau: float, low_band: int = 8):
+    """The decode branch (perplexity_eval.py:575-673): q (B, Hq, 1, d); per
+    batch element and kv head, qn = element G // 2 of the sorted
+    Walsh-subspace norms of the group's queries, and complete tile t is
+    evicted when qn * norm_cache[kv, t] / (64 d) <= tau; the partial last
+    tile is always attended.  Returns a dict: out (float64), evict,
+    qn, skipped, max_q, max_k, h_score."""
+    B, Hq, _, d = np.asarray(q).shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    T = Skv // TILE_SIZE
+    qh = q_high_norm_exact(_as_f32(q)[:, :, 0], low_band)  # (B, Hq)
+    qn = np.sort(qh.reshape(B, Hkv, G), axis=2)[:, :, G // 2]
+    nf = float(TILE_SIZE * d)
+    nc = _as_f32(norm_cache)
+    evict = np.zeros((B, Hkv, T), dtype=bool)
+    for b in range(B):
+        for h in range(Hkv):
+            for t in range(T):
+                evict[b, h, t] = (float(qn[b, h]) * float(nc[h, t])) / nf <= tau
+    out, _ = hook_causal_attention(q, k, v, G, evict)
+    max_q = np.maximum(qn.max(axis=1).astype(np.float64), 0.0)
+    max_k = np.full(B, max(0.0, float(nc[:Hkv, :T].max())) if T else 0.0)
+    return {"out": out, "evict": evict, "qn": qn, "skipped": evict.reshape(B, -1).sum(axis=1),
+            "max_q": max_q, "max_k": max_k, "h_score": max_q / (max_k + 1e-10)}

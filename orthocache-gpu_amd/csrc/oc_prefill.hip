@@ -1,0 +1,605 @@
+// The model-side attention hook's device work (declared in
+// include/orthocache_hip.h): causal GQA prefill attention that skips the
+// evicted 64-token tiles, the per-row q norms, an exact k-th-smallest
+// selection (the median of those norms) and the per-kv-head gate over cached
+// K band norms.
+//
+// Prefill attention is a flash-attention forward pass on the matrix cores.
+// A wave owns 16 consecutive query positions of one q head (the 16 rows of
+// the 16x16 MFMA tiles) and walks the 64-token K/V tiles its causal window
+// reaches, skipping the tiles the mask evicts: S = q.K^T, online softmax with
+// a per-row causal limit, O += P.V.  A workgroup is 4 waves = 64 positions of
+// one head; the workgroups of one kv group run next to each other on one XCD,
+// so the K/V tiles they share stay in that XCD's L2.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "oc_kernels.h"
+#include "oc_status.h"
+#include "orthocache_hip.h"
+
+namespace oc {
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * kWave;
+// -(1e-10) * ln(1e-10): what one zero probability adds to the entropy of a
+// softmax row whose probabilities are clamped to >= 1e-10 before the log
+constexpr float kZeroPTerm = 2.302585093e-9f;
+
+struct PrefillArgs {
+  const char* q;
+  const char* k;
+  const char* v;
+  char* out;
+  int64_t q_sb, q_sh, q_ss;  // byte strides (batch, head, position)
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int32_t B, Hq, Hkv, G, Sq, Skv, T;  // T: full tiles the mask covers
+  const uint8_t* mask;                // (B, Hkv, >= T) evict flags or null
+  int64_t m_sb, m_sh;
+  float scale;
+  float* entropy;  // (B, Hq, Sq) or null
+  int32_t qblocks;
+  int32_t dtype;
+};
+
+// Online-softmax state of the wave's 16 rows, MFMA output layout: lane
+// 16r + x keeps rows 4r + i (i = 0..3); l and e are the lane's partial sums
+// over its tokens, m is shared by the row's 16 lanes.
+struct PfState {
+  float m[4];
+  float l[4];
+  float e[4];  // sum of e^(s - m) * s (entropy)
+  int n[4];    // attended tokens of the row (entropy)
+};
+
+// Causal online-softmax update from one tile's raw logits c (row 4r + i,
+// token 16 tb + x in lane 16r + x, register i); token tok0 + j is visible to
+// row i when tok0 + j < nvis[i].  p goes to sp[row * 64 + token].
+template <int D, bool ENT>
+__device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&accp)[D / 16], const f32x4 (&c)[4], float* sp,
+                                           float scale, const int (&nvis)[4], int tok0, int lane) {
+  const int x = lane & 15;
+  const int r = lane >> 4;
+  float v[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) v[tb][i] = tok0 + 16 * tb + x < nvis[i] ? c[tb][i] * scale : -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float mt = fmaxf(fmaxf(v[0][i], v[1][i]), fmaxf(v[2][i], v[3][i]));
+    mt = fmaxf(mt, xpair<8>(mt));
+    mt = fmaxf(mt, xpair<4>(mt));
+    mt = fmaxf(mt, xpair<2>(mt));
+    mt = fmaxf(mt, xpair<1>(mt));
+    const float mn = fmaxf(st.m[i], mt);
+    const float alpha = __expf(st.m[i] - mn);
+    st.m[i] = mn;
+    float ls = 0.f, es = 0.f;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const bool ok = tok0 + 16 * tb + x < nvis[i];
+      const float pp = __expf(v[tb][i] - mn);
+      ls += pp;
+      if constexpr (ENT) es = ok ? __builtin_fmaf(pp, v[tb][i], es) : es;
+      v[tb][i] = pp;
+    }
+    st.l[i] = __builtin_fmaf(st.l[i], alpha, ls);
+    if constexpr (ENT) {
+      st.e[i] = __builtin_fmaf(st.e[i], alpha, es);
+      st.n[i] += min(max(nvis[i] - tok0, 0), 64);
+    }
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) sp[(4 * r + i) * 64 + 16 * tb + x] = v[tb][i];
+}
+
+// q of the wave's 16 rows as MFMA A operands.  16-bit: lane 16kg + x holds
+// elements 32dc + 8kg .. +8 of row x for instruction dc.  float32 (16x16x4
+// instructions): lane 16kg + x holds column kg*D/4 + dc of row x for
+// instruction dc.  Rows past q_len read as zero.
+template <int DT, int D>
+struct PfQ {
+  static constexpr bool F32 = DT == OC_F32;
+  uint32_t w[F32 ? D / 4 : D / 8];
+};
+
+template <int DT, int D>
+__device__ __forceinline__ void pf_load_q(const PrefillArgs& a, const char* qh, int pos0, int lane, PfQ<DT, D>& q) {
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+  const bool ok = pos0 + x < a.Sq;
+  const char* rowp = qh + (int64_t)(pos0 + x) * a.q_ss;
+  if constexpr (DT == OC_F32) {
+#pragma unroll
+    for (int j = 0; j < D / 16; ++j) {
+      uint4 u = {0u, 0u, 0u, 0u};
+      if (ok) u = *reinterpret_cast<const uint4*>(rowp + 4 * (kg * (D / 4) + 4 * j));
+      q.w[4 * j] = u.x;
+      q.w[4 * j + 1] = u.y;
+      q.w[4 * j + 2] = u.z;
+      q.w[4 * j + 3] = u.w;
+    }
+  } else {
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) {
+      uint4 u = {0u, 0u, 0u, 0u};
+      if (ok) u = *reinterpret_cast<const uint4*>(rowp + 2 * (32 * dc + 8 * kg));
+      q.w[4 * dc] = u.x;
+      q.w[4 * dc + 1] = u.y;
+      q.w[4 * dc + 2] = u.z;
+      q.w[4 * dc + 3] = u.w;
+    }
+  }
+}
+
+// K tile t as MFMA B operands, straight from HBM (one buffer descriptor per
+// 16-token block whose size is the block's part below kv_len, so tokens past
+// kv_len read as zero).  16-bit: lane 16kg + x holds token 16tb + x,
+// elements 32dc + 8kg .. +8 in kb[tb][4dc .. 4dc + 4).  float32: lane
+// 16kg + x holds token 16tb + x, columns kg*D/4 .. + D/4 in kb[tb][..].
+template <int DT, int D>
+struct PfK {
+  static constexpr int W = DT == OC_F32 ? D / 4 : D / 8;
+  uint32_t w[4][W];
+};
+
+template <int DT, int D>
+__device__ __forceinline__ void pf_load_k(const PrefillArgs& a, const char* kh, int t, int lane, PfK<DT, D>& kb) {
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+  const int64_t ts = a.k_ss;
+  const char* base = kh + (int64_t)t * 64 * ts;
+  const int nbytes = (int)(min(a.Skv - t * 64, 64) * ts);
+  const int voff = x * (int)ts + (DT == OC_F32 ? kg * D : 16 * kg);
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int rb = 16 * tb * (int)ts;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
+#pragma unroll
+    for (int j = 0; j < PfK<DT, D>::W / 4; ++j) {
+      // float32: 16 consecutive bytes per load; 16-bit: 32-column steps of 64 bytes
+      const int off = DT == OC_F32 ? 16 * j : 64 * j;
+      const auto u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + off, 0, 0);
+      kb.w[tb][4 * j] = u[0];
+      kb.w[tb][4 * j + 1] = u[1];
+      kb.w[tb][4 * j + 2] = u[2];
+      kb.w[tb][4 * j + 3] = u[3];
+    }
+  }
+}
+
+// V tile t into the wave's LDS slot, row-major [token][D], by direct-to-LDS
+// buffer loads (16 bytes per lane, 1 KiB per instruction); tokens past
+// kv_len read as zero.
+template <int DT, int D>
+__device__ __forceinline__ void pf_load_v(const PrefillArgs& a, const char* vh, int t, int lane, char* sv) {
+  constexpr int ES = DT == OC_F32 ? 4 : 2;
+  constexpr int TPI = 1024 / (ES * D);
+  constexpr int LPT = 64 / TPI;
+  const int64_t ts = a.v_ss;
+  const char* base = vh + (int64_t)t * 64 * ts;
+  const int nbytes = (int)(min(a.Skv - t * 64, 64) * ts);
+  const int voff = (lane / LPT) * (int)ts + 16 * (lane % LPT);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < 64 / TPI; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 1024), 16,
+                                             voff + i * TPI * (int)ts, 0, 0, 0);
+}
+
+template <int DT, int D>
+__device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const PfK<DT, D>& kb, f32x4 (&c)[4]) {
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (DT == OC_F32) {
+#pragma unroll
+      for (int dc = 0; dc < D / 4; ++dc)
+        c[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(q.w[dc]), __uint_as_float(kb.w[tb][dc]), c[tb],
+                                                     0, 0, 0);
+    } else {
+#pragma unroll
+      for (int dc = 0; dc < D / 32; ++dc) {
+        const uint32_t aq[4] = {q.w[4 * dc], q.w[4 * dc + 1], q.w[4 * dc + 2], q.w[4 * dc + 3]};
+        const uint32_t bk[4] = {kb.w[tb][4 * dc], kb.w[tb][4 * dc + 1], kb.w[tb][4 * dc + 2], kb.w[tb][4 * dc + 3]};
+        c[tb] = mfma_qk<DT>(aq, bk, c[tb]);
+      }
+    }
+  }
+}
+
+// float32 p.V: A = P[row x][token 4kc + kg] (exact), B = V[token 4kc + kg][16nc + x].
+template <int D>
+__device__ __forceinline__ void pf_pv_f32(f32x4 (&accp)[D / 16], const float* sp, const float* sv, int lane) {
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+#pragma unroll 4
+  for (int kc = 0; kc < 16; ++kc) {
+    const float pa = sp[x * 64 + 4 * kc + kg];
+    const float* vr = sv + (4 * kc + kg) * D + x;
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc)
+      accp[nc] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vr[16 * nc], accp[nc], 0, 0, 0);
+  }
+}
+
+template <int DT, int D>
+struct PfLds {
+  static constexpr int kV = 64 * D * (DT == OC_F32 ? 4 : 2);
+  static constexpr int kP = 16 * 64 * 4;
+  static constexpr int kWaveBytes = kV + kP;
+};
+
+template <int DT, int D, bool ENT>
+__global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) char sh[kPfWaves * PfLds<DT, D>::kWaveBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // XCD-aware order: consecutive workgroups go to different XCDs, so work
+  // item w is placed so that items w, w+1, .. run on one XCD; items walk the
+  // query blocks from the last (longest causal window) to the first, heads
+  // fastest, so the G heads of one kv group share an XCD's L2.
+  const int nb = gridDim.x;
+  const int i = blockIdx.x;
+  const int w = (nb % 8 == 0) ? (i % 8) * (nb / 8) + i / 8 : i;
+  const int bh = w % (a.B * a.Hq);
+  const int qb = a.qblocks - 1 - w / (a.B * a.Hq);
+  const int b = bh / a.Hq;
+  const int h = bh % a.Hq;
+  const int kv = h / a.G;
+  const int pos0 = qb * 64 + 16 * wave;
+  if (pos0 >= a.Sq) return;  // no barrier below: waves are independent
+  char* my = sh + wave * PfLds<DT, D>::kWaveBytes;
+  char* sv = my;
+  float* sp = reinterpret_cast<float*>(my + PfLds<DT, D>::kV);
+
+  const int off = a.Skv - a.Sq;  // query s sees keys j <= s + off
+  const int r = lane >> 4;
+  const int x = lane & 15;
+  int nvis[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const int pos = pos0 + 4 * r + ii;
+    nvis[ii] = pos < a.Sq ? min(max(pos + off + 1, 0), a.Skv) : 0;
+  }
+  const int last = min(pos0 + 15, a.Sq - 1);
+  const int nvis_max = min(max(last + off + 1, 0), a.Skv);
+  const int tend = (nvis_max + 63) / 64;
+
+  PfQ<DT, D> q;
+  pf_load_q<DT, D>(a, a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh, pos0, lane, q);
+  const char* kh = a.k + (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
+  const char* vh = a.v + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh;
+  const uint8_t* mrow = a.mask ? a.mask + (int64_t)b * a.m_sb + (int64_t)kv * a.m_sh : nullptr;
+
+  PfState st;
+  f32x4 accp[D / 16];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    st.m[ii] = kM0;
+    st.l[ii] = 0.f;
+    st.e[ii] = 0.f;
+    st.n[ii] = 0;
+  }
+#pragma unroll
+  for (int nc = 0; nc < D / 16; ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int t = 0; t < tend; ++t) {
+    if (mrow && t < a.T && mrow[t]) continue;  // evicted tile (uniform over the wave)
+    PfK<DT, D> kb;
+    pf_load_k<DT, D>(a, kh, t, lane, kb);
+    pf_load_v<DT, D>(a, vh, t, lane, sv);
+    f32x4 c[4];
+    pf_logits<DT, D>(q, kb, c);
+    pf_softmax<D, ENT>(st, accp, c, sp, a.scale, nvis, t * 64, lane);
+    // the V tile's direct-to-LDS loads and the p stores have landed
+    __builtin_amdgcn_s_waitcnt(0);
+    if constexpr (DT == OC_F32)
+      pf_pv_f32<D>(accp, sp, reinterpret_cast<const float*>(sv), lane);
+    else
+      tile_pv_mfma<DT, D, 16>(accp, sp, reinterpret_cast<const uint16_t*>(sv), lane);
+    // every lane's reads of sp and sv are done before the next tile's writes
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+
+  // row sums over the 16 lanes of each row, then out = acc / max(l, 1e-9)
+  char* ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    float l = st.l[ii];
+    l += xpair<8>(l);
+    l += xpair<4>(l);
+    l += xpair<2>(l);
+    l += xpair<1>(l);
+    const int pos = pos0 + 4 * r + ii;
+    const float inv = 1.f / fmaxf(l, 1e-9f);
+    if (pos < a.Sq) {
+#pragma unroll
+      for (int nc = 0; nc < D / 16; ++nc)
+        store_scalar(ob + (int64_t)pos * a.o_ss + (int64_t)(16 * nc + x) * (DT == OC_F32 ? 4 : 2), a.dtype,
+                     accp[nc][ii] * inv);
+    }
+    if constexpr (ENT) {
+      float e = st.e[ii];
+      e += xpair<8>(e);
+      e += xpair<4>(e);
+      e += xpair<2>(e);
+      e += xpair<1>(e);
+      if (pos < a.Sq && x == 0) {
+        // H = -sum p ln p with p = e^(s - m) / l: m + ln l - (sum e^(s-m) s) / l,
+        // plus the clamp term of the probabilities that are exactly zero
+        const float hz = (float)(a.Skv - st.n[ii]) * kZeroPTerm;
+        const float H = l > 0.f ? st.m[ii] + logf(l) - e / l + hz : (float)a.Skv * kZeroPTerm;
+        a.entropy[((int64_t)b * a.Hq + h) * a.Sq + pos] = H;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ gate helpers
+
+__device__ __forceinline__ float pf_load_elem(const char* p, int dtype) {
+  if (dtype == OC_F32) return *reinterpret_cast<const float*>(p);
+  const uint16_t u = *reinterpret_cast<const uint16_t*>(p);
+  if (dtype == OC_BF16) return __uint_as_float((uint32_t)u << 16);
+  return (float)__builtin_bit_cast(_Float16, u);
+}
+
+// One wave per row of a 3-index view: ||row||_2, or with low_band > 0 its
+// Walsh-subspace high part sqrt(max(0, ||row||^2 - sum_i S_i^2 / bs)) (S_i:
+// sums of blocks of bs = d / low_band elements).
+__global__ __launch_bounds__(256) void row_norms_kernel(const char* x, int dtype, int64_t n0, int64_t n1,
+                                                        int64_t n2, int64_t s0, int64_t s1, int64_t s2, int d,
+                                                        int low_band, float* out) {
+  __shared__ float sh[4][1024];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  if (r >= n0 * n1 * n2) return;
+  const int64_t i2 = r % n2, i1 = (r / n2) % n1, i0 = r / (n1 * n2);
+  const char* p = x + i0 * s0 + i1 * s1 + i2 * s2;
+  const int es = dtype == OC_F32 ? 4 : 2;
+  float ss = 0.f;
+  for (int c = lane; c < d; c += 64) {
+    const float v = pf_load_elem(p + (int64_t)c * es, dtype);
+    sh[wave][c] = v;
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if (low_band > 0) {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int bs = d / low_band;
+    float lo = 0.f;
+    for (int i = lane; i < low_band; i += 64) {
+      float s = 0.f;
+      for (int k = 0; k < bs; ++k) s += sh[wave][i * bs + k];
+      lo = __builtin_fmaf(s, s, lo);
+    }
+    for (int o = 32; o > 0; o >>= 1) lo += __shfl_xor(lo, o, 64);
+    lo /= (float)bs;
+    ss = ss - lo;
+    ss = ss < 0.f ? 0.f : ss;
+  }
+  if (lane == 0) out[r] = __builtin_sqrtf(ss);
+}
+
+// k-th smallest (0-based) of n non-negative floats per row by a radix
+// select over their bit patterns (monotone for x >= 0; NaN sorts last):
+// four 8-bit passes, each a 256-bin LDS histogram, then the bin holding
+// rank k.  One workgroup per row.
+__global__ __launch_bounds__(256) void kth_smallest_kernel(const float* x, int64_t n, int64_t row_stride, int64_t k,
+                                                           float* out) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t sel[2];
+  const float* row = x + (int64_t)blockIdx.x * row_stride;
+  uint32_t prefix = 0, pmask = 0;
+  uint64_t rank = (uint64_t)k;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[threadIdx.x] = 0;
+    __syncthreads();
+    for (int64_t j = threadIdx.x; j < n; j += 256) {
+      const uint32_t u = __float_as_uint(row[j]);
+      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint64_t acc = 0;
+      int bin = 255;
+      for (int i = 0; i < 256; ++i) {
+        if (acc + hist[i] > rank) {
+          bin = i;
+          break;
+        }
+        acc += hist[i];
+      }
+      sel[0] = (uint32_t)bin;
+      sel[1] = (uint32_t)(rank - acc);
+    }
+    __syncthreads();
+    prefix |= sel[0] << shift;
+    pmask |= 255u << shift;
+    rank = sel[1];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = __uint_as_float(prefix);
+}
+
+// One workgroup per (batch, kv head): qn = max of the group's G per-head
+// norms (NaN-propagating) or the element of rank G/2 of their sorted order
+// (ties counted by index), then mask[t] = qn * kn[t] <= tau_norm for t <
+// num_tiles and 0 up to mask_cols (keep_pol: 1 = attend instead).
+__global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, int Hkv, int G, int reduce,
+                                                         const float* kn, int64_t kn_sb, int64_t kn_sh,
+                                                         int num_tiles, int mask_cols, float tau_norm, int keep_pol,
+                                                         uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out) {
+  __shared__ float s_qn;
+  const int bk = blockIdx.x;
+  const int b = bk / Hkv;
+  const int kv = bk % Hkv;
+  const float* qh = qn_heads + ((int64_t)b * Hkv + kv) * G;
+  if (threadIdx.x == 0) {
+    float qn = 0.f;
+    if (reduce == OC_GROUP_MAX) {
+      bool nan = false;
+      float best = -__builtin_inff();
+      for (int g = 0; g < G; ++g) {
+        nan = nan || __builtin_isnan(qh[g]);
+        best = qh[g] > best ? qh[g] : best;
+      }
+      qn = nan ? __builtin_nanf("") : best;
+    } else {
+      const int want = G / 2;
+      for (int g = 0; g < G; ++g) {
+        int below = 0;
+        for (int j = 0; j < G; ++j) below += (qh[j] < qh[g] || (qh[j] == qh[g] && j < g)) ? 1 : 0;
+        if (below == want) qn = qh[g];
+      }
+    }
+    s_qn = qn;
+    if (qn_out) qn_out[bk] = qn;
+  }
+  __syncthreads();
+  const float qn = s_qn;
+  const float* knr = kn + (int64_t)b * kn_sb + (int64_t)kv * kn_sh;
+  uint8_t* mr = mask + (int64_t)b * m_sb + (int64_t)kv * m_sh;
+  for (int t = threadIdx.x; t < mask_cols; t += 256) {
+    const bool ev = t < num_tiles && qn * knr[t] <= tau_norm;
+    mr[t] = (ev != (keep_pol != 0)) ? 1 : 0;
+  }
+}
+
+bool pf_float_dtype(int dt) { return dt == OC_F32 || dt == OC_F16 || dt == OC_BF16; }
+
+template <int DT, int D>
+int launch_prefill(const PrefillArgs& a, hipStream_t s, unsigned blocks) {
+  if (a.entropy)
+    hipLaunchKernelGGL((prefill_kernel<DT, D, true>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<DT, D, false>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "prefill launch");
+}
+
+template <int DT>
+int launch_prefill_d(const PrefillArgs& a, int d, hipStream_t s, unsigned blocks) {
+  return d == 64 ? launch_prefill<DT, 64>(a, s, blocks) : launch_prefill<DT, 128>(a, s, blocks);
+}
+
+}  // namespace
+}  // namespace oc
+
+using namespace oc;
+
+extern "C" int oc_prefill_attention(const oc_prefill_params* p, void* stream) {
+  if (!p) return fail(OC_ERR_INVALID, "NULL params");
+  if (!p->q || !p->k || !p->v || !p->out) return fail(OC_ERR_INVALID, "NULL tensor pointer");
+  if (!pf_float_dtype(p->dtype)) return fail(OC_ERR_UNSUPPORTED, "prefill dtype %d (float32, float16, bfloat16)",
+                                             p->dtype);
+  if (p->head_dim != 64 && p->head_dim != 128) return fail(OC_ERR_UNSUPPORTED, "head_dim %d (64 or 128)", p->head_dim);
+  if (p->batch < 0 || p->num_q_heads < 0 || p->num_kv_heads < 1 || p->q_len < 0 || p->kv_len < 0)
+    return fail(OC_ERR_INVALID, "bad sizes");
+  if (p->num_q_heads % p->num_kv_heads) return fail(OC_ERR_INVALID, "num_q_heads %d not a multiple of num_kv_heads %d",
+                                                    p->num_q_heads, p->num_kv_heads);
+  const int es = p->dtype == OC_F32 ? 4 : 2;
+  // 16-byte vector loads: rows and bases 16-byte aligned
+  const int64_t strides[] = {p->q_stride_b, p->q_stride_h, p->q_stride_s, p->k_stride_b, p->k_stride_h,
+                             p->k_stride_s, p->v_stride_b, p->v_stride_h, p->v_stride_s};
+  for (int64_t st : strides)
+    if ((st * es) % 16) return fail(OC_ERR_INVALID, "q/k/v strides must be multiples of 16 bytes");
+  if (((uintptr_t)p->q | (uintptr_t)p->k | (uintptr_t)p->v) % 16) return fail(OC_ERR_INVALID, "q/k/v not 16-byte aligned");
+  if (p->k_stride_s * es * 64 > 0x7FFFFFFF || p->v_stride_s * es * 64 > 0x7FFFFFFF)
+    return fail(OC_ERR_UNSUPPORTED, "token stride too large");
+  if (p->k_stride_s < p->head_dim || p->v_stride_s < p->head_dim)
+    return fail(OC_ERR_INVALID, "token stride smaller than head_dim");
+  if (p->tile_mask && p->tile_mask_cols < p->kv_len / 64)
+    return fail(OC_ERR_INVALID, "tile_mask has %d columns, kv_len needs %d", p->tile_mask_cols, p->kv_len / 64);
+  if (p->batch == 0 || p->num_q_heads == 0 || p->q_len == 0) return OC_OK;
+  PrefillArgs a{};
+  a.q = (const char*)p->q;
+  a.k = (const char*)p->k;
+  a.v = (const char*)p->v;
+  a.out = (char*)p->out;
+  a.q_sb = p->q_stride_b * es, a.q_sh = p->q_stride_h * es, a.q_ss = p->q_stride_s * es;
+  a.k_sb = p->k_stride_b * es, a.k_sh = p->k_stride_h * es, a.k_ss = p->k_stride_s * es;
+  a.v_sb = p->v_stride_b * es, a.v_sh = p->v_stride_h * es, a.v_ss = p->v_stride_s * es;
+  a.o_sb = p->out_stride_b * es, a.o_sh = p->out_stride_h * es, a.o_ss = p->out_stride_s * es;
+  a.B = p->batch, a.Hq = p->num_q_heads, a.Hkv = p->num_kv_heads, a.G = p->num_q_heads / p->num_kv_heads;
+  a.Sq = p->q_len, a.Skv = p->kv_len, a.T = p->kv_len / 64;
+  a.mask = p->tile_mask, a.m_sb = p->tile_mask_stride_b, a.m_sh = p->tile_mask_stride_h;
+  a.scale = p->scale;
+  a.entropy = p->entropy;
+  a.qblocks = (p->q_len + 63) / 64;
+  a.dtype = p->dtype;
+  const int64_t blocks = (int64_t)a.qblocks * a.B * a.Hq;
+  if (blocks > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many query blocks");
+  const hipStream_t s = (hipStream_t)stream;
+  switch (p->dtype) {
+    case OC_F32: return launch_prefill_d<OC_F32>(a, p->head_dim, s, (unsigned)blocks);
+    case OC_F16: return launch_prefill_d<OC_F16>(a, p->head_dim, s, (unsigned)blocks);
+    default: return launch_prefill_d<OC_BF16>(a, p->head_dim, s, (unsigned)blocks);
+  }
+}
+
+extern "C" int oc_row_norms(const void* x, int32_t dtype, int64_t n0, int64_t n1, int64_t n2, int64_t stride0,
+                            int64_t stride1, int64_t stride2, int32_t head_dim, int32_t low_band, float* out,
+                            void* stream) {
+  if (!x || !out) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (!pf_float_dtype(dtype)) return fail(OC_ERR_INVALID, "dtype %d", dtype);
+  if (n0 < 0 || n1 < 0 || n2 < 0 || head_dim < 1 || head_dim > 1024) return fail(OC_ERR_INVALID, "bad sizes");
+  if (low_band < 0 || (low_band > 0 && head_dim % low_band))
+    return fail(OC_ERR_INVALID, "head_dim %d not divisible by low_band %d", head_dim, low_band);
+  const int64_t rows = n0 * n1 * n2;
+  if (rows == 0) return OC_OK;
+  const int64_t blocks = (rows + 3) / 4;
+  if (blocks > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many rows");
+  const int es = dtype == OC_F32 ? 4 : 2;
+  hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const char*)x,
+                     dtype, n0, n1, n2, stride0 * es, stride1 * es, stride2 * es, head_dim, low_band, out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "row-norm launch");
+}
+
+extern "C" int oc_kth_smallest(const float* x, int64_t rows, int64_t n, int64_t row_stride, int64_t k, float* out,
+                               void* stream) {
+  if (!x || !out) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (rows < 0 || n < 1 || k < 0 || k >= n || row_stride < n) return fail(OC_ERR_INVALID, "bad sizes (k must be < n)");
+  if (rows > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many rows");
+  if (rows == 0) return OC_OK;
+  hipLaunchKernelGGL(kth_smallest_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x, n, row_stride,
+                     k, out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "select launch");
+}
+
+extern "C" int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv_heads, int32_t G, int32_t reduce,
+                             const float* k_norms, int64_t k_norms_stride_b, int64_t k_norms_stride_h,
+                             int32_t num_tiles, int32_t mask_cols, double tau_norm, int32_t keep_polarity,
+                             uint8_t* mask, int64_t mask_stride_b, int64_t mask_stride_h, float* group_norms,
+                             void* stream) {
+  if (!q_norms || !k_norms || !mask) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (batch < 0 || num_kv_heads < 0 || G < 1 || num_tiles < 0 || mask_cols < num_tiles)
+    return fail(OC_ERR_INVALID, "bad sizes");
+  if (reduce != OC_GROUP_MAX && reduce != OC_GROUP_MEDIAN) return fail(OC_ERR_INVALID, "reduce %d", reduce);
+  const int64_t wgs = (int64_t)batch * num_kv_heads;
+  if (wgs == 0) return OC_OK;
+  if (wgs > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many heads");
+  hipLaunchKernelGGL(group_gate_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, q_norms,
+                     num_kv_heads, G, reduce, k_norms, k_norms_stride_b, k_norms_stride_h, num_tiles, mask_cols,
+                     (float)tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "group-gate launch");
+}
+
+extern "C" size_t oc_prefill_params_bytes(void) { return sizeof(oc_prefill_params); }

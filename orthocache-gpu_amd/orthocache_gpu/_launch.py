@@ -156,8 +156,10 @@ class KVLayout:
         return d
 
 
-def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor]) -> KVLayout:
-    """(rows, S, d) K/V views (last dimension contiguous, any other strides)."""
+def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail: bool = False) -> KVLayout:
+    """(rows, S, d) K/V views (last dimension contiguous, any other strides).
+    The tiles are the S // 64 complete ones; with partial_tail a last
+    partial tile is included (as a row length of S)."""
     rows, s_len, d = keys.shape
     if values is not None and values.shape != keys.shape:
         raise ValueError(f"keys {tuple(keys.shape)} and values {tuple(values.shape)} must have the same shape")
@@ -165,11 +167,16 @@ def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor]) -> KVLayout:
     keys = last_dim_ready(keys, d)
     if values is not None:
         values = last_dim_ready(values, d)
-    return KVLayout(
+    kv = KVLayout(
         k=keys, v=values, head_dim=d, num_rows=rows, num_tiles=s_len // TILE_SIZE,
         k_row_stride=keys.stride(0), k_token_stride=keys.stride(1),
         v_row_stride=0 if values is None else values.stride(0),
         v_token_stride=0 if values is None else values.stride(1))
+    if partial_tail and s_len % TILE_SIZE:
+        kv.num_tiles += 1
+        kv.lengths = torch.full((1,), s_len, dtype=torch.int32, device=keys.device)
+        kv.rows_per_length = max(rows, 1)
+    return kv
 
 
 def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -251,7 +258,8 @@ class DecodeResult:
 def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float, mode: int = N.OC_MODE_SINGLE_PASS,
            scores: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_splits: Optional[int] = None,
            out_dtype: torch.dtype, want_keep: bool = False, want_partials: bool = False,
-           out: Optional[torch.Tensor] = None, splits_per_group: Optional[int] = None) -> DecodeResult:
+           out: Optional[torch.Tensor] = None, splits_per_group: Optional[int] = None,
+           tile_mask: Optional[torch.Tensor] = None) -> DecodeResult:
     """One oc_decode call.  q is (rows*G, d) with a contiguous last dimension.
     With want_partials the per-split partial states (one workgroup per
     logical split) are returned as (m, l, acc) of shapes (rows*G, P) and
@@ -299,6 +307,11 @@ def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float
     p.out_row_stride = out.stride(0)
     p.keep_out = _ptr(keep)
     p.keep_row_stride = 0 if keep is None else keep.stride(0)
+    if tile_mask is not None:
+        if (tile_mask.dtype != torch.uint8 or tile_mask.dim() != 2 or tile_mask.shape[0] < kv.num_rows
+                or tile_mask.stride(1) != 1 or tile_mask.device != device):
+            raise ValueError(f"tile_mask must be a uint8 ({kv.num_rows}, tiles) tensor on {device}")
+        p.tile_mask, p.tile_mask_row_stride = tile_mask.data_ptr(), tile_mask.stride(0)
     partials = None
     if want_partials:
         pm = torch.empty((rows_q, P), dtype=torch.float32, device=device)
@@ -574,3 +587,115 @@ def vscale_mode(v_scale, num_rows: int, num_tiles: int, device) -> Tuple[int, Op
     if vs.shape[1] < num_tiles:
         raise ValueError(f"v_scale has {vs.shape[1]} tiles per row, need {num_tiles}")
     return N.OC_VSCALE_TILE, vs.contiguous()
+
+
+# ------------------------------------------------------------ model hook
+
+def row_norms(x: torch.Tensor, low_band: int = 0) -> torch.Tensor:
+    """oc_row_norms over the last dimension of a (n0, n1, n2, d) view (any
+    strides, last dimension contiguous): float32 (n0, n1, n2); low_band > 0
+    gives the Walsh-subspace high part."""
+    device = require_gpu(x)
+    if x.dim() != 4:
+        raise ValueError(f"row_norms expects a 4-d view, got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    n0, n1, n2, d = x.shape
+    out = torch.empty((n0, n1, n2), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_row_norms", N.lib().oc_row_norms(
+            x.data_ptr(), dtype_code(x.dtype, "x", allow_fp8=False), n0, n1, n2, x.stride(0), x.stride(1),
+            x.stride(2), d, low_band, out.data_ptr(), ctypes.c_void_p(current_stream(device))))
+    return out
+
+
+def kth_smallest(x: torch.Tensor, k: int) -> torch.Tensor:
+    """oc_kth_smallest: the k-th smallest (0-based) of each row of a float32
+    (rows, n) tensor of non-negative values."""
+    device = require_gpu(x)
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        x = x.to(torch.float32).contiguous().reshape(x.shape[0], -1)
+    rows, n = x.shape
+    out = torch.empty((rows,), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_kth_smallest", N.lib().oc_kth_smallest(
+            x.data_ptr(), rows, n, x.stride(0), k, out.data_ptr(), ctypes.c_void_p(current_stream(device))))
+    return out
+
+
+def group_gate(q_norms: torch.Tensor, k_norms: torch.Tensor, num_kv_heads: int, G: int, num_tiles: int,
+               mask_cols: int, tau_norm: float, reduce: int, keep_polarity: bool = False
+               ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """oc_group_gate.  q_norms: float32 (batch, num_kv_heads * G); k_norms:
+    float32 (batch or 1, num_kv_heads, >= num_tiles) (a batch of 1 is shared
+    by every batch entry).  Returns (mask uint8 (batch, num_kv_heads,
+    mask_cols), group norms float32 (batch, num_kv_heads))."""
+    device = require_gpu(q_norms, k_norms)
+    B = q_norms.shape[0]
+    q_norms = q_norms.to(torch.float32).contiguous()
+    if q_norms.numel() != B * num_kv_heads * G:
+        raise ValueError(f"q_norms must hold {B} x {num_kv_heads * G} values")
+    if (k_norms.dtype != torch.float32 or k_norms.dim() != 3 or k_norms.shape[1] != num_kv_heads
+            or k_norms.shape[2] < num_tiles or k_norms.stride(2) != 1 or k_norms.shape[0] not in (1, B)):
+        raise ValueError(f"k_norms must be a float32 (batch or 1, {num_kv_heads}, >= {num_tiles}) tensor")
+    ksb = 0 if k_norms.shape[0] == 1 else k_norms.stride(0)
+    mask = torch.empty((B, num_kv_heads, max(mask_cols, 1)), dtype=torch.uint8, device=device)
+    gn = torch.empty((B, num_kv_heads), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_group_gate", N.lib().oc_group_gate(
+            q_norms.data_ptr(), B, num_kv_heads, G, reduce, k_norms.data_ptr(), ksb, k_norms.stride(1),
+            num_tiles, mask_cols, float(tau_norm), 1 if keep_polarity else 0, mask.data_ptr(), mask.stride(0),
+            mask.stride(1), gn.data_ptr(), ctypes.c_void_p(current_stream(device))))
+    return mask, gn
+
+
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, tile_mask: Optional[torch.Tensor] = None,
+                      scale: Optional[float] = None, want_entropy: bool = False
+                      ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """oc_prefill_attention: causal GQA attention of q (B, Hq, Sq, d) over k, v
+    (B, Hkv, Skv, d) (last dimensions contiguous, other strides free),
+    skipping the tiles whose tile_mask (B, Hkv, >= Skv // 64) byte is set.
+    Returns (out (B, Hq, Sq, d) in q's dtype, entropy float32 (B, Hq, Sq) or
+    None)."""
+    device = require_gpu(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape:
+        raise ValueError(f"q (B, Hq, Sq, d) and k, v (B, Hkv, Skv, d) expected, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    B, Hq, Sq, d = q.shape
+    if k.shape[0] != B or k.shape[3] != d or Hq % k.shape[1]:
+        raise ValueError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k and v must share a dtype ({q.dtype}, {k.dtype}, {v.dtype})")
+    q, k, v = (_ready16(t) for t in (q, k, v))
+    Hkv, Skv = k.shape[1], k.shape[2]
+    out = torch.empty((B, Hq, Sq, d), dtype=q.dtype, device=device)
+    ent = torch.empty((B, Hq, Sq), dtype=torch.float32, device=device) if want_entropy else None
+    p = N.OcPrefillParams()
+    p.q, (p.q_stride_b, p.q_stride_h, p.q_stride_s) = q.data_ptr(), q.stride()[:3]
+    p.k, (p.k_stride_b, p.k_stride_h, p.k_stride_s) = k.data_ptr(), k.stride()[:3]
+    p.v, (p.v_stride_b, p.v_stride_h, p.v_stride_s) = v.data_ptr(), v.stride()[:3]
+    p.out, (p.out_stride_b, p.out_stride_h, p.out_stride_s) = out.data_ptr(), out.stride()[:3]
+    p.dtype = dtype_code(q.dtype, "q", allow_fp8=False)
+    p.batch, p.num_q_heads, p.num_kv_heads, p.q_len, p.kv_len, p.head_dim = B, Hq, Hkv, Sq, Skv, d
+    if tile_mask is not None:
+        if (tile_mask.dtype != torch.uint8 or tile_mask.dim() != 3 or tile_mask.shape[:2] != (B, Hkv)
+                or tile_mask.stride(2) != 1 or tile_mask.device != device):
+            raise ValueError(f"tile_mask must be a uint8 ({B}, {Hkv}, tiles) tensor on {device}")
+        p.tile_mask, p.tile_mask_stride_b, p.tile_mask_stride_h = (tile_mask.data_ptr(), tile_mask.stride(0),
+                                                                   tile_mask.stride(1))
+        p.tile_mask_cols = tile_mask.shape[2]
+    p.scale = float(scale) if scale is not None else 1.0 / (d ** 0.5)
+    p.entropy = _ptr(ent)
+    with torch.cuda.device(device):
+        N.check("oc_prefill_attention", N.lib().oc_prefill_attention(
+            ctypes.byref(p), ctypes.c_void_p(current_stream(device))))
+    return out, ent
+
+
+def _ready16(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its last dimension is contiguous and its base and every
+    other stride are 16-byte aligned (the kernels' vector loads), else a
+    contiguous copy."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()

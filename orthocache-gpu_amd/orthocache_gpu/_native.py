@@ -30,6 +30,7 @@ OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE = 0, 1, 3
 OC_VSCALE_NONE, OC_VSCALE_TILE = 0, 1
 # q norm of the decode gate
 OC_QNORM_SPATIAL, OC_QNORM_WALSH_HIGH = 0, 1
+OC_GROUP_MAX, OC_GROUP_MEDIAN = 0, 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -71,6 +72,20 @@ class OcDecodeParams(ctypes.Structure):
     ]
 
 
+class OcPrefillParams(ctypes.Structure):
+    _fields_ = [
+        ("q", _p), ("q_stride_b", _i64), ("q_stride_h", _i64), ("q_stride_s", _i64),
+        ("k", _p), ("k_stride_b", _i64), ("k_stride_h", _i64), ("k_stride_s", _i64),
+        ("v", _p), ("v_stride_b", _i64), ("v_stride_h", _i64), ("v_stride_s", _i64),
+        ("out", _p), ("out_stride_b", _i64), ("out_stride_h", _i64), ("out_stride_s", _i64),
+        ("dtype", _i32), ("batch", _i32), ("num_q_heads", _i32), ("num_kv_heads", _i32),
+        ("q_len", _i32), ("kv_len", _i32), ("head_dim", _i32),
+        ("tile_mask", _p), ("tile_mask_stride_b", _i64), ("tile_mask_stride_h", _i64),
+        ("tile_mask_cols", _i32), ("scale", ctypes.c_float),
+        ("entropy", _p),
+    ]
+
+
 # every function declared in include/orthocache_hip.h: name -> (restype, argtypes)
 SIGNATURES = {
     "oc_score_tiles": (_i32, [ctypes.POINTER(OcKvDesc), ctypes.c_double, _p, _p, _p, _p, _i64, _p]),
@@ -83,6 +98,12 @@ SIGNATURES = {
     "oc_q_high_norms": (_i32, [_p, _i32, _i64, _i32, _i64, _i32, _p, _p]),
     "oc_apply_tile_mask": (_i32, [_p, _i32, _i32, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p]),
     "oc_tile_mask_from_blocks": (_i32, [_p, _p, _i32, _i32, _i32, _p, _p, _p]),
+    "oc_row_norms": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p]),
+    "oc_kth_smallest": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p]),
+    "oc_group_gate": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i64, _i64, _i32, _i32, ctypes.c_double, _i32, _p,
+                             _i64, _i64, _p, _p]),
+    "oc_prefill_attention": (_i32, [ctypes.POINTER(OcPrefillParams), _p]),
+    "oc_prefill_params_bytes": (ctypes.c_size_t, []),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
@@ -131,6 +152,9 @@ def lib():
                     "orthocache_gpu: struct layout mismatch between the binding and "
                     f"{LIB_PATH} ({kv_sz.value}/{p_sz.value} vs "
                     f"{ctypes.sizeof(OcKvDesc)}/{ctypes.sizeof(OcDecodeParams)} bytes)")
+            if handle.oc_prefill_params_bytes() != ctypes.sizeof(OcPrefillParams):
+                raise RuntimeError("orthocache_gpu: oc_prefill_params layout mismatch between the binding and "
+                                   f"{LIB_PATH}")
             _lib = handle
     return _lib
 

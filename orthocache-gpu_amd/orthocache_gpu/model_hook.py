@@ -1,0 +1,298 @@
+"""Model-side attention hook: drop-in equivalents of the reference's
+OrthoCache_GQA_Attention, ResidualGovernor, EntropyGovernor and
+patch_model_attention (eval/perplexity_eval.py:236-318, :320-741).
+
+The hook sits where a decoder layer calls scaled-dot-product attention,
+after the Q/K/V projections and RoPE, with q (batch, num_q_heads, q_len,
+head_dim) and k, v (batch, num_kv_heads, kv_len, head_dim):
+
+* kv_len < 64: causal attention, nothing gated (perplexity_eval.py:388-395).
+* q_len == 1 with a populated SpectralNormCache: the decode branch
+  (perplexity_eval.py:575-673).  Per (batch, kv head): the median of the
+  group's Walsh-subspace q norms (rank G // 2 of their sorted order) times
+  the cached ||K_high||_F of each complete tile, over 64 * head_dim, at or
+  below tau evicts the tile; the surviving tiles (and the partial last
+  tile) are attended by the split-K decode kernel (oc_decode with a tile
+  mask), which never reads an evicted tile's K or V.
+* otherwise the prefill branch (perplexity_eval.py:399-545): per q head the
+  lower median over positions of ||q||_2, the max over the group, times the
+  tile's ||(W64 K_t)[48:64]||_F over 64 * head_dim, at or below tau evicts
+  the tile for every query of the group; causal attention over the rest
+  (oc_prefill_attention), the attention entropy when the governor reads
+  it, and the band norms go to the norm cache.
+
+Statistics, governor updates and norm-cache contents follow the reference
+call for call (one entry per batch element per layer call), gathered from
+the device with one transfer per call.  Differences, all keyword-only or
+invisible at the reference's inputs:
+
+* ``score_new_tiles=True`` scores the tiles that complete during decode
+  into the norm cache, from each call's own K, before the gate reads them
+  (the reference leaves them at 0, so its decode gate evicts them);
+  default False, the reference behaviour.
+* a key/value already expanded to num_q_heads heads (transformers' SDPA
+  path when a mask is passed) is reduced to its distinct kv heads.
+* the band norms come from the SpectralNormCache kernel, which clamps
+  norms below 1e-38 to 0 where the reference's prefill does not; a float32
+  norm is either 0 or above 3e-23, so the stored values are the same.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _launch as X
+from . import _native as N
+
+TILE = 64
+_HIGH_BAND = (48, 64)  # (tile_size * 3) // 4 .. tile_size (perplexity_eval.py:441-442)
+_LOW_BAND = 8          # _compute_q_high_norm's default (perplexity_eval.py:547)
+
+
+class ResidualGovernor:
+    """tau_effective = tau_base * max(0, 1 - alpha * sum of the earlier layers'
+    eviction rates) (perplexity_eval.py:236-276)."""
+
+    def __init__(self, alpha: float = 0.5):
+        self.alpha = alpha
+        self.eps_accum = 0.0
+        self.layer_history = []
+
+    def reset(self):
+        self.eps_accum = 0.0
+        self.layer_history = []
+
+    def get_tau_effective(self, tau_base: float) -> float:
+        return tau_base * max(0.0, 1.0 - self.alpha * self.eps_accum)
+
+    def report_layer(self, eviction_rate: float):
+        self.layer_history.append(eviction_rate)
+        self.eps_accum += eviction_rate
+
+
+class EntropyGovernor(ResidualGovernor):
+    """The residual governor's tau times 2 * sigmoid(beta * (H - h_median)),
+    H the attention entropy of the current layer (perplexity_eval.py:279-318)."""
+
+    def __init__(self, alpha: float = 0.5, beta: float = 1.0, h_median: float = 1.56):
+        super().__init__(alpha=alpha)
+        self.beta = beta
+        self.h_median = h_median
+        self.current_entropy = None
+
+    def set_entropy(self, entropy: float):
+        self.current_entropy = entropy
+
+    def get_tau_effective(self, tau_base: float) -> float:
+        tau = super().get_tau_effective(tau_base)
+        if self.current_entropy is not None:
+            tau *= 2.0 / (1.0 + math.exp(-self.beta * (self.current_entropy - self.h_median)))
+        return tau
+
+
+def _empty_stats() -> dict:
+    return {
+        'total_tiles': 0, 'evicted_tiles': 0, 'layers_processed': 0, 'cs_bounds': [],
+        'hallucination_scores': [], 'q_search_intensity': [], 'k_info_density': [],
+        'decode_steps': 0, 'decode_tiles_skipped': 0, 'decode_tiles_total': 0,
+    }
+
+
+class OrthoCache_GQA_Attention:
+    """Cauchy-Schwarz spectral gate + attention in place of a decoder layer's
+    SDPA call (perplexity_eval.py:320-689).  All device work runs in
+    liborthocache_hip; the class keeps the reference's attributes
+    (tau, verbose, governor, norm_cache, stats) and methods."""
+
+    def __init__(self, tau: float = 1.0, verbose: bool = False,
+                 governor: Optional[ResidualGovernor] = None, *, score_new_tiles: bool = False):
+        self.tau = tau
+        self.verbose = verbose
+        self.governor = governor
+        self.norm_cache = None
+        self.score_new_tiles = score_new_tiles
+        self._prefill_tiles = 0  # complete tiles of the last prefill
+        self.stats = _empty_stats()
+
+    def reset_stats(self):
+        self.stats = _empty_stats()
+
+    @property
+    def eviction_rate(self) -> float:
+        if self.stats['total_tiles'] == 0:
+            return 0.0
+        return self.stats['evicted_tiles'] / self.stats['total_tiles']
+
+    # ------------------------------------------------------------ dispatch
+
+    def orthocache_attention(self, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                             num_query_groups: int) -> torch.Tensor:
+        """(batch, num_q_heads, q_len, head_dim) attention output in query's
+        dtype (perplexity_eval.py:366-545)."""
+        key, value = _distinct_kv(query, key, value, num_query_groups)
+        q_len, kv_len = query.shape[2], key.shape[2]
+        if kv_len < TILE:
+            return self._dense_attention(query, key, value, num_query_groups)
+        if q_len == 1 and self.norm_cache is not None and self.norm_cache.is_populated:
+            return self._decode_attention(query, key, value, num_query_groups)
+        return self._prefill_attention(query, key, value, num_query_groups)
+
+    def _tau(self) -> float:
+        return self.governor.get_tau_effective(self.tau) if self.governor is not None else self.tau
+
+    # ------------------------------------------------------------ prefill
+
+    def _prefill_attention(self, query, key, value, G):
+        B, Hq, Sq, d = query.shape
+        Hkv, Skv = key.shape[1], key.shape[2]
+        T = Skv // TILE
+        tau = self._tau()
+        # ||(W64 K_t)[48:64]||_F of every complete tile, (B, Hkv, T)
+        kn = torch.empty((B * Hkv, T), dtype=torch.float32, device=key.device)
+        X.band_norms(X.rows_layout(key.reshape(B * Hkv, Skv, d), None), 0, T, _HIGH_BAND, kn)
+        kn = kn.view(B, Hkv, T)
+        # per q head: lower median over positions of ||q||_2; the group's max
+        med = X.kth_smallest(X.row_norms(query).view(B * Hq, Sq), (Sq - 1) // 2).view(B, Hq)
+        evict, qn = X.group_gate(med, kn, Hkv, G, T, T, tau * TILE * d, N.OC_GROUP_MAX)
+        want_entropy = self.governor is not None and hasattr(self.governor, 'set_entropy')
+        out, ent = X.prefill_attention(query, key, value, tile_mask=evict, want_entropy=want_entropy)
+        if self.norm_cache is not None:
+            self._store_norms(kn[B - 1], Hkv, T)
+        self._prefill_tiles = T
+        # one transfer: per batch element [evicted, max q norm, max k norm, mean entropy]
+        zeros = torch.zeros((B,), dtype=torch.float32, device=query.device)
+        host = torch.stack([
+            evict.view(B, -1).sum(1, dtype=torch.int64).to(torch.float32),
+            qn.amax(1).clamp(min=0.0),
+            kn.reshape(B, -1).amax(1).clamp(min=0.0),
+            ent.view(B, -1).mean(1) if ent is not None else zeros,
+        ]).cpu().double()
+        for b in range(B):
+            evicted = int(host[0, b])
+            self.stats['total_tiles'] += Hkv * T
+            self.stats['evicted_tiles'] += evicted
+            self._exhaust(float(host[1, b]), float(host[2, b]))
+            if self.governor is not None and Hkv * T > 0:
+                self.governor.report_layer(evicted / (Hkv * T))
+            if want_entropy:
+                self.governor.set_entropy(float(host[3, b]))
+                self.stats['entropy'] = float(host[3, b])
+        self.stats['layers_processed'] += 1
+        return out
+
+    def _store_norms(self, kn_last: torch.Tensor, Hkv: int, T: int) -> None:
+        """The reference's per-batch loop writes cache[kv_h, t] for every batch
+        element in turn, so the last one's norms remain (perplexity_eval.py:472-477)."""
+        nc = self.norm_cache
+        if Hkv > nc.num_kv_heads or T > nc.max_tiles:
+            raise IndexError(f"norm cache ({nc.num_kv_heads} heads x {nc.max_tiles} tiles) is smaller than the "
+                             f"prefill ({Hkv} heads x {T} tiles)")
+        nc.cache[:Hkv, :T].copy_(kn_last)
+        nc.valid_tiles[:Hkv].clamp_(min=T)
+        nc._populated = True
+
+    def _exhaust(self, max_q: float, max_k: float) -> None:
+        self.stats['hallucination_scores'].append(max_q / (max_k + 1e-10))
+        self.stats['q_search_intensity'].append(max_q)
+        self.stats['k_info_density'].append(max_k)
+
+    # ------------------------------------------------------------ decode
+
+    def _compute_q_high_norm(self, q_vec: torch.Tensor, low_band: int = _LOW_BAND) -> float:
+        """||q_high||_2 of one head_dim vector (perplexity_eval.py:547-573)."""
+        return float(X.row_norms(q_vec.reshape(1, 1, 1, -1), low_band=low_band).item())
+
+    def _decode_attention(self, query, key, value, G):
+        B, Hq, _, d = query.shape
+        Hkv, Skv = key.shape[1], key.shape[2]
+        T = Skv // TILE
+        tiles = (Skv + TILE - 1) // TILE
+        tau = self._tau()
+        nc = self.norm_cache
+        if Hkv > nc.num_kv_heads or T > nc.max_tiles:
+            raise IndexError(f"norm cache ({nc.num_kv_heads} heads x {nc.max_tiles} tiles) is smaller than the "
+                             f"context ({Hkv} heads x {T} tiles)")
+        if self.score_new_tiles and T > self._prefill_tiles:
+            # the tiles completed since the prefill, scored from this call's K
+            nc.update_tiles(key[B - 1], self._prefill_tiles, T - self._prefill_tiles)
+        norms = nc.cache[:Hkv].unsqueeze(0)
+        qh = X.row_norms(query, low_band=_LOW_BAND).view(B, Hq)
+        # 1 = attend: complete tiles that pass the gate, and the partial last tile
+        keep, med = X.group_gate(qh, norms, Hkv, G, T, tiles, tau * TILE * d, N.OC_GROUP_MEDIAN, keep_polarity=True)
+        kv = X.rows_layout(key.reshape(B * Hkv, Skv, d), value.reshape(B * Hkv, Skv, d), partial_tail=True)
+        res = X.decode(kv, query.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0,
+                       mode=N.OC_MODE_CACHED, out_dtype=query.dtype, tile_mask=keep.view(B * Hkv, -1))
+        host = torch.stack([
+            (keep[:, :, :T] == 0).view(B, -1).sum(1, dtype=torch.int64).to(torch.float32),
+            med.amax(1).clamp(min=0.0),
+            norms[0, :, :T].amax().clamp(min=0.0).expand(B) if T > 0 else torch.zeros(
+                (B,), dtype=torch.float32, device=query.device),
+        ]).cpu().double()
+        for b in range(B):
+            skipped = int(host[0, b])
+            self._exhaust(float(host[1, b]), float(host[2, b]))
+            self.stats['decode_steps'] += 1
+            self.stats['decode_tiles_skipped'] += skipped
+            self.stats['decode_tiles_total'] += T * Hkv
+            if self.governor is not None and T > 0:
+                self.governor.report_layer(skipped / (T * Hkv))
+        self.stats['layers_processed'] += 1
+        return res.out.view(B, Hq, 1, d)
+
+    # ------------------------------------------------------------ dense
+
+    def _dense_attention(self, query, key, value, G):
+        """Causal attention with nothing gated (perplexity_eval.py:675-689)."""
+        key, value = _distinct_kv(query, key, value, G)
+        out, _ = X.prefill_attention(query, key, value)
+        return out
+
+
+def _distinct_kv(query, key, value, G):
+    """k, v with num_kv_heads = num_q_heads / G heads: a k, v already expanded
+    to num_q_heads heads by repeat_kv (head j copied to j*G .. j*G + G - 1)
+    is reduced to every G-th head."""
+    if G > 1 and key.shape[1] == query.shape[1]:
+        return key[:, ::G], value[:, ::G]
+    return key, value
+
+
+def patch_model_attention(model, orthocache: OrthoCache_GQA_Attention, min_layer: int = 0):
+    """Route the SDPA call of every decoder layer >= min_layer of a
+    transformers Llama-style model through `orthocache`
+    (perplexity_eval.py:693-741): during the layer's forward,
+    torch.nn.functional.scaled_dot_product_attention is replaced by the
+    hook (its mask, dropout and scale arguments are ignored, as there: the
+    hook is causal with scale 1/sqrt(head_dim))."""
+    num_kv_heads = model.config.num_key_value_heads
+    num_q_heads = model.config.num_attention_heads
+    G = num_q_heads // num_kv_heads
+    layers = model.model.layers
+    patched = 0
+    for idx, layer in enumerate(layers):
+        if idx < min_layer:
+            continue
+        attn = layer.self_attn
+
+        def make(original):
+            def patched_forward(*args, **kwargs):
+                def intercept(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False, scale=None,
+                              enable_gqa=False):
+                    return orthocache.orthocache_attention(query, key, value, num_query_groups=G)
+
+                saved = F.scaled_dot_product_attention
+                F.scaled_dot_product_attention = intercept
+                try:
+                    return original(*args, **kwargs)
+                finally:
+                    F.scaled_dot_product_attention = saved
+            return patched_forward
+
+        attn.forward = make(attn.forward)
+        patched += 1
+    print(f"  Patched {patched}/{len(layers)} layers (G={G}, layers {min_layer}-{len(layers) - 1})")
+    return model

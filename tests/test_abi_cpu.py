@@ -85,6 +85,41 @@ def test_gate_and_norm_cache_argument_checks():
     assert L.oc_apply_tile_mask(256, N.OC_F32, 4, 100, 100, None, 4, 2, 64, 1, None) == N.OC_ERR_INVALID
 
 
+def test_hook_entry_point_argument_checks():
+    """oc_prefill_attention, oc_row_norms, oc_kth_smallest and oc_group_gate
+    validate on the host; none of these calls launches."""
+    import ctypes
+    from orthocache_gpu import _native as N
+    L = N.lib()
+    assert L.oc_prefill_params_bytes() == ctypes.sizeof(N.OcPrefillParams)
+    p = N.OcPrefillParams()
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    assert b"NULL" in L.oc_last_error()
+    p.q = p.k = p.v = p.out = 256
+    p.dtype, p.head_dim, p.batch, p.num_q_heads, p.num_kv_heads, p.q_len, p.kv_len = N.OC_BF16, 96, 1, 4, 2, 8, 64
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_UNSUPPORTED
+    assert b"head_dim" in L.oc_last_error()
+    p.head_dim, p.dtype = 64, N.OC_FP8_E4M3FN
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_UNSUPPORTED
+    p.dtype, p.num_kv_heads = N.OC_F16, 3
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    assert b"multiple" in L.oc_last_error()
+    p.num_kv_heads, p.k_stride_s = 2, 65  # 130-byte token stride breaks the 16-byte loads
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    assert b"16 bytes" in L.oc_last_error()
+    p.k_stride_s, p.v_stride_s, p.q_stride_s = 64, 64, 64
+    p.tile_mask, p.tile_mask_cols, p.kv_len = 256, 1, 200
+    assert L.oc_prefill_attention(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    assert b"tile_mask" in L.oc_last_error()
+    assert L.oc_row_norms(256, N.OC_F32, 1, 1, 4, 0, 0, 64, 60, 8, 256, None) == N.OC_ERR_INVALID
+    assert b"low_band" in L.oc_last_error()
+    assert L.oc_kth_smallest(256, 2, 5, 5, 5, 256, None) == N.OC_ERR_INVALID
+    assert L.oc_kth_smallest(256, 2, 5, 4, 1, 256, None) == N.OC_ERR_INVALID
+    assert L.oc_group_gate(256, 1, 2, 4, 7, 256, 0, 8, 4, 4, 1.0, 0, 256, 8, 4, None, None) == N.OC_ERR_INVALID
+    assert L.oc_group_gate(256, 1, 2, 4, N.OC_GROUP_MAX, 256, 0, 8, 5, 4, 1.0, 0, 256, 8, 4, None,
+                           None) == N.OC_ERR_INVALID
+
+
 def test_reference_assertion_messages():
     """test_fp8.py:128-158 and test_paged_eviction.py:139-159 of the reference."""
     from orthocache_gpu import (fused_orthocache_attention, fused_orthocache_attention_paged,

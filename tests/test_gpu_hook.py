@@ -1,0 +1,241 @@
+"""GPU parity of the model-side hook (OrthoCache_GQA_Attention and its
+kernels) against the oracle: oc_prefill_attention (causal GQA attention
+with evicted tiles and the attention entropy), oc_row_norms,
+oc_kth_smallest, oc_group_gate, the hook's prefill and decode branches
+call for call (outputs, statistics, norm cache, governor), and a
+transformers Llama model patched with the hook.
+
+Bars: float32 outputs within 1e-5 (+1e-5 relative); float16 / bfloat16
+outputs within 2e-3 plus half an output ulp of the float64 oracle; masks and
+selections bit-exact (thresholds placed away from every decision); entropy
+within 1e-4.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import orthocache_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import orthocache_gpu._native as N
+    N.lib()
+    yield
+
+
+def np64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _tol(dtype, ref):
+    if dtype == "f32":
+        return 1e-5 + 1e-5 * np.abs(ref)
+    return 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == "bf16" else 2.0 ** -11)
+
+
+def _qkv(B, Hq, Hkv, Sq, Skv, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, Sq, Hq, d), generator=g).to(TD[dtype]).to(DEV)
+    k = torch.randn((B, Hkv, Skv + 5, d), generator=g).to(TD[dtype]).to(DEV)
+    v = torch.randn((B, Hkv, Skv, d), generator=g).to(TD[dtype]).to(DEV)
+    # q as the (B, S, H, d) -> (B, H, S, d) view a decoder layer passes; k a
+    # slice of a longer cache (strides of Skv + 5 tokens)
+    return q.transpose(1, 2), k[:, :, :Skv], v
+
+
+CASES = [  # B, Hq, Hkv, Sq, Skv, d
+    (2, 8, 2, 200, 200, 64),    # prefill with a partial last tile
+    (1, 4, 4, 37, 300, 128),    # chunk of queries at the end of a longer context
+    (1, 4, 1, 100, 64, 64),     # more queries than keys: the first 36 see none
+    (2, 8, 2, 1, 333, 128),     # one query
+    (1, 16, 2, 130, 130, 128),  # G = 8
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("masked", [False, True])
+def test_prefill_attention_vs_oracle(dtype, case, masked):
+    from orthocache_gpu import _launch as X
+    B, Hq, Hkv, Sq, Skv, d = case
+    G = Hq // Hkv
+    q, k, v = _qkv(B, Hq, Hkv, Sq, Skv, d, dtype, seed=sum(case))
+    evict = None
+    tm = None
+    if masked:
+        evict = torch.rand((B, Hkv, Skv // 64), generator=torch.Generator().manual_seed(3)) < 0.5
+        tm = evict.to(torch.uint8).to(DEV)
+    print(f"prefill {dtype} {case} masked={masked}", flush=True)
+    out, ent = X.prefill_attention(q, k, v, tile_mask=tm, want_entropy=True)
+    torch.cuda.synchronize()
+    ref, ref_ent = O.hook_causal_attention(np64(q), np64(k), np64(v), G,
+                                           None if evict is None else evict.numpy())
+    ref = O.round_to(ref, dtype) if dtype != "f32" else ref
+    assert out.dtype == q.dtype and out.shape == (B, Hq, Sq, d)
+    err = np.abs(np64(out) - ref)
+    assert (err <= _tol(dtype, ref)).all(), float(err.max())
+    np.testing.assert_allclose(np64(ent), ref_ent, atol=1e-4, rtol=1e-5)
+
+
+def test_row_norms_and_selection():
+    from orthocache_gpu import _launch as X
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn((2, 70, 6, 64), generator=g).transpose(1, 2).to(DEV)  # (2, 6, 70, 64) strided
+    got = X.row_norms(x)
+    np.testing.assert_allclose(np64(got), np.linalg.norm(np64(x), axis=-1), rtol=2e-6)
+    hi = X.row_norms(x, low_band=8)
+    np.testing.assert_allclose(np64(hi), O.q_high_norm_exact(x.float().cpu().numpy(), 8), rtol=8 * 2.0 ** -23,
+                               atol=1e-6)
+    for n in (1, 2, 7, 1000, 4097):
+        vals = torch.rand((5, n), generator=g) * 10
+        vals[:, ::3] = vals[:, ::3].round()  # ties
+        vals[1, :n // 2] = 0.0
+        srt = np.sort(vals.numpy(), axis=1)
+        for k in {0, (n - 1) // 2, n - 1}:
+            sel = X.kth_smallest(vals.to(DEV), k)
+            assert np.array_equal(sel.cpu().numpy(), srt[:, k]), (n, k)
+
+
+@pytest.mark.parametrize("reduce", ["max", "median"])
+def test_group_gate_vs_loops(reduce):
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rng = np.random.default_rng(5)
+    B, Hkv, G, T, cols = 3, 4, 4, 37, 40
+    qn = rng.uniform(0, 20, size=(B, Hkv * G)).astype(np.float32)
+    kn = rng.uniform(0, 30, size=(B, Hkv, 48)).astype(np.float32)
+    tau_norm = 150.0
+    mode = N.OC_GROUP_MAX if reduce == "max" else N.OC_GROUP_MEDIAN
+    for keep in (False, True):
+        for shared in (False, True):
+            kn_t = torch.from_numpy(kn[:1] if shared else kn).to(DEV)
+            mask, gn = X.group_gate(torch.from_numpy(qn).to(DEV), kn_t, Hkv, G, T, cols, tau_norm, mode,
+                                    keep_polarity=keep)
+            mask, gn = mask.cpu().numpy(), gn.cpu().numpy()
+            for b in range(B):
+                for h in range(Hkv):
+                    grp = qn[b, h * G:(h + 1) * G]
+                    want = grp.max() if reduce == "max" else np.sort(grp)[G // 2]
+                    assert gn[b, h] == want
+                    knr = kn[0 if shared else b, h]
+                    for t in range(cols):
+                        ev = t < T and np.float32(want) * knr[t] <= np.float32(tau_norm)
+                        assert mask[b, h, t] == (int(not ev) if keep else int(ev))
+
+
+def _gap_tau(prods):
+    """a threshold in the widest relative gap of the middle half of prods"""
+    p = np.sort(prods.ravel())
+    p = p[p > 0]
+    lo, hi = len(p) // 4, 3 * len(p) // 4
+    gaps = p[lo + 1:hi + 1] / p[lo:hi]
+    i = lo + int(np.argmax(gaps))
+    assert p[i + 1] / p[i] > 1 + 1e-4
+    return float(np.sqrt(p[i] * p[i + 1]))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_hook_prefill_then_decode_vs_oracle(dtype):
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention, ResidualGovernor
+    from orthocache_gpu.norm_cache import SpectralNormCache
+    B, Hq, Hkv, d, S = 2, 8, 2, 64, 320
+    G = Hq // Hkv
+    q, k, v = _qkv(B, Hq, Hkv, S, S + 10, d, dtype, seed=11)
+    kp, vp = k[:, :, :S], v[:, :, :S]
+    probe = O.hook_prefill(np64(q), np64(kp), np64(vp), G, tau=-1.0)
+    tau = _gap_tau(probe["qn"][:, :, None].astype(np.float64) * probe["k_norms"] / (64 * d))
+    gov = ResidualGovernor(alpha=0.5)
+    hook = OrthoCache_GQA_Attention(tau=tau, governor=gov)
+    hook.norm_cache = SpectralNormCache(Hkv, 16, torch.device(DEV))
+    print(f"hook prefill {dtype} tau={tau}", flush=True)
+    out = hook.orthocache_attention(q, kp, vp, G)
+    ref = O.hook_prefill(np64(q), np64(kp), np64(vp), G, tau)
+    r = O.round_to(ref["out"], dtype) if dtype != "f32" else ref["out"]
+    assert (np.abs(np64(out) - r) <= _tol(dtype, r)).all()
+    T = S // 64
+    assert 0 < ref["evict"].sum() < B * Hkv * T
+    assert hook.stats['total_tiles'] == B * Hkv * T
+    assert hook.stats['evicted_tiles'] == int(ref["evicted"].sum())
+    np.testing.assert_allclose(hook.stats['hallucination_scores'], ref["h_score"], rtol=1e-5)
+    np.testing.assert_allclose(hook.stats['q_search_intensity'], ref["max_q"], rtol=1e-5)
+    np.testing.assert_allclose(hook.stats['k_info_density'], ref["max_k"], rtol=1e-5)
+    np.testing.assert_allclose(gov.layer_history, ref["evicted"] / (Hkv * T), rtol=1e-12)
+    nc = hook.norm_cache
+    np.testing.assert_allclose(np64(nc.cache[:, :T]), ref["k_norms"][B - 1], rtol=4 * 2.0 ** -23)
+    assert nc.valid_tiles.cpu().tolist() == [T, T] and nc.is_populated
+    # decode: one query per head over 330 keys (5 complete tiles and 10 tokens)
+    hook.governor = None
+    q1 = q[:, :, -1:]
+    nc_np = np64(nc.cache)
+    probe = O.hook_decode(np64(q1), np64(k), np64(v), nc_np, G, tau=-1.0)
+    hook.tau = _gap_tau(probe["qn"][:, :, None].astype(np.float64) * nc_np[None, :, :T] / (64 * d))
+    print(f"hook decode {dtype} tau={hook.tau}", flush=True)
+    out1 = hook.orthocache_attention(q1, k, v, G)
+    ref1 = O.hook_decode(np64(q1), np64(k), np64(v), nc_np, G, hook.tau)
+    r1 = O.round_to(ref1["out"], dtype) if dtype != "f32" else ref1["out"]
+    assert out1.shape == (B, Hq, 1, d)
+    assert (np.abs(np64(out1) - r1) <= _tol(dtype, r1)).all()
+    assert 0 < ref1["skipped"].sum() < B * Hkv * T
+    assert hook.stats['decode_steps'] == B
+    assert hook.stats['decode_tiles_skipped'] == int(ref1["skipped"].sum())
+    assert hook.stats['decode_tiles_total'] == B * Hkv * T
+    np.testing.assert_allclose(hook.stats['hallucination_scores'][B:], ref1["h_score"], rtol=1e-5)
+    assert hook.stats['layers_processed'] == 2
+
+
+def test_hook_entropy_governor_and_short_context():
+    from orthocache_gpu.model_hook import EntropyGovernor, OrthoCache_GQA_Attention
+    B, Hq, Hkv, d, S = 2, 4, 2, 128, 150
+    q, k, v = _qkv(B, Hq, Hkv, S, S, d, "f32", seed=12)
+    gov = EntropyGovernor(alpha=0.5, beta=1.0, h_median=1.56)
+    hook = OrthoCache_GQA_Attention(tau=-1.0, governor=gov)
+    hook.orthocache_attention(q, k, v, 2)
+    ref = O.hook_prefill(np64(q), np64(k), np64(v), 2, -1.0)
+    np.testing.assert_allclose(gov.current_entropy, ref["entropy"][-1], rtol=1e-5)
+    np.testing.assert_allclose(hook.stats['entropy'], ref["entropy"][-1], rtol=1e-5)
+    assert hook.norm_cache is None and hook.stats['evicted_tiles'] == 0
+    # under 64 keys: dense causal attention, no statistics
+    qs, ks, vs = _qkv(1, 4, 2, 40, 40, 64, "bf16", seed=13)
+    out = OrthoCache_GQA_Attention(tau=1.0).orthocache_attention(qs, ks, vs, 2)
+    ref_s, _ = O.hook_causal_attention(np64(qs), np64(ks), np64(vs), 2)
+    r = O.round_to(ref_s, "bf16")
+    assert (np.abs(np64(out) - r) <= _tol("bf16", r)).all()
+
+
+def test_hf_llama_patched_matches_dense():
+    transformers = pytest.importorskip("transformers")
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention, patch_model_attention
+    from orthocache_gpu.norm_cache import SpectralNormCache
+    cfg = transformers.LlamaConfig(vocab_size=128, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    model = transformers.LlamaForCausalLM(cfg).to(DEV).eval()
+    ids = torch.randint(0, 128, (2, 104), generator=torch.Generator().manual_seed(1)).to(DEV)
+
+    def run():
+        with torch.no_grad():
+            o = model(ids[:, :100], use_cache=True)
+            logits, past = [o.logits[:, -1]], o.past_key_values
+            for s in range(100, 104):
+                o = model(ids[:, s:s + 1], past_key_values=past, use_cache=True)
+                logits.append(o.logits[:, -1])
+                past = o.past_key_values
+        return torch.stack(logits)
+
+    want = run()
+    hook = OrthoCache_GQA_Attention(tau=-1.0)  # nothing is evicted: the hook must equal dense attention
+    hook.norm_cache = SpectralNormCache(2, 8, torch.device(DEV))
+    patch_model_attention(model, hook)
+    got = run()
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
+    assert hook.stats['layers_processed'] == 2 * 5
+    assert hook.stats['decode_steps'] == 2 * 2 * 4 and hook.stats['decode_tiles_skipped'] == 0

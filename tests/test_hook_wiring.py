@@ -1,0 +1,82 @@
+"""CPU tests of the model hook's host logic: patch_model_attention routes
+every decoder layer >= min_layer of a transformers Llama model through the
+hook with (batch, heads, seq, head_dim) tensors (a tiny random-init model;
+the hook's attention is replaced by torch's SDPA here, since the kernels
+need the GPU), and the governors follow the reference's formulas."""
+
+import math
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+
+
+def _tiny_llama(layers=3):
+    cfg = transformers.LlamaConfig(vocab_size=96, hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                                   num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    return transformers.LlamaForCausalLM(cfg).eval()
+
+
+def test_patch_routes_sdpa_through_hook():
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention, patch_model_attention
+    model = _tiny_llama()
+    ids = torch.randint(0, 96, (2, 40), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        want = model(ids).logits
+    hook = OrthoCache_GQA_Attention(tau=0.5)
+    seen = []
+    sdpa = torch.nn.functional.scaled_dot_product_attention  # the patch swaps the module attribute
+
+    def fake(query, key, value, num_query_groups):
+        seen.append((tuple(query.shape), tuple(key.shape), num_query_groups))
+        return sdpa(query, key, value, is_causal=query.shape[2] > 1, enable_gqa=True)
+
+    hook.orthocache_attention = fake
+    patch_model_attention(model, hook, min_layer=1)
+    with torch.no_grad():
+        got = model(ids).logits
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+    assert seen == [((2, 4, 40, 32), (2, 2, 40, 32), 2)] * 2  # layers 1 and 2 only
+    # the module-level SDPA is restored after each layer
+    assert torch.nn.functional.scaled_dot_product_attention is sdpa
+
+
+def test_governors():
+    from oracle import orthocache_oracle as O
+    from orthocache_gpu.model_hook import EntropyGovernor, ResidualGovernor
+    g = ResidualGovernor(alpha=0.5)
+    for r in (0.2, 0.3):
+        g.report_layer(r)
+    assert g.get_tau_effective(2.0) == O.residual_tau(2.0, 0.5, [0.2, 0.3])
+    assert g.layer_history == [0.2, 0.3]
+    g.reset()
+    assert g.eps_accum == 0.0 and g.get_tau_effective(2.0) == 2.0
+    e = EntropyGovernor(alpha=0.5, beta=2.0, h_median=1.0)
+    assert e.get_tau_effective(1.0) == 1.0
+    e.report_layer(0.4)
+    e.set_entropy(1.5)
+    assert math.isclose(e.get_tau_effective(1.0), O.entropy_tau(1.0, 0.5, [0.4], 2.0, 1.0, 1.5), rel_tol=1e-15)
+
+
+def test_hook_stats_shape():
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention
+    h = OrthoCache_GQA_Attention(tau=2.0)
+    assert h.eviction_rate == 0.0 and h.norm_cache is None
+    assert set(h.stats) == {'total_tiles', 'evicted_tiles', 'layers_processed', 'cs_bounds',
+                            'hallucination_scores', 'q_search_intensity', 'k_info_density', 'decode_steps',
+                            'decode_tiles_skipped', 'decode_tiles_total'}
+    h.stats['total_tiles'], h.stats['evicted_tiles'] = 10, 4
+    assert h.eviction_rate == 0.4
+    h.reset_stats()
+    assert h.stats['total_tiles'] == 0
+
+
+def test_hook_fails_loudly_on_cpu_tensors():
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention
+    q = torch.randn(1, 4, 70, 64)
+    k = torch.randn(1, 2, 70, 64)
+    with pytest.raises((RuntimeError, ValueError)):
+        OrthoCache_GQA_Attention(tau=1.0).orthocache_attention(q, k, k, 2)
