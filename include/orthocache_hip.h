@@ -49,6 +49,11 @@
  *   oc_group_gate   <- the per-(kv head, tile) Cauchy-Schwarz compares of the
  *                      prefill and decode branches (perplexity_eval.py:476-491,
  *                      :639-657)
+ * orthocache_forward(mode='compact') (src/orthocache_gpu/ of the reference tree):
+ *   oc_block_spectra <- fwht_512 (fwht.py:6-45) with compute_spectral_bands,
+ *                      compute_spectral_decay_ratio, compute_block_energy and
+ *                      compute_query_aware_bounds (spectral_energy.py:26-200)
+ *   oc_stream_compact <- stream_compact (adaptive_attention.py:33-45)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -316,6 +321,58 @@ int oc_prefill_attention(const oc_prefill_params* p, void* stream);
 
 /* sizeof(oc_prefill_params) as compiled, for binding checks */
 size_t oc_prefill_params_bytes(void);
+
+/*
+ * oc_block_spectra -- statistics of the normalised natural-order 512-point
+ * Walsh-Hadamard transform X = H512 K_b / sqrt(512) of every 512-token
+ * block b and head h of K (seq, num_heads, head_dim), as written by
+ * fwht_512 (fwht.py:6-45), accumulated in float32:
+ *   e_low  = sum_{u in [1, 64)}    ||X[u]||^2    e_mid = sum_{u in [64, 256)} ||X[u]||^2
+ *   e_high = sum_{u in [256, 512)} ||X[u]||^2    zeta  = e_high / (e_low + 1e-6)
+ *   e_ac   = e_low + e_mid + e_high (all rows but DC)
+ *   energy = sum_t ||k_t||^2 (compute_block_energy)
+ *   block_mean[b, h, :] = X[0] / sqrt(512)
+ * each (num_blocks, num_heads) float32, any may be NULL.  With q (q_len,
+ * num_heads, head_dim) given, the query-aware bounds of
+ * compute_query_aware_bounds (spectral_energy.py:140-180)
+ *   bound[s, b, h] = (q_s . block_mean + ||q_s|| sqrt(e_ac)) / sqrt(head_dim)
+ * go to bounds (q_len, num_blocks, num_heads) and their max over s to
+ * max_bound (num_blocks, num_heads), each if given.  block_size must be
+ * 512; head_dim a multiple of 8 up to 256; K rows 16-byte aligned.
+ */
+typedef struct oc_spectra_params {
+  const void* k;
+  int32_t dtype;                  /* OC_F32 / OC_F16 / OC_BF16 */
+  int32_t num_blocks, num_heads, head_dim, block_size;
+  int64_t k_token_stride, k_head_stride;  /* elements */
+  const void* q;                  /* (q_len, num_heads, head_dim) or NULL */
+  int32_t q_dtype, q_len;
+  int64_t q_token_stride, q_head_stride;  /* elements */
+  float* e_low;
+  float* e_mid;
+  float* e_high;
+  float* zeta;
+  float* e_ac;
+  float* energy;
+  float* block_mean;              /* (num_blocks, num_heads, head_dim) */
+  float* bounds;                  /* (q_len, num_blocks, num_heads) */
+  float* max_bound;               /* (num_blocks, num_heads) */
+} oc_spectra_params;
+
+int oc_block_spectra(const oc_spectra_params* p, void* stream);
+
+/* sizeof(oc_spectra_params) as compiled, for binding checks */
+size_t oc_spectra_params_bytes(void);
+
+/*
+ * oc_stream_compact -- the active-first stable permutation of num_blocks
+ * blocks (block_mask != 0 = retained): indices[r] (int64) is the r-th
+ * retained block, followed by the evicted blocks in order, and
+ * *num_active the retained count (device int32).  Replaces stream_compact
+ * (adaptive_attention.py:33-45), an argsort of where(mask, i, n + i).
+ */
+int oc_stream_compact(const uint8_t* block_mask, int32_t num_blocks, int64_t* indices, int32_t* num_active,
+                      void* stream);
 
 /* decode parameters; see oc_decode */
 typedef struct oc_decode_params {

@@ -31,6 +31,10 @@ paths with the same per-head, per-tile loop structure:
   of the reference tree: prefill branch :399-545, decode branch :575-673,
   dense fallback :675-689); ``torch_lower_median`` <- torch.median(dim)
   (:456); ``residual_tau`` / ``entropy_tau`` <- the governors (:236-318)
+* ``fwht512``, ``block_spectra``, ``compact_forward`` <- the 512-token
+  compact pipeline of orthocache_forward (fwht.py:6-45,
+  spectral_energy.py:20-233, perfect_eviction.py:75-186,
+  adaptive_attention.py:29-215, pipeline.py:458-583 of src/orthocache_gpu/)
 
 (all paths relative to ``src/orthocache_gpu/triton_kernels/`` or
 ``src/orthocache_gpu/`` of the reference tree).
@@ -68,6 +72,11 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   attention == ln n, the median rank rules on explicit lists, and the
   gate's decisions by an explicit per-(kv head, tile) loop
   (tests/test_oracle_hook.py).
+* compact pipeline: fwht512 against the Sylvester matrix H512 / sqrt(512)
+  and its involution, the band energies against closed forms (E_high =
+  1/2 sum ||k_j - k_{j+256}||^2) and Parseval, constant blocks with zero AC
+  energy, the bound >= every logit of the block (Cauchy-Schwarz), and
+  stream compaction against torch.argsort (tests/test_oracle_compact.py).
 """
 
 from __future__ import annotations
@@ -829,3 +838,110 @@ def hook_decode(q, k, v, norm_cache: np.ndarray, G: int, tau: float, low_band: i
     max_k = np.full(B, max(0.0, float(nc[:Hkv, :T].max())) if T else 0.0)
     return {"out": out, "evict": evict, "qn": qn, "skipped": evict.reshape(B, -1).sum(axis=1),
             "max_q": max_q, "max_k": max_k, "h_score": max_q / (max_k + 1e-10)}
+
+
+# ---------------------------------------------------------------- compact pipeline
+# src/orthocache_gpu/ of the reference tree
+
+COMPACT_BLOCK = 512
+F32_UNDERFLOW = 88.72  # perfect_eviction.py:47
+
+
+def fwht512(x: np.ndarray) -> np.ndarray:
+    """Normalised natural-order 512-point Walsh-Hadamard transform along axis
+    0 (fwht.py:6-45: nine radix-2 stages, each pairing the elements whose
+    index differs in one bit, then / sqrt(512)), float64."""
+    y = np.array(x, dtype=np.float64).copy()
+    n = y.shape[0]
+    assert n == COMPACT_BLOCK
+    h = 1
+    while h < n:
+        y = y.reshape(n // (2 * h), 2, h, *y.shape[1:])
+        a, b = y[:, 0].copy(), y[:, 1].copy()
+        y[:, 0], y[:, 1] = a + b, a - b
+        y = y.reshape(n, *y.shape[3:])
+        h *= 2
+    return y / math.sqrt(n)
+
+
+def block_spectra(keys: np.ndarray, q: Optional[np.ndarray] = None):
+    """Per 512-token block b and head h of keys (S, H, d): the band energies
+    of fwht512 (spectral_energy.py:68-105; [1,64), [64,256), [256,512)),
+    zeta = high / (low + 1e-6) (:108-137), AC energy (rows 1..511), spatial
+    energy (:20-34), block mean = X[0] / sqrt(512), and with q (Sq, H, d)
+    the query-aware bounds (:140-176) (Sq, nb, H) -- all float64."""
+    k = np.asarray(keys, dtype=np.float64)
+    S, H, d = k.shape
+    nb = S // COMPACT_BLOCK
+    out = {n: np.zeros((nb, H)) for n in ("e_low", "e_mid", "e_high", "zeta", "e_ac", "energy")}
+    out["block_mean"] = np.zeros((nb, H, d))
+    for b in range(nb):
+        for h in range(H):
+            blk = k[b * COMPACT_BLOCK:(b + 1) * COMPACT_BLOCK, h]
+            X = fwht512(blk)
+            e = np.sum(X * X, axis=1)
+            out["e_low"][b, h] = e[1:64].sum()
+            out["e_mid"][b, h] = e[64:256].sum()
+            out["e_high"][b, h] = e[256:].sum()
+            out["zeta"][b, h] = out["e_high"][b, h] / (out["e_low"][b, h] + 1e-6)
+            out["e_ac"][b, h] = e[1:].sum()
+            out["energy"][b, h] = np.sum(blk * blk)
+            out["block_mean"][b, h] = X[0] / math.sqrt(COMPACT_BLOCK)
+    if q is not None:
+        qq = np.asarray(q, dtype=np.float64)
+        align = np.einsum("qhd,bhd->qbh", qq, out["block_mean"]) / math.sqrt(d)
+        resid = np.linalg.norm(qq, axis=-1)[:, None, :] * np.sqrt(out["e_ac"])[None] / math.sqrt(d)
+        out["bounds"] = align + resid
+        out["max_bound"] = out["bounds"].max(axis=0)
+    return out
+
+
+def compact_forward(q, keys, values, zeta_max: float = 5.0, tau: Optional[float] = None):
+    """orthocache_forward(mode='compact') past the crossover bypass
+    (pipeline.py:458-555): tau = mean - std (unbiased) of the max bounds
+    when not given (:571-583); (block, head) retained iff max bound >= tau
+    and zeta <= zeta_max (spectral_energy.py:198-233); a block is attended
+    when any head retains it; every query attends every key of the attended
+    blocks (adaptive_attention.py:46-91, online softmax from -1e30).
+    Returns (out float64 (Sq, H, d), info dict: tau, block_mask, unified,
+    retained, zeta stats, perfect / statistical counts)."""
+    q64 = np.asarray(q, dtype=np.float64)
+    k64 = np.asarray(keys, dtype=np.float64)
+    v64 = np.asarray(values, dtype=np.float64)
+    Sq, H, d = q64.shape
+    spec = block_spectra(k64, q64)
+    mb = spec["max_bound"]
+    nb = mb.shape[0]
+    if tau is None:
+        tau = float(mb.mean() - mb.std(ddof=1))
+    block_mask = (mb >= tau) & (spec["zeta"] <= zeta_max)
+    unified = block_mask.any(axis=1)
+    retained = int(unified.sum())
+    zah = spec["zeta"].mean(axis=1)
+    # perfect-eviction classification (perfect_eviction.py:75-186)
+    z_max = float(mb[unified].max()) if retained else 0.0
+    qmax = np.linalg.norm(q64, axis=-1).max(axis=0)
+    beta = (qmax[None, :] * np.sqrt(np.maximum(spec["energy"], 0.0)) / math.sqrt(d)).max(axis=1)
+    gap = z_max - beta
+    perfect = int(((~unified) & (gap >= F32_UNDERFLOW)).sum())
+    statistical = int(((~unified) & (gap < F32_UNDERFLOW)).sum())
+    out = np.zeros((Sq, H, d))
+    if retained:
+        keep = np.repeat(unified, COMPACT_BLOCK)
+        for h in range(H):
+            kk = k64[:nb * COMPACT_BLOCK, h][keep]
+            vv = v64[:nb * COMPACT_BLOCK, h][keep]
+            lg = q64[:, h] @ kk.T / math.sqrt(d)
+            p = np.exp(lg - lg.max(axis=1, keepdims=True))
+            out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ vv
+    return out, {"tau": tau, "block_mask": block_mask, "unified": unified, "retained": retained,
+                 "zeta_mean": float(zah.mean()), "zeta_std": float(zah.std(ddof=1)) if nb > 1 else float("nan"),
+                 "zeta_min": float(zah.min()), "zeta_max_observed": float(zah.max()),
+                 "perfect": perfect, "statistical": statistical, "spectra": spec}
+
+
+def stream_compact(mask: np.ndarray):
+    """(active-first stable order, count) (adaptive_attention.py:29-43)."""
+    mask = np.asarray(mask, dtype=bool)
+    idx = [i for i in range(mask.size) if mask[i]] + [i for i in range(mask.size) if not mask[i]]
+    return np.array(idx, dtype=np.int64), int(mask.sum())

@@ -1,0 +1,306 @@
+// The 512-token block spectra of orthocache_forward(mode='compact') and its
+// stream compaction (declared in include/orthocache_hip.h).
+//
+// The normalised 512-point Walsh-Hadamard transform along tokens, X =
+// H512 K / sqrt(512) in natural (Hadamard) order, factors over the token
+// index t = 64 th + tl and the sequency u = 64 uh + ul as H512[u, t] =
+// H8[uh, th] H64[ul, tl].  With Z_uh[tl] = sum_th H8[uh, th] K[64 th + tl]
+// (an 8-point transform across the block's eight 64-token chunks),
+// X[64 uh + ul] = (H64 Z_uh)[ul] / sqrt(512), and by Parseval over ul
+//   sum_ul ||X[64 uh + ul]||^2 = ||Z_uh||_F^2 / 8.
+// So the bands [64, 256) (uh = 1..3) and [256, 512) (uh = 4..7) are sums of
+// squares of the 8-point outputs, computed in registers as the block
+// streams in; the band [1, 64) and the DC row need the 64-point transform
+// of Z_0 along tl, done per column from LDS.  Every band energy is a sum of
+// squares, so near-zero bands stay exact-ish instead of cancelling.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "oc_status.h"
+#include "orthocache_hip.h"
+
+namespace oc {
+namespace {
+
+constexpr int kSpThreads = 256;
+constexpr int kBlock = 512;
+constexpr int kMaxD = 256;
+
+struct SpecArgs {
+  const char* k;
+  int64_t k_ts, k_hs;  // byte strides: token, head
+  int32_t H, d, nb, dtype;
+  const char* q;       // (Sq, H, d) or null
+  int64_t q_ss, q_hs;  // byte strides
+  int32_t Sq, q_dtype;
+  float* e_low;
+  float* e_mid;
+  float* e_high;
+  float* zeta;
+  float* e_ac;
+  float* energy;
+  float* mean;        // (nb, H, d) block mean = DC / sqrt(512), or null
+  float* bounds;      // (Sq, nb, H) or null
+  float* max_bound;   // (nb, H) or null
+};
+
+__device__ __forceinline__ float sp_load(const char* p, int dtype) {
+  if (dtype == OC_F32) return *reinterpret_cast<const float*>(p);
+  const uint16_t u = *reinterpret_cast<const uint16_t*>(p);
+  if (dtype == OC_BF16) return __uint_as_float((uint32_t)u << 16);
+  return (float)__builtin_bit_cast(_Float16, u);
+}
+
+// eight consecutive elements of a row (16-byte aligned for 16-bit types,
+// 32-byte for float32)
+template <int DT>
+__device__ __forceinline__ void load8(const char* p, float (&x)[8]) {
+  if constexpr (DT == OC_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 16);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == OC_BF16) {
+        x[2 * i] = __uint_as_float(w[i] << 16);
+        x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+      } else {
+        x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFFu));
+        x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float block_sum(float v, float* sh_red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh_red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < kSpThreads / 64; ++i) s += sh_red[i];
+  return s;
+}
+
+__device__ __forceinline__ float block_max(float v, float* sh_red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh_red[w] = v;
+  __syncthreads();
+  float s = sh_red[0];
+  for (int i = 1; i < kSpThreads / 64; ++i) s = fmaxf(s, sh_red[i]);
+  return s;
+}
+
+// One workgroup per (512-token block, head).  Thread (tg, cg) owns columns
+// 8cg .. 8cg + 8 and the within-chunk positions tl = tg + i * TG.
+template <int DT>
+__global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecArgs a) {
+  __shared__ float sh_z[64 * kMaxD];  // Z_0[tl][c]
+  __shared__ float sh_mean[kMaxD];
+  __shared__ float sh_red[kSpThreads / 64];
+  const int blk = blockIdx.x;
+  const int h = blockIdx.y;
+  const int d = a.d;
+  const int CG = d / 8;
+  const int TG = kSpThreads / CG;
+  const int tid = threadIdx.x;
+  const int cg = tid % CG;
+  const int tg = tid / CG;
+  const char* kb = a.k + (int64_t)blk * kBlock * a.k_ts + (int64_t)h * a.k_hs + (int64_t)cg * 8 * (DT == OC_F32 ? 4 : 2);
+  float e_mid = 0.f, e_high = 0.f, energy = 0.f;
+  for (int tl = tg; tl < 64; tl += TG) {
+    float x[8][8];  // [th][column]
+#pragma unroll
+    for (int th = 0; th < 8; ++th) load8<DT>(kb + (int64_t)(64 * th + tl) * a.k_ts, x[th]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float z[8];
+#pragma unroll
+      for (int th = 0; th < 8; ++th) {
+        z[th] = x[th][c];
+        energy = __builtin_fmaf(z[th], z[th], energy);
+      }
+      // natural-order 8-point Walsh-Hadamard transform over th (unnormalised)
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (!(i & m)) {
+            const float u = z[i], v = z[i + m];
+            z[i] = u + v;
+            z[i + m] = u - v;
+          }
+#pragma unroll
+      for (int uh = 1; uh < 4; ++uh) e_mid = __builtin_fmaf(z[uh], z[uh], e_mid);
+#pragma unroll
+      for (int uh = 4; uh < 8; ++uh) e_high = __builtin_fmaf(z[uh], z[uh], e_high);
+      sh_z[tl * d + 8 * cg + c] = z[0];
+    }
+  }
+  __syncthreads();
+  // 64-point transform of Z_0 along tl, one column per thread
+  float e_low = 0.f, dc2 = 0.f;
+  if (tid < d) {
+    float y[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) y[i] = sh_z[i * d + tid];
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1)
+#pragma unroll
+      for (int i = 0; i < 64; ++i)
+        if (!(i & m)) {
+          const float u = y[i], v = y[i + m];
+          y[i] = u + v;
+          y[i + m] = u - v;
+        }
+#pragma unroll
+    for (int i = 1; i < 64; ++i) e_low = __builtin_fmaf(y[i], y[i], e_low);
+    dc2 = y[0] * y[0];
+    sh_mean[tid] = y[0] * (1.0f / 512.0f);  // DC / sqrt(512) with DC = sum_t k_t / sqrt(512)
+  }
+  const float s_mid = block_sum(e_mid, sh_red) * 0.125f;
+  const float s_high = block_sum(e_high, sh_red) * 0.125f;
+  const float s_low = block_sum(e_low, sh_red) * (1.0f / 512.0f);
+  const float s_energy = block_sum(energy, sh_red);
+  (void)dc2;
+  const float s_ac = s_low + s_mid + s_high;
+  const int64_t o = (int64_t)blk * a.H + h;
+  if (tid == 0) {
+    if (a.e_low) a.e_low[o] = s_low;
+    if (a.e_mid) a.e_mid[o] = s_mid;
+    if (a.e_high) a.e_high[o] = s_high;
+    if (a.zeta) a.zeta[o] = s_high / (s_low + 1e-6f);
+    if (a.e_ac) a.e_ac[o] = s_ac;
+    if (a.energy) a.energy[o] = s_energy;
+  }
+  __syncthreads();  // sh_mean complete
+  if (a.mean && tid < d) a.mean[o * d + tid] = sh_mean[tid];
+  if (!a.q) return;
+  // query-aware bounds: (q . mean + ||q|| sqrt(E_ac)) / sqrt(d)
+  const float inv_sd = 1.0f / __builtin_sqrtf((float)d);
+  const float sq_ac = __builtin_sqrtf(fmaxf(s_ac, 0.f));
+  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
+  float best = -__builtin_inff();
+  for (int s = tid; s < a.Sq; s += kSpThreads) {
+    const char* qr = a.q + (int64_t)s * a.q_ss + (int64_t)h * a.q_hs;
+    float dot = 0.f, nn = 0.f;
+    for (int c = 0; c < d; ++c) {
+      const float qv = sp_load(qr + (int64_t)c * qes, a.q_dtype);
+      dot = __builtin_fmaf(qv, sh_mean[c], dot);
+      nn = __builtin_fmaf(qv, qv, nn);
+    }
+    const float bnd = dot * inv_sd + __builtin_sqrtf(nn) * sq_ac * inv_sd;
+    if (a.bounds) a.bounds[((int64_t)s * a.nb + blk) * a.H + h] = bnd;
+    best = fmaxf(best, bnd);
+  }
+  best = block_max(best, sh_red);
+  if (tid == 0 && a.max_bound) a.max_bound[o] = best;
+}
+
+// Active-first stable order of n blocks (stream compaction): out[r] = the
+// r-th retained block, then the evicted ones in order; *num_active = the
+// retained count.  One workgroup of 1024 threads, chunked prefix sums.
+__global__ __launch_bounds__(1024) void stream_compact_kernel(const uint8_t* mask, int n, int64_t* out,
+                                                              int32_t* num_active) {
+  __shared__ int sh[1024];
+  __shared__ int sh_total;
+  const int tid = threadIdx.x;
+  int cnt = 0;
+  for (int i = tid; i < n; i += 1024) cnt += mask[i] ? 1 : 0;
+  for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+  if (tid == 0) sh_total = 0;
+  __syncthreads();
+  if ((tid & 63) == 0) atomicAdd(&sh_total, cnt);
+  __syncthreads();
+  const int total = sh_total;
+  int base_a = 0;
+  for (int c0 = 0; c0 < n; c0 += 1024) {
+    const int i = c0 + tid;
+    const int f = (i < n && mask[i]) ? 1 : 0;
+    sh[tid] = f;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+      const int v = tid >= off ? sh[tid - off] : 0;
+      __syncthreads();
+      sh[tid] += v;
+      __syncthreads();
+    }
+    const int incl = sh[tid];
+    const int chunk_a = sh[1023];
+    if (i < n) {
+      const int ra = base_a + incl - f;           // retained before i
+      const int r = f ? ra : total + (i - ra);     // evicted before i: i - ra
+      out[r] = i;
+    }
+    base_a += chunk_a;
+    __syncthreads();
+  }
+  if (tid == 0 && num_active) *num_active = total;
+}
+
+template <int DT>
+int launch_spectrum(const SpecArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(block_spectrum_kernel<DT>, dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "block-spectrum launch");
+}
+
+}  // namespace
+}  // namespace oc
+
+using namespace oc;
+
+extern "C" int oc_block_spectra(const oc_spectra_params* p, void* stream) {
+  if (!p || !p->k) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (p->dtype != OC_F32 && p->dtype != OC_F16 && p->dtype != OC_BF16) return fail(OC_ERR_INVALID, "dtype %d", p->dtype);
+  if (p->block_size != kBlock) return fail(OC_ERR_UNSUPPORTED, "block_size %d (the transform is 512-point)", p->block_size);
+  if (p->head_dim < 8 || p->head_dim > kMaxD || p->head_dim % 8)
+    return fail(OC_ERR_UNSUPPORTED, "head_dim %d (a multiple of 8 up to %d)", p->head_dim, kMaxD);
+  if (p->num_blocks < 0 || p->num_heads < 0 || p->q_len < 0) return fail(OC_ERR_INVALID, "bad sizes");
+  const int es = p->dtype == OC_F32 ? 4 : 2;
+  if ((p->k_token_stride * es) % 16 || (p->k_head_stride * es) % 16 || ((uintptr_t)p->k % 16))
+    return fail(OC_ERR_INVALID, "K rows must be 16-byte aligned");
+  if (p->q && p->q_dtype != OC_F32 && p->q_dtype != OC_F16 && p->q_dtype != OC_BF16)
+    return fail(OC_ERR_INVALID, "q dtype %d", p->q_dtype);
+  if ((p->bounds || p->max_bound) && !p->q) return fail(OC_ERR_INVALID, "bounds need q");
+  if (p->num_blocks == 0 || p->num_heads == 0) return OC_OK;
+  if (p->num_heads > 65535) return fail(OC_ERR_UNSUPPORTED, "num_heads > 65535");
+  SpecArgs a{};
+  a.k = (const char*)p->k;
+  a.k_ts = p->k_token_stride * es, a.k_hs = p->k_head_stride * es;
+  a.H = p->num_heads, a.d = p->head_dim, a.nb = p->num_blocks, a.dtype = p->dtype;
+  a.q = (const char*)p->q;
+  const int qes = p->q_dtype == OC_F32 ? 4 : 2;
+  a.q_ss = p->q_token_stride * qes, a.q_hs = p->q_head_stride * qes;
+  a.Sq = p->q ? p->q_len : 0;
+  a.q_dtype = p->q_dtype;
+  a.e_low = p->e_low, a.e_mid = p->e_mid, a.e_high = p->e_high, a.zeta = p->zeta;
+  a.e_ac = p->e_ac, a.energy = p->energy, a.mean = p->block_mean;
+  a.bounds = p->bounds, a.max_bound = p->max_bound;
+  const hipStream_t s = (hipStream_t)stream;
+  switch (p->dtype) {
+    case OC_F32: return launch_spectrum<OC_F32>(a, s);
+    case OC_F16: return launch_spectrum<OC_F16>(a, s);
+    default: return launch_spectrum<OC_BF16>(a, s);
+  }
+}
+
+extern "C" int oc_stream_compact(const uint8_t* block_mask, int32_t num_blocks, int64_t* indices,
+                                 int32_t* num_active, void* stream) {
+  if (!block_mask || !indices) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (num_blocks < 0) return fail(OC_ERR_INVALID, "bad sizes");
+  if (num_blocks == 0) return OC_OK;
+  hipLaunchKernelGGL(stream_compact_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, block_mask, num_blocks,
+                     indices, num_active);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "stream-compact launch");
+}
+
+extern "C" size_t oc_spectra_params_bytes(void) { return sizeof(oc_spectra_params); }

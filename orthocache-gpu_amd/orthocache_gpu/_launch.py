@@ -699,3 +699,63 @@ def _ready16(t: torch.Tensor) -> torch.Tensor:
     es = t.element_size()
     ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
     return t if ok else t.contiguous()
+
+
+# ------------------------------------------------------------ 512-token spectra
+
+SPECTRA_BLOCK = 512
+
+
+def block_spectra(keys: torch.Tensor, q: Optional[torch.Tensor] = None, *, want_bounds: bool = False,
+                  want_mean: bool = False) -> Dict[str, torch.Tensor]:
+    """oc_block_spectra over the complete 512-token blocks of keys (S, H, d)
+    (last dimension contiguous).  Returns float32 tensors e_low, e_mid,
+    e_high, zeta, e_ac, energy (num_blocks, H); block_mean (num_blocks, H,
+    d) with want_mean; with q (Sq, H, d): max_bound (num_blocks, H) and,
+    with want_bounds, bounds (Sq, num_blocks, H)."""
+    device = require_gpu(keys) if q is None else require_gpu(keys, q)
+    if keys.dim() != 3:
+        raise ValueError(f"keys must be (seq_len, num_heads, head_dim), got {tuple(keys.shape)}")
+    keys = _ready16(keys)
+    S, H, d = keys.shape
+    nb = S // SPECTRA_BLOCK
+    f32 = dict(dtype=torch.float32, device=device)
+    out = {name: torch.empty((nb, H), **f32) for name in ("e_low", "e_mid", "e_high", "zeta", "e_ac", "energy")}
+    p = N.OcSpectraParams()
+    p.k, p.dtype = keys.data_ptr(), dtype_code(keys.dtype, "keys", allow_fp8=False)
+    p.num_blocks, p.num_heads, p.head_dim, p.block_size = nb, H, d, SPECTRA_BLOCK
+    p.k_token_stride, p.k_head_stride = keys.stride(0), keys.stride(1)
+    for name, t in out.items():
+        setattr(p, name, t.data_ptr())
+    if want_mean:
+        out["block_mean"] = torch.empty((nb, H, d), **f32)
+        p.block_mean = out["block_mean"].data_ptr()
+    if q is not None:
+        if q.dim() != 3 or q.shape[1:] != (H, d):
+            raise ValueError(f"q must be (seq_len_q, {H}, {d}), got {tuple(q.shape)}")
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        p.q, p.q_dtype, p.q_len = q.data_ptr(), dtype_code(q.dtype, "q", allow_fp8=False), q.shape[0]
+        p.q_token_stride, p.q_head_stride = q.stride(0), q.stride(1)
+        out["max_bound"] = torch.empty((nb, H), **f32)
+        p.max_bound = out["max_bound"].data_ptr()
+        if want_bounds:
+            out["bounds"] = torch.empty((q.shape[0], nb, H), **f32)
+            p.bounds = out["bounds"].data_ptr()
+    with torch.cuda.device(device):
+        N.check("oc_block_spectra", N.lib().oc_block_spectra(ctypes.byref(p),
+                                                             ctypes.c_void_p(current_stream(device))))
+    return out
+
+
+def stream_compact(block_mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """oc_stream_compact: (indices int64 (n,), num_active int32 (1,)) on the device."""
+    device = require_gpu(block_mask)
+    m = block_mask.reshape(-1).to(torch.uint8).contiguous()
+    n = m.numel()
+    idx = torch.empty((n,), dtype=torch.int64, device=device)
+    cnt = torch.zeros((1,), dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_stream_compact", N.lib().oc_stream_compact(
+            m.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(), ctypes.c_void_p(current_stream(device))))
+    return idx, cnt

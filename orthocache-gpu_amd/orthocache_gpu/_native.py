@@ -86,6 +86,16 @@ class OcPrefillParams(ctypes.Structure):
     ]
 
 
+class OcSpectraParams(ctypes.Structure):
+    _fields_ = [
+        ("k", _p), ("dtype", _i32), ("num_blocks", _i32), ("num_heads", _i32), ("head_dim", _i32),
+        ("block_size", _i32), ("k_token_stride", _i64), ("k_head_stride", _i64),
+        ("q", _p), ("q_dtype", _i32), ("q_len", _i32), ("q_token_stride", _i64), ("q_head_stride", _i64),
+        ("e_low", _p), ("e_mid", _p), ("e_high", _p), ("zeta", _p), ("e_ac", _p), ("energy", _p),
+        ("block_mean", _p), ("bounds", _p), ("max_bound", _p),
+    ]
+
+
 # every function declared in include/orthocache_hip.h: name -> (restype, argtypes)
 SIGNATURES = {
     "oc_score_tiles": (_i32, [ctypes.POINTER(OcKvDesc), ctypes.c_double, _p, _p, _p, _p, _i64, _p]),
@@ -104,6 +114,9 @@ SIGNATURES = {
                              _i64, _i64, _p, _p]),
     "oc_prefill_attention": (_i32, [ctypes.POINTER(OcPrefillParams), _p]),
     "oc_prefill_params_bytes": (ctypes.c_size_t, []),
+    "oc_block_spectra": (_i32, [ctypes.POINTER(OcSpectraParams), _p]),
+    "oc_spectra_params_bytes": (ctypes.c_size_t, []),
+    "oc_stream_compact": (_i32, [_p, _i32, _p, _p, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
@@ -152,9 +165,10 @@ def lib():
                     "orthocache_gpu: struct layout mismatch between the binding and "
                     f"{LIB_PATH} ({kv_sz.value}/{p_sz.value} vs "
                     f"{ctypes.sizeof(OcKvDesc)}/{ctypes.sizeof(OcDecodeParams)} bytes)")
-            if handle.oc_prefill_params_bytes() != ctypes.sizeof(OcPrefillParams):
-                raise RuntimeError("orthocache_gpu: oc_prefill_params layout mismatch between the binding and "
-                                   f"{LIB_PATH}")
+            for fn, st in (("oc_prefill_params_bytes", OcPrefillParams), ("oc_spectra_params_bytes", OcSpectraParams)):
+                if getattr(handle, fn)() != ctypes.sizeof(st):
+                    raise RuntimeError(f"orthocache_gpu: {st.__name__} layout mismatch between the binding and "
+                                       f"{LIB_PATH}")
             _lib = handle
     return _lib
 

@@ -1,4 +1,4 @@
-"""orthocache_forward for MI355X (modes 'triton_fused' and 'dense').
+"""orthocache_forward for MI355X (modes 'compact', 'triton_fused' and 'dense').
 
 Drop-in for src/orthocache_gpu/pipeline.py of the reference for the decode
 path: same signature, BypassFlag / TelemetryLevel / GPUProfile types,
@@ -6,8 +6,10 @@ crossover bypass and metadata.  'triton_fused' runs the zeta-gated split-K
 decode (fused_orthocache_attention_v2) on a strided (heads, seq, dim) view
 of the (seq, heads, dim) caches -- no permute().contiguous() copy
 (pipeline.py:437-439 copies all of K and V on every call).  'dense' runs the
-same decode kernel with the gate off.  The 512-token 'compact' mode and its
-spectral pipeline are not part of this build and raise NotImplementedError.
+same decode kernel with the gate off.  'compact' (the 512-token spectral
+pipeline) computes every block's spectra and query-aware bounds in one
+oc_block_spectra pass and attends the retained blocks with the decode
+kernel on a tile mask (spectral_energy.py, adaptive_attention.py).
 """
 
 from __future__ import annotations
@@ -194,7 +196,9 @@ def orthocache_forward(
 
     q (Sq, H, d), keys/values (S, H, d).  mode='triton_fused' decodes the
     first query token with the zeta-gated split-K kernel and returns
-    (1, H, d); mode='dense' returns dense attention (Sq, H, d).
+    (1, H, d); mode='dense' returns dense attention (Sq, H, d);
+    mode='compact' returns (Sq, H, d) bfloat16 over the retained 512-token
+    blocks.
     """
     seq_len_k, num_heads, head_dim = keys.shape
     seq_len_q = q.shape[0]
@@ -247,8 +251,72 @@ def orthocache_forward(
             metadata["bypass_flags"] = int(BypassFlag.TRITON_FUSED)
             metadata["gpu_profile"] = hw_profile.name
         return output, metadata
-    if mode == "compact":
-        raise NotImplementedError(
-            "orthocache_forward(mode='compact') (512-token spectral compaction) is not part of the "
-            "MI355X build; use mode='triton_fused' or mode='dense'")
-    raise ValueError(f"Unknown mode: {mode!r}. Use 'dense', 'compact', or 'triton_fused'.")
+    if mode != "compact":
+        raise ValueError(f"Unknown mode: {mode!r}. Use 'dense', 'compact', or 'triton_fused'.")
+    # --- adaptive crossover bypass (pipeline.py:384-406) ---
+    dynamic_threshold = hw_profile.crossover_seq_len
+    if seq_len_k < dynamic_threshold:
+        t0 = time.perf_counter()
+        output = _dense_attention(q, keys, values, head_dim)
+        torch.cuda.synchronize(q.device)
+        if telemetry >= TelemetryLevel.FLAGS:
+            flags = BypassFlag.CROSSOVER_BYPASS
+            if hw_profile.compute_class == "unknown":
+                flags |= BypassFlag.HW_AUTO_DETECTED
+            metadata["latency_ms"] = (time.perf_counter() - t0) * 1000
+            metadata["eviction_rate"] = 0.0
+            metadata["bypass_flags"] = int(flags)
+            metadata["crossover_threshold"] = dynamic_threshold
+            metadata["gpu_profile"] = hw_profile.name
+        if telemetry >= TelemetryLevel.VERBOSE:
+            metadata["crossover_reason"] = format_bypass_reason(flags, seq_len_k, dynamic_threshold, hw_profile)
+        return output, metadata
+    return _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, metadata)
+
+
+def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, metadata):
+    """The compact pipeline (pipeline.py:458-555): one oc_block_spectra pass
+    gives zeta, the query-aware bounds (max over queries), the block
+    energies and the retained-logit estimate; the two-gate mask
+    (compute_multiband_mask) keeps a (block, head) when its bound >= tau and
+    zeta <= zeta_max; a block is attended when any head keeps it
+    (adaptive_attention.orthocache_attention on the tile mask)."""
+    from .adaptive_attention import orthocache_attention
+    from .perfect_eviction import classify_eviction
+    from .spectral_energy import _check
+    t_spectral = time.perf_counter()
+    _check(keys, block_size)
+    spec = X.block_spectra(keys, q)
+    zeta, max_bounds = spec["zeta"], spec["max_bound"]
+    if tau is None:
+        tau = float((max_bounds.mean() - max_bounds.std()).item())  # _compute_auto_tau (pipeline.py:571-583)
+        metadata["tau_auto"] = True
+    else:
+        metadata["tau_auto"] = False
+    metadata["tau"] = tau
+    block_mask = (max_bounds >= tau) & (zeta <= zeta_max)
+    unified = block_mask.any(dim=-1)
+    zeta_any_head = zeta.mean(dim=-1)
+    stats = torch.stack([zeta_any_head.mean(), zeta_any_head.std(), zeta_any_head.min(), zeta_any_head.max(),
+                         unified.sum().to(torch.float32)]).tolist()
+    metadata["spectral_ms"] = (time.perf_counter() - t_spectral) * 1000
+    metadata["zeta_mean"], metadata["zeta_std"], metadata["zeta_min"], metadata["zeta_max_observed"] = stats[:4]
+    retained = int(stats[4])
+    metadata["blocks_retained"] = retained
+    metadata["blocks_evicted"] = int(num_blocks - retained)
+    metadata["eviction_rate"] = float(1.0 - retained / num_blocks)
+    # perfect / statistical regimes of the evicted blocks (pipeline.py:483-527)
+    z_max = max_bounds[unified].max() if retained else torch.tensor(0.0, device=q.device)
+    em = classify_eviction(q, spec["energy"], z_max, block_mask, head_dim)
+    metadata["perfect_eviction_blocks"] = em.num_perfect
+    metadata["statistical_eviction_blocks"] = em.num_statistical
+    metadata["perfect_eviction_rate"] = (em.num_perfect / max(1, num_blocks - retained)
+                                         if num_blocks > retained else 0.0)
+    t_attn = time.perf_counter()
+    output, _ = orthocache_attention(q, keys, values, unified, block_size=block_size)
+    torch.cuda.synchronize(q.device)
+    t_end = time.perf_counter()
+    metadata["compact_num_active"] = retained
+    metadata["attention_ms"] = (t_end - t_attn) * 1000
+    metadata["total_ms"] = (t_end - t_spectral) * 1000
+    return output, metadata

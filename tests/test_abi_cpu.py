@@ -120,6 +120,25 @@ def test_hook_entry_point_argument_checks():
                            None) == N.OC_ERR_INVALID
 
 
+def test_spectra_argument_checks():
+    import ctypes
+    from orthocache_gpu import _native as N
+    L = N.lib()
+    assert L.oc_spectra_params_bytes() == ctypes.sizeof(N.OcSpectraParams)
+    p = N.OcSpectraParams()
+    assert L.oc_block_spectra(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    p.k, p.dtype, p.num_blocks, p.num_heads, p.head_dim, p.block_size = 256, N.OC_BF16, 2, 2, 64, 256
+    p.k_token_stride, p.k_head_stride = 128, 64
+    assert L.oc_block_spectra(ctypes.byref(p), None) == N.OC_ERR_UNSUPPORTED
+    assert b"512" in L.oc_last_error()
+    p.block_size, p.head_dim = 512, 12
+    assert L.oc_block_spectra(ctypes.byref(p), None) == N.OC_ERR_UNSUPPORTED
+    p.head_dim, p.max_bound = 64, 256
+    assert L.oc_block_spectra(ctypes.byref(p), None) == N.OC_ERR_INVALID
+    assert b"need q" in L.oc_last_error()
+    assert L.oc_stream_compact(None, 4, 256, None, None) == N.OC_ERR_INVALID
+
+
 def test_reference_assertion_messages():
     """test_fp8.py:128-158 and test_paged_eviction.py:139-159 of the reference."""
     from orthocache_gpu import (fused_orthocache_attention, fused_orthocache_attention_paged,
@@ -166,7 +185,7 @@ def test_pipeline_host_logic():
     assert TelemetryLevel.SILENT < TelemetryLevel.FLAGS < TelemetryLevel.VERBOSE
     q = torch.randn(1, 2, 64)
     k = torch.randn(1024, 2, 64)
-    with pytest.raises(NotImplementedError, match="compact"):
+    with pytest.raises(RuntimeError, match="GPU"):  # no CPU fallback
         orthocache_forward(q, k, k, mode="compact")
     with pytest.raises(ValueError, match="Unknown mode"):
         orthocache_forward(q, k, k, mode="bogus")

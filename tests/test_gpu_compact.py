@@ -1,0 +1,164 @@
+"""GPU parity of orthocache_forward(mode='compact') and its 512-token
+spectral pipeline against the oracle: oc_block_spectra (band energies,
+zeta, AC and spatial energy, block mean, query-aware bounds), stream
+compaction, the spectral_energy / adaptive_attention / perfect_eviction
+functions and the whole compact forward (gates, metadata, output).
+
+Bars: energies and bounds within 1e-5 relative (float32 sums against the
+float64 oracle); masks and orders exact (data built with margins: smooth
+blocks have zeta < 1, noise blocks zeta > 100, thresholds placed in gaps);
+outputs (always bfloat16, as the reference returns) within 2e-3 plus half
+a bfloat16 ulp.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import orthocache_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import orthocache_gpu._native as N
+    N.lib()
+    yield
+
+
+def np64(t):
+    return t.detach().double().cpu().numpy()
+
+
+_W = O.fwht512(np.eye(512))  # H512 / sqrt(512), symmetric
+
+
+def _keys(nb, H, d, noise_blocks, seed, dtype):
+    """Blocks W @ C: smooth (C on rows 1..4) or noise (C on rows 256..511,
+    for every head of the blocks in noise_blocks), plus 0.05 white noise."""
+    rng = np.random.default_rng(seed)
+    k = np.zeros((nb * 512, H, d))
+    for b in range(nb):
+        for h in range(H):
+            c = np.zeros((512, d))
+            if b in noise_blocks:
+                c[256:] = rng.standard_normal((256, d))
+            else:
+                c[1:5] = 4 * rng.standard_normal((4, d))
+                c[0] = rng.standard_normal(d)
+            k[512 * b:512 * (b + 1), h] = _W @ c + 0.05 * rng.standard_normal((512, d))
+    return torch.from_numpy(k).to(TD[dtype])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("d", [64, 128])
+def test_block_spectra_vs_oracle(dtype, d):
+    from orthocache_gpu import _launch as X
+    k = _keys(5, 3, d, {1, 3}, seed=d, dtype=dtype)
+    q = torch.randn((4, 3, d), generator=torch.Generator().manual_seed(1)).to(TD[dtype])
+    kt = torch.cat([k, k[:100]]).to(DEV)  # 100 tokens past the last block are not read
+    got = X.block_spectra(kt, q.to(DEV), want_bounds=True, want_mean=True)
+    ref = O.block_spectra(np64(k), np64(q))
+    for name in ("e_low", "e_mid", "e_high", "e_ac", "energy", "zeta", "max_bound"):
+        np.testing.assert_allclose(np64(got[name]), ref[name], rtol=1e-5, atol=1e-6, err_msg=name)
+    np.testing.assert_allclose(np64(got["block_mean"]), ref["block_mean"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(np64(got["bounds"]), ref["bounds"], rtol=1e-5, atol=1e-5)
+    z = np64(got["zeta"])
+    assert (z[[1, 3]] > 100).all() and (z[[0, 2, 4]] < 1).all()
+
+
+def test_stream_compact_and_spectral_api():
+    from orthocache_gpu import spectral_energy as SE
+    from orthocache_gpu.adaptive_attention import stream_compact
+    rng = np.random.default_rng(5)
+    for n in (1, 5, 1500, 3000):
+        m = rng.random(n) < 0.3
+        idx, cnt = stream_compact(torch.from_numpy(m).to(DEV))
+        ref_idx, ref_cnt = O.stream_compact(m)
+        assert cnt == ref_cnt and np.array_equal(idx.cpu().numpy(), ref_idx)
+    k = _keys(3, 2, 64, {2}, seed=6, dtype="f32")
+    q = torch.randn((2, 2, 64), generator=torch.Generator().manual_seed(2))
+    ref = O.block_spectra(np64(k), np64(q))
+    kd, qd = k.to(DEV), q.to(DEV)
+    dc, lo, mid, hi = SE.compute_spectral_bands(kd)
+    np.testing.assert_allclose(np64(dc), ref["block_mean"] * math.sqrt(512), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(np64(SE.compute_spectral_decay_ratio(kd)), ref["zeta"], rtol=1e-5)
+    np.testing.assert_allclose(np64(SE.compute_block_energy(kd)), ref["energy"], rtol=1e-5)
+    np.testing.assert_allclose(np64(SE.compute_query_aware_bounds(qd, kd)), ref["bounds"], rtol=1e-5, atol=1e-5)
+    tau = float(np.median(ref["max_bound"]))
+    assert np.array_equal(SE.compute_query_aware_mask(qd, kd, tau).cpu().numpy(), ref["max_bound"] >= tau)
+    mm = SE.compute_multiband_mask(qd, kd, tau, 5.0).cpu().numpy()
+    assert np.array_equal(mm, (ref["max_bound"] >= tau) & (ref["zeta"] <= 5.0))
+    with pytest.raises(RuntimeError, match="invalid"):
+        SE.compute_spectral_decay_ratio(kd[:700])
+    with pytest.raises(NotImplementedError):
+        SE.compute_spectral_bands(kd, band_low=(1, 32))
+
+
+def _gap_tau(vals):
+    v = np.sort(vals.ravel())
+    gaps = v[1:] - v[:-1]
+    i = int(np.argmax(gaps[len(v) // 4:3 * len(v) // 4])) + len(v) // 4
+    return float(0.5 * (v[i] + v[i + 1]))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("sq", [1, 3, 70])
+def test_compact_forward_vs_oracle(dtype, sq):
+    from orthocache_gpu import orthocache_forward
+    nb, H, d = 16, 4, 128
+    k = _keys(nb, H, d, {1, 2, 5, 8, 9, 13}, seed=sq, dtype=dtype)
+    g = torch.Generator().manual_seed(sq)
+    v = torch.randn((nb * 512, H, d), generator=g).to(TD[dtype])
+    q = torch.randn((sq, H, d), generator=g).to(TD[dtype])
+    probe = O.block_spectra(np64(k), np64(q))
+    tau = _gap_tau(probe["max_bound"][probe["zeta"] <= 5.0])  # splits the smooth blocks' bounds
+    out, meta = orthocache_forward(q.to(DEV), k.to(DEV), v.to(DEV), zeta_max=5.0, tau=tau, mode="compact")
+    ref, info = O.compact_forward(np64(q), np64(k), np64(v), zeta_max=5.0, tau=tau)
+    assert out.dtype == torch.bfloat16 and out.shape == (sq, H, d)
+    r = O.round_to(ref, "bf16")
+    assert (np.abs(np64(out) - r) <= 2e-3 + np.abs(r) * 2.0 ** -8).all()
+    assert 0 < info["retained"] < nb
+    assert meta["blocks_retained"] == info["retained"] and meta["compact_num_active"] == info["retained"]
+    assert meta["blocks_evicted"] == nb - info["retained"]
+    assert meta["eviction_rate"] == pytest.approx(1 - info["retained"] / nb)
+    assert meta["tau"] == tau and meta["tau_auto"] is False
+    for key in ("zeta_mean", "zeta_std", "zeta_min", "zeta_max_observed"):
+        assert meta[key] == pytest.approx(info[key], rel=1e-4), key
+    assert meta["perfect_eviction_blocks"] == info["perfect"]
+    assert meta["statistical_eviction_blocks"] == info["statistical"]
+    for key in ("spectral_ms", "attention_ms", "total_ms", "actual_mode"):
+        assert key in meta
+
+
+def test_compact_auto_tau_bypass_and_zero_active():
+    from orthocache_gpu import orthocache_forward
+    nb, H, d = 8, 2, 64
+    k = _keys(nb, H, d, {3}, seed=9, dtype="f32")
+    g = torch.Generator().manual_seed(9)
+    v = torch.randn((nb * 512, H, d), generator=g)
+    q = torch.randn((2, H, d), generator=g)
+    out, meta = orthocache_forward(q.to(DEV), k.to(DEV), v.to(DEV), mode="compact")
+    ref, info = O.compact_forward(np64(q), np64(k), np64(v))
+    assert meta["tau_auto"] is True and meta["tau"] == pytest.approx(info["tau"], rel=1e-5)
+    mb = info["spectra"]["max_bound"]
+    if np.abs(mb - info["tau"]).min() > 1e-4 * abs(info["tau"]):
+        assert meta["blocks_retained"] == info["retained"]
+        r = O.round_to(ref, "bf16")
+        assert (np.abs(np64(out) - r) <= 2e-3 + np.abs(r) * 2.0 ** -8).all()
+    # nothing passes the zeta gate: zeros in q's dtype
+    out0, meta0 = orthocache_forward(q.to(DEV), k.to(DEV), v.to(DEV), mode="compact", zeta_max=-1.0, tau=-1e30)
+    assert meta0["blocks_retained"] == 0 and not out0.any() and out0.dtype == q.dtype
+    # under the MI355X crossover (1024 keys): dense attention, bypass flags
+    out_b, meta_b = orthocache_forward(q.to(DEV), k[:512].to(DEV), v[:512].to(DEV), mode="compact")
+    assert meta_b["bypass_flags"] & 1 and meta_b["eviction_rate"] == 0.0
+    dense = np.stack([O.dense_decode(np64(q[:, h]), np.repeat(np64(k[None, :512, h]), 2, 0),
+                                     np.repeat(np64(v[None, :512, h]), 2, 0)) for h in range(H)], axis=1)
+    np.testing.assert_allclose(np64(out_b), dense, atol=1e-5, rtol=1e-5)
