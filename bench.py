@@ -62,10 +62,11 @@ def parse():
     ap.add_argument("--extra-configs", type=int, default=1,
                     help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
     ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read",
-                                       "paged", "fp8"],
+                                       "paged", "fp8", "hook", "compact"],
                     default=None,
-                    help="time only this decode variant of the primary batch, or a plain 1 GiB device copy "
-                         "(the reference kernel for scaling the profiler's byte counters)")
+                    help="time only this decode variant of the primary batch, a plain 1 GiB device copy "
+                         "(the reference kernel for scaling the profiler's byte counters), the model hook's "
+                         "prefill attention kernel (hook) or the compact pipeline (compact)")
     return ap.parse_args()
 
 
@@ -381,6 +382,86 @@ def cpu_baseline(setup, seconds):
             "host_cpus": os.cpu_count()}
 
 
+def _event_us(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        fn()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / steps
+
+
+def hook_measure(steps, warmup):
+    """The model hook's causal prefill attention kernel (oc_prefill_attention)
+    at a TinyLlama-1.1B layer (32 q / 4 kv heads, head_dim 64, float32 as the
+    reference's evaluation runs it, and bfloat16) and a Llama-3-8B layer (32 / 8,
+    head_dim 128, bfloat16), 2048 / 4096 tokens, without eviction and with half
+    of the tiles evicted; torch's SDPA (causal, GQA) timed beside it.  FLOPs
+    are 4 * head_dim per (query, attended key)."""
+    import torch
+    from orthocache_gpu import _launch as X
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for B, Hq, Hkv, S, d, dt in ((1, 32, 4, 2048, 64, torch.float32), (1, 32, 4, 2048, 64, torch.bfloat16),
+                                 (1, 32, 8, 4096, 128, torch.bfloat16)):
+        q = torch.randn((B, Hq, S, d), device="cuda", generator=g).to(dt)
+        k = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)
+        v = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)
+        ev = (torch.rand((B, Hkv, S // 64), device="cuda", generator=g) < 0.5).to(torch.uint8)
+        flops = B * Hq * (S * (S + 1) / 2) * 4 * d
+        us = _event_us(lambda: X.prefill_attention(q, k, v), steps, warmup)
+        us_ev = _event_us(lambda: X.prefill_attention(q, k, v, tile_mask=ev), steps, warmup)
+        sdpa = _event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                                                  enable_gqa=True), steps, warmup)
+        print(json.dumps({"only": "hook", "kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                          "tokens": S, "head_dim": d, "dtype": str(dt).replace("torch.", ""),
+                          "us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
+                          "us_half_evicted": round(us_ev, 1), "torch_sdpa_us": round(sdpa, 1)}), flush=True)
+
+
+def compact_measure(steps, warmup):
+    """orthocache_forward(mode='compact') on a 32768-token, 32-head,
+    head_dim-128 bfloat16 cache whose 512-token blocks are half smooth, half
+    noise (W512 C with C on the low or the high sequency rows): the block
+    spectrum kernel alone (HBM bytes = the K cache) and the whole forward
+    (spectra, gates, metadata, attention) against mode='dense'."""
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import orthocache_forward
+    S, H, d = 32768, 32, 128
+    nb = S // 512
+    g = torch.Generator(device="cuda").manual_seed(0)
+    i = torch.arange(512, device="cuda")
+    pc = torch.zeros((512, 512), dtype=torch.int64, device="cuda")
+    x = i[:, None] & i[None, :]
+    while bool(x.any()):
+        pc += x & 1
+        x = x >> 1
+    w = (1.0 - 2.0 * (pc % 2).float()) / 512 ** 0.5
+    c = torch.zeros((nb, H, 512, d), device="cuda")
+    noise = torch.rand((nb,), device="cuda", generator=g) < 0.5
+    c[~noise, :, 1:5] = 4 * torch.randn((int((~noise).sum()), H, 4, d), device="cuda", generator=g)
+    c[noise, :, 256:] = torch.randn((int(noise.sum()), H, 256, d), device="cuda", generator=g)
+    k = (w @ c + 0.05 * torch.randn(c.shape, device="cuda", generator=g))  # (nb, H, 512, d)
+    k = k.permute(0, 2, 1, 3).reshape(S, H, d).to(torch.bfloat16).contiguous()
+    v = torch.randn((S, H, d), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((1, H, d), device="cuda", generator=g).to(torch.bfloat16)
+    del c
+    us_spec = _event_us(lambda: X.block_spectra(k, q), steps, warmup)
+    _, meta = orthocache_forward(q, k, v, mode="compact", tau=-1e30)
+    us_c = _event_us(lambda: orthocache_forward(q, k, v, mode="compact", tau=-1e30), steps, warmup)
+    us_d = _event_us(lambda: orthocache_forward(q, k, v, mode="dense"), steps, warmup)
+    kb = S * H * d * 2
+    print(json.dumps({"only": "compact", "tokens": S, "heads": H, "head_dim": d, "dtype": "bfloat16",
+                      "eviction_rate": meta["eviction_rate"], "block_spectrum_us": round(us_spec, 1),
+                      "block_spectrum_gbps": round(kb / us_spec / 1e3, 1), "compact_forward_us": round(us_c, 1),
+                      "dense_forward_us": round(us_d, 1)}), flush=True)
+
+
 def read_probe(steps, warmup, nbytes=2 << 30):
     """Achievable HBM read bandwidth: oc_hbm_read_probe (128-bit loads, four
     in flight per thread) over a 2 GiB buffer, best grid size."""
@@ -452,6 +533,12 @@ def main():
         return
     if args.only == "read":
         print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))
+        return
+    if args.only == "hook":
+        hook_measure(args.steps, args.warmup)
+        return
+    if args.only == "compact":
+        compact_measure(args.steps, args.warmup)
         return
     if args.only in ("paged", "fp8"):
         variants = tuple(args.variants.split(",")) if args.variants else ("cached", "single_pass", "dense")

@@ -54,6 +54,9 @@
  *                      compute_spectral_decay_ratio, compute_block_energy and
  *                      compute_query_aware_bounds (spectral_energy.py:26-200)
  *   oc_stream_compact <- stream_compact (adaptive_attention.py:33-45)
+ *   oc_compact_gate  <- compute_multiband_mask, _compute_auto_tau, the zeta
+ *                      statistics and classify_eviction as orthocache_forward
+ *                      runs them (pipeline.py:458-527)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -357,12 +360,32 @@ typedef struct oc_spectra_params {
   float* block_mean;              /* (num_blocks, num_heads, head_dim) */
   float* bounds;                  /* (q_len, num_blocks, num_heads) */
   float* max_bound;               /* (num_blocks, num_heads) */
+  float* q_norm_max;              /* (num_heads,) max over queries of ||q_s|| */
 } oc_spectra_params;
 
 int oc_block_spectra(const oc_spectra_params* p, void* stream);
 
 /* sizeof(oc_spectra_params) as compiled, for binding checks */
 size_t oc_spectra_params_bytes(void);
+
+/*
+ * oc_compact_gate -- the compact pipeline's gates and statistics from
+ * oc_block_spectra's outputs, in one workgroup (pipeline.py:458-527):
+ * tau = the given value, or with tau_auto mean - std (unbiased) of
+ * max_bound (_compute_auto_tau, pipeline.py:571-583); (b, h) is retained iff
+ * max_bound >= tau and zeta <= zeta_max (compute_multiband_mask);
+ * block_mask[b] = any head retained; tile_mask[b * tiles_per_block + i] =
+ * block_mask[b]; stats[0..8] = tau, mean / std (unbiased) / min / max over
+ * blocks of the head-mean zeta, the retained count, and the perfect and
+ * statistical counts of the evicted blocks: beta_b = max_h q_norm_max[h]
+ * sqrt(energy[b, h]) / sqrt(head_dim), z_max = the largest max_bound of a
+ * retained block (0 if none), perfect iff z_max - beta_b >= underflow
+ * (classify_eviction, perfect_eviction.py:107-186); stats[8] = z_max.
+ */
+int oc_compact_gate(const float* max_bound, const float* zeta, const float* energy, const float* q_norm_max,
+                    int32_t num_blocks, int32_t num_heads, int32_t head_dim, double tau, int32_t tau_auto,
+                    double zeta_max, double underflow, int32_t tiles_per_block, uint8_t* block_mask,
+                    uint8_t* tile_mask, float* stats, void* stream);
 
 /*
  * oc_stream_compact -- the active-first stable permutation of num_blocks

@@ -43,6 +43,7 @@ struct SpecArgs {
   float* mean;        // (nb, H, d) block mean = DC / sqrt(512), or null
   float* bounds;      // (Sq, nb, H) or null
   float* max_bound;   // (nb, H) or null
+  float* q_norm_max;  // (H,) max_s ||q_s|| or null
 };
 
 __device__ __forceinline__ float sp_load(const char* p, int dtype) {
@@ -99,15 +100,18 @@ __device__ __forceinline__ float block_max(float v, float* sh_red) {
 }
 
 // One workgroup per (512-token block, head).  Thread (tg, cg) owns columns
-// 8cg .. 8cg + 8 and the within-chunk positions tl = tg + i * TG.
-template <int DT>
+// 8cg .. 8cg + 8 and the within-chunk positions tl = tg + i * TG.  D is the
+// head_dim for 64 and 128 (the loop over tl unrolls, so a thread's loads are
+// all in flight together) and 0 for any other multiple of 8 up to 256.
+template <int DT, int D>
 __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecArgs a) {
-  __shared__ float sh_z[64 * kMaxD];  // Z_0[tl][c]
-  __shared__ float sh_mean[kMaxD];
+  constexpr int DMAX = D ? D : kMaxD;
+  __shared__ float sh_z[64 * DMAX];  // Z_0[tl][c]
+  __shared__ float sh_mean[DMAX];
   __shared__ float sh_red[kSpThreads / 64];
   const int blk = blockIdx.x;
   const int h = blockIdx.y;
-  const int d = a.d;
+  const int d = D ? D : a.d;
   const int CG = d / 8;
   const int TG = kSpThreads / CG;
   const int tid = threadIdx.x;
@@ -115,7 +119,12 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   const int tg = tid / CG;
   const char* kb = a.k + (int64_t)blk * kBlock * a.k_ts + (int64_t)h * a.k_hs + (int64_t)cg * 8 * (DT == OC_F32 ? 4 : 2);
   float e_mid = 0.f, e_high = 0.f, energy = 0.f;
-  for (int tl = tg; tl < 64; tl += TG) {
+  // positions per thread: 64 / TG when TG divides 64 (D = 64, 128), else a bound
+  constexpr int TPT = D ? 64 / (kSpThreads / (D / 8)) : 64;
+#pragma unroll
+  for (int i = 0; i < TPT; ++i) {
+    const int tl = tg + i * TG;
+    if (!D && tl >= 64) break;
     float x[8][8];  // [th][column]
 #pragma unroll
     for (int th = 0; th < 8; ++th) load8<DT>(kb + (int64_t)(64 * th + tl) * a.k_ts, x[th]);
@@ -150,7 +159,7 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   if (tid < d) {
     float y[64];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) y[i] = sh_z[i * d + tid];
+    for (int i = 0; i < 64; ++i) y[i] = sh_z[i * d + tid];  // consecutive threads, consecutive words
 #pragma unroll
     for (int m = 1; m < 64; m <<= 1)
 #pragma unroll
@@ -188,6 +197,7 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   const float sq_ac = __builtin_sqrtf(fmaxf(s_ac, 0.f));
   const int qes = a.q_dtype == OC_F32 ? 4 : 2;
   float best = -__builtin_inff();
+  float qbest = 0.f;
   for (int s = tid; s < a.Sq; s += kSpThreads) {
     const char* qr = a.q + (int64_t)s * a.q_ss + (int64_t)h * a.q_hs;
     float dot = 0.f, nn = 0.f;
@@ -199,9 +209,115 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
     const float bnd = dot * inv_sd + __builtin_sqrtf(nn) * sq_ac * inv_sd;
     if (a.bounds) a.bounds[((int64_t)s * a.nb + blk) * a.H + h] = bnd;
     best = fmaxf(best, bnd);
+    qbest = fmaxf(qbest, __builtin_sqrtf(nn));
   }
   best = block_max(best, sh_red);
   if (tid == 0 && a.max_bound) a.max_bound[o] = best;
+  if (blk == 0 && a.q_norm_max) {
+    qbest = block_max(qbest, sh_red);
+    if (tid == 0) a.q_norm_max[h] = qbest;
+  }
+}
+
+// The compact pipeline's gates and statistics in one workgroup over the
+// (block, head) table (pipeline.py:458-527): tau (given, or mean - unbiased
+// std of the max bounds), the two-gate mask, the any-head block mask and its
+// tile expansion, the zeta statistics of the per-block head means, the
+// retained count, the largest retained bound and the perfect / statistical
+// regimes of the evicted blocks.  stats: [tau, zeta mean, zeta std, zeta
+// min, zeta max, retained, perfect, statistical, z_max].
+__global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, const float* zeta, const float* energy,
+                                                            const float* qmax, int nb, int H, int d, float tau_in,
+                                                            int tau_auto, float zeta_max, float underflow,
+                                                            int tiles_per_block, uint8_t* unified,
+                                                            uint8_t* tile_mask, float* stats) {
+  __shared__ float sh_f[32];
+  __shared__ float sh_bcast[4];
+  const int tid = threadIdx.x;
+  const int n = nb * H;
+  auto bsum = [&](float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if ((tid & 63) == 0) sh_f[tid >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < 16; ++i) t += sh_f[i];
+    return t;
+  };
+  auto bmax = [&](float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    __syncthreads();
+    if ((tid & 63) == 0) sh_f[tid >> 6] = v;
+    __syncthreads();
+    float t = sh_f[0];
+    for (int i = 1; i < 16; ++i) t = fmaxf(t, sh_f[i]);
+    return t;
+  };
+  float tau = tau_in;
+  if (tau_auto) {
+    float s = 0.f;
+    for (int i = tid; i < n; i += 1024) s += mb[i];
+    const float mean = bsum(s) / (float)n;
+    float v = 0.f;
+    for (int i = tid; i < n; i += 1024) v = __builtin_fmaf(mb[i] - mean, mb[i] - mean, v);
+    const float var = bsum(v) / (float)(n - 1);  // n = 1: NaN, as torch.std
+    tau = mean - __builtin_sqrtf(var);
+  }
+  // per block: any head retained, head-mean zeta, beta = max_h qmax_h sqrt(E) / sqrt(d)
+  float zs = 0.f, zmin = __builtin_inff(), zmx = -__builtin_inff(), ret = 0.f, zbest = -__builtin_inff();
+  const float isd = 1.0f / __builtin_sqrtf((float)d);
+  for (int b = tid; b < nb; b += 1024) {
+    bool any = false;
+    float zsum = 0.f, bmx = -__builtin_inff();
+    for (int h = 0; h < H; ++h) {
+      const float m = mb[b * H + h], z = zeta[b * H + h];
+      any = any || (m >= tau && z <= zeta_max);
+      zsum += z;
+      bmx = fmaxf(bmx, m);
+    }
+    unified[b] = any ? 1 : 0;
+    for (int t = 0; t < tiles_per_block; ++t) tile_mask[(int64_t)b * tiles_per_block + t] = any ? 1 : 0;
+    const float za = zsum / (float)H;
+    zs += za;
+    zmin = fminf(zmin, za);
+    zmx = fmaxf(zmx, za);
+    ret += any ? 1.f : 0.f;
+    if (any) zbest = fmaxf(zbest, bmx);
+  }
+  const float zmean = bsum(zs) / (float)nb;
+  zmin = -bmax(-zmin);
+  zmx = bmax(zmx);
+  const float retained = bsum(ret);
+  float zmax_ret = bmax(zbest);
+  if (retained == 0.f) zmax_ret = 0.f;
+  float zv = 0.f, perf = 0.f, stat = 0.f;
+  for (int b = tid; b < nb; b += 1024) {
+    float zsum = 0.f, beta = -__builtin_inff();
+    for (int h = 0; h < H; ++h) {
+      zsum += zeta[b * H + h];
+      beta = fmaxf(beta, qmax[h] * __builtin_sqrtf(fmaxf(energy[b * H + h], 0.f)) * isd);
+    }
+    const float za = zsum / (float)H;
+    zv = __builtin_fmaf(za - zmean, za - zmean, zv);
+    if (!unified[b]) {
+      if (zmax_ret - beta >= underflow) perf += 1.f;
+      else stat += 1.f;
+    }
+  }
+  const float zvar = bsum(zv) / (float)(nb - 1);
+  const float np_ = bsum(perf), ns_ = bsum(stat);
+  (void)sh_bcast;
+  if (tid == 0) {
+    stats[0] = tau;
+    stats[1] = zmean;
+    stats[2] = __builtin_sqrtf(zvar);
+    stats[3] = zmin;
+    stats[4] = zmx;
+    stats[5] = retained;
+    stats[6] = np_;
+    stats[7] = ns_;
+    stats[8] = zmax_ret;
+  }
 }
 
 // Active-first stable order of n blocks (stream compaction): out[r] = the
@@ -247,7 +363,12 @@ __global__ __launch_bounds__(1024) void stream_compact_kernel(const uint8_t* mas
 
 template <int DT>
 int launch_spectrum(const SpecArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(block_spectrum_kernel<DT>, dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+  if (a.d == 128)
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 128>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+  else if (a.d == 64)
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 64>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 0>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "block-spectrum launch");
 }
@@ -269,7 +390,7 @@ extern "C" int oc_block_spectra(const oc_spectra_params* p, void* stream) {
     return fail(OC_ERR_INVALID, "K rows must be 16-byte aligned");
   if (p->q && p->q_dtype != OC_F32 && p->q_dtype != OC_F16 && p->q_dtype != OC_BF16)
     return fail(OC_ERR_INVALID, "q dtype %d", p->q_dtype);
-  if ((p->bounds || p->max_bound) && !p->q) return fail(OC_ERR_INVALID, "bounds need q");
+  if ((p->bounds || p->max_bound || p->q_norm_max) && !p->q) return fail(OC_ERR_INVALID, "bounds need q");
   if (p->num_blocks == 0 || p->num_heads == 0) return OC_OK;
   if (p->num_heads > 65535) return fail(OC_ERR_UNSUPPORTED, "num_heads > 65535");
   SpecArgs a{};
@@ -283,7 +404,7 @@ extern "C" int oc_block_spectra(const oc_spectra_params* p, void* stream) {
   a.q_dtype = p->q_dtype;
   a.e_low = p->e_low, a.e_mid = p->e_mid, a.e_high = p->e_high, a.zeta = p->zeta;
   a.e_ac = p->e_ac, a.energy = p->energy, a.mean = p->block_mean;
-  a.bounds = p->bounds, a.max_bound = p->max_bound;
+  a.bounds = p->bounds, a.max_bound = p->max_bound, a.q_norm_max = p->q_norm_max;
   const hipStream_t s = (hipStream_t)stream;
   switch (p->dtype) {
     case OC_F32: return launch_spectrum<OC_F32>(a, s);
@@ -301,6 +422,20 @@ extern "C" int oc_stream_compact(const uint8_t* block_mask, int32_t num_blocks, 
                      indices, num_active);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "stream-compact launch");
+}
+
+extern "C" int oc_compact_gate(const float* max_bound, const float* zeta, const float* energy, const float* q_norm_max,
+                               int32_t num_blocks, int32_t num_heads, int32_t head_dim, double tau, int32_t tau_auto,
+                               double zeta_max, double underflow, int32_t tiles_per_block, uint8_t* block_mask,
+                               uint8_t* tile_mask, float* stats, void* stream) {
+  if (!max_bound || !zeta || !energy || !q_norm_max || !block_mask || !tile_mask || !stats)
+    return fail(OC_ERR_INVALID, "NULL pointer");
+  if (num_blocks < 1 || num_heads < 1 || head_dim < 1 || tiles_per_block < 1) return fail(OC_ERR_INVALID, "bad sizes");
+  hipLaunchKernelGGL(compact_gate_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, max_bound, zeta, energy,
+                     q_norm_max, num_blocks, num_heads, head_dim, (float)tau, tau_auto, (float)zeta_max,
+                     (float)underflow, tiles_per_block, block_mask, tile_mask, stats);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "compact-gate launch");
 }
 
 extern "C" size_t oc_spectra_params_bytes(void) { return sizeof(oc_spectra_params); }

@@ -707,12 +707,13 @@ SPECTRA_BLOCK = 512
 
 
 def block_spectra(keys: torch.Tensor, q: Optional[torch.Tensor] = None, *, want_bounds: bool = False,
-                  want_mean: bool = False) -> Dict[str, torch.Tensor]:
+                  want_mean: bool = False, want_qnorm: bool = False) -> Dict[str, torch.Tensor]:
     """oc_block_spectra over the complete 512-token blocks of keys (S, H, d)
     (last dimension contiguous).  Returns float32 tensors e_low, e_mid,
     e_high, zeta, e_ac, energy (num_blocks, H); block_mean (num_blocks, H,
-    d) with want_mean; with q (Sq, H, d): max_bound (num_blocks, H) and,
-    with want_bounds, bounds (Sq, num_blocks, H)."""
+    d) with want_mean; with q (Sq, H, d): max_bound (num_blocks, H),
+    with want_bounds bounds (Sq, num_blocks, H), with want_qnorm
+    q_norm_max (H,) = max over queries of ||q_s||."""
     device = require_gpu(keys) if q is None else require_gpu(keys, q)
     if keys.dim() != 3:
         raise ValueError(f"keys must be (seq_len, num_heads, head_dim), got {tuple(keys.shape)}")
@@ -742,6 +743,9 @@ def block_spectra(keys: torch.Tensor, q: Optional[torch.Tensor] = None, *, want_
         if want_bounds:
             out["bounds"] = torch.empty((q.shape[0], nb, H), **f32)
             p.bounds = out["bounds"].data_ptr()
+        if want_qnorm:
+            out["q_norm_max"] = torch.empty((H,), **f32)
+            p.q_norm_max = out["q_norm_max"].data_ptr()
     with torch.cuda.device(device):
         N.check("oc_block_spectra", N.lib().oc_block_spectra(ctypes.byref(p),
                                                              ctypes.c_void_p(current_stream(device))))
@@ -759,3 +763,24 @@ def stream_compact(block_mask: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor
         N.check("oc_stream_compact", N.lib().oc_stream_compact(
             m.data_ptr(), n, idx.data_ptr(), cnt.data_ptr(), ctypes.c_void_p(current_stream(device))))
     return idx, cnt
+
+
+def compact_gate(spec: Dict[str, torch.Tensor], head_dim: int, tau: Optional[float], zeta_max: float,
+                 underflow: float, tiles_per_block: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """oc_compact_gate on block_spectra(..., q, want_qnorm=True) outputs:
+    (block mask uint8 (nb,), tile mask uint8 (nb * tiles_per_block,), stats
+    float32 (9,): tau, zeta mean/std/min/max, retained, perfect,
+    statistical, z_max)."""
+    mb = spec["max_bound"]
+    device = require_gpu(mb)
+    nb, H = mb.shape
+    bm = torch.empty((nb,), dtype=torch.uint8, device=device)
+    tm = torch.empty((nb * tiles_per_block,), dtype=torch.uint8, device=device)
+    st = torch.empty((9,), dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_compact_gate", N.lib().oc_compact_gate(
+            mb.data_ptr(), spec["zeta"].data_ptr(), spec["energy"].data_ptr(), spec["q_norm_max"].data_ptr(),
+            nb, H, head_dim, 0.0 if tau is None else float(tau), 1 if tau is None else 0, float(zeta_max),
+            float(underflow), tiles_per_block, bm.data_ptr(), tm.data_ptr(), st.data_ptr(),
+            ctypes.c_void_p(current_stream(device))))
+    return bm, tm, st

@@ -92,7 +92,7 @@ class OcSpectraParams(ctypes.Structure):
         ("block_size", _i32), ("k_token_stride", _i64), ("k_head_stride", _i64),
         ("q", _p), ("q_dtype", _i32), ("q_len", _i32), ("q_token_stride", _i64), ("q_head_stride", _i64),
         ("e_low", _p), ("e_mid", _p), ("e_high", _p), ("zeta", _p), ("e_ac", _p), ("energy", _p),
-        ("block_mean", _p), ("bounds", _p), ("max_bound", _p),
+        ("block_mean", _p), ("bounds", _p), ("max_bound", _p), ("q_norm_max", _p),
     ]
 
 
@@ -117,6 +117,8 @@ SIGNATURES = {
     "oc_block_spectra": (_i32, [ctypes.POINTER(OcSpectraParams), _p]),
     "oc_spectra_params_bytes": (ctypes.c_size_t, []),
     "oc_stream_compact": (_i32, [_p, _i32, _p, _p, _p]),
+    "oc_compact_gate": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, ctypes.c_double, _i32, ctypes.c_double,
+                               ctypes.c_double, _i32, _p, _p, _p, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),

@@ -35,7 +35,6 @@ def orthocache_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     global BS
     BS = block_size
     device = X.require_gpu(q, k_cache, v_cache)
-    seq_q, nh, hd = q.shape
     seq_k = k_cache.shape[0]
     nb = block_mask.shape[0]
     keep = block_mask.to(device=device, dtype=torch.bool)
@@ -44,22 +43,32 @@ def orthocache_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
         return torch.zeros_like(q), {'num_active': 0, 'eviction_rate': 1.0, 'path': 'zero'}
     if block_size % X.TILE_SIZE:
         raise NotImplementedError(f"block_size {block_size} is not a multiple of the 64-token tile")
-    tpb = block_size // X.TILE_SIZE
-    if nb * block_size > seq_k:
-        raise ValueError(f"block_mask covers {nb * block_size} tokens, the cache holds {seq_k}")
-    # one row per head over the blocks the mask covers; tiles of kept blocks attend
-    kv = X.rows_layout(k_cache[:nb * block_size].permute(1, 0, 2), v_cache[:nb * block_size].permute(1, 0, 2))
-    tile_mask = keep.to(torch.uint8).repeat_interleave(tpb).unsqueeze(0).expand(nh, -1)
-    out = torch.empty((seq_q, nh, hd), dtype=torch.bfloat16, device=device)
-    for s0 in range(0, seq_q, _Q_CHUNK):
-        qq = q[s0:s0 + _Q_CHUNK].permute(1, 0, 2).contiguous()  # (heads, g, d)
-        g = qq.shape[1]
-        res = X.decode(kv, qq.reshape(nh * g, hd), g, gate=N.OC_GATE_MASK, threshold=0.0, mode=N.OC_MODE_CACHED,
-                       out_dtype=torch.bfloat16, tile_mask=tile_mask)
-        out[s0:s0 + g] = res.out.view(nh, g, hd).permute(1, 0, 2)
+    tiles = keep.to(torch.uint8).repeat_interleave(block_size // X.TILE_SIZE)
+    out = attend_tiles(q, k_cache, v_cache, tiles, nb * block_size)
     return out, {
         'num_active': num_active,
         'num_blocks': seq_k // block_size,
         'eviction_rate': 1.0 - num_active / (seq_k // block_size),
         'path': 'masked_decode',
     }
+
+
+def attend_tiles(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, tile_mask: torch.Tensor,
+                 tokens: int) -> torch.Tensor:
+    """Every query of q (seq_q, heads, d) over the first `tokens` keys of
+    k_cache / v_cache (seq_k, heads, d), attending the 64-token tiles whose
+    tile_mask byte (uint8 (tokens // 64,), shared by the heads) is set;
+    bfloat16 (seq_q, heads, d)."""
+    seq_q, nh, hd = q.shape
+    if tokens > k_cache.shape[0] or tokens % X.TILE_SIZE:
+        raise ValueError(f"{tokens} tokens: more than the cache holds or not whole tiles")
+    kv = X.rows_layout(k_cache[:tokens].permute(1, 0, 2), v_cache[:tokens].permute(1, 0, 2))
+    tm = tile_mask.reshape(1, -1).expand(nh, -1)
+    out = torch.empty((seq_q, nh, hd), dtype=torch.bfloat16, device=q.device)
+    for s0 in range(0, seq_q, _Q_CHUNK):
+        qq = q[s0:s0 + _Q_CHUNK].permute(1, 0, 2).contiguous()  # (heads, g, d)
+        g = qq.shape[1]
+        res = X.decode(kv, qq.reshape(nh * g, hd), g, gate=N.OC_GATE_MASK, threshold=0.0, mode=N.OC_MODE_CACHED,
+                       out_dtype=torch.bfloat16, tile_mask=tm)
+        out[s0:s0 + g] = res.out.view(nh, g, hd).permute(1, 0, 2)
+    return out

@@ -277,43 +277,39 @@ def orthocache_forward(
 def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, metadata):
     """The compact pipeline (pipeline.py:458-555): one oc_block_spectra pass
     gives zeta, the query-aware bounds (max over queries), the block
-    energies and the retained-logit estimate; the two-gate mask
-    (compute_multiband_mask) keeps a (block, head) when its bound >= tau and
-    zeta <= zeta_max; a block is attended when any head keeps it
-    (adaptive_attention.orthocache_attention on the tile mask)."""
-    from .adaptive_attention import orthocache_attention
-    from .perfect_eviction import classify_eviction
+    energies and the largest query norm; one oc_compact_gate launch gives
+    tau (auto: mean - std of the bounds), the two-gate mask (a (block, head)
+    is kept when its bound >= tau and zeta <= zeta_max,
+    compute_multiband_mask), the any-head block mask and its tile mask, the
+    zeta statistics and the eviction regimes; the decode kernel then attends
+    the retained blocks' tiles (adaptive_attention.attend_tiles).  One
+    device-to-host transfer carries the statistics."""
+    from .adaptive_attention import attend_tiles
+    from .perfect_eviction import FLOAT32_UNDERFLOW_THRESHOLD
     from .spectral_energy import _check
     t_spectral = time.perf_counter()
     _check(keys, block_size)
-    spec = X.block_spectra(keys, q)
-    zeta, max_bounds = spec["zeta"], spec["max_bound"]
-    if tau is None:
-        tau = float((max_bounds.mean() - max_bounds.std()).item())  # _compute_auto_tau (pipeline.py:571-583)
-        metadata["tau_auto"] = True
-    else:
-        metadata["tau_auto"] = False
-    metadata["tau"] = tau
-    block_mask = (max_bounds >= tau) & (zeta <= zeta_max)
-    unified = block_mask.any(dim=-1)
-    zeta_any_head = zeta.mean(dim=-1)
-    stats = torch.stack([zeta_any_head.mean(), zeta_any_head.std(), zeta_any_head.min(), zeta_any_head.max(),
-                         unified.sum().to(torch.float32)]).tolist()
+    spec = X.block_spectra(keys, q, want_qnorm=True)
+    _, tile_mask, stats = X.compact_gate(spec, head_dim, tau, zeta_max, FLOAT32_UNDERFLOW_THRESHOLD,
+                                         block_size // X.TILE_SIZE)
+    st = stats.tolist()
+    metadata["tau_auto"] = tau is None
+    metadata["tau"] = st[0] if tau is None else tau
     metadata["spectral_ms"] = (time.perf_counter() - t_spectral) * 1000
-    metadata["zeta_mean"], metadata["zeta_std"], metadata["zeta_min"], metadata["zeta_max_observed"] = stats[:4]
-    retained = int(stats[4])
+    metadata["zeta_mean"], metadata["zeta_std"], metadata["zeta_min"], metadata["zeta_max_observed"] = st[1:5]
+    retained = int(st[5])
     metadata["blocks_retained"] = retained
     metadata["blocks_evicted"] = int(num_blocks - retained)
     metadata["eviction_rate"] = float(1.0 - retained / num_blocks)
-    # perfect / statistical regimes of the evicted blocks (pipeline.py:483-527)
-    z_max = max_bounds[unified].max() if retained else torch.tensor(0.0, device=q.device)
-    em = classify_eviction(q, spec["energy"], z_max, block_mask, head_dim)
-    metadata["perfect_eviction_blocks"] = em.num_perfect
-    metadata["statistical_eviction_blocks"] = em.num_statistical
-    metadata["perfect_eviction_rate"] = (em.num_perfect / max(1, num_blocks - retained)
+    metadata["perfect_eviction_blocks"] = int(st[6])
+    metadata["statistical_eviction_blocks"] = int(st[7])
+    metadata["perfect_eviction_rate"] = (int(st[6]) / max(1, num_blocks - retained)
                                          if num_blocks > retained else 0.0)
     t_attn = time.perf_counter()
-    output, _ = orthocache_attention(q, keys, values, unified, block_size=block_size)
+    if retained:
+        output = attend_tiles(q, keys, values, tile_mask, num_blocks * block_size)
+    else:
+        output = torch.zeros_like(q)
     torch.cuda.synchronize(q.device)
     t_end = time.perf_counter()
     metadata["compact_num_active"] = retained
