@@ -141,77 +141,98 @@ __device__ __forceinline__ void pf_load_q(const PrefillArgs& a, const char* qh, 
   }
 }
 
-// K tile t as MFMA B operands, straight from HBM (one buffer descriptor per
-// 16-token block whose size is the block's part below kv_len, so tokens past
-// kv_len read as zero).  16-bit: lane 16kg + x holds token 16tb + x,
-// elements 32dc + 8kg .. +8 in kb[tb][4dc .. 4dc + 4).  float32: lane
-// 16kg + x holds token 16tb + x, columns kg*D/4 .. + D/4 in kb[tb][..].
+// The workgroup's shared K/V tiles: K and V of one 64-token tile, row-major
+// [token][D], in STAGES LDS stages.  The 256 threads stage the next tile
+// through registers: each loads its 16-byte chunks while the waves compute
+// the current tile, and stores them once that compute is done.  K's chunks
+// are XOR-swizzled per row (chunk c of row r sits at c ^ swz(r)) so that the
+// 16 rows one B-operand read touches fall in distinct LDS banks.
 template <int DT, int D>
-struct PfK {
-  static constexpr int W = DT == OC_F32 ? D / 4 : D / 8;
-  uint32_t w[4][W];
+struct PfTile {
+  static constexpr int ES = DT == OC_F32 ? 4 : 2;
+  static constexpr int ROW = D * ES;                      // bytes per token row
+  static constexpr int LPT = ROW / 16;                    // 16-byte chunks per row
+  static constexpr int RB = ROW >= 256 ? 1 : 256 / ROW;   // rows per 256-byte bank line
+  static constexpr int KV = 64 * ROW;                     // bytes of one K (or V) tile
+  static constexpr int NL = KV / (kPfThreads * 16);       // chunks per thread per matrix
+  static constexpr int STAGES = 2 * KV <= 32768 ? 2 : 1;
+  static constexpr int P = 16 * 64 * 4;                   // a wave's p tile
+  static constexpr int LDS = STAGES * 2 * KV + kPfWaves * P;
+  __device__ static int swz(int r) { return (r / RB) % LPT; }
 };
 
 template <int DT, int D>
-__device__ __forceinline__ void pf_load_k(const PrefillArgs& a, const char* kh, int t, int lane, PfK<DT, D>& kb) {
-  const int x = lane & 15;
-  const int kg = lane >> 4;
-  const int64_t ts = a.k_ss;
-  const char* base = kh + (int64_t)t * 64 * ts;
-  const int nbytes = (int)(min(a.Skv - t * 64, 64) * ts);
-  const int voff = x * (int)ts + (DT == OC_F32 ? kg * D : 16 * kg);
+struct PfStage {
+  uint4 k[PfTile<DT, D>::NL];
+  uint4 v[PfTile<DT, D>::NL];
+};
+
+// global -> registers: chunk g = tid + 256 j of the tile is row g / LPT,
+// chunk g % LPT; rows at or past kv_len read as zero (buffer range check)
+template <int DT, int D>
+__device__ __forceinline__ void pf_fetch(const PrefillArgs& a, const char* kh, const char* vh, int t, int tid,
+                                         PfStage<DT, D>& st) {
+  using L = PfTile<DT, D>;
+  const int nvalid = min(a.Skv - t * 64, 64);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(kh + (int64_t)t * 64 * a.k_ss), (short)0, nvalid * (int)a.k_ss, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(vh + (int64_t)t * 64 * a.v_ss), (short)0, nvalid * (int)a.v_ss, 0x00020000);
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int rb = 16 * tb * (int)ts;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(base + rb), (short)0, max(nbytes - rb, 0), 0x00020000);
-#pragma unroll
-    for (int j = 0; j < PfK<DT, D>::W / 4; ++j) {
-      // float32: 16 consecutive bytes per load; 16-bit: 32-column steps of 64 bytes
-      const int off = DT == OC_F32 ? 16 * j : 64 * j;
-      const auto u = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + off, 0, 0);
-      kb.w[tb][4 * j] = u[0];
-      kb.w[tb][4 * j + 1] = u[1];
-      kb.w[tb][4 * j + 2] = u[2];
-      kb.w[tb][4 * j + 3] = u[3];
-    }
+  for (int j = 0; j < L::NL; ++j) {
+    const int g = tid + kPfThreads * j;
+    const int r = g / L::LPT, c = g % L::LPT;
+    const auto uk = __builtin_amdgcn_raw_buffer_load_b128(rk, r * (int)a.k_ss + 16 * c, 0, 0);
+    const auto uv = __builtin_amdgcn_raw_buffer_load_b128(rv, r * (int)a.v_ss + 16 * c, 0, 0);
+    st.k[j] = uint4{uk[0], uk[1], uk[2], uk[3]};
+    st.v[j] = uint4{uv[0], uv[1], uv[2], uv[3]};
   }
 }
 
-// V tile t into the wave's LDS slot, row-major [token][D], by direct-to-LDS
-// buffer loads (16 bytes per lane, 1 KiB per instruction); tokens past
-// kv_len read as zero.
+// registers -> an LDS stage (K swizzled, V plain)
 template <int DT, int D>
-__device__ __forceinline__ void pf_load_v(const PrefillArgs& a, const char* vh, int t, int lane, char* sv) {
-  constexpr int ES = DT == OC_F32 ? 4 : 2;
-  constexpr int TPI = 1024 / (ES * D);
-  constexpr int LPT = 64 / TPI;
-  const int64_t ts = a.v_ss;
-  const char* base = vh + (int64_t)t * 64 * ts;
-  const int nbytes = (int)(min(a.Skv - t * 64, 64) * ts);
-  const int voff = (lane / LPT) * (int)ts + 16 * (lane % LPT);
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
+__device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char* sk, char* sv) {
+  using L = PfTile<DT, D>;
 #pragma unroll
-  for (int i = 0; i < 64 / TPI; ++i)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 1024), 16,
-                                             voff + i * TPI * (int)ts, 0, 0, 0);
+  for (int j = 0; j < L::NL; ++j) {
+    const int g = tid + kPfThreads * j;
+    const int r = g / L::LPT, c = g % L::LPT;
+    *reinterpret_cast<uint4*>(sk + r * L::ROW + 16 * (c ^ L::swz(r))) = st.k[j];
+    *reinterpret_cast<uint4*>(sv + r * L::ROW + 16 * c) = st.v[j];
+  }
 }
 
+// S = q.K^T of one tile from the LDS stage: c[tb] = rows x tokens 16tb ..
+// 16-bit: the B operand of instruction dc is row 16tb + x, logical chunk
+// 4dc + kg; float32: 4 columns kg*D/4 + 4j .. per read feed instructions
+// 4j .. 4j + 3.
 template <int DT, int D>
-__device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const PfK<DT, D>& kb, f32x4 (&c)[4]) {
+__device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const char* sk, int lane, f32x4 (&c)[4]) {
+  using L = PfTile<DT, D>;
+  const int x = lane & 15;
+  const int kg = lane >> 4;
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) {
     c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = 16 * tb + x;
+    const char* rowp = sk + r * L::ROW;
+    const int sw = L::swz(r);
     if constexpr (DT == OC_F32) {
 #pragma unroll
-      for (int dc = 0; dc < D / 4; ++dc)
-        c[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(q.w[dc]), __uint_as_float(kb.w[tb][dc]), c[tb],
-                                                     0, 0, 0);
+      for (int j = 0; j < D / 16; ++j) {
+        const uint4 u = *reinterpret_cast<const uint4*>(rowp + 16 * ((kg * (D / 16) + j) ^ sw));
+        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          c[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(q.w[4 * j + e]), __uint_as_float(uw[e]),
+                                                       c[tb], 0, 0, 0);
+      }
     } else {
 #pragma unroll
       for (int dc = 0; dc < D / 32; ++dc) {
+        const uint4 u = *reinterpret_cast<const uint4*>(rowp + 16 * ((4 * dc + kg) ^ sw));
         const uint32_t aq[4] = {q.w[4 * dc], q.w[4 * dc + 1], q.w[4 * dc + 2], q.w[4 * dc + 3]};
-        const uint32_t bk[4] = {kb.w[tb][4 * dc], kb.w[tb][4 * dc + 1], kb.w[tb][4 * dc + 2], kb.w[tb][4 * dc + 3]};
+        const uint32_t bk[4] = {u.x, u.y, u.z, u.w};
         c[tb] = mfma_qk<DT>(aq, bk, c[tb]);
       }
     }
@@ -233,18 +254,13 @@ __device__ __forceinline__ void pf_pv_f32(f32x4 (&accp)[D / 16], const float* sp
   }
 }
 
-template <int DT, int D>
-struct PfLds {
-  static constexpr int kV = 64 * D * (DT == OC_F32 ? 4 : 2);
-  static constexpr int kP = 16 * 64 * 4;
-  static constexpr int kWaveBytes = kV + kP;
-};
-
 template <int DT, int D, bool ENT>
 __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) char sh[kPfWaves * PfLds<DT, D>::kWaveBytes];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  using L = PfTile<DT, D>;
+  __shared__ __attribute__((aligned(16))) char sh[L::LDS];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   // XCD-aware order: consecutive workgroups go to different XCDs, so work
   // item w is placed so that items w, w+1, .. run on one XCD; items walk the
   // query blocks from the last (longest causal window) to the first, heads
@@ -258,10 +274,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
   const int h = bh % a.Hq;
   const int kv = h / a.G;
   const int pos0 = qb * 64 + 16 * wave;
-  if (pos0 >= a.Sq) return;  // no barrier below: waves are independent
-  char* my = sh + wave * PfLds<DT, D>::kWaveBytes;
-  char* sv = my;
-  float* sp = reinterpret_cast<float*>(my + PfLds<DT, D>::kV);
+  float* sp = reinterpret_cast<float*>(sh + L::STAGES * 2 * L::KV + wave * L::P);
 
   const int off = a.Skv - a.Sq;  // query s sees keys j <= s + off
   const int r = lane >> 4;
@@ -272,15 +285,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
     const int pos = pos0 + 4 * r + ii;
     nvis[ii] = pos < a.Sq ? min(max(pos + off + 1, 0), a.Skv) : 0;
   }
-  const int last = min(pos0 + 15, a.Sq - 1);
-  const int nvis_max = min(max(last + off + 1, 0), a.Skv);
-  const int tend = (nvis_max + 63) / 64;
+  // this wave's tiles, and the workgroup's (its last query's window)
+  const int tend = pos0 < a.Sq ? (min(max(min(pos0 + 15, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64 : 0;
+  const int wg_tend = (min(max(min(qb * 64 + 63, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
 
   PfQ<DT, D> q;
   pf_load_q<DT, D>(a, a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh, pos0, lane, q);
   const char* kh = a.k + (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
   const char* vh = a.v + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh;
   const uint8_t* mrow = a.mask ? a.mask + (int64_t)b * a.m_sb + (int64_t)kv * a.m_sh : nullptr;
+  auto next_kept = [&](int t) {  // first retained tile >= t (uniform over the workgroup)
+    while (t < wg_tend && mrow && t < a.T && mrow[t]) ++t;
+    return t;
+  };
 
   PfState st;
   f32x4 accp[D / 16];
@@ -294,22 +311,35 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
 #pragma unroll
   for (int nc = 0; nc < D / 16; ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t = 0; t < tend; ++t) {
-    if (mrow && t < a.T && mrow[t]) continue;  // evicted tile (uniform over the wave)
-    PfK<DT, D> kb;
-    pf_load_k<DT, D>(a, kh, t, lane, kb);
-    pf_load_v<DT, D>(a, vh, t, lane, sv);
-    f32x4 c[4];
-    pf_logits<DT, D>(q, kb, c);
-    pf_softmax<D, ENT>(st, accp, c, sp, a.scale, nvis, t * 64, lane);
-    // the V tile's direct-to-LDS loads and the p stores have landed
-    __builtin_amdgcn_s_waitcnt(0);
-    if constexpr (DT == OC_F32)
-      pf_pv_f32<D>(accp, sp, reinterpret_cast<const float*>(sv), lane);
-    else
-      tile_pv_mfma<DT, D, 16>(accp, sp, reinterpret_cast<const uint16_t*>(sv), lane);
-    // every lane's reads of sp and sv are done before the next tile's writes
-    __builtin_amdgcn_s_waitcnt(0);
+  auto stage_k = [&](int s) { return sh + s * 2 * L::KV; };
+  auto stage_v = [&](int s) { return sh + s * 2 * L::KV + L::KV; };
+  PfStage<DT, D> reg;
+  int t = next_kept(0);
+  if (t < wg_tend) {
+    pf_fetch<DT, D>(a, kh, vh, t, tid, reg);
+    pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
+  }
+  int s = 0;
+  while (t < wg_tend) {
+    // stage s is complete; every wave is done with the tile before (stage s ^ 1)
+    __syncthreads();
+    const int tn = next_kept(t + 1);
+    if (tn < wg_tend) pf_fetch<DT, D>(a, kh, vh, tn, tid, reg);  // in flight during this tile
+    if (t < tend) {
+      f32x4 c[4];
+      pf_logits<DT, D>(q, stage_k(s), lane, c);
+      pf_softmax<D, ENT>(st, accp, c, sp, a.scale, nvis, t * 64, lane);
+      // the p stores have landed (LDS counter only: the prefetch stays in flight)
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      if constexpr (DT == OC_F32)
+        pf_pv_f32<D>(accp, sp, reinterpret_cast<const float*>(stage_v(s)), lane);
+      else
+        tile_pv_mfma<DT, D, 16>(accp, sp, reinterpret_cast<const uint16_t*>(stage_v(s)), lane);
+    }
+    if constexpr (L::STAGES == 1) __syncthreads();  // the only stage is free again
+    if (tn < wg_tend) pf_stash<DT, D>(reg, tid, stage_k(L::STAGES - 1 - s), stage_v(L::STAGES - 1 - s));
+    s = L::STAGES - 1 - s;
+    t = tn;
   }
 
   // row sums over the 16 lanes of each row, then out = acc / max(l, 1e-9)
