@@ -754,7 +754,6 @@ struct MfmaT {
 
 // four fp8 values (one word) -> two words of bf16 pairs
 __device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
   hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
@@ -1952,7 +1951,6 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
       acc = __builtin_fmaf(aw, e, acc);
       l = __builtin_fmaf(sh_l[w][g], e, l);
     }
-    const int64_t qh = (int64_t)row * a.G + g0 + g;
     const int64_t pidx = pbase + (int64_t)(g0 + g) * hstride + (int64_t)gidx * qstride;
     // agent-scope stores write through this XCD's L2, so the fused merge
     // (possibly on another XCD) reads them without a cache write-back

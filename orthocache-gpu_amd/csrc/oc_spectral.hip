@@ -121,7 +121,8 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   float e_mid = 0.f, e_high = 0.f, energy = 0.f;
   // positions per thread: 64 / TG when TG divides 64 (D = 64, 128), else a bound
   constexpr int TPT = D ? 64 / (kSpThreads / (D / 8)) : 64;
-#pragma unroll
+  constexpr int UNROLL = D ? TPT : 1;
+#pragma unroll UNROLL
   for (int i = 0; i < TPT; ++i) {
     const int tl = tg + i * TG;
     if (!D && tl >= 64) break;
