@@ -239,3 +239,32 @@ def test_hf_llama_patched_matches_dense():
     torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
     assert hook.stats['layers_processed'] == 2 * 5
     assert hook.stats['decode_steps'] == 2 * 2 * 4 and hook.stats['decode_tiles_skipped'] == 0
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_hook_decode_scores_new_tiles_and_whole_tiles(dtype):
+    """score_new_tiles=True (extension): tiles completed after the prefill are
+    scored from the call's own K before the gate reads them; a context of whole
+    tiles (no partial last tile) decodes like the oracle."""
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention
+    from orthocache_gpu.norm_cache import SpectralNormCache
+    B, Hq, Hkv, d, S0, S1 = 1, 4, 2, 128, 192, 384  # prefill 3 tiles, decode over 6
+    G = Hq // Hkv
+    q, k, v = _qkv(B, Hq, Hkv, S0, S1, d, dtype, seed=21)
+    hook = OrthoCache_GQA_Attention(tau=-1.0, score_new_tiles=True)
+    hook.norm_cache = SpectralNormCache(Hkv, 8, torch.device(DEV))
+    hook.orthocache_attention(q, k[:, :, :S0], v[:, :, :S0], G)
+    q1 = q[:, :, -1:]
+    nc_before = np64(hook.norm_cache.cache).copy()
+    want_norms = O.hook_tile_norms(np64(k))[0]  # (Hkv, 6)
+    np.testing.assert_allclose(nc_before[:, :3], want_norms[:, :3], rtol=4 * 2.0 ** -23)
+    assert not nc_before[:, 3:].any()
+    probe = O.hook_decode(np64(q1), np64(k), np64(v), want_norms, G, tau=-1.0)
+    hook.tau = _gap_tau(probe["qn"][:, :, None].astype(np.float64) * want_norms[None] / (64 * d))
+    out = hook.orthocache_attention(q1, k, v, G)
+    np.testing.assert_allclose(np64(hook.norm_cache.cache[:, :6]), want_norms, rtol=4 * 2.0 ** -23)
+    ref = O.hook_decode(np64(q1), np64(k), np64(v), want_norms, G, hook.tau)
+    r = O.round_to(ref["out"], dtype)
+    assert (np.abs(np64(out) - r) <= _tol(dtype, r)).all()
+    assert hook.stats['decode_tiles_skipped'] == int(ref["skipped"].sum())
+    assert 0 < ref["skipped"].sum() < Hkv * 6
