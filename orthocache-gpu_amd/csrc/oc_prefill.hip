@@ -46,60 +46,56 @@ struct PrefillArgs {
   int32_t dtype;
 };
 
-// Online-softmax state of the wave's 16 rows, MFMA output layout: lane
-// 16r + x keeps rows 4r + i (i = 0..3); l and e are the lane's partial sums
-// over its tokens, m is shared by the row's 16 lanes.
+// Online-softmax state in the transposed layout: lane 16r + x works on
+// query x (scores of tokens 16tb + 4r + i, i = 0..3, in c[tb][i]); m is
+// shared by the query's four lanes x, x + 16, x + 32, x + 48, and l, e are
+// their partial sums.
 struct PfState {
-  float m[4];
-  float l[4];
-  float e[4];  // sum of e^(s - m) * s (entropy)
-  int n[4];    // attended tokens of the row (entropy)
+  float m;
+  float l;
+  float e;  // sum of e^(s - m) * s (entropy)
+  int n;    // attended tokens of the query (entropy)
 };
 
-// Causal online-softmax update from one tile's raw logits c (row 4r + i,
-// token 16 tb + x in lane 16r + x, register i); token tok0 + j is visible to
-// row i when tok0 + j < nvis[i].  p goes to sp[row * 64 + token].
+// Causal online-softmax update of one tile's raw scores c (transposed
+// layout); token tok0 + j is visible to the lane's query when tok0 + j <
+// nvis.  c becomes e^(s - m) and the accumulators are rescaled.
 template <int D, bool ENT>
-__device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&accp)[D / 16], const f32x4 (&c)[4], float* sp,
-                                           float scale, const int (&nvis)[4], int tok0, int lane) {
-  const int x = lane & 15;
+__device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f32x4 (&c)[4], float scale, int nvis,
+                                           int tok0, int lane) {
   const int r = lane >> 4;
-  float v[4][4];
+  float mt = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) v[tb][i] = tok0 + 16 * tb + x < nvis[i] ? c[tb][i] * scale : -__builtin_inff();
+    for (int i = 0; i < 4; ++i) {
+      const float v = tok0 + 16 * tb + 4 * r + i < nvis ? c[tb][i] * scale : -__builtin_inff();
+      c[tb][i] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, xpair<16>(mt));
+  mt = fmaxf(mt, xpair<32>(mt));
+  const float mn = fmaxf(st.m, mt);
+  const float alpha = __expf(st.m - mn);
+  st.m = mn;
+  float ls = 0.f, es = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float mt = fmaxf(fmaxf(v[0][i], v[1][i]), fmaxf(v[2][i], v[3][i]));
-    mt = fmaxf(mt, xpair<8>(mt));
-    mt = fmaxf(mt, xpair<4>(mt));
-    mt = fmaxf(mt, xpair<2>(mt));
-    mt = fmaxf(mt, xpair<1>(mt));
-    const float mn = fmaxf(st.m[i], mt);
-    const float alpha = __expf(st.m[i] - mn);
-    st.m[i] = mn;
-    float ls = 0.f, es = 0.f;
+  for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const bool ok = tok0 + 16 * tb + x < nvis[i];
-      const float pp = __expf(v[tb][i] - mn);
+    for (int i = 0; i < 4; ++i) {
+      const float v = c[tb][i];
+      const float pp = __expf(v - mn);
       ls += pp;
-      if constexpr (ENT) es = ok ? __builtin_fmaf(pp, v[tb][i], es) : es;
-      v[tb][i] = pp;
+      if constexpr (ENT) es = pp > 0.f ? __builtin_fmaf(pp, v, es) : es;
+      c[tb][i] = pp;
     }
-    st.l[i] = __builtin_fmaf(st.l[i], alpha, ls);
-    if constexpr (ENT) {
-      st.e[i] = __builtin_fmaf(st.e[i], alpha, es);
-      st.n[i] += min(max(nvis[i] - tok0, 0), 64);
-    }
-#pragma unroll
-    for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha;
+  st.l = __builtin_fmaf(st.l, alpha, ls);
+  if constexpr (ENT) {
+    st.e = __builtin_fmaf(st.e, alpha, es);
+    st.n += min(max(nvis - tok0, 0), 64);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) sp[(4 * r + i) * 64 + 16 * tb + x] = v[tb][i];
+  for (int nc = 0; nc < D / 16; ++nc) acc[nc] *= alpha;
 }
 
 // q of the wave's 16 rows as MFMA A operands.  16-bit: lane 16kg + x holds
@@ -156,8 +152,7 @@ struct PfTile {
   static constexpr int KV = 64 * ROW;                     // bytes of one K (or V) tile
   static constexpr int NL = KV / (kPfThreads * 16);       // chunks per thread per matrix
   static constexpr int STAGES = 2 * KV <= 32768 ? 2 : 1;
-  static constexpr int P = 16 * 64 * 4;                   // a wave's p tile
-  static constexpr int LDS = STAGES * 2 * KV + kPfWaves * P;
+  static constexpr int LDS = STAGES * 2 * KV;
   __device__ static int swz(int r) { return (r / RB) % LPT; }
 };
 
@@ -189,7 +184,17 @@ __device__ __forceinline__ void pf_fetch(const PrefillArgs& a, const char* kh, c
   }
 }
 
-// registers -> an LDS stage (K swizzled, V plain)
+// LDS row of V's token t (16-bit): within each 32-token block, token
+// 16a + 4g + b goes to row 8g + 4a + b, so that the transposing read of rows
+// 8g .. 8g + 7 hands lane group g the tokens 4g + b and 16 + 4g + b -- the
+// tokens whose scores the lane holds (tile_pv_t).  float32 V stays in order.
+template <int DT>
+__device__ __forceinline__ int pf_vrow(int t) {
+  if constexpr (DT == OC_F32) return t;
+  return (t & ~31) + 8 * ((t >> 2) & 3) + 4 * ((t >> 4) & 1) + (t & 3);
+}
+
+// registers -> an LDS stage (K swizzled, V rows permuted for 16-bit)
 template <int DT, int D>
 __device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char* sk, char* sv) {
   using L = PfTile<DT, D>;
@@ -198,14 +203,15 @@ __device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char
     const int g = tid + kPfThreads * j;
     const int r = g / L::LPT, c = g % L::LPT;
     *reinterpret_cast<uint4*>(sk + r * L::ROW + 16 * (c ^ L::swz(r))) = st.k[j];
-    *reinterpret_cast<uint4*>(sv + r * L::ROW + 16 * c) = st.v[j];
+    *reinterpret_cast<uint4*>(sv + pf_vrow<DT>(r) * L::ROW + 16 * c) = st.v[j];
   }
 }
 
-// S = q.K^T of one tile from the LDS stage: c[tb] = rows x tokens 16tb ..
-// 16-bit: the B operand of instruction dc is row 16tb + x, logical chunk
-// 4dc + kg; float32: 4 columns kg*D/4 + 4j .. per read feed instructions
-// 4j .. 4j + 3.
+// S^T = K.q^T of one tile from the LDS stage: c[tb][i] is the score of
+// token 16tb + 4r + i for query x in lane 16r + x.  K is the A operand:
+// 16-bit instruction dc takes row 16tb + x, logical chunk 4dc + kg; float32
+// reads 4 columns kg*D/4 + 4j .. for instructions 4j .. 4j + 3; q (the B
+// operand) is in the same registers as before.
 template <int DT, int D>
 __device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const char* sk, int lane, f32x4 (&c)[4]) {
   using L = PfTile<DT, D>;
@@ -224,7 +230,7 @@ __device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const char* sk, i
         const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          c[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(q.w[4 * j + e]), __uint_as_float(uw[e]),
+          c[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(uw[e]), __uint_as_float(q.w[4 * j + e]),
                                                        c[tb], 0, 0, 0);
       }
     } else {
@@ -233,24 +239,77 @@ __device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const char* sk, i
         const uint4 u = *reinterpret_cast<const uint4*>(rowp + 16 * ((4 * dc + kg) ^ sw));
         const uint32_t aq[4] = {q.w[4 * dc], q.w[4 * dc + 1], q.w[4 * dc + 2], q.w[4 * dc + 3]};
         const uint32_t bk[4] = {u.x, u.y, u.z, u.w};
-        c[tb] = mfma_qk<DT>(aq, bk, c[tb]);
+        c[tb] = mfma_qk<DT>(bk, aq, c[tb]);
       }
     }
   }
 }
 
-// float32 p.V: A = P[row x][token 4kc + kg] (exact), B = V[token 4kc + kg][16nc + x].
-template <int D>
-__device__ __forceinline__ void pf_pv_f32(f32x4 (&accp)[D / 16], const float* sp, const float* sv, int lane) {
+// O^T += V^T P^T on the matrix cores (transposed layout): acc[nc][i] is
+// output column 16nc + 4r + i of query x in lane 16r + x.  16-bit: per
+// 32-token block j, A = V^T read with ds_read_b64_tr_b16 from the permuted
+// rows (lane group g gets tokens 32j + 4g + b and 32j + 16 + 4g + b), B =
+// the lane's own eight probabilities c[2j][b], c[2j + 1][b] as a 16-bit
+// high part plus the 16-bit rounding of the remainder (two instructions).
+// float32: 16x16x4 steps over (tb, i), A = V[16tb + 4r + i][16nc + x], B =
+// c[tb][i], exact.
+template <int DT, int D>
+__device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4], const char* svb, int lane) {
   const int x = lane & 15;
   const int kg = lane >> 4;
-#pragma unroll 4
-  for (int kc = 0; kc < 16; ++kc) {
-    const float pa = sp[x * 64 + 4 * kc + kg];
-    const float* vr = sv + (4 * kc + kg) * D + x;
+  if constexpr (DT == OC_F32) {
+    const float* sv = reinterpret_cast<const float*>(svb);
 #pragma unroll
-    for (int nc = 0; nc < D / 16; ++nc)
-      accp[nc] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vr[16 * nc], accp[nc], 0, 0, 0);
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float* vr = sv + (16 * tb + 4 * kg + i) * D + x;
+#pragma unroll
+        for (int nc = 0; nc < D / 16; ++nc)
+          acc[nc] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * nc], c[tb][i], acc[nc], 0, 0, 0);
+      }
+  } else {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const uint16_t* sv = reinterpret_cast<const uint16_t*>(svb);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float pv[8];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        pv[b] = c[2 * j][b];
+        pv[4 + b] = c[2 * j + 1][b];
+      }
+      uint32_t bhi[4], blo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (DT == OC_BF16) {
+          const __bf16 h0 = (__bf16)pv[2 * e], h1 = (__bf16)pv[2 * e + 1];
+          const __bf16 l0 = (__bf16)(pv[2 * e] - (float)h0), l1 = (__bf16)(pv[2 * e + 1] - (float)h1);
+          bhi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          blo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        } else {
+          const _Float16 h0 = (_Float16)pv[2 * e], h1 = (_Float16)pv[2 * e + 1];
+          const _Float16 l0 = (_Float16)(pv[2 * e] - (float)h0), l1 = (_Float16)(pv[2 * e + 1] - (float)h1);
+          bhi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+          blo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+      }
+      // lane x of group kg reads rows 32j + 8kg + 4h + x/4 (h = 0, 1)
+      const uint16_t* rowp = sv + (32 * j + 8 * kg + (x >> 2)) * D + 4 * (x & 3);
+#pragma unroll
+      for (int nc = 0; nc < D / 16; ++nc) {
+        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
+        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
+        const uint32_t av[4] = {(uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16),
+                                (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16),
+                                (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16),
+                                (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16)};
+        acc[nc] = mfma_qk<DT>(av, bhi, acc[nc]);
+        acc[nc] = mfma_qk<DT>(av, blo, acc[nc]);
+      }
+    }
   }
 }
 
@@ -274,17 +333,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
   const int h = bh % a.Hq;
   const int kv = h / a.G;
   const int pos0 = qb * 64 + 16 * wave;
-  float* sp = reinterpret_cast<float*>(sh + L::STAGES * 2 * L::KV + wave * L::P);
 
   const int off = a.Skv - a.Sq;  // query s sees keys j <= s + off
   const int r = lane >> 4;
   const int x = lane & 15;
-  int nvis[4];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    const int pos = pos0 + 4 * r + ii;
-    nvis[ii] = pos < a.Sq ? min(max(pos + off + 1, 0), a.Skv) : 0;
-  }
+  const int qpos = pos0 + x;  // this lane's query
+  const int nvis = qpos < a.Sq ? min(max(qpos + off + 1, 0), a.Skv) : 0;
   // this wave's tiles, and the workgroup's (its last query's window)
   const int tend = pos0 < a.Sq ? (min(max(min(pos0 + 15, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64 : 0;
   const int wg_tend = (min(max(min(qb * 64 + 63, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
@@ -299,15 +353,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
     return t;
   };
 
-  PfState st;
+  PfState st{kM0, 0.f, 0.f, 0};
   f32x4 accp[D / 16];
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    st.m[ii] = kM0;
-    st.l[ii] = 0.f;
-    st.e[ii] = 0.f;
-    st.n[ii] = 0;
-  }
 #pragma unroll
   for (int nc = 0; nc < D / 16; ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -328,13 +375,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
     if (t < tend) {
       f32x4 c[4];
       pf_logits<DT, D>(q, stage_k(s), lane, c);
-      pf_softmax<D, ENT>(st, accp, c, sp, a.scale, nvis, t * 64, lane);
-      // the p stores have landed (LDS counter only: the prefetch stays in flight)
-      __builtin_amdgcn_s_waitcnt(0xC07F);
-      if constexpr (DT == OC_F32)
-        pf_pv_f32<D>(accp, sp, reinterpret_cast<const float*>(stage_v(s)), lane);
-      else
-        tile_pv_mfma<DT, D, 16>(accp, sp, reinterpret_cast<const uint16_t*>(stage_v(s)), lane);
+      pf_softmax<D, ENT>(st, accp, c, a.scale, nvis, t * 64, lane);
+      pf_pv<DT, D>(accp, c, stage_v(s), lane);
     }
     if constexpr (L::STAGES == 1) __syncthreads();  // the only stage is free again
     if (tn < wg_tend) pf_stash<DT, D>(reg, tid, stage_k(L::STAGES - 1 - s), stage_v(L::STAGES - 1 - s));
@@ -342,36 +384,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
     t = tn;
   }
 
-  // row sums over the 16 lanes of each row, then out = acc / max(l, 1e-9)
-  char* ob = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+  // sums over the query's four lanes, then out = acc / max(l, 1e-9): lane
+  // 16r + x writes columns 16nc + 4r .. + 4 of query x
+  float l = st.l;
+  l += xpair<16>(l);
+  l += xpair<32>(l);
+  const float inv = 1.f / fmaxf(l, 1e-9f);
+  if (qpos < a.Sq) {
+    char* orow = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qpos * a.o_ss;
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) {
-    float l = st.l[ii];
-    l += xpair<8>(l);
-    l += xpair<4>(l);
-    l += xpair<2>(l);
-    l += xpair<1>(l);
-    const int pos = pos0 + 4 * r + ii;
-    const float inv = 1.f / fmaxf(l, 1e-9f);
-    if (pos < a.Sq) {
+    for (int nc = 0; nc < D / 16; ++nc) {
+      const int col = 16 * nc + 4 * r;
+      if constexpr (DT == OC_F32) {
+        *reinterpret_cast<float4*>(orow + 4 * col) =
+            float4{accp[nc][0] * inv, accp[nc][1] * inv, accp[nc][2] * inv, accp[nc][3] * inv};
+      } else {
 #pragma unroll
-      for (int nc = 0; nc < D / 16; ++nc)
-        store_scalar(ob + (int64_t)pos * a.o_ss + (int64_t)(16 * nc + x) * (DT == OC_F32 ? 4 : 2), a.dtype,
-                     accp[nc][ii] * inv);
-    }
-    if constexpr (ENT) {
-      float e = st.e[ii];
-      e += xpair<8>(e);
-      e += xpair<4>(e);
-      e += xpair<2>(e);
-      e += xpair<1>(e);
-      if (pos < a.Sq && x == 0) {
-        // H = -sum p ln p with p = e^(s - m) / l: m + ln l - (sum e^(s-m) s) / l,
-        // plus the clamp term of the probabilities that are exactly zero
-        const float hz = (float)(a.Skv - st.n[ii]) * kZeroPTerm;
-        const float H = l > 0.f ? st.m[ii] + logf(l) - e / l + hz : (float)a.Skv * kZeroPTerm;
-        a.entropy[((int64_t)b * a.Hq + h) * a.Sq + pos] = H;
+        for (int e = 0; e < 4; ++e) store_scalar(orow + 2 * (col + e), a.dtype, accp[nc][e] * inv);
       }
+    }
+  }
+  if constexpr (ENT) {
+    float e = st.e;
+    e += xpair<16>(e);
+    e += xpair<32>(e);
+    if (qpos < a.Sq && r == 0) {
+      // H = -sum p ln p with p = e^(s - m) / l: m + ln l - (sum e^(s-m) s) / l,
+      // plus the clamp term of the probabilities that are exactly zero
+      const float hz = (float)(a.Skv - st.n) * kZeroPTerm;
+      const float H = l > 0.f ? st.m + logf(l) - e / l + hz : (float)a.Skv * kZeroPTerm;
+      a.entropy[((int64_t)b * a.Hq + h) * a.Sq + qpos] = H;
     }
   }
 }
@@ -549,6 +591,9 @@ extern "C" int oc_prefill_attention(const oc_prefill_params* p, void* stream) {
   for (int64_t st : strides)
     if ((st * es) % 16) return fail(OC_ERR_INVALID, "q/k/v strides must be multiples of 16 bytes");
   if (((uintptr_t)p->q | (uintptr_t)p->k | (uintptr_t)p->v) % 16) return fail(OC_ERR_INVALID, "q/k/v not 16-byte aligned");
+  if (p->dtype == OC_F32 && ((uintptr_t)p->out % 16 || (p->out_stride_b * es) % 16 || (p->out_stride_h * es) % 16 ||
+                             (p->out_stride_s * es) % 16))
+    return fail(OC_ERR_INVALID, "float32 out rows must be 16-byte aligned");
   if (p->k_stride_s * es * 64 > 0x7FFFFFFF || p->v_stride_s * es * 64 > 0x7FFFFFFF)
     return fail(OC_ERR_UNSUPPORTED, "token stride too large");
   if (p->k_stride_s < p->head_dim || p->v_stride_s < p->head_dim)
