@@ -8,9 +8,10 @@
 // A wave owns 16 consecutive query positions of one q head (the 16 rows of
 // the 16x16 MFMA tiles) and walks the 64-token K/V tiles its causal window
 // reaches, skipping the tiles the mask evicts: S = q.K^T, online softmax with
-// a per-row causal limit, O += P.V.  A workgroup is 4 waves = 64 positions of
-// one head; the workgroups of one kv group run next to each other on one XCD,
-// so the K/V tiles they share stay in that XCD's L2.
+// a per-row causal limit, O += P.V.  A workgroup is 8 waves = 128 positions
+// of one head sharing each K/V tile through LDS; the workgroups of one kv
+// group run next to each other on one XCD, so the K/V tiles they share stay
+// in that XCD's L2.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -22,7 +23,8 @@
 namespace oc {
 namespace {
 
-constexpr int kPfWaves = 4;
+constexpr int kPfWaves = 8;
+constexpr int kPfRows = 16 * kPfWaves;  // query positions per workgroup
 constexpr int kPfThreads = kPfWaves * kWave;
 // -(1e-10) * ln(1e-10): what one zero probability adds to the entropy of a
 // softmax row whose probabilities are clamped to >= 1e-10 before the log
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
   const int b = bh / a.Hq;
   const int h = bh % a.Hq;
   const int kv = h / a.G;
-  const int pos0 = qb * 64 + 16 * wave;
+  const int pos0 = qb * kPfRows + 16 * wave;
 
   const int off = a.Skv - a.Sq;  // query s sees keys j <= s + off
   const int r = lane >> 4;
@@ -341,7 +343,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
   const int nvis = qpos < a.Sq ? min(max(qpos + off + 1, 0), a.Skv) : 0;
   // this wave's tiles, and the workgroup's (its last query's window)
   const int tend = pos0 < a.Sq ? (min(max(min(pos0 + 15, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64 : 0;
-  const int wg_tend = (min(max(min(qb * 64 + 63, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
+  const int wg_tend = (min(max(min(qb * kPfRows + kPfRows - 1, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
 
   PfQ<DT, D> q;
   pf_load_q<DT, D>(a, a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh, pos0, lane, q);
@@ -615,7 +617,7 @@ extern "C" int oc_prefill_attention(const oc_prefill_params* p, void* stream) {
   a.mask = p->tile_mask, a.m_sb = p->tile_mask_stride_b, a.m_sh = p->tile_mask_stride_h;
   a.scale = p->scale;
   a.entropy = p->entropy;
-  a.qblocks = (p->q_len + 63) / 64;
+  a.qblocks = (p->q_len + kPfRows - 1) / kPfRows;
   a.dtype = p->dtype;
   const int64_t blocks = (int64_t)a.qblocks * a.B * a.Hq;
   if (blocks > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many query blocks");
