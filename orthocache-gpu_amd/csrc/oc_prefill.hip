@@ -96,8 +96,11 @@ __device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f3
     st.e = __builtin_fmaf(st.e, alpha, es);
     st.n += min(max(nvis - tok0, 0), 64);
   }
+  // most tiles leave every running max unchanged (alpha == 1 in every lane)
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-  for (int nc = 0; nc < D / 16; ++nc) acc[nc] *= alpha;
+    for (int nc = 0; nc < D / 16; ++nc) acc[nc] *= alpha;
+  }
 }
 
 // q of the wave's 16 rows as MFMA A operands.  16-bit: lane 16kg + x holds
