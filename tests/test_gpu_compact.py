@@ -162,3 +162,75 @@ def test_compact_auto_tau_bypass_and_zero_active():
     dense = np.stack([O.dense_decode(np64(q[:, h]), np.repeat(np64(k[None, :512, h]), 2, 0),
                                      np.repeat(np64(v[None, :512, h]), 2, 0)) for h in range(H)], axis=1)
     np.testing.assert_allclose(np64(out_b), dense, atol=1e-5, rtol=1e-5)
+
+
+def _walsh_coherent(head_dim, seed, scale=0.5):
+    """sum of the natural-order Walsh rows 1..15 of length 512 with N(0, scale^2) coefficients"""
+    rng = np.random.RandomState(seed)
+    i = np.arange(512)
+    blk = np.zeros((512, head_dim))
+    for j in range(1, 16):
+        w = np.where(np.vectorize(lambda x: bin(x & j).count("1") % 2)(i), -1.0, 1.0)
+        blk += np.outer(w, rng.randn(head_dim) * scale)
+    return blk
+
+
+def test_zeta_separates_coherent_from_noise_at_equal_variance():
+    """tests/test_spectral_bands.py:130-218 of the reference: a Walsh-coherent
+    block has zeta < 0.01, white noise scaled to the same spatial variance has
+    zeta > 1 -- no spatial statistic tells them apart."""
+    from orthocache_gpu.spectral_energy import compute_spectral_decay_ratio, compute_spectral_bands
+    a = _walsh_coherent(64, 2026)
+    b = np.random.RandomState(42).randn(512, 64)
+    ma, mb = a.mean(0), b.mean(0)
+    b = mb + (b - mb) * np.sqrt(np.sum((a - ma) ** 2) / np.sum((b - mb) ** 2))
+    k = torch.from_numpy(np.stack([a, b])[:, :, None, :].reshape(1024, 1, 64).astype(np.float32)).to(DEV)
+    z = np64(compute_spectral_decay_ratio(k))[:, 0]
+    assert z[0] < 0.01 and z[1] > 1.0
+    dc, lo, mid, hi = compute_spectral_bands(k)
+    total = np64(lo + mid + hi)[:, 0] + np.sum(np64(dc) ** 2, axis=-1)[:, 0]
+    np.testing.assert_allclose(total, np.sum(np64(k).reshape(2, 512, 64) ** 2, axis=(1, 2)), rtol=1e-5)
+
+
+def test_multiband_mask_applies_both_gates():
+    """tests/test_spectral_bands.py:220-: block 0 alternating-sign noise is
+    evicted by the zeta gate even with a bound gate that passes everything."""
+    from orthocache_gpu.spectral_energy import compute_multiband_mask, compute_query_aware_mask
+    rng = np.random.RandomState(42)
+    keys = rng.randn(1024, 1, 64).astype(np.float32)
+    keys[:512, 0, :] *= np.where(np.arange(512) % 2 == 0, 5.0, -5.0)[:, None]
+    q = rng.randn(1, 1, 64).astype(np.float32)
+    kd, qd = torch.from_numpy(keys).to(DEV), torch.from_numpy(q).to(DEV)
+    m = compute_multiband_mask(qd, kd, -100.0, 1.0).cpu().numpy()
+    ref = O.block_spectra(keys, q)
+    assert np.array_equal(m, (ref["max_bound"] >= -100.0) & (ref["zeta"] <= 1.0))
+    assert not m[0, 0]
+    assert compute_query_aware_mask(qd, kd, -100.0).all()
+
+
+def test_orthocache_attention_api():
+    """tests/test_adaptive_attention.py of the reference: stream compaction of
+    all-active / all-evicted masks, zeros (q's dtype) when nothing is active,
+    bfloat16 (seq_q, heads, d) output, the eviction-rate statistic, and every
+    block active equal to dense attention."""
+    from orthocache_gpu.adaptive_attention import orthocache_attention, stream_compact
+    idx, n = stream_compact(torch.ones(6, dtype=torch.bool, device=DEV))
+    assert n == 6 and idx.tolist() == list(range(6))
+    idx, n = stream_compact(torch.zeros(6, dtype=torch.bool, device=DEV))
+    assert n == 0 and idx.tolist() == list(range(6))
+    idx, n = stream_compact(torch.tensor([False, True, False, True], device=DEV))
+    assert n == 2 and idx.tolist() == [1, 3, 0, 2]
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((3, 2, 64), generator=g).to(DEV)
+    k = torch.randn((2048, 2, 64), generator=g).to(DEV)
+    v = torch.randn((2048, 2, 64), generator=g).to(DEV)
+    out, st = orthocache_attention(q, k, v, torch.zeros(4, dtype=torch.bool, device=DEV))
+    assert not out.any() and out.dtype == q.dtype and st["num_active"] == 0 and st["eviction_rate"] == 1.0
+    out, st = orthocache_attention(q, k, v, torch.tensor([True, False, True, True], device=DEV))
+    assert out.dtype == torch.bfloat16 and out.shape == (3, 2, 64)
+    assert st["num_active"] == 3 and st["num_blocks"] == 4 and st["eviction_rate"] == pytest.approx(0.25)
+    out, _ = orthocache_attention(q, k, v, torch.ones(4, dtype=torch.bool, device=DEV))
+    dense = np.stack([O.dense_decode(np64(q[:, h]), np.repeat(np64(k[None, :, h]), 3, 0),
+                                     np.repeat(np64(v[None, :, h]), 3, 0)) for h in range(2)], axis=1)
+    r = O.round_to(dense, "bf16")
+    assert (np.abs(np64(out) - r) <= 2e-3 + np.abs(r) * 2.0 ** -8).all()
