@@ -417,10 +417,42 @@ def hook_measure(steps, warmup):
         us_ev = _event_us(lambda: X.prefill_attention(q, k, v, tile_mask=ev), steps, warmup)
         sdpa = _event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
                                                                                   enable_gqa=True), steps, warmup)
-        print(json.dumps({"only": "hook", "kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
-                          "tokens": S, "head_dim": d, "dtype": str(dt).replace("torch.", ""),
-                          "us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
-                          "us_half_evicted": round(us_ev, 1), "torch_sdpa_us": round(sdpa, 1)}), flush=True)
+        line = {"only": "hook", "kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                "tokens": S, "head_dim": d, "dtype": str(dt).replace("torch.", ""),
+                "us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
+                "us_half_evicted": round(us_ev, 1), "torch_sdpa_us": round(sdpa, 1)}
+        if dt == torch.float32:
+            line["cpu_baseline"] = _hook_cpu(q, k, v, Hq // Hkv)
+        print(json.dumps(line), flush=True)
+
+
+def _hook_cpu(q, k, v, G):
+    """The hook's prefill branch on the CPU oracle (float64 numpy, one core's
+    BLAS) for one kv group of the workload, scaled to all of them."""
+    import time
+    from oracle import orthocache_oracle as O
+    qs = q[:, :G].double().cpu().numpy()
+    ks, vs = k[:, :1].double().cpu().numpy(), v[:, :1].double().cpu().numpy()
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))  # numpy's BLAS threads
+    t0 = time.perf_counter()
+    O.hook_prefill(qs, ks, vs, G, tau=0.0)
+    sec = (time.perf_counter() - t0) * k.shape[1]
+    return {"value": round(sec * 1e6, 1), "unit": "us per call", "cores": nthreads, "kind": "port",
+            "sample": f"1 of {k.shape[1]} kv groups ({G} q heads) timed, scaled"}
+
+
+def _compact_cpu(q, k, v, heads):
+    """The compact forward on the CPU oracle for `heads` of the heads, scaled."""
+    import time
+    from oracle import orthocache_oracle as O
+    H = k.shape[1]
+    qs, ks, vs = (t[:, :heads].float().cpu().numpy() for t in (q, k, v))
+    t0 = time.perf_counter()
+    O.compact_forward(qs, ks, vs, zeta_max=5.0, tau=-1e30)
+    sec = (time.perf_counter() - t0) * H / heads
+    return {"value": round(sec * 1e6, 1), "unit": "us per call",
+            "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), "kind": "port",
+            "sample": f"{heads} of {H} heads timed, scaled"}
 
 
 def compact_measure(steps, warmup):
@@ -459,7 +491,7 @@ def compact_measure(steps, warmup):
     print(json.dumps({"only": "compact", "tokens": S, "heads": H, "head_dim": d, "dtype": "bfloat16",
                       "eviction_rate": meta["eviction_rate"], "block_spectrum_us": round(us_spec, 1),
                       "block_spectrum_gbps": round(kb / us_spec / 1e3, 1), "compact_forward_us": round(us_c, 1),
-                      "dense_forward_us": round(us_d, 1)}), flush=True)
+                      "dense_forward_us": round(us_d, 1), "cpu_baseline": _compact_cpu(q, k, v, 2)}), flush=True)
 
 
 def read_probe(steps, warmup, nbytes=2 << 30):
