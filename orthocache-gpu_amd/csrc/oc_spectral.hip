@@ -264,26 +264,47 @@ __global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, con
     const float var = bsum(v) / (float)(n - 1);  // n = 1: NaN, as torch.std
     tau = mean - __builtin_sqrtf(var);
   }
-  // per block: any head retained, head-mean zeta, beta = max_h qmax_h sqrt(E) / sqrt(d)
-  float zs = 0.f, zmin = __builtin_inff(), zmx = -__builtin_inff(), ret = 0.f, zbest = -__builtin_inff();
+  // per block (one wave per block, lanes over heads): any head retained,
+  // head-mean zeta, largest bound, beta = max_h qmax_h sqrt(E) / sqrt(d)
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const float isd = 1.0f / __builtin_sqrtf((float)d);
-  for (int b = tid; b < nb; b += 1024) {
+  auto wsum = [](float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+  };
+  auto wmax = [](float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+  };
+  struct Blk {
+    bool any;
+    float za, bmx, beta;
+  };
+  auto block_stats = [&](int b) {
     bool any = false;
-    float zsum = 0.f, bmx = -__builtin_inff();
-    for (int h = 0; h < H; ++h) {
-      const float m = mb[b * H + h], z = zeta[b * H + h];
+    float zsum = 0.f, bmx = -__builtin_inff(), beta = -__builtin_inff();
+    for (int h = lane; h < H; h += 64) {
+      const float m = mb[(int64_t)b * H + h], z = zeta[(int64_t)b * H + h];
       any = any || (m >= tau && z <= zeta_max);
       zsum += z;
       bmx = fmaxf(bmx, m);
+      beta = fmaxf(beta, qmax[h] * __builtin_sqrtf(fmaxf(energy[(int64_t)b * H + h], 0.f)) * isd);
     }
-    unified[b] = any ? 1 : 0;
-    for (int t = 0; t < tiles_per_block; ++t) tile_mask[(int64_t)b * tiles_per_block + t] = any ? 1 : 0;
-    const float za = zsum / (float)H;
-    zs += za;
-    zmin = fminf(zmin, za);
-    zmx = fmaxf(zmx, za);
-    ret += any ? 1.f : 0.f;
-    if (any) zbest = fmaxf(zbest, bmx);
+    return Blk{__ballot(any) != 0, wsum(zsum) / (float)H, wmax(bmx), wmax(beta)};
+  };
+  float zs = 0.f, zmin = __builtin_inff(), zmx = -__builtin_inff(), ret = 0.f, zbest = -__builtin_inff();
+  for (int b = wave; b < nb; b += 16) {
+    const Blk k = block_stats(b);
+    for (int t = lane; t < tiles_per_block; t += 64) tile_mask[(int64_t)b * tiles_per_block + t] = k.any ? 1 : 0;
+    if (lane == 0) {
+      unified[b] = k.any ? 1 : 0;
+      zs += k.za;
+      zmin = fminf(zmin, k.za);
+      zmx = fmaxf(zmx, k.za);
+      ret += k.any ? 1.f : 0.f;
+      if (k.any) zbest = fmaxf(zbest, k.bmx);
+    }
   }
   const float zmean = bsum(zs) / (float)nb;
   zmin = -bmax(-zmin);
@@ -292,17 +313,14 @@ __global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, con
   float zmax_ret = bmax(zbest);
   if (retained == 0.f) zmax_ret = 0.f;
   float zv = 0.f, perf = 0.f, stat = 0.f;
-  for (int b = tid; b < nb; b += 1024) {
-    float zsum = 0.f, beta = -__builtin_inff();
-    for (int h = 0; h < H; ++h) {
-      zsum += zeta[b * H + h];
-      beta = fmaxf(beta, qmax[h] * __builtin_sqrtf(fmaxf(energy[b * H + h], 0.f)) * isd);
-    }
-    const float za = zsum / (float)H;
-    zv = __builtin_fmaf(za - zmean, za - zmean, zv);
-    if (!unified[b]) {
-      if (zmax_ret - beta >= underflow) perf += 1.f;
-      else stat += 1.f;
+  for (int b = wave; b < nb; b += 16) {
+    const Blk k = block_stats(b);
+    if (lane == 0) {
+      zv = __builtin_fmaf(k.za - zmean, k.za - zmean, zv);
+      if (!k.any) {
+        if (zmax_ret - k.beta >= underflow) perf += 1.f;
+        else stat += 1.f;
+      }
     }
   }
   const float zvar = bsum(zv) / (float)(nb - 1);
