@@ -72,3 +72,31 @@ def attend_tiles(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
                        out_dtype=torch.bfloat16, tile_mask=tm)
         out[s0:s0 + g] = res.out.view(nh, g, hd).permute(1, 0, 2)
     return out
+
+
+def orthocache_attention_batched(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                                 block_mask: torch.Tensor, block_size: int = 512) -> tuple:
+    """q (batch, seq_q, heads, d), k_cache / v_cache (batch, seq_k, heads, d),
+    one block_mask (num_blocks,) shared by the batch.  Returns (bfloat16
+    (batch, seq_q, heads, d), stats) (adaptive_attention.py:246-294)."""
+    global BS
+    BS = block_size
+    device = X.require_gpu(q, k_cache, v_cache)
+    seq_k = k_cache.shape[1]
+    nb = block_mask.shape[0]
+    keep = block_mask.to(device=device, dtype=torch.bool)
+    num_active = int(keep.sum().item())
+    if num_active == 0:
+        return torch.zeros_like(q), {'num_active': 0, 'eviction_rate': 1.0, 'path': 'zero'}
+    if block_size % X.TILE_SIZE:
+        raise NotImplementedError(f"block_size {block_size} is not a multiple of the 64-token tile")
+    tiles = keep.to(torch.uint8).repeat_interleave(block_size // X.TILE_SIZE)
+    out = torch.stack([attend_tiles(q[b], k_cache[b], v_cache[b], tiles, nb * block_size)
+                       for b in range(q.shape[0])])
+    return out, {
+        'num_active': num_active,
+        'num_blocks': seq_k // block_size,
+        'eviction_rate': 1.0 - num_active / (seq_k // block_size),
+        'batch_size': q.shape[0],
+        'path': 'masked_decode',
+    }

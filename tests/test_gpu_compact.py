@@ -234,3 +234,20 @@ def test_orthocache_attention_api():
                                      np.repeat(np64(v[None, :, h]), 3, 0)) for h in range(2)], axis=1)
     r = O.round_to(dense, "bf16")
     assert (np.abs(np64(out) - r) <= 2e-3 + np.abs(r) * 2.0 ** -8).all()
+
+
+def test_orthocache_attention_batched():
+    from orthocache_gpu.adaptive_attention import orthocache_attention, orthocache_attention_batched
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn((2, 3, 2, 64), generator=g).to(DEV)
+    k = torch.randn((2, 1536, 2, 64), generator=g).to(DEV)
+    v = torch.randn((2, 1536, 2, 64), generator=g).to(DEV)
+    mask = torch.tensor([True, False, True], device=DEV)
+    out, st = orthocache_attention_batched(q, k, v, mask)
+    assert out.shape == (2, 3, 2, 64) and out.dtype == torch.bfloat16
+    assert st["batch_size"] == 2 and st["num_active"] == 2 and st["eviction_rate"] == pytest.approx(1 / 3)
+    for b in range(2):
+        one, _ = orthocache_attention(q[b], k[b], v[b], mask)
+        assert torch.equal(out[b], one)
+    zero, st0 = orthocache_attention_batched(q, k, v, torch.zeros(3, dtype=torch.bool, device=DEV))
+    assert not zero.any() and st0["num_active"] == 0
