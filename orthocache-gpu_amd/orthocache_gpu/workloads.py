@@ -85,6 +85,35 @@ def make_kv(rows: int, seq_len: int, head_dim: int, *, noise_frac: float = 0.5, 
     return KVWorkload(kq, vq, noise, ks, vs)
 
 
+def make_kv_literal(rows: int, seq_len: int, head_dim: int, *, dtype=torch.float32, seed: int = 0):
+    """The config text read literally, with the Walsh rows along head_dim:
+    every token's key is a combination of natural-order rows of H_head_dim
+    with its own N(0, 1) coefficients -- rows 1..4 (plus 0.05 N(0, 1)) in
+    half the tiles, rows head_dim/2 .. head_dim-1 in the other half.  Along
+    the tokens every tile is then white noise, so the 64-point token-axis
+    zeta of every tile centres on 32/7 (about 4.58) whatever its label, and
+    zeta_max = 5 evicts a label-independent share (about 12% of the "noise"
+    and 40% of the "smooth" tiles at head_dim 128)."""
+    g = torch.Generator().manual_seed(seed)
+    i = torch.arange(head_dim)
+    pc = torch.zeros((head_dim, head_dim), dtype=torch.int64)
+    x = i[:, None] & i[None, :]
+    while bool(x.any()):
+        pc += x & 1
+        x = x >> 1
+    wd = (1.0 - 2.0 * (pc % 2).float()) / head_dim ** 0.5    # H_d / sqrt(d), rows = sequency basis
+    t_count = seq_len // TILE
+    coef = torch.zeros((rows, t_count, TILE, head_dim))
+    noise = torch.rand((rows, t_count), generator=g) < 0.5
+    low = torch.randn((rows, t_count, TILE, 4), generator=g)
+    high = torch.randn((rows, t_count, TILE, head_dim // 2), generator=g)
+    coef[..., 1:5] = low * (~noise)[..., None, None]
+    coef[..., head_dim // 2:] = high * noise[..., None, None]
+    k = coef @ wd
+    k += 0.05 * torch.randn(k.shape, generator=g) * (~noise)[..., None, None]
+    return k.reshape(rows, seq_len, head_dim).to(dtype), noise
+
+
 def quantize_fp8_tiles(x: torch.Tensor):
     """Per-(row, 64-token tile) scale = amax/448 (1 for an all-zero tile);
     returns (e4m3fn tensor, (rows, T) float32 scales)."""

@@ -299,3 +299,18 @@ def test_fp8_table_and_encoder():
     enc = O.fp8_encode(x)
     ref_codes = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(enc, ref_codes)
+
+
+def test_literal_head_dim_reading_does_not_separate_the_tiles():
+    """The config text read with the Walsh rows along head_dim (the literal
+    reading) makes every tile white noise along the tokens: zeta centres on
+    32/7 for "smooth" and "noise" tiles alike, and zeta_max = 5 evicts a
+    label-independent share of both -- why the benchmarks build the tiles
+    along the tokens, as the reference's own benchmark does."""
+    from orthocache_gpu.workloads import make_kv_literal
+    keys, noise = make_kv_literal(8, 64 * 200, 128, seed=3)
+    _, zeta = O.fwht_scores(keys.reshape(-1, 128).numpy(), 5.0)[:2]
+    zeta, noise = np.asarray(zeta), noise.reshape(-1).numpy()
+    for part in (zeta[noise], zeta[~noise]):
+        assert abs(float(np.median(part)) - 32 / 7) < 0.3
+        assert 0.05 < float((part > 5.0).mean()) < 0.6
