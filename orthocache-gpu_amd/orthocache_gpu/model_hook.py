@@ -22,8 +22,10 @@ head_dim) and k, v (batch, num_kv_heads, kv_len, head_dim):
   it, and the band norms go to the norm cache.
 
 Statistics, governor updates and norm-cache contents follow the reference
-call for call (one entry per batch element per layer call), gathered from
-the device with one transfer per call.  Differences, all keyword-only or
+call for call (one entry per batch element per layer call).  The per-call
+values are reduced on the GPU and reach the host when `stats` is read (one
+transfer for all calls since the last read), or at once when a governor
+needs them for the next layer's tau.  Differences, all keyword-only or
 invisible at the reference's inputs:
 
 * ``score_new_tiles=True`` scores the tiles that complete during decode
@@ -94,12 +96,63 @@ class EntropyGovernor(ResidualGovernor):
         return tau
 
 
+class _Stats(dict):
+    """The hook's statistics (the reference's `stats` dict).  Each call's
+    values are reduced on the GPU and wait here as device tensors with the
+    function that folds them in; the first read of the dict moves all waiting
+    values to the host in one transfer and folds them in call order, so a
+    patched model's forward does not stop for them.  A governor needs each
+    layer's eviction rate before the next layer's tau, so with a governor
+    every call folds at once."""
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self._pending = []
+        self._folding = False
+
+    _MAX_PENDING = 256  # calls held before a fold (bounds the device tensors kept alive)
+
+    def defer(self, fold, dev: torch.Tensor) -> None:
+        self._pending.append((fold, dev))
+        if len(self._pending) >= self._MAX_PENDING:
+            self.fold()
+
+    def fold(self) -> None:
+        if not self._pending or self._folding:
+            return
+        pending, self._pending = self._pending, []
+        host = torch.cat([d.reshape(-1).to(torch.float64) for _, d in pending]).cpu()
+        self._folding = True
+        try:
+            i = 0
+            for fn, d in pending:
+                fn(host[i:i + d.numel()].view(d.shape))
+                i += d.numel()
+        finally:
+            self._folding = False
+
+
+def _folding(name):
+    base = getattr(dict, name)
+
+    def method(self, *args, **kw):
+        self.fold()
+        return base(self, *args, **kw)
+    method.__name__ = name
+    return method
+
+
+for _name in ('__getitem__', '__setitem__', '__delitem__', '__contains__', '__iter__', '__len__', '__repr__',
+              '__eq__', 'get', 'keys', 'values', 'items', 'copy', 'pop', 'popitem', 'setdefault', 'update'):
+    setattr(_Stats, _name, _folding(_name))
+
+
 def _empty_stats() -> dict:
-    return {
+    return _Stats({
         'total_tiles': 0, 'evicted_tiles': 0, 'layers_processed': 0, 'cs_bounds': [],
         'hallucination_scores': [], 'q_search_intensity': [], 'k_info_density': [],
         'decode_steps': 0, 'decode_tiles_skipped': 0, 'decode_tiles_total': 0,
-    }
+    })
 
 
 class OrthoCache_GQA_Attention:
@@ -163,25 +216,31 @@ class OrthoCache_GQA_Attention:
         if self.norm_cache is not None:
             self._store_norms(kn[B - 1], Hkv, T)
         self._prefill_tiles = T
-        # one transfer: per batch element [evicted, max q norm, max k norm, mean entropy]
+        # per batch element [evicted, max q norm, max k norm, mean entropy], reduced on the GPU
         zeros = torch.zeros((B,), dtype=torch.float32, device=query.device)
-        host = torch.stack([
+        dev = torch.stack([
             evict.view(B, -1).sum(1, dtype=torch.int64).to(torch.float32),
             qn.amax(1).clamp(min=0.0),
             kn.reshape(B, -1).amax(1).clamp(min=0.0),
             ent.view(B, -1).mean(1) if ent is not None else zeros,
-        ]).cpu().double()
-        for b in range(B):
-            evicted = int(host[0, b])
-            self.stats['total_tiles'] += Hkv * T
-            self.stats['evicted_tiles'] += evicted
-            self._exhaust(float(host[1, b]), float(host[2, b]))
-            if self.governor is not None and Hkv * T > 0:
-                self.governor.report_layer(evicted / (Hkv * T))
-            if want_entropy:
-                self.governor.set_entropy(float(host[3, b]))
-                self.stats['entropy'] = float(host[3, b])
-        self.stats['layers_processed'] += 1
+        ])
+        stats, gov = self.stats, self.governor
+
+        def fold(host):
+            for b in range(B):
+                evicted = int(host[0, b])
+                stats['total_tiles'] += Hkv * T
+                stats['evicted_tiles'] += evicted
+                _exhaust(stats, float(host[1, b]), float(host[2, b]))
+                if gov is not None and Hkv * T > 0:
+                    gov.report_layer(evicted / (Hkv * T))
+                if want_entropy:
+                    gov.set_entropy(float(host[3, b]))
+                    stats['entropy'] = float(host[3, b])
+            stats['layers_processed'] += 1
+        stats.defer(fold, dev)
+        if gov is not None:
+            stats.fold()
         return out
 
     def _store_norms(self, kn_last: torch.Tensor, Hkv: int, T: int) -> None:
@@ -195,10 +254,6 @@ class OrthoCache_GQA_Attention:
         nc.valid_tiles[:Hkv].clamp_(min=T)
         nc._populated = True
 
-    def _exhaust(self, max_q: float, max_k: float) -> None:
-        self.stats['hallucination_scores'].append(max_q / (max_k + 1e-10))
-        self.stats['q_search_intensity'].append(max_q)
-        self.stats['k_info_density'].append(max_k)
 
     # ------------------------------------------------------------ decode
 
@@ -226,21 +281,27 @@ class OrthoCache_GQA_Attention:
         kv = X.rows_layout(key.reshape(B * Hkv, Skv, d), value.reshape(B * Hkv, Skv, d), partial_tail=True)
         res = X.decode(kv, query.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0,
                        mode=N.OC_MODE_CACHED, out_dtype=query.dtype, tile_mask=keep.view(B * Hkv, -1))
-        host = torch.stack([
+        dev = torch.stack([
             (keep[:, :, :T] == 0).view(B, -1).sum(1, dtype=torch.int64).to(torch.float32),
             med.amax(1).clamp(min=0.0),
             norms[0, :, :T].amax().clamp(min=0.0).expand(B) if T > 0 else torch.zeros(
                 (B,), dtype=torch.float32, device=query.device),
-        ]).cpu().double()
-        for b in range(B):
-            skipped = int(host[0, b])
-            self._exhaust(float(host[1, b]), float(host[2, b]))
-            self.stats['decode_steps'] += 1
-            self.stats['decode_tiles_skipped'] += skipped
-            self.stats['decode_tiles_total'] += T * Hkv
-            if self.governor is not None and T > 0:
-                self.governor.report_layer(skipped / (T * Hkv))
-        self.stats['layers_processed'] += 1
+        ])
+        stats, gov = self.stats, self.governor
+
+        def fold(host):
+            for b in range(B):
+                skipped = int(host[0, b])
+                _exhaust(stats, float(host[1, b]), float(host[2, b]))
+                stats['decode_steps'] += 1
+                stats['decode_tiles_skipped'] += skipped
+                stats['decode_tiles_total'] += T * Hkv
+                if gov is not None and T > 0:
+                    gov.report_layer(skipped / (T * Hkv))
+            stats['layers_processed'] += 1
+        stats.defer(fold, dev)
+        if gov is not None:
+            stats.fold()
         return res.out.view(B, Hq, 1, d)
 
     # ------------------------------------------------------------ dense
@@ -250,6 +311,13 @@ class OrthoCache_GQA_Attention:
         key, value = _distinct_kv(query, key, value, G)
         out, _ = X.prefill_attention(query, key, value)
         return out
+
+
+def _exhaust(stats, max_q: float, max_k: float) -> None:
+    """The hallucination-exhaust entries of one batch element (perplexity_eval.py:506-510)."""
+    stats['hallucination_scores'].append(max_q / (max_k + 1e-10))
+    stats['q_search_intensity'].append(max_q)
+    stats['k_info_density'].append(max_k)
 
 
 def _distinct_kv(query, key, value, G):

@@ -80,3 +80,26 @@ def test_hook_fails_loudly_on_cpu_tensors():
     k = torch.randn(1, 2, 70, 64)
     with pytest.raises((RuntimeError, ValueError)):
         OrthoCache_GQA_Attention(tau=1.0).orthocache_attention(q, k, k, 2)
+
+
+def test_stats_fold_lazily_in_call_order():
+    """Per-call values wait on the device and are folded, in order, by the
+    first read of the dict (one transfer)."""
+    from orthocache_gpu.model_hook import _empty_stats
+    st = _empty_stats()
+    seen = []
+
+    def make(i):
+        def fold(host):
+            seen.append((i, host.tolist()))
+            st['layers_processed'] += 1
+        return fold
+    for i in range(3):
+        st.defer(make(i), torch.tensor([float(i), 2.0 * i]))
+    assert seen == []
+    assert st['layers_processed'] == 3
+    assert seen == [(0, [0.0, 0.0]), (1, [1.0, 2.0]), (2, [2.0, 4.0])]
+    for i in range(300):  # the pending list is bounded
+        st.defer(make(i), torch.tensor([1.0]))
+    assert len(st._pending) < 256
+    assert dict.__getitem__(st, 'layers_processed') >= 3 + 256
