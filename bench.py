@@ -464,6 +464,7 @@ def compact_measure(steps, warmup):
     import torch
     from orthocache_gpu import _launch as X
     from orthocache_gpu import orthocache_forward
+    from orthocache_gpu.adaptive_attention import attend_tiles
     S, H, d = 32768, 32, 128
     nb = S // 512
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -483,14 +484,28 @@ def compact_measure(steps, warmup):
     v = torch.randn((S, H, d), device="cuda", generator=g).to(torch.bfloat16)
     q = torch.randn((1, H, d), device="cuda", generator=g).to(torch.bfloat16)
     del c
-    us_spec = _event_us(lambda: X.block_spectra(k, q), steps, warmup)
+    # two K/V sets, alternated by the timed loops: 268 MB of K alone is about
+    # the size of the 256 MB Infinity Cache
+    sets = [(k, v), (k.clone(), v.clone())]
+    turn = [0]
+
+    def kv():
+        turn[0] ^= 1
+        return sets[turn[0]]
+
+    us_spec = _event_us(lambda: X.block_spectra(kv()[0], q), steps, warmup)
+    spec = X.block_spectra(k, q, want_qnorm=True)
+    us_gate = _event_us(lambda: X.compact_gate(spec, d, -1e30, 5.0, 88.72, 8), steps, warmup)
+    _, tmask, _ = X.compact_gate(spec, d, -1e30, 5.0, 88.72, 8)
+    us_attn = _event_us(lambda: attend_tiles(q, *kv(), tmask, S), steps, warmup)
     _, meta = orthocache_forward(q, k, v, mode="compact", tau=-1e30)
-    us_c = _event_us(lambda: orthocache_forward(q, k, v, mode="compact", tau=-1e30), steps, warmup)
-    us_d = _event_us(lambda: orthocache_forward(q, k, v, mode="dense"), steps, warmup)
+    us_c = _event_us(lambda: orthocache_forward(q, *kv(), mode="compact", tau=-1e30), steps, warmup)
+    us_d = _event_us(lambda: orthocache_forward(q, *kv(), mode="dense"), steps, warmup)
     kb = S * H * d * 2
     print(json.dumps({"only": "compact", "tokens": S, "heads": H, "head_dim": d, "dtype": "bfloat16",
                       "eviction_rate": meta["eviction_rate"], "block_spectrum_us": round(us_spec, 1),
-                      "block_spectrum_gbps": round(kb / us_spec / 1e3, 1), "compact_forward_us": round(us_c, 1),
+                      "block_spectrum_gbps": round(kb / us_spec / 1e3, 1), "compact_gate_us": round(us_gate, 1),
+                      "masked_attention_us": round(us_attn, 1), "compact_forward_us": round(us_c, 1),
                       "dense_forward_us": round(us_d, 1), "cpu_baseline": _compact_cpu(q, k, v, 2)}), flush=True)
 
 

@@ -910,21 +910,10 @@ def compact_forward(q, keys, values, zeta_max: float = 5.0, tau: Optional[float]
     v64 = np.asarray(values, dtype=np.float64)
     Sq, H, d = q64.shape
     spec = block_spectra(k64, q64)
-    mb = spec["max_bound"]
-    nb = mb.shape[0]
-    if tau is None:
-        tau = float(mb.mean() - mb.std(ddof=1))
-    block_mask = (mb >= tau) & (spec["zeta"] <= zeta_max)
-    unified = block_mask.any(axis=1)
-    retained = int(unified.sum())
-    zah = spec["zeta"].mean(axis=1)
-    # perfect-eviction classification (perfect_eviction.py:75-186)
-    z_max = float(mb[unified].max()) if retained else 0.0
-    qmax = np.linalg.norm(q64, axis=-1).max(axis=0)
-    beta = (qmax[None, :] * np.sqrt(np.maximum(spec["energy"], 0.0)) / math.sqrt(d)).max(axis=1)
-    gap = z_max - beta
-    perfect = int(((~unified) & (gap >= F32_UNDERFLOW)).sum())
-    statistical = int(((~unified) & (gap < F32_UNDERFLOW)).sum())
+    g = compact_gate(spec["max_bound"], spec["zeta"], spec["energy"], np.linalg.norm(q64, axis=-1).max(axis=0), d,
+                     zeta_max, tau)
+    tau, unified, retained = g["tau"], g["unified"], g["retained"]
+    nb = unified.shape[0]
     out = np.zeros((Sq, H, d))
     if retained:
         keep = np.repeat(unified, COMPACT_BLOCK)
@@ -934,10 +923,39 @@ def compact_forward(q, keys, values, zeta_max: float = 5.0, tau: Optional[float]
             lg = q64[:, h] @ kk.T / math.sqrt(d)
             p = np.exp(lg - lg.max(axis=1, keepdims=True))
             out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ vv
-    return out, {"tau": tau, "block_mask": block_mask, "unified": unified, "retained": retained,
-                 "zeta_mean": float(zah.mean()), "zeta_std": float(zah.std(ddof=1)) if nb > 1 else float("nan"),
-                 "zeta_min": float(zah.min()), "zeta_max_observed": float(zah.max()),
-                 "perfect": perfect, "statistical": statistical, "spectra": spec}
+    return out, dict(g, spectra=spec)
+
+
+def compact_gate(max_bound, zeta, energy, qmax, d: int, zeta_max: float, tau: Optional[float] = None):
+    """The compact forward's gates and statistics from the (block, head)
+    tables (pipeline.py:463-527): tau = mean - unbiased std of the max
+    bounds when not given (:571-583); (block, head) kept iff max bound >= tau
+    and zeta <= zeta_max (spectral_energy.py:198-233); a block is attended
+    when any head keeps it; zeta statistics over the per-block head means
+    (pipeline.py:482-487); z_max = the largest retained max bound, beta =
+    max_h qmax_h sqrt(E) / sqrt(d), and an evicted block is perfect iff
+    z_max - beta >= the float32 underflow margin (perfect_eviction.py:75-186).
+    qmax (H,) is the largest query norm per head."""
+    mb = np.asarray(max_bound, dtype=np.float64)
+    zeta = np.asarray(zeta, dtype=np.float64)
+    energy = np.asarray(energy, dtype=np.float64)
+    qmax = np.asarray(qmax, dtype=np.float64)
+    nb = mb.shape[0]
+    if tau is None:
+        tau = float(mb.mean() - mb.std(ddof=1))
+    block_mask = (mb >= tau) & (zeta <= zeta_max)
+    unified = block_mask.any(axis=1)
+    retained = int(unified.sum())
+    zah = zeta.mean(axis=1)
+    z_max = float(mb[unified].max()) if retained else 0.0
+    beta = (qmax[None, :] * np.sqrt(np.maximum(energy, 0.0)) / math.sqrt(d)).max(axis=1)
+    gap = z_max - beta
+    perfect = int(((~unified) & (gap >= F32_UNDERFLOW)).sum())
+    statistical = int(((~unified) & (gap < F32_UNDERFLOW)).sum())
+    return {"tau": tau, "block_mask": block_mask, "unified": unified, "retained": retained,
+            "zeta_mean": float(zah.mean()), "zeta_std": float(zah.std(ddof=1)) if nb > 1 else float("nan"),
+            "zeta_min": float(zah.min()), "zeta_max_observed": float(zah.max()), "z_max": z_max,
+            "perfect": perfect, "statistical": statistical}
 
 
 def stream_compact(mask: np.ndarray):

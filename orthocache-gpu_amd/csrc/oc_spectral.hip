@@ -17,6 +17,7 @@
 
 #include <cmath>
 
+#include "oc_kernels.h"
 #include "oc_status.h"
 #include "orthocache_hip.h"
 
@@ -77,19 +78,8 @@ __device__ __forceinline__ void load8(const char* p, float (&x)[8]) {
   }
 }
 
-__device__ __forceinline__ float block_sum(float v, float* sh_red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sh_red[w] = v;
-  __syncthreads();
-  float s = 0.f;
-  for (int i = 0; i < kSpThreads / 64; ++i) s += sh_red[i];
-  return s;
-}
-
 __device__ __forceinline__ float block_max(float v, float* sh_red) {
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  v = wave_max(v);
   const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh_red[w] = v;
@@ -109,8 +99,10 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   __shared__ float sh_z[64 * DMAX];  // Z_0[tl][c]
   __shared__ float sh_mean[DMAX];
   __shared__ float sh_red[kSpThreads / 64];
-  const int blk = blockIdx.x;
-  const int h = blockIdx.y;
+  // consecutive workgroups take the heads of one block, so the workgroups
+  // in flight together read whole token rows of the (S, H, d) cache
+  const int h = blockIdx.x;
+  const int blk = blockIdx.y;
   const int d = D ? D : a.d;
   const int CG = d / 8;
   const int TG = kSpThreads / CG;
@@ -118,6 +110,22 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   const int cg = tid % CG;
   const int tg = tid / CG;
   const char* kb = a.k + (int64_t)blk * kBlock * a.k_ts + (int64_t)h * a.k_hs + (int64_t)cg * 8 * (DT == OC_F32 ? 4 : 2);
+  // the bounds: wave w takes queries w, w + 4, ..., lane l columns l, l + 64, ...;
+  // the wave's first query is requested before the block streams in
+  constexpr int QPL = (DMAX + 63) / 64;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
+  auto load_q = [&](int s, float (&qv)[QPL]) {
+    const char* qr = a.q + (int64_t)s * a.q_ss + (int64_t)h * a.q_hs;
+#pragma unroll
+    for (int k = 0; k < QPL; ++k) {
+      const int c = lane + 64 * k;
+      qv[k] = c < d ? sp_load(qr + (int64_t)c * qes, a.q_dtype) : 0.f;
+    }
+  };
+  float q0[QPL];
+  if (a.q && wave < a.Sq) load_q(wave, q0);
   float e_mid = 0.f, e_high = 0.f, energy = 0.f;
   // positions per thread: 64 / TG when TG divides 64 (D = 64, 128), else a bound
   constexpr int TPT = D ? 64 / (kSpThreads / (D / 8)) : 64;
@@ -175,10 +183,25 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
     dc2 = y[0] * y[0];
     sh_mean[tid] = y[0] * (1.0f / 512.0f);  // DC / sqrt(512) with DC = sum_t k_t / sqrt(512)
   }
-  const float s_mid = block_sum(e_mid, sh_red) * 0.125f;
-  const float s_high = block_sum(e_high, sh_red) * 0.125f;
-  const float s_low = block_sum(e_low, sh_red) * (1.0f / 512.0f);
-  const float s_energy = block_sum(energy, sh_red);
+  // the four band sums in one reduction: lanes, then the four waves in LDS
+  __shared__ float sh_sum[kSpThreads / 64][4];
+  float r4[4] = {e_mid, e_high, e_low, energy};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r4[j] = wave_sum(r4[j]);
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sh_sum[wave][j] = r4[j];
+  }
+  __syncthreads();  // also: sh_mean complete
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r4[j] = sh_sum[0][j];
+    for (int w = 1; w < kSpThreads / 64; ++w) r4[j] += sh_sum[w][j];
+  }
+  const float s_mid = r4[0] * 0.125f;
+  const float s_high = r4[1] * 0.125f;
+  const float s_low = r4[2] * (1.0f / 512.0f);
+  const float s_energy = r4[3];
   (void)dc2;
   const float s_ac = s_low + s_mid + s_high;
   const int64_t o = (int64_t)blk * a.H + h;
@@ -190,33 +213,71 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
     if (a.e_ac) a.e_ac[o] = s_ac;
     if (a.energy) a.energy[o] = s_energy;
   }
-  __syncthreads();  // sh_mean complete
   if (a.mean && tid < d) a.mean[o * d + tid] = sh_mean[tid];
   if (!a.q) return;
   // query-aware bounds: (q . mean + ||q|| sqrt(E_ac)) / sqrt(d)
   const float inv_sd = 1.0f / __builtin_sqrtf((float)d);
   const float sq_ac = __builtin_sqrtf(fmaxf(s_ac, 0.f));
-  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
   float best = -__builtin_inff();
   float qbest = 0.f;
-  for (int s = tid; s < a.Sq; s += kSpThreads) {
-    const char* qr = a.q + (int64_t)s * a.q_ss + (int64_t)h * a.q_hs;
-    float dot = 0.f, nn = 0.f;
-    for (int c = 0; c < d; ++c) {
-      const float qv = sp_load(qr + (int64_t)c * qes, a.q_dtype);
-      dot = __builtin_fmaf(qv, sh_mean[c], dot);
-      nn = __builtin_fmaf(qv, qv, nn);
+  for (int s = wave; s < a.Sq; s += kSpThreads / 64) {
+    float qv[QPL];
+    if (s == wave) {
+#pragma unroll
+      for (int k = 0; k < QPL; ++k) qv[k] = q0[k];
+    } else {
+      load_q(s, qv);
     }
-    const float bnd = dot * inv_sd + __builtin_sqrtf(nn) * sq_ac * inv_sd;
-    if (a.bounds) a.bounds[((int64_t)s * a.nb + blk) * a.H + h] = bnd;
+    float dot = 0.f, nn = 0.f;
+#pragma unroll
+    for (int k = 0; k < QPL; ++k) {
+      const int c = lane + 64 * k;
+      if (c < d) {
+        dot = __builtin_fmaf(qv[k], sh_mean[c], dot);
+        nn = __builtin_fmaf(qv[k], qv[k], nn);
+      }
+    }
+    dot = wave_sum(dot);
+    nn = wave_sum(nn);
+    const float qn = __builtin_sqrtf(nn);
+    const float bnd = dot * inv_sd + qn * sq_ac * inv_sd;
+    if (a.bounds && lane == 0) a.bounds[((int64_t)s * a.nb + blk) * a.H + h] = bnd;
     best = fmaxf(best, bnd);
-    qbest = fmaxf(qbest, __builtin_sqrtf(nn));
+    qbest = fmaxf(qbest, qn);
   }
   best = block_max(best, sh_red);
   if (tid == 0 && a.max_bound) a.max_bound[o] = best;
   if (blk == 0 && a.q_norm_max) {
     qbest = block_max(qbest, sh_red);
     if (tid == 0) a.q_norm_max[h] = qbest;
+  }
+}
+
+constexpr int kGateLds = 2048;   // (block, head) entries staged in LDS by the gate kernel
+constexpr int kGateHeads = 256;  // query norms staged with them
+constexpr int kGateBlocks = 2048;  // blocks whose per-block results the gate kernel keeps in LDS
+constexpr int kGateWaves = 16;
+
+// N values reduced over the 1024-thread workgroup at once: a DPP reduction
+// per wave, then the 16 wave results from LDS (bit j of max_mask: maximum,
+// else sum; identical result in every thread, fixed order).
+template <int N>
+__device__ __forceinline__ void gate_reduce(float (&v)[N], unsigned max_mask, float (*sh)[8]) {
+  static_assert(N <= 8, "at most eight values per reduction");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = ((max_mask >> j) & 1) ? wave_max(v[j]) : wave_sum(v[j]);
+  __syncthreads();  // the previous reduction's reads of sh are done
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) sh[wave][j] = v[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    float t = sh[0][j];
+    for (int w = 1; w < kGateWaves; ++w) t = ((max_mask >> j) & 1) ? fmaxf(t, sh[w][j]) : t + sh[w][j];
+    v[j] = t;
   }
 }
 
@@ -232,51 +293,51 @@ __global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, con
                                                             int tau_auto, float zeta_max, float underflow,
                                                             int tiles_per_block, uint8_t* unified,
                                                             uint8_t* tile_mask, float* stats) {
-  __shared__ float sh_f[32];
-  __shared__ float sh_bcast[4];
+  __shared__ float sh_f[kGateWaves][8];
+  // the (block, head) tables and the query norms staged in LDS when they
+  // fit, every load in flight at once; otherwise read from global memory
+  __shared__ float sh_mb[kGateLds], sh_zeta[kGateLds], sh_en[kGateLds], sh_qmax[kGateHeads];
+  // per-block results of the first pass (any head kept, head-mean zeta, beta)
+  __shared__ float sh_za[kGateBlocks], sh_beta[kGateBlocks];
+  __shared__ uint8_t sh_any[kGateBlocks];
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int n = nb * H;
-  auto bsum = [&](float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const bool staged = n <= kGateLds && H <= kGateHeads;
+  const bool cache_blk = nb <= kGateBlocks;
+  if (staged) {
+#pragma unroll
+    for (int k = 0; k < kGateLds / 1024; ++k) {
+      const int i = tid + 1024 * k;
+      if (i < n) {
+        sh_mb[i] = mb[i];
+        sh_zeta[i] = zeta[i];
+        sh_en[i] = energy[i];
+      }
+    }
+    if (tid < H) sh_qmax[tid] = qmax[tid];
     __syncthreads();
-    if ((tid & 63) == 0) sh_f[tid >> 6] = v;
-    __syncthreads();
-    float t = 0.f;
-    for (int i = 0; i < 16; ++i) t += sh_f[i];
-    return t;
-  };
-  auto bmax = [&](float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    __syncthreads();
-    if ((tid & 63) == 0) sh_f[tid >> 6] = v;
-    __syncthreads();
-    float t = sh_f[0];
-    for (int i = 1; i < 16; ++i) t = fmaxf(t, sh_f[i]);
-    return t;
-  };
+    mb = sh_mb;
+    zeta = sh_zeta;
+    energy = sh_en;
+    qmax = sh_qmax;
+  }
   float tau = tau_in;
   if (tau_auto) {
-    float s = 0.f;
-    for (int i = tid; i < n; i += 1024) s += mb[i];
-    const float mean = bsum(s) / (float)n;
-    float v = 0.f;
-    for (int i = tid; i < n; i += 1024) v = __builtin_fmaf(mb[i] - mean, mb[i] - mean, v);
-    const float var = bsum(v) / (float)(n - 1);  // n = 1: NaN, as torch.std
+    float s[1] = {0.f};
+    for (int i = tid; i < n; i += 1024) s[0] += mb[i];
+    gate_reduce<1>(s, 0u, sh_f);
+    const float mean = s[0] / (float)n;
+    float v[1] = {0.f};
+    for (int i = tid; i < n; i += 1024) v[0] = __builtin_fmaf(mb[i] - mean, mb[i] - mean, v[0]);
+    gate_reduce<1>(v, 0u, sh_f);
+    const float var = v[0] / (float)(n - 1);  // n = 1: NaN, as torch.std
     tau = mean - __builtin_sqrtf(var);
   }
   // per block (one wave per block, lanes over heads): any head retained,
   // head-mean zeta, largest bound, beta = max_h qmax_h sqrt(E) / sqrt(d)
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
   const float isd = 1.0f / __builtin_sqrtf((float)d);
-  auto wsum = [](float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-  };
-  auto wmax = [](float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-  };
   struct Blk {
     bool any;
     float za, bmx, beta;
@@ -291,50 +352,59 @@ __global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, con
       bmx = fmaxf(bmx, m);
       beta = fmaxf(beta, qmax[h] * __builtin_sqrtf(fmaxf(energy[(int64_t)b * H + h], 0.f)) * isd);
     }
-    return Blk{__ballot(any) != 0, wsum(zsum) / (float)H, wmax(bmx), wmax(beta)};
+    return Blk{__ballot(any) != 0, wave_sum(zsum) / (float)H, wave_max(bmx), wave_max(beta)};
   };
-  float zs = 0.f, zmin = __builtin_inff(), zmx = -__builtin_inff(), ret = 0.f, zbest = -__builtin_inff();
-  for (int b = wave; b < nb; b += 16) {
+  // r1: zeta sum, retained (sums); -zeta min, zeta max, best retained bound (maxima)
+  float r1[5] = {0.f, 0.f, -__builtin_inff(), -__builtin_inff(), -__builtin_inff()};
+  for (int b = wave; b < nb; b += kGateWaves) {
     const Blk k = block_stats(b);
     for (int t = lane; t < tiles_per_block; t += 64) tile_mask[(int64_t)b * tiles_per_block + t] = k.any ? 1 : 0;
     if (lane == 0) {
       unified[b] = k.any ? 1 : 0;
-      zs += k.za;
-      zmin = fminf(zmin, k.za);
-      zmx = fmaxf(zmx, k.za);
-      ret += k.any ? 1.f : 0.f;
-      if (k.any) zbest = fmaxf(zbest, k.bmx);
-    }
-  }
-  const float zmean = bsum(zs) / (float)nb;
-  zmin = -bmax(-zmin);
-  zmx = bmax(zmx);
-  const float retained = bsum(ret);
-  float zmax_ret = bmax(zbest);
-  if (retained == 0.f) zmax_ret = 0.f;
-  float zv = 0.f, perf = 0.f, stat = 0.f;
-  for (int b = wave; b < nb; b += 16) {
-    const Blk k = block_stats(b);
-    if (lane == 0) {
-      zv = __builtin_fmaf(k.za - zmean, k.za - zmean, zv);
-      if (!k.any) {
-        if (zmax_ret - k.beta >= underflow) perf += 1.f;
-        else stat += 1.f;
+      if (cache_blk) {
+        sh_any[b] = k.any ? 1 : 0;
+        sh_za[b] = k.za;
+        sh_beta[b] = k.beta;
       }
+      r1[0] += k.za;
+      r1[1] += k.any ? 1.f : 0.f;
+      r1[2] = fmaxf(r1[2], -k.za);
+      r1[3] = fmaxf(r1[3], k.za);
+      if (k.any) r1[4] = fmaxf(r1[4], k.bmx);
     }
   }
-  const float zvar = bsum(zv) / (float)(nb - 1);
-  const float np_ = bsum(perf), ns_ = bsum(stat);
-  (void)sh_bcast;
+  gate_reduce<5>(r1, 0x1Cu, sh_f);  // its barriers also publish sh_any / sh_za / sh_beta
+  const float zmean = r1[0] / (float)nb;
+  const float retained = r1[1];
+  const float zmin = -r1[2], zmx = r1[3];
+  const float zmax_ret = retained == 0.f ? 0.f : r1[4];
+  // r2: squared zeta deviations, perfect and statistical evictions
+  float r2[3] = {0.f, 0.f, 0.f};
+  auto regime = [&](bool any, float za, float beta) {
+    r2[0] = __builtin_fmaf(za - zmean, za - zmean, r2[0]);
+    if (!any) {
+      if (zmax_ret - beta >= underflow) r2[1] += 1.f;
+      else r2[2] += 1.f;
+    }
+  };
+  if (cache_blk) {
+    for (int b = tid; b < nb; b += 1024) regime(sh_any[b] != 0, sh_za[b], sh_beta[b]);
+  } else {
+    for (int b = wave; b < nb; b += kGateWaves) {
+      const Blk k = block_stats(b);
+      if (lane == 0) regime(k.any, k.za, k.beta);
+    }
+  }
+  gate_reduce<3>(r2, 0u, sh_f);
   if (tid == 0) {
     stats[0] = tau;
     stats[1] = zmean;
-    stats[2] = __builtin_sqrtf(zvar);
+    stats[2] = __builtin_sqrtf(r2[0] / (float)(nb - 1));
     stats[3] = zmin;
     stats[4] = zmx;
     stats[5] = retained;
-    stats[6] = np_;
-    stats[7] = ns_;
+    stats[6] = r2[1];
+    stats[7] = r2[2];
     stats[8] = zmax_ret;
   }
 }
@@ -383,11 +453,11 @@ __global__ __launch_bounds__(1024) void stream_compact_kernel(const uint8_t* mas
 template <int DT>
 int launch_spectrum(const SpecArgs& a, hipStream_t s) {
   if (a.d == 128)
-    hipLaunchKernelGGL((block_spectrum_kernel<DT, 128>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 128>), dim3(a.H, a.nb), dim3(kSpThreads), 0, s, a);
   else if (a.d == 64)
-    hipLaunchKernelGGL((block_spectrum_kernel<DT, 64>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 64>), dim3(a.H, a.nb), dim3(kSpThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((block_spectrum_kernel<DT, 0>), dim3(a.nb, a.H), dim3(kSpThreads), 0, s, a);
+    hipLaunchKernelGGL((block_spectrum_kernel<DT, 0>), dim3(a.H, a.nb), dim3(kSpThreads), 0, s, a);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "block-spectrum launch");
 }
@@ -411,7 +481,7 @@ extern "C" int oc_block_spectra(const oc_spectra_params* p, void* stream) {
     return fail(OC_ERR_INVALID, "q dtype %d", p->q_dtype);
   if ((p->bounds || p->max_bound || p->q_norm_max) && !p->q) return fail(OC_ERR_INVALID, "bounds need q");
   if (p->num_blocks == 0 || p->num_heads == 0) return OC_OK;
-  if (p->num_heads > 65535) return fail(OC_ERR_UNSUPPORTED, "num_heads > 65535");
+  if (p->num_blocks > 65535) return fail(OC_ERR_UNSUPPORTED, "num_blocks > 65535 (33553920 tokens)");
   SpecArgs a{};
   a.k = (const char*)p->k;
   a.k_ts = p->k_token_stride * es, a.k_hs = p->k_head_stride * es;

@@ -17,6 +17,7 @@ from __future__ import annotations
 import dataclasses
 import enum
 import math
+import threading
 import time
 
 import torch
@@ -227,7 +228,6 @@ def orthocache_forward(
     if mode == "dense":
         t0 = time.perf_counter()
         output = _dense_attention(q, keys, values, head_dim)
-        torch.cuda.synchronize(q.device)
         metadata["latency_ms"] = (time.perf_counter() - t0) * 1000
         metadata["eviction_rate"] = 0.0
         return output, metadata
@@ -258,7 +258,6 @@ def orthocache_forward(
     if seq_len_k < dynamic_threshold:
         t0 = time.perf_counter()
         output = _dense_attention(q, keys, values, head_dim)
-        torch.cuda.synchronize(q.device)
         if telemetry >= TelemetryLevel.FLAGS:
             flags = BypassFlag.CROSSOVER_BYPASS
             if hw_profile.compute_class == "unknown":
@@ -274,6 +273,19 @@ def orthocache_forward(
     return _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, metadata)
 
 
+_STATS_HOST = threading.local()
+
+
+def _stats_buffer(n: int) -> torch.Tensor:
+    """A pinned float32 host buffer of n values per thread, reused by every
+    compact call of the thread (each call reads it before returning)."""
+    buf = getattr(_STATS_HOST, "buf", None)
+    if buf is None or buf.numel() != n:
+        buf = torch.empty((n,), dtype=torch.float32, pin_memory=True)
+        _STATS_HOST.buf = buf
+    return buf
+
+
 def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, metadata):
     """The compact pipeline (pipeline.py:458-555): one oc_block_spectra pass
     gives zeta, the query-aware bounds (max over queries), the block
@@ -282,8 +294,14 @@ def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, m
     is kept when its bound >= tau and zeta <= zeta_max,
     compute_multiband_mask), the any-head block mask and its tile mask, the
     zeta statistics and the eviction regimes; the decode kernel then attends
-    the retained blocks' tiles (adaptive_attention.attend_tiles).  One
-    device-to-host transfer carries the statistics."""
+    the retained blocks' tiles (adaptive_attention.attend_tiles).
+
+    The attention is launched before the statistics are read: they travel
+    to pinned host memory behind an event, so the host waits for the
+    spectra and the gate only and the attention runs on behind the return
+    (the reference returns without a synchronisation as well).  With no
+    block retained the launched attention reads nothing and the output is
+    zeros of q's dtype, as the reference returns."""
     from .adaptive_attention import attend_tiles
     from .perfect_eviction import FLOAT32_UNDERFLOW_THRESHOLD
     from .spectral_energy import _check
@@ -292,10 +310,19 @@ def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, m
     spec = X.block_spectra(keys, q, want_qnorm=True)
     _, tile_mask, stats = X.compact_gate(spec, head_dim, tau, zeta_max, FLOAT32_UNDERFLOW_THRESHOLD,
                                          block_size // X.TILE_SIZE)
-    st = stats.tolist()
+    host = _stats_buffer(stats.numel())
+    ready = torch.cuda.Event()
+    with torch.cuda.device(q.device):
+        host.copy_(stats, non_blocking=True)
+        ready.record(torch.cuda.current_stream(q.device))
+    t_attn = time.perf_counter()
+    output = attend_tiles(q, keys, values, tile_mask, num_blocks * block_size)
+    t_launched = time.perf_counter()
+    ready.synchronize()
+    st = host.tolist()
     metadata["tau_auto"] = tau is None
     metadata["tau"] = st[0] if tau is None else tau
-    metadata["spectral_ms"] = (time.perf_counter() - t_spectral) * 1000
+    metadata["spectral_ms"] = (time.perf_counter() - t_spectral - (t_launched - t_attn)) * 1000
     metadata["zeta_mean"], metadata["zeta_std"], metadata["zeta_min"], metadata["zeta_max_observed"] = st[1:5]
     retained = int(st[5])
     metadata["blocks_retained"] = retained
@@ -305,14 +332,10 @@ def _compact(q, keys, values, block_size, zeta_max, tau, num_blocks, head_dim, m
     metadata["statistical_eviction_blocks"] = int(st[7])
     metadata["perfect_eviction_rate"] = (int(st[6]) / max(1, num_blocks - retained)
                                          if num_blocks > retained else 0.0)
-    t_attn = time.perf_counter()
-    if retained:
-        output = attend_tiles(q, keys, values, tile_mask, num_blocks * block_size)
-    else:
+    if not retained:
         output = torch.zeros_like(q)
-    torch.cuda.synchronize(q.device)
     t_end = time.perf_counter()
     metadata["compact_num_active"] = retained
-    metadata["attention_ms"] = (t_end - t_attn) * 1000
+    metadata["attention_ms"] = (t_launched - t_attn) * 1000
     metadata["total_ms"] = (t_end - t_spectral) * 1000
     return output, metadata

@@ -102,6 +102,49 @@ def test_stream_compact_and_spectral_api():
         SE.compute_spectral_bands(kd, band_low=(1, 32))
 
 
+@pytest.mark.parametrize("nb,H", [(32, 64), (40, 64), (9, 300), (1, 5)])
+def test_compact_gate_kernel_vs_oracle(nb, H):
+    """oc_compact_gate on synthetic tables, with the (block, head) entries
+    staged in LDS (nb * H <= 2048 and H <= 256) and read from global memory
+    (2560 entries; 300 heads): masks, counts and regimes exact, statistics
+    within 1e-5.  Data with margins: kept bounds in [200, 210], evicted in
+    [0, 100] (tau = 150), zeta < 1 or > 100 (zeta_max = 5), evicted blocks'
+    beta about 10 (perfect: gap ~ 195) or 150 (statistical: gap ~ 55)."""
+    from orthocache_gpu import _launch as X
+    rng = np.random.default_rng(nb * 1000 + H)
+    d = 64
+    kind = rng.integers(0, 3, nb)  # 0 kept, 1 evicted perfect, 2 evicted statistical
+    kind[0] = 0
+    mb = np.where(kind[:, None] == 0, rng.uniform(200, 210, (nb, H)), rng.uniform(0, 100, (nb, H)))
+    zeta = np.where(rng.random((nb, H)) < 0.8, rng.uniform(0, 1, (nb, H)), rng.uniform(100, 1e4, (nb, H)))
+    zeta[kind == 0, 0] = 0.5  # a kept block has a head that passes both gates
+    beta = np.where(kind == 2, 150.0, 10.0)[:, None] * rng.uniform(0.9, 1.0, (nb, H))
+    energy = (beta * math.sqrt(d)) ** 2  # beta = qmax * sqrt(E) / sqrt(d) with qmax = 1
+    qmax = np.ones(H)
+    spec = {"max_bound": torch.tensor(mb, dtype=torch.float32, device=DEV),
+            "zeta": torch.tensor(zeta, dtype=torch.float32, device=DEV),
+            "energy": torch.tensor(energy, dtype=torch.float32, device=DEV),
+            "q_norm_max": torch.tensor(qmax, dtype=torch.float32, device=DEV)}
+    f32 = lambda x: np.asarray(x, dtype=np.float32)
+    for tau in (150.0, None):
+        bm, tm, st = X.compact_gate(spec, d, tau, 5.0, O.F32_UNDERFLOW, 8)
+        ref = O.compact_gate(f32(mb), f32(zeta), f32(energy), qmax, d, 5.0, tau)
+        if tau is None:
+            assert float(st[0]) == pytest.approx(ref["tau"], rel=1e-5)
+            if np.abs(f32(mb) - ref["tau"]).min() < 1e-4 * abs(ref["tau"]):
+                continue
+        assert np.array_equal(bm.cpu().numpy().astype(bool), ref["unified"])
+        assert np.array_equal(tm.cpu().numpy().astype(bool), np.repeat(ref["unified"], 8))
+        s = st.cpu().numpy().astype(np.float64)
+        assert int(s[5]) == ref["retained"] and int(s[6]) == ref["perfect"] and int(s[7]) == ref["statistical"]
+        if tau is not None:
+            assert ref["perfect"] + ref["statistical"] == int((kind != 0).sum())
+        for i, key in ((1, "zeta_mean"), (3, "zeta_min"), (4, "zeta_max_observed"), (8, "z_max")):
+            assert s[i] == pytest.approx(ref[key], rel=1e-5), key
+        if nb > 1:
+            assert s[2] == pytest.approx(ref["zeta_std"], rel=1e-4)
+
+
 def _gap_tau(vals):
     v = np.sort(vals.ravel())
     gaps = v[1:] - v[:-1]

@@ -212,15 +212,17 @@ def test_v2_random_vs_oracle(dtype, d, num_splits):
     assert_out(out, O.round_to(ref, dtype), dtype, "v2")
 
 
-@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 8, 12])
-@pytest.mark.parametrize("mode", ["single_pass", "cached"])
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
-@pytest.mark.parametrize("d", [128, 64])
+# head_dim 128 over every group size and both 16-bit types; head_dim 64 on a
+# reduced grid (bf16, G in 1/4/8)
+_V3_GRID = [(G, mode, dtype, 128) for G in (1, 2, 3, 4, 5, 8, 12) for mode in ("single_pass", "cached")
+            for dtype in ("bf16", "f16")]
+_V3_GRID += [(G, mode, "bf16", 64) for G in (1, 4, 8) for mode in ("single_pass", "cached")]
+
+
+@pytest.mark.parametrize("G,mode,dtype,d", _V3_GRID)
 def test_v3_random_vs_oracle(G, mode, dtype, d):
     from orthocache_gpu import fused_orthocache_attention_v3_gqa, score_tiles
     from orthocache_gpu.workloads import calibrate_tau, make_q
-    if d == 64 and (dtype == "f16" or G not in (1, 4, 8)):
-        pytest.skip("reduced grid for head_dim 64")
     tdt = TORCH_DT[dtype]
     wl = _mixed(2, 17, d, dtype, seed=G)
     q = make_q(2, G, d, dtype=tdt, seed=G + 1, low_band_heads=min(2, G))
