@@ -47,34 +47,41 @@ struct SpecArgs {
   float* q_norm_max;  // (H,) max_s ||q_s|| or null
 };
 
-__device__ __forceinline__ float sp_load(const char* p, int dtype) {
-  if (dtype == OC_F32) return *reinterpret_cast<const float*>(p);
-  const uint16_t u = *reinterpret_cast<const uint16_t*>(p);
-  if (dtype == OC_BF16) return __uint_as_float((uint32_t)u << 16);
-  return (float)__builtin_bit_cast(_Float16, u);
+// 16-byte pieces of one token position: the eight chunk values (th) of a
+// thread's eight columns, fetched raw so that no use of the loaded words
+// (no wait) sits among the loads
+template <int DT>
+struct SpRaw {
+  static constexpr int N = DT == OC_F32 ? 16 : 8;
+  uint4 w[N];
+};
+
+template <int DT>
+__device__ __forceinline__ void sp_fetch(const char* p, int64_t th_stride, SpRaw<DT>& r) {
+#pragma unroll
+  for (int th = 0; th < 8; ++th) {
+    const char* pt = p + th * th_stride;
+    if constexpr (DT == OC_F32) {
+      r.w[2 * th] = *reinterpret_cast<const uint4*>(pt);
+      r.w[2 * th + 1] = *reinterpret_cast<const uint4*>(pt + 16);
+    } else {
+      r.w[th] = *reinterpret_cast<const uint4*>(pt);
+    }
+  }
 }
 
-// eight consecutive elements of a row (16-byte aligned for 16-bit types,
-// 32-byte for float32)
+// column c of chunk th as float
 template <int DT>
-__device__ __forceinline__ void load8(const char* p, float (&x)[8]) {
+__device__ __forceinline__ float sp_elem(const SpRaw<DT>& r, int th, int c) {
   if constexpr (DT == OC_F32) {
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 16);
-    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    const uint4 u = r.w[2 * th + c / 4];
+    const uint32_t x = (c & 3) == 0 ? u.x : (c & 3) == 1 ? u.y : (c & 3) == 2 ? u.z : u.w;
+    return __uint_as_float(x);
   } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == OC_BF16) {
-        x[2 * i] = __uint_as_float(w[i] << 16);
-        x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-      } else {
-        x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFFu));
-        x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
-      }
-    }
+    const uint4 u = r.w[th];
+    const uint32_t x = (c >> 1) == 0 ? u.x : (c >> 1) == 1 ? u.y : (c >> 1) == 2 ? u.z : u.w;
+    if constexpr (DT == OC_BF16) return __uint_as_float((c & 1) ? (x & 0xFFFF0000u) : (x << 16));
+    else return (float)__builtin_bit_cast(_Float16, (uint16_t)((c & 1) ? (x >> 16) : (x & 0xFFFFu)));
   }
 }
 
@@ -89,16 +96,24 @@ __device__ __forceinline__ float block_max(float v, float* sh_red) {
   return s;
 }
 
-// One workgroup per (512-token block, head).  Thread (tg, cg) owns columns
-// 8cg .. 8cg + 8 and the within-chunk positions tl = tg + i * TG.  D is the
-// head_dim for 64 and 128 (the loop over tl unrolls, so a thread's loads are
-// all in flight together) and 0 for any other multiple of 8 up to 256.
+// a q element's raw bits (zero-extended 16-bit, or float32) and its value
+__device__ __forceinline__ float sp_q_value(uint32_t bits, int dtype) {
+  if (dtype == OC_F32) return __uint_as_float(bits);
+  if (dtype == OC_BF16) return __uint_as_float(bits << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
 template <int DT, int D>
 __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecArgs a) {
   constexpr int DMAX = D ? D : kMaxD;
-  __shared__ float sh_z[64 * DMAX];  // Z_0[tl][c]
-  __shared__ float sh_mean[DMAX];
-  __shared__ float sh_red[kSpThreads / 64];
+  // Z_0[tl][c]; once the transform has read it (after the barrier that
+  // follows), row 0 holds the block mean (each thread writes its own
+  // column) and entries d .. d + 20 the reduction scratch, so the whole
+  // workgroup's LDS is 32 KiB at d = 128 (five workgroups per CU)
+  __shared__ float sh_z[64 * DMAX];
+  float* sh_mean = sh_z;
+  float (*sh_sum)[4] = reinterpret_cast<float (*)[4]>(sh_z + (D ? D : a.d));
+  float* sh_red = sh_z + (D ? D : a.d) + 4 * (kSpThreads / 64);
   // consecutive workgroups take the heads of one block, so the workgroups
   // in flight together read whole token rows of the (S, H, d) cache
   const int h = blockIdx.x;
@@ -115,34 +130,34 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   constexpr int QPL = (DMAX + 63) / 64;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
-  auto load_q = [&](int s, float (&qv)[QPL]) {
+  // raw bits, converted where used: columns past d read column d - 1 (in
+  // bounds) and are zeroed at the conversion
+  auto load_q = [&](int s, uint32_t (&qr_bits)[QPL]) {
     const char* qr = a.q + (int64_t)s * a.q_ss + (int64_t)h * a.q_hs;
+    if (a.q_dtype == OC_F32) {
 #pragma unroll
-    for (int k = 0; k < QPL; ++k) {
-      const int c = lane + 64 * k;
-      qv[k] = c < d ? sp_load(qr + (int64_t)c * qes, a.q_dtype) : 0.f;
+      for (int k = 0; k < QPL; ++k)
+        qr_bits[k] = *reinterpret_cast<const uint32_t*>(qr + (int64_t)min(lane + 64 * k, d - 1) * 4);
+    } else {
+#pragma unroll
+      for (int k = 0; k < QPL; ++k)
+        qr_bits[k] = *reinterpret_cast<const uint16_t*>(qr + (int64_t)min(lane + 64 * k, d - 1) * 2);
     }
   };
-  float q0[QPL];
+  uint32_t q0[QPL];
+#pragma unroll
+  for (int k = 0; k < QPL; ++k) q0[k] = 0u;
   if (a.q && wave < a.Sq) load_q(wave, q0);
   float e_mid = 0.f, e_high = 0.f, energy = 0.f;
-  // positions per thread: 64 / TG when TG divides 64 (D = 64, 128), else a bound
-  constexpr int TPT = D ? 64 / (kSpThreads / (D / 8)) : 64;
-  constexpr int UNROLL = D ? TPT : 1;
-#pragma unroll UNROLL
-  for (int i = 0; i < TPT; ++i) {
-    const int tl = tg + i * TG;
-    if (!D && tl >= 64) break;
-    float x[8][8];  // [th][column]
-#pragma unroll
-    for (int th = 0; th < 8; ++th) load8<DT>(kb + (int64_t)(64 * th + tl) * a.k_ts, x[th]);
+  // one token position tl of the thread: energies, the 8-point transform
+  // over the chunks th, Z_0 to LDS
+  auto consume = [&](int tl, const SpRaw<DT>& r) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float z[8];
 #pragma unroll
       for (int th = 0; th < 8; ++th) {
-        z[th] = x[th][c];
+        z[th] = sp_elem<DT>(r, th, c);
         energy = __builtin_fmaf(z[th], z[th], energy);
       }
       // natural-order 8-point Walsh-Hadamard transform over th (unnormalised)
@@ -160,6 +175,27 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
 #pragma unroll
       for (int uh = 4; uh < 8; ++uh) e_high = __builtin_fmaf(z[uh], z[uh], e_high);
       sh_z[tl * d + 8 * cg + c] = z[0];
+    }
+  };
+  const int64_t th_stride = 64 * a.k_ts;
+  if constexpr (D != 0) {
+    // TG divides 64: 64 / TG positions per thread, the next position's
+    // loads issued before the current one is consumed
+    constexpr int TPT = 64 / (kSpThreads / (D / 8));
+    SpRaw<DT> rb[2];
+    sp_fetch<DT>(kb + (int64_t)tg * a.k_ts, th_stride, rb[0]);
+#pragma unroll
+    for (int i = 0; i < TPT; ++i) {
+      if (i + 1 < TPT) sp_fetch<DT>(kb + (int64_t)(tg + (i + 1) * TG) * a.k_ts, th_stride, rb[(i + 1) & 1]);
+      consume(tg + i * TG, rb[i & 1]);
+    }
+  } else if (tg < TG) {
+    // any other head_dim: positions tg, tg + TG, ... < 64; the threads past
+    // TG * CG (when CG does not divide 256) take none
+    for (int tl = tg; tl < 64; tl += TG) {
+      SpRaw<DT> r;
+      sp_fetch<DT>(kb + (int64_t)tl * a.k_ts, th_stride, r);
+      consume(tl, r);
     }
   }
   __syncthreads();
@@ -184,10 +220,10 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
     sh_mean[tid] = y[0] * (1.0f / 512.0f);  // DC / sqrt(512) with DC = sum_t k_t / sqrt(512)
   }
   // the four band sums in one reduction: lanes, then the four waves in LDS
-  __shared__ float sh_sum[kSpThreads / 64][4];
   float r4[4] = {e_mid, e_high, e_low, energy};
 #pragma unroll
   for (int j = 0; j < 4; ++j) r4[j] = wave_sum(r4[j]);
+  __syncthreads();  // every column of Z_0 has been read: the scratch entries are free
   if (lane == 0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) sh_sum[wave][j] = r4[j];
@@ -221,20 +257,21 @@ __global__ __launch_bounds__(kSpThreads) void block_spectrum_kernel(const SpecAr
   float best = -__builtin_inff();
   float qbest = 0.f;
   for (int s = wave; s < a.Sq; s += kSpThreads / 64) {
-    float qv[QPL];
+    uint32_t qb[QPL];
     if (s == wave) {
 #pragma unroll
-      for (int k = 0; k < QPL; ++k) qv[k] = q0[k];
+      for (int k = 0; k < QPL; ++k) qb[k] = q0[k];
     } else {
-      load_q(s, qv);
+      load_q(s, qb);
     }
     float dot = 0.f, nn = 0.f;
 #pragma unroll
     for (int k = 0; k < QPL; ++k) {
       const int c = lane + 64 * k;
       if (c < d) {
-        dot = __builtin_fmaf(qv[k], sh_mean[c], dot);
-        nn = __builtin_fmaf(qv[k], qv[k], nn);
+        const float qv = sp_q_value(qb[k], a.q_dtype);
+        dot = __builtin_fmaf(qv, sh_mean[c], dot);
+        nn = __builtin_fmaf(qv, qv, nn);
       }
     }
     dot = wave_sum(dot);

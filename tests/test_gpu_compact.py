@@ -57,8 +57,12 @@ def _keys(nb, H, d, noise_blocks, seed, dtype):
     return torch.from_numpy(k).to(TD[dtype])
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("d", [64, 128])
+# d = 96 and 40: the generic head_dim path, whose eight-column groups (12, 5)
+# do not divide the 256 threads
+_SPEC_GRID = [(dt, d) for dt in ("f32", "bf16", "f16") for d in (64, 128)] + [("bf16", 96), ("f32", 40)]
+
+
+@pytest.mark.parametrize("dtype,d", _SPEC_GRID)
 def test_block_spectra_vs_oracle(dtype, d):
     from orthocache_gpu import _launch as X
     k = _keys(5, 3, d, {1, 3}, seed=d, dtype=dtype)
