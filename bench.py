@@ -400,14 +400,14 @@ def hook_measure(steps, warmup):
     """The model hook's causal prefill attention kernel (oc_prefill_attention)
     at a TinyLlama-1.1B layer (32 q / 4 kv heads, head_dim 64, float32 as the
     reference's evaluation runs it, and bfloat16) and a Llama-3-8B layer (32 / 8,
-    head_dim 128, bfloat16), 2048 / 4096 tokens, without eviction and with half
+    head_dim 128, bfloat16 and float16), 2048 / 4096 tokens, without eviction and with half
     of the tiles evicted; torch's SDPA (causal, GQA) timed beside it.  FLOPs
     are 4 * head_dim per (query, attended key)."""
     import torch
     from orthocache_gpu import _launch as X
     g = torch.Generator(device="cuda").manual_seed(0)
     for B, Hq, Hkv, S, d, dt in ((1, 32, 4, 2048, 64, torch.float32), (1, 32, 4, 2048, 64, torch.bfloat16),
-                                 (1, 32, 8, 4096, 128, torch.bfloat16)):
+                                 (1, 32, 8, 4096, 128, torch.bfloat16), (1, 32, 8, 4096, 128, torch.float16)):
         q = torch.randn((B, Hq, S, d), device="cuda", generator=g).to(dt)
         k = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)
         v = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)

@@ -254,8 +254,10 @@ __device__ __forceinline__ void pf_logits(const PfQ<DT, D>& q, const char* sk, i
 // output column 16nc + 4r + i of query x in lane 16r + x.  16-bit: per
 // 32-token block j, A = V^T read with ds_read_b64_tr_b16 from the permuted
 // rows (lane group g gets tokens 32j + 4g + b and 32j + 16 + 4g + b), B =
-// the lane's own eight probabilities c[2j][b], c[2j + 1][b] as a 16-bit
-// high part plus the 16-bit rounding of the remainder (two instructions).
+// the lane's own eight probabilities c[2j][b], c[2j + 1][b]: float16 rounds
+// them once (relative error at most 2^-12); bfloat16 sends a 16-bit high
+// part plus the 16-bit rounding of the remainder (two instructions), since
+// one rounding (2^-9) moves short causal rows past the output tolerance.
 // float32: 16x16x4 steps over (tb, i), A = V[16tb + 4r + i][16nc + x], B =
 // c[tb][i], exact.
 template <int DT, int D>
@@ -294,9 +296,7 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
           blo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
         } else {
           const _Float16 h0 = (_Float16)pv[2 * e], h1 = (_Float16)pv[2 * e + 1];
-          const _Float16 l0 = (_Float16)(pv[2 * e] - (float)h0), l1 = (_Float16)(pv[2 * e + 1] - (float)h1);
           bhi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-          blo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
         }
       }
       // lane x of group kg reads rows 32j + 8kg + 4h + x/4 (h = 0, 1)
@@ -312,7 +312,7 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
                                 (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16),
                                 (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16)};
         acc[nc] = mfma_qk<DT>(av, bhi, acc[nc]);
-        acc[nc] = mfma_qk<DT>(av, blo, acc[nc]);
+        if constexpr (DT == OC_BF16) acc[nc] = mfma_qk<DT>(av, blo, acc[nc]);
       }
     }
   }
