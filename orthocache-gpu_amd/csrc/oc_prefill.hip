@@ -159,6 +159,14 @@ struct PfTile {
   static constexpr int STAGES = 2 * KV <= 32768 ? 2 : 1;
   static constexpr int LDS = STAGES * 2 * KV;
   __device__ static int swz(int r) { return (r / RB) % LPT; }
+  // 16-bit V: the 32-byte column pair p of LDS row r is stored at pair
+  // p ^ vswz(r).  A transposing read takes one pair of the 16 rows
+  // 8g + i (+ 4h), g, i < 4; vswz gives those rows distinct pairs (each
+  // bank slot used twice) instead of one pair 16 times over.
+  static constexpr int PAIRS = ROW / 32;
+  __device__ static int vswz(int r) {
+    return PAIRS >= 8 ? (r & 3) + 4 * ((r >> 3) & 1) : ((r & 3) >> 1) + 2 * ((r >> 3) & 1);
+  }
 };
 
 template <int DT, int D>
@@ -208,7 +216,12 @@ __device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char
     const int g = tid + kPfThreads * j;
     const int r = g / L::LPT, c = g % L::LPT;
     *reinterpret_cast<uint4*>(sk + r * L::ROW + 16 * (c ^ L::swz(r))) = st.k[j];
-    *reinterpret_cast<uint4*>(sv + pf_vrow<DT>(r) * L::ROW + 16 * c) = st.v[j];
+    if constexpr (DT == OC_F32) {
+      *reinterpret_cast<uint4*>(sv + r * L::ROW + 16 * c) = st.v[j];
+    } else {
+      const int vr = pf_vrow<DT>(r);
+      *reinterpret_cast<uint4*>(sv + vr * L::ROW + 16 * (c ^ (2 * L::vswz(vr)))) = st.v[j];
+    }
   }
 }
 
@@ -299,14 +312,17 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
           bhi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
         }
       }
-      // lane x of group kg reads rows 32j + 8kg + 4h + x/4 (h = 0, 1)
-      const uint16_t* rowp = sv + (32 * j + 8 * kg + (x >> 2)) * D + 4 * (x & 3);
+      // lane x of group kg reads rows 32j + 8kg + 4h + x/4 (h = 0, 1), column
+      // pair nc stored at nc ^ vswz(row) (the same for h = 0, 1 and every j)
+      const int vrow = 32 * j + 8 * kg + (x >> 2);
+      const int vt = PfTile<DT, D>::vswz(vrow);
+      const uint16_t* rowp = sv + vrow * D + 4 * (x & 3);
 #pragma unroll
       for (int nc = 0; nc < D / 16; ++nc) {
         const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
+            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vt)));
         const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
+            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vt)));
         const uint32_t av[4] = {(uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16),
                                 (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16),
                                 (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16),
