@@ -51,34 +51,48 @@ struct PrefillArgs {
 // Online-softmax state in the transposed layout: lane 16r + x works on
 // query x (scores of tokens 16tb + 4r + i, i = 0..3, in c[tb][i]); m is
 // shared by the query's four lanes x, x + 16, x + 32, x + 48, and l, e are
-// their partial sums.
+// their partial sums.  Scores are kept in base-2 units (s * log2 e), so
+// that each probability is one exp2.
 struct PfState {
-  float m;
+  float m;  // running max, base-2 units
   float l;
-  float e;  // sum of e^(s - m) * s (entropy)
+  float e;  // sum of 2^(s2 - m) * s2 (entropy), base-2 units
   int n;    // attended tokens of the query (entropy)
 };
 
 // Causal online-softmax update of one tile's raw scores c (transposed
 // layout); token tok0 + j is visible to the lane's query when tok0 + j <
-// nvis.  c becomes e^(s - m) and the accumulators are rescaled.
+// nvis.  full (wave-uniform): every token of the tile is visible to every
+// query of the wave (no mask needed).  scale2 = softmax scale * log2 e.
+// c becomes 2^(s2 - m) and the accumulators are rescaled.
 template <int D, bool ENT>
-__device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f32x4 (&c)[4], float scale, int nvis,
-                                           int tok0, int lane) {
+__device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f32x4 (&c)[4], float scale2, int nvis,
+                                           int tok0, bool full, int lane) {
   const int r = lane >> 4;
   float mt = -__builtin_inff();
+  if (full) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = tok0 + 16 * tb + 4 * r + i < nvis ? c[tb][i] * scale : -__builtin_inff();
-      c[tb][i] = v;
-      mt = fmaxf(mt, v);
-    }
+      for (int i = 0; i < 4; ++i) {
+        const float v = c[tb][i] * scale2;
+        c[tb][i] = v;
+        mt = fmaxf(mt, v);
+      }
+  } else {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = tok0 + 16 * tb + 4 * r + i < nvis ? c[tb][i] * scale2 : -__builtin_inff();
+        c[tb][i] = v;
+        mt = fmaxf(mt, v);
+      }
+  }
   mt = fmaxf(mt, xpair<16>(mt));
   mt = fmaxf(mt, xpair<32>(mt));
   const float mn = fmaxf(st.m, mt);
-  const float alpha = __expf(st.m - mn);
+  const float alpha = __builtin_amdgcn_exp2f(st.m - mn);
   st.m = mn;
   float ls = 0.f, es = 0.f;
 #pragma unroll
@@ -86,7 +100,7 @@ __device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f3
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float v = c[tb][i];
-      const float pp = __expf(v - mn);
+      const float pp = __builtin_amdgcn_exp2f(v - mn);
       ls += pp;
       if constexpr (ENT) es = pp > 0.f ? __builtin_fmaf(pp, v, es) : es;
       c[tb][i] = pp;
@@ -175,17 +189,30 @@ struct PfStage {
   uint4 v[PfTile<DT, D>::NL];
 };
 
+// a wave-uniform pointer as scalar registers
+__device__ __forceinline__ const char* pf_uniform(const char* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 // global -> registers: chunk g = tid + 256 j of the tile is row g / LPT,
 // chunk g % LPT; rows at or past kv_len read as zero (buffer range check)
 template <int DT, int D>
 __device__ __forceinline__ void pf_fetch(const PrefillArgs& a, const char* kh, const char* vh, int t, int tid,
                                          PfStage<DT, D>& st) {
   using L = PfTile<DT, D>;
+  // every value of the resources is wave-uniform; saying so keeps the
+  // compiler from wrapping each load in a readfirstlane loop
+  t = __builtin_amdgcn_readfirstlane(t);
   const int nvalid = min(a.Skv - t * 64, 64);
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(kh + (int64_t)t * 64 * a.k_ss), (short)0, nvalid * (int)a.k_ss, 0x00020000);
+      (void*)pf_uniform(kh + (int64_t)t * 64 * a.k_ss), (short)0,
+      __builtin_amdgcn_readfirstlane(nvalid * (int)a.k_ss), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(vh + (int64_t)t * 64 * a.v_ss), (short)0, nvalid * (int)a.v_ss, 0x00020000);
+      (void*)pf_uniform(vh + (int64_t)t * 64 * a.v_ss), (short)0,
+      __builtin_amdgcn_readfirstlane(nvalid * (int)a.v_ss), 0x00020000);
 #pragma unroll
   for (int j = 0; j < L::NL; ++j) {
     const int g = tid + kPfThreads * j;
@@ -323,10 +350,9 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
             (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vt)));
         const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vt)));
-        const uint32_t av[4] = {(uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16),
-                                (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16),
-                                (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16),
-                                (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16)};
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
+        const uint32_t av[4] = {w0[0], w0[1], w1[0], w1[1]};
         acc[nc] = mfma_qk<DT>(av, bhi, acc[nc]);
         if constexpr (DT == OC_BF16) acc[nc] = mfma_qk<DT>(av, blo, acc[nc]);
       }
@@ -335,7 +361,8 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
 }
 
 template <int DT, int D, bool ENT>
-__global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 4))) void prefill_kernel(
+    const PrefillArgs a) {
   using L = PfTile<DT, D>;
   __shared__ __attribute__((aligned(16))) char sh[L::LDS];
   const int tid = threadIdx.x;
@@ -360,6 +387,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
   const int x = lane & 15;
   const int qpos = pos0 + x;  // this lane's query
   const int nvis = qpos < a.Sq ? min(max(qpos + off + 1, 0), a.Skv) : 0;
+  // the wave's smallest window (its first query's); lanes past Sq are not
+  // masked on full tiles, their results are never written
+  const int nvis_w = min(max(pos0 + off + 1, 0), a.Skv);
+  const float scale2 = a.scale * 1.4426950408889634f;  // log2 e
   // this wave's tiles, and the workgroup's (its last query's window)
   const int tend = pos0 < a.Sq ? (min(max(min(pos0 + 15, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64 : 0;
   const int wg_tend = (min(max(min(qb * kPfRows + kPfRows - 1, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
@@ -396,7 +427,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
     if (t < tend) {
       f32x4 c[4];
       pf_logits<DT, D>(q, stage_k(s), lane, c);
-      pf_softmax<D, ENT>(st, accp, c, a.scale, nvis, t * 64, lane);
+      pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
       pf_pv<DT, D>(accp, c, stage_v(s), lane);
     }
     if constexpr (L::STAGES == 1) __syncthreads();  // the only stage is free again
@@ -433,7 +464,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_kernel(const PrefillArgs a
       // H = -sum p ln p with p = e^(s - m) / l: m + ln l - (sum e^(s-m) s) / l,
       // plus the clamp term of the probabilities that are exactly zero
       const float hz = (float)(a.Skv - st.n) * kZeroPTerm;
-      const float H = l > 0.f ? st.m + logf(l) - e / l + hz : (float)a.Skv * kZeroPTerm;
+      constexpr float kLn2 = 0.6931471805599453f;
+      const float H = l > 0.f ? kLn2 * (st.m - e / l) + logf(l) + hz : (float)a.Skv * kZeroPTerm;
       a.entropy[((int64_t)b * a.Hq + h) * a.Sq + qpos] = H;
     }
   }
