@@ -234,6 +234,52 @@ __device__ __forceinline__ int pf_vrow(int t) {
   return (t & ~31) + 8 * ((t >> 2) & 3) + 4 * ((t >> 4) & 1) + (t & 3);
 }
 
+// 16 bytes per lane from a buffer straight to LDS: lane i's bytes land at
+// dst + 16 i (dst wave-uniform)
+__device__ __forceinline__ void pf_load_lds16(__amdgpu_buffer_rsrc_t r, char* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
+// token of LDS row r of a 16-bit V stage (the inverse of pf_vrow)
+__device__ __forceinline__ int pf_vtok(int r) {
+  return (r & ~31) + 16 * ((r >> 2) & 1) + 4 * ((r >> 3) & 3) + (r & 3);
+}
+
+// global -> an LDS stage directly (two-stage tiles): each wave's load
+// instruction fills a contiguous 1 KiB of the stage, slot g = tid + 512 j
+// (row g / LPT, chunk g % LPT), so the lane filling a slot loads the chunk
+// that the layout keeps there: K chunk c ^ swz(row); 16-bit V the token
+// pf_vtok(row), chunk c ^ 2 vswz(row).  Rows at or past kv_len read as zero
+// (buffer range check).  Default cache policy: the G query heads' workgroups
+// of a kv head read the same tiles.
+template <int DT, int D>
+__device__ __forceinline__ void pf_fetch_lds(const PrefillArgs& a, const char* kh, const char* vh, int t, int tid,
+                                             char* sk, char* sv) {
+  using L = PfTile<DT, D>;
+  t = __builtin_amdgcn_readfirstlane(t);
+  const int nvalid = min(a.Skv - t * 64, 64);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)pf_uniform(kh + (int64_t)t * 64 * a.k_ss), (short)0,
+      __builtin_amdgcn_readfirstlane(nvalid * (int)a.k_ss), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)pf_uniform(vh + (int64_t)t * 64 * a.v_ss), (short)0,
+      __builtin_amdgcn_readfirstlane(nvalid * (int)a.v_ss), 0x00020000);
+  const int wbase = __builtin_amdgcn_readfirstlane(tid & ~63);  // the wave's first slot
+#pragma unroll
+  for (int j = 0; j < L::NL; ++j) {
+    const int g = tid + kPfThreads * j;
+    const int r = g / L::LPT, c = g % L::LPT;
+    const int slot0 = 16 * (wbase + kPfThreads * j);
+    pf_load_lds16(rk, sk + slot0, r * (int)a.k_ss + 16 * (c ^ L::swz(r)));
+    int vt = r, vc = c;
+    if constexpr (DT != OC_F32) {
+      vt = pf_vtok(r);
+      vc = c ^ (2 * L::vswz(r));
+    }
+    pf_load_lds16(rv, sv + slot0, vt * (int)a.v_ss + 16 * vc);
+  }
+}
+
 // registers -> an LDS stage (K swizzled, V rows permuted for 16-bit)
 template <int DT, int D>
 __device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char* sk, char* sv) {
@@ -412,28 +458,51 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
 
   auto stage_k = [&](int s) { return sh + s * 2 * L::KV; };
   auto stage_v = [&](int s) { return sh + s * 2 * L::KV + L::KV; };
-  PfStage<DT, D> reg;
   int t = next_kept(0);
-  if (t < wg_tend) {
-    pf_fetch<DT, D>(a, kh, vh, t, tid, reg);
-    pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
-  }
-  int s = 0;
-  while (t < wg_tend) {
-    // stage s is complete; every wave is done with the tile before (stage s ^ 1)
-    __syncthreads();
-    const int tn = next_kept(t + 1);
-    if (tn < wg_tend) pf_fetch<DT, D>(a, kh, vh, tn, tid, reg);  // in flight during this tile
-    if (t < tend) {
-      f32x4 c[4];
-      pf_logits<DT, D>(q, stage_k(s), lane, c);
-      pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
-      pf_pv<DT, D>(accp, c, stage_v(s), lane);
+  if constexpr (L::STAGES == 2) {
+    // two stages: the next tile goes straight to the other stage while this
+    // one is used; each wave waits for its own loads before the barrier
+    // that opens the stage to the workgroup
+    if (t < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, t, tid, stage_k(0), stage_v(0));
+    __builtin_amdgcn_s_waitcnt(0);
+    int s = 0;
+    while (t < wg_tend) {
+      // stage s is complete; every wave is done with the tile before (stage s ^ 1)
+      __syncthreads();
+      const int tn = next_kept(t + 1);
+      if (tn < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, tn, tid, stage_k(1 - s), stage_v(1 - s));
+      if (t < tend) {
+        f32x4 c[4];
+        pf_logits<DT, D>(q, stage_k(s), lane, c);
+        pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
+        pf_pv<DT, D>(accp, c, stage_v(s), lane);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      s = 1 - s;
+      t = tn;
     }
-    if constexpr (L::STAGES == 1) __syncthreads();  // the only stage is free again
-    if (tn < wg_tend) pf_stash<DT, D>(reg, tid, stage_k(L::STAGES - 1 - s), stage_v(L::STAGES - 1 - s));
-    s = L::STAGES - 1 - s;
-    t = tn;
+  } else {
+    // one stage (float32, head_dim 128): the next tile waits in registers
+    // and is written to the stage once every wave is done with it
+    PfStage<DT, D> reg;
+    if (t < wg_tend) {
+      pf_fetch<DT, D>(a, kh, vh, t, tid, reg);
+      pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
+    }
+    while (t < wg_tend) {
+      __syncthreads();  // the stage is complete
+      const int tn = next_kept(t + 1);
+      if (tn < wg_tend) pf_fetch<DT, D>(a, kh, vh, tn, tid, reg);  // in flight during this tile
+      if (t < tend) {
+        f32x4 c[4];
+        pf_logits<DT, D>(q, stage_k(0), lane, c);
+        pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
+        pf_pv<DT, D>(accp, c, stage_v(0), lane);
+      }
+      __syncthreads();  // the stage is free again
+      if (tn < wg_tend) pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
+      t = tn;
+    }
   }
 
   // sums over the query's four lanes, then out = acc / max(l, 1e-9): lane
