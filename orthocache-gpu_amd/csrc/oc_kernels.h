@@ -890,10 +890,36 @@ struct MState {
   float l[4];
 };
 
+// LDS layout of the matrix-core decode's V tile: the 16-byte chunk c of row
+// r is stored at chunk c ^ v_xor(r).  A transposing read (tile_pv_mfma)
+// takes one column piece of 16 rows (16-bit) or 32 rows (fp8) whose stride
+// is a multiple of the bank line; the XOR gives them distinct bank slots
+// (each slot used twice) instead of one slot 16 times over.
+template <int DT, int D>
+__device__ __forceinline__ int v_xor(int r) {
+  if constexpr (DT == OC_FP8_E4M3FN) {
+    if constexpr (D == 128) return (r >> 1) & 7;
+    else if constexpr (D == 64) return (r >> 2) & 3;
+    else return 0;
+  } else {
+    if constexpr (D == 128) return 2 * ((r & 3) + 4 * ((r >> 3) & 1));
+    else if constexpr (D == 64) return 2 * (((r & 3) >> 1) + 2 * ((r >> 3) & 1));
+    else return 0;
+  }
+}
+
+// 16 bytes per lane from a buffer straight to LDS (non-temporal): lane i's
+// bytes land at dst + 16 i (dst wave-uniform)
+__device__ __forceinline__ void v_load_lds16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0,
+                                           kStreamAux);
+}
+
 // V tile of one 64-token tile into the wave's LDS slot, row-major
-// [token][D] 16-bit, by direct-to-LDS buffer loads (16 bytes per lane, one
-// 1 KiB instruction per 1024 / (2 D) tokens); tokens at or past n_tok read
-// as zero through the descriptor's range check.
+// [token][D] with the chunk order of v_xor, by direct-to-LDS buffer loads
+// (16 bytes per lane, one 1 KiB instruction per 1024 / (es D) tokens: the
+// lane filling slot (row, chunk c) loads chunk c ^ v_xor(row)); tokens at
+// or past n_tok read as zero through the descriptor's range check.
 template <int DT, int D, bool PAGED>
 __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
                                            uint16_t* sv, const TilePages& pg) {
@@ -901,7 +927,10 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
   constexpr int LPT = 64 / TPI;        // lanes per token
   const int64_t ts = a.v_tok_stride;
   const int tok0 = t * 64;
-  const int voff = (lane / LPT) * (int)ts + 16 * (lane % LPT);
+  const int rl = lane / LPT, cl = lane % LPT;
+  const int voff = rl * (int)ts;
+  // byte offset of the lane's chunk in instruction i (rows i * TPI + rl)
+  auto chunk = [&](int i) { return 16 * (cl ^ v_xor<DT, D>(i * TPI + rl)); };
   if constexpr (PAGED) {
     // one descriptor per 16-token block (in one page), 16 / TPI instructions each
 #pragma unroll
@@ -912,9 +941,7 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
           __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, pg.n[tb] * (int)ts, 0x00020000);
 #pragma unroll
       for (int j = 0; j < 16 / TPI; ++j)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)(sv + (tb * (16 / TPI) + j) * 512), 16,
-            voff + j * TPI * (int)ts, 0, 0, kStreamAux);
+        v_load_lds16(rs, sv + (tb * (16 / TPI) + j) * 512, voff + chunk(tb * (16 / TPI) + j) + j * TPI * (int)ts);
     }
   } else {
     const char* base = a.v + (int64_t)row * a.v_row_stride + tok0 * ts;
@@ -922,8 +949,7 @@ __device__ __forceinline__ void load_v_lds(const DecodeArgs& a, const RowInfo& r
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
 #pragma unroll
     for (int i = 0; i < 64 / TPI; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(sv + i * 512),
-                                               16, voff + i * TPI * (int)ts, 0, 0, kStreamAux);
+      v_load_lds16(rs, sv + i * 512, voff + chunk(i) + i * TPI * (int)ts);
   }
 }
 
@@ -1126,30 +1152,38 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
         alo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
       }
     }
-    // rows of this lane's transposing reads: 32*tb2 + 8*kg + 4*h + x/4
-    const uint16_t* rowp = sv + (32 * tb2 + 8 * kg + (x >> 2)) * D + 4 * (x & 3);
+    // rows of this lane's transposing reads: 32*tb2 + 8*kg + 4*h + x/4; the
+    // column pieces sit at the chunk order of v_xor, whose XOR is the same
+    // for h = 0 and 1
+    const int vrow = 32 * tb2 + 8 * kg + (x >> 2);
+    const int vx = v_xor<DT, D>(vrow) >> 1;  // 16-bit: XOR of the 32-byte column pair
+    const uint16_t* rowp = sv + vrow * D + 4 * (x & 3);
     // fp8 V: ds_read_b64_tr_b8 with lane x addressing row 32*tb2 + 8*kg +
     // x/2, bytes 16*nc + 8*(x%2) .. +8 returns V[32*tb2 + 8*kg + e][16*nc + x]
     // in byte e (e = 0..7; checked on the GPU with an in-bounds probe)
-    const uint8_t* rowp8 = reinterpret_cast<const uint8_t*>(sv) + (32 * tb2 + 8 * kg + (x >> 1)) * D + 8 * (x & 1);
+    const int vrow8 = 32 * tb2 + 8 * kg + (x >> 1);
+    const int vx8 = v_xor<DT, D>(vrow8);  // fp8: XOR of the 16-byte chunk
+    const uint8_t* rowp8 = reinterpret_cast<const uint8_t*>(sv) + vrow8 * D + 8 * (x & 1);
 #pragma unroll
     for (int nc = 0; nc < D / 16; ++nc) {
       uint32_t bk[4];
       if constexpr (DT == OC_FP8_E4M3FN) {
         typedef int i32x2 __attribute__((ext_vector_type(2)));
         const i32x2 b8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * nc));
+            (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * (nc ^ vx8)));
         fp8x4_to_bf16((uint32_t)b8[0], bk[0], bk[1]);
         fp8x4_to_bf16((uint32_t)b8[1], bk[2], bk[3]);
       } else {
         const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * nc));
+            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vx)));
         const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * nc));
-        bk[0] = (uint32_t)(uint16_t)b0[0] | ((uint32_t)(uint16_t)b0[1] << 16);
-        bk[1] = (uint32_t)(uint16_t)b0[2] | ((uint32_t)(uint16_t)b0[3] << 16);
-        bk[2] = (uint32_t)(uint16_t)b1[0] | ((uint32_t)(uint16_t)b1[1] << 16);
-        bk[3] = (uint32_t)(uint16_t)b1[2] | ((uint32_t)(uint16_t)b1[3] << 16);
+            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vx)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
+        bk[0] = w0[0];
+        bk[1] = w0[1];
+        bk[2] = w1[0];
+        bk[3] = w1[1];
       }
       accp[nc] = mfma_qk<MfmaT<DT>::value>(ahi, bk, accp[nc]);
       accp[nc] = mfma_qk<MfmaT<DT>::value>(alo, bk, accp[nc]);
