@@ -1305,7 +1305,7 @@ __device__ __forceinline__ bool flat_map(const DecodeArgs& a, int qcap, int* sh_
 
 // The tile loop, the wave merge and the partial-state write of one
 // workgroup (see decode_kernel).
-template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK>
+template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK, bool LOOP>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& ri, int row, const TileList& tl, int g0,
                                             float qmax, bool qnan, const float* sh_qf,
                                             const uint32_t* sh_qp, float (*sh_m)[GT], float (*sh_l)[GT],
@@ -1442,8 +1442,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     // a block id outside the pool (paged): raised once after the loop, so no
     // global atomic sits among the tile loads
     bool bad_page = false;
-    if (cached || a.gate == OC_GATE_NONE) {
-      // cached or dense decode: every listed tile is attended
+    if constexpr (LOOP) {
+      // cached or dense decode (LOOP, fixed at launch: the same condition as
+      // cached || gate == NONE): every listed tile is attended
       for (int t = next_tile(); t >= 0; t = next_tile()) {
         const int valid = min(64, ri.n_tok - t * 64);
         TilePages pg{};
@@ -1725,7 +1726,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
 // exactly one logical split's state.
 // Two waves per SIMD (<= 256 VGPRs) except for float32 K/V, whose raw K and
 // V tiles alone take 256 registers.
-template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK>
+template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK, bool LOOP>
 __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
     const DecodeArgs a) {
   constexpr int kDW = DecWaves<DT, D>::value;
@@ -1950,12 +1951,12 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     r1 = (int)((uint64_t)total * (gidx + 1) / (uint32_t)npg);
   }
 
-  decode_body<DT, D, GT, DOT2, PAGED, MQK>(a, ri, row, tl, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
+  decode_body<DT, D, GT, DOT2, PAGED, MQK, LOOP>(a, ri, row, tl, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
                                            pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v,
                                            reinterpret_cast<uint8_t*>(sh_bits));
   __syncthreads();
   // matrix-core single pass: the keep flags staged in LDS in list order
-  if (MQK && a.mode != OC_MODE_CACHED && a.gate != OC_GATE_NONE && a.keep_out && blockIdx.z == 0) {
+  if (MQK && !LOOP && a.keep_out && blockIdx.z == 0) {
     if (tl.n <= kKeepLds) {
       const uint8_t* sh_keep = reinterpret_cast<const uint8_t*>(sh_bits);
       for (int x = threadIdx.x; x < tl.n; x += kDT) {
@@ -2150,15 +2151,25 @@ hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_band(const DecodeArgs& a, int head_dim, hipStream_t st);
 
-template <int DT, int HD, bool DOT2, bool PG, bool MQ>
+template <int DT, int HD, bool DOT2, bool PG, bool MQ, bool LOOP>
 inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   const dim3 block(DecWaves<DT, HD>::value * kWave);
   switch (gt) {
-    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
   }
+}
+
+// matrix-core kernels come in two variants: every listed tile attended
+// (cached or dense decode) or the single-pass gate, so that each carries
+// only its own loop's registers
+template <int DT, int HD, bool PG>
+inline void launch_decode_mq(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  const bool loop = (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) || a.gate == OC_GATE_NONE;
+  if (loop) launch_decode_gt<DT, HD, true, PG, true, true>(a, gt, grid, st);
+  else launch_decode_gt<DT, HD, true, PG, true, false>(a, gt, grid, st);
 }
 
 // q . k on the matrix cores for contiguous 16-bit K (q of the same type)
@@ -2169,18 +2180,18 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
   // (a 16-token block inside one page)
   if constexpr (DOT2) {
     if (!a.paged) {
-      launch_decode_gt<DT, HD, true, false, true>(a, gt, grid, st);
+      launch_decode_mq<DT, HD, false>(a, gt, grid, st);
       return;
     }
     if (a.bs_log2 >= 4) {
-      launch_decode_gt<DT, HD, true, true, true>(a, gt, grid, st);
+      launch_decode_mq<DT, HD, true>(a, gt, grid, st);
       return;
     }
   }
   // VALU path (v_dot2 q.k for 16-bit K and q of the same type)
   constexpr bool VDOT2 = DOT2 && DT != OC_FP8_E4M3FN;
-  if (a.paged) launch_decode_gt<DT, HD, VDOT2, true, false>(a, gt, grid, st);
-  else launch_decode_gt<DT, HD, VDOT2, false, false>(a, gt, grid, st);
+  if (a.paged) launch_decode_gt<DT, HD, VDOT2, true, false, false>(a, gt, grid, st);
+  else launch_decode_gt<DT, HD, VDOT2, false, false, false>(a, gt, grid, st);
 }
 
 #define OC_DECODE_CASES(DT, DOT2)                                 \
