@@ -224,23 +224,16 @@ __device__ __forceinline__ void pf_fetch(const PrefillArgs& a, const char* kh, c
   }
 }
 
-// LDS row of V's token t (16-bit): within each 32-token block, token
-// 16a + 4g + b goes to row 8g + 4a + b, so that the transposing read of rows
-// 8g .. 8g + 7 hands lane group g the tokens 4g + b and 16 + 4g + b -- the
-// tokens whose scores the lane holds (tile_pv_t).  float32 V stays in order.
-template <int DT>
-__device__ __forceinline__ int pf_vrow(int t) {
-  if constexpr (DT == OC_F32) return t;
-  return (t & ~31) + 8 * ((t >> 2) & 3) + 4 * ((t >> 4) & 1) + (t & 3);
-}
-
 // 16 bytes per lane from a buffer straight to LDS: lane i's bytes land at
 // dst + 16 i (dst wave-uniform)
 __device__ __forceinline__ void pf_load_lds16(__amdgpu_buffer_rsrc_t r, char* dst, int voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
 }
 
-// token of LDS row r of a 16-bit V stage (the inverse of pf_vrow)
+// Token kept in LDS row r of a 16-bit V stage: within each 32-token block,
+// token 16a + 4g + b sits in row 8g + 4a + b, so that the transposing read
+// of rows 8g .. 8g + 7 hands lane group g the tokens 4g + b and 16 + 4g + b
+// -- the tokens whose scores the lane holds (pf_pv).
 __device__ __forceinline__ int pf_vtok(int r) {
   return (r & ~31) + 16 * ((r >> 2) & 1) + 4 * ((r >> 3) & 3) + (r & 3);
 }
@@ -280,21 +273,19 @@ __device__ __forceinline__ void pf_fetch_lds(const PrefillArgs& a, const char* k
   }
 }
 
-// registers -> an LDS stage (K swizzled, V rows permuted for 16-bit)
+// registers -> the LDS stage (single-stage tiles: float32 at head_dim 128;
+// 16-bit tiles always have two stages and load straight into LDS): K
+// swizzled, V in token order
 template <int DT, int D>
 __device__ __forceinline__ void pf_stash(const PfStage<DT, D>& st, int tid, char* sk, char* sv) {
   using L = PfTile<DT, D>;
+  static_assert(DT == OC_F32, "only float32 tiles are staged through registers");
 #pragma unroll
   for (int j = 0; j < L::NL; ++j) {
     const int g = tid + kPfThreads * j;
     const int r = g / L::LPT, c = g % L::LPT;
     *reinterpret_cast<uint4*>(sk + r * L::ROW + 16 * (c ^ L::swz(r))) = st.k[j];
-    if constexpr (DT == OC_F32) {
-      *reinterpret_cast<uint4*>(sv + r * L::ROW + 16 * c) = st.v[j];
-    } else {
-      const int vr = pf_vrow<DT>(r);
-      *reinterpret_cast<uint4*>(sv + vr * L::ROW + 16 * (c ^ (2 * L::vswz(vr)))) = st.v[j];
-    }
+    *reinterpret_cast<uint4*>(sv + r * L::ROW + 16 * c) = st.v[j];
   }
 }
 
