@@ -979,13 +979,24 @@ __device__ __forceinline__ void tile_softmax_regs(MState& ms, f32x4 (&accp)[D / 
                                                   float lscale, float vmul, int valid, int lane) {
   const int x = lane & 15;
   const int r = lane >> 4;
+  // the state is kept in base-2 units (logit * log2 e), so each
+  // probability is one exp2; it is converted back where it leaves the wave
+  const float lscale2 = lscale * 1.4426950408889634f;
   float v[4][4];
+  if (valid >= 64) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const bool tok_ok = 16 * tb + x < valid;
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[tb][i] * lscale : -__builtin_inff();
+      for (int i = 0; i < 4; ++i) v[tb][i] = c[tb][i] * lscale2;
+  } else {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const bool tok_ok = 16 * tb + x < valid;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[tb][i] = tok_ok ? c[tb][i] * lscale2 : -__builtin_inff();
+    }
   }
+  float alpha[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float mt = fmaxf(fmaxf(v[0][i], v[1][i]), fmaxf(v[2][i], v[3][i]));
@@ -994,18 +1005,30 @@ __device__ __forceinline__ void tile_softmax_regs(MState& ms, f32x4 (&accp)[D / 
     mt = fmaxf(mt, xpair<2>(mt));
     mt = fmaxf(mt, xpair<1>(mt));
     const float mn = fmaxf(ms.m[i], mt);
-    const float alpha = __expf(ms.m[i] - mn);
+    alpha[i] = __builtin_amdgcn_exp2f(ms.m[i] - mn);
     ms.m[i] = mn;
     float ls = 0.f;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
-      const float pp = __expf(v[tb][i] - mn);
+      const float pp = __builtin_amdgcn_exp2f(v[tb][i] - mn);
       ls += pp;
-      v[tb][i] = pp * vmul;
+      v[tb][i] = pp;
     }
-    ms.l[i] = __builtin_fmaf(ms.l[i], alpha, ls);
+    ms.l[i] = __builtin_fmaf(ms.l[i], alpha[i], ls);
+  }
+  // most tiles leave every running max unchanged (alpha == 1 in every lane)
+  if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f || alpha[2] != 1.f || alpha[3] != 1.f)) {
 #pragma unroll
-    for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int nc = 0; nc < D / 16; ++nc) accp[nc][i] *= alpha[i];
+  }
+  // V's per-tile scale (fp8 V) folded into the probabilities p.V uses
+  if (vmul != 1.f) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[tb][i] *= vmul;
   }
   if (r < (GT + 3) / 4) {
 #pragma unroll
@@ -1558,6 +1581,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
       // head g, column 16nc + x sits in lane 16 (g / 4) + x, register g % 4 of
       // accp[nc].  It goes to the wave's (now idle) V slot.
       mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms.m[g & 3]), 16 * (g >> 2)));
+      // base-2 units back to natural ones; an empty state keeps kM0
+      if (mg != kM0) mg *= 0.6931471805599453f;
       lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(row16_sum(ms.l[g & 3])), 16 * (g >> 2)));
       float* ao = reinterpret_cast<float*>(sv);
 #pragma unroll
