@@ -281,12 +281,17 @@ int oc_kth_smallest(const float* x, int64_t rows, int64_t n, int64_t row_stride,
  * attend, oc_decode's OC_GATE_MASK convention).  tau_norm = tau * 64 *
  * head_dim: the hook compares qn * ||K_high|| / (64 * head_dim) with tau
  * (perplexity_eval.py:476-491 with the max of the per-head medians,
- * :639-657 with the median of the Walsh-subspace norms).
+ * :639-657 with the median of the Walsh-subspace norms).  gate_stats (if
+ * given, float32 (batch * num_kv_heads, 3)): per (b, h) the number of
+ * evicted tiles t < num_tiles, qn and the largest k_norms entry of the
+ * tiles t < num_tiles (NaN if one is NaN, -inf if there are none) -- the
+ * hook's per-call statistics (evicted tiles, q and K information density)
+ * before its reductions over heads and its clamp at 0.
  */
 int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv_heads, int32_t G, int32_t reduce,
                   const float* k_norms, int64_t k_norms_stride_b, int64_t k_norms_stride_h, int32_t num_tiles,
                   int32_t mask_cols, double tau_norm, int32_t keep_polarity, uint8_t* mask, int64_t mask_stride_b,
-                  int64_t mask_stride_h, float* group_norms, void* stream);
+                  int64_t mask_stride_h, float* group_norms, float* gate_stats, void* stream);
 
 /*
  * oc_prefill_attention -- causal GQA attention of q_len queries over kv_len

@@ -628,8 +628,10 @@ __global__ __launch_bounds__(256) void kth_smallest_kernel(const float* x, int64
 __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, int Hkv, int G, int reduce,
                                                          const float* kn, int64_t kn_sb, int64_t kn_sh,
                                                          int num_tiles, int mask_cols, float tau_norm, int keep_pol,
-                                                         uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out) {
+                                                         uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out,
+                                                         float* stats) {
   __shared__ float s_qn;
+  __shared__ float s_red[2][4];
   const int bk = blockIdx.x;
   const int b = bk / Hkv;
   const int kv = bk % Hkv;
@@ -659,9 +661,39 @@ __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, 
   const float qn = s_qn;
   const float* knr = kn + (int64_t)b * kn_sb + (int64_t)kv * kn_sh;
   uint8_t* mr = mask + (int64_t)b * m_sb + (int64_t)kv * m_sh;
+  float nev = 0.f, kmax = -__builtin_inff();
+  bool knan = false;
   for (int t = threadIdx.x; t < mask_cols; t += 256) {
-    const bool ev = t < num_tiles && qn * knr[t] <= tau_norm;
+    const bool full = t < num_tiles;
+    const bool ev = full && qn * knr[t] <= tau_norm;
     mr[t] = (ev != (keep_pol != 0)) ? 1 : 0;
+    if (full) {
+      nev += ev ? 1.f : 0.f;
+      kmax = fmaxf(kmax, knr[t]);
+      knan = knan || __builtin_isnan(knr[t]);
+    }
+  }
+  if (stats) {
+    // per (b, kv head): evicted complete tiles, the group norm and the
+    // largest K norm of the complete tiles (NaN if any is NaN, -inf if
+    // none), unclamped: the hook clamps after its reductions over heads
+    nev = wave_sum(nev);
+    kmax = wave_max(kmax);
+    const bool wnan = __ballot(knan) != 0;
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      s_red[0][w] = nev;
+      s_red[1][w] = wnan ? __builtin_nanf("") : kmax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float* o = stats + (int64_t)bk * 3;
+      o[0] = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+      o[1] = qn;
+      float m = s_red[1][0];
+      for (int i = 1; i < 4; ++i) m = (__builtin_isnan(m) || __builtin_isnan(s_red[1][i])) ? __builtin_nanf("") : fmaxf(m, s_red[1][i]);
+      o[2] = m;
+    }
   }
 }
 
@@ -775,7 +807,7 @@ extern "C" int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv
                              const float* k_norms, int64_t k_norms_stride_b, int64_t k_norms_stride_h,
                              int32_t num_tiles, int32_t mask_cols, double tau_norm, int32_t keep_polarity,
                              uint8_t* mask, int64_t mask_stride_b, int64_t mask_stride_h, float* group_norms,
-                             void* stream) {
+                             float* gate_stats, void* stream) {
   if (!q_norms || !k_norms || !mask) return fail(OC_ERR_INVALID, "NULL pointer");
   if (batch < 0 || num_kv_heads < 0 || G < 1 || num_tiles < 0 || mask_cols < num_tiles)
     return fail(OC_ERR_INVALID, "bad sizes");
@@ -785,7 +817,7 @@ extern "C" int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv
   if (wgs > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many heads");
   hipLaunchKernelGGL(group_gate_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, q_norms,
                      num_kv_heads, G, reduce, k_norms, k_norms_stride_b, k_norms_stride_h, num_tiles, mask_cols,
-                     (float)tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms);
+                     (float)tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms, gate_stats);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "group-gate launch");
 }

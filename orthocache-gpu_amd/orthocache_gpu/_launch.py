@@ -624,12 +624,14 @@ def kth_smallest(x: torch.Tensor, k: int) -> torch.Tensor:
 
 
 def group_gate(q_norms: torch.Tensor, k_norms: torch.Tensor, num_kv_heads: int, G: int, num_tiles: int,
-               mask_cols: int, tau_norm: float, reduce: int, keep_polarity: bool = False
-               ) -> Tuple[torch.Tensor, torch.Tensor]:
+               mask_cols: int, tau_norm: float, reduce: int, keep_polarity: bool = False, want_stats: bool = False):
     """oc_group_gate.  q_norms: float32 (batch, num_kv_heads * G); k_norms:
     float32 (batch or 1, num_kv_heads, >= num_tiles) (a batch of 1 is shared
     by every batch entry).  Returns (mask uint8 (batch, num_kv_heads,
-    mask_cols), group norms float32 (batch, num_kv_heads))."""
+    mask_cols), group norms float32 (batch, num_kv_heads)), plus with
+    want_stats float32 (batch, num_kv_heads, 3): evicted complete tiles, the
+    group norm and the largest K norm of the complete tiles (NaN if one is
+    NaN, -inf if there are none)."""
     device = require_gpu(q_norms, k_norms)
     B = q_norms.shape[0]
     q_norms = q_norms.to(torch.float32).contiguous()
@@ -641,12 +643,13 @@ def group_gate(q_norms: torch.Tensor, k_norms: torch.Tensor, num_kv_heads: int, 
     ksb = 0 if k_norms.shape[0] == 1 else k_norms.stride(0)
     mask = torch.empty((B, num_kv_heads, max(mask_cols, 1)), dtype=torch.uint8, device=device)
     gn = torch.empty((B, num_kv_heads), dtype=torch.float32, device=device)
+    st = torch.empty((B, num_kv_heads, 3), dtype=torch.float32, device=device) if want_stats else None
     with torch.cuda.device(device):
         N.check("oc_group_gate", N.lib().oc_group_gate(
             q_norms.data_ptr(), B, num_kv_heads, G, reduce, k_norms.data_ptr(), ksb, k_norms.stride(1),
             num_tiles, mask_cols, float(tau_norm), 1 if keep_polarity else 0, mask.data_ptr(), mask.stride(0),
-            mask.stride(1), gn.data_ptr(), ctypes.c_void_p(current_stream(device))))
-    return mask, gn
+            mask.stride(1), gn.data_ptr(), _ptr(st), ctypes.c_void_p(current_stream(device))))
+    return (mask, gn, st) if want_stats else (mask, gn)
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, tile_mask: Optional[torch.Tensor] = None,

@@ -111,7 +111,7 @@ SIGNATURES = {
     "oc_row_norms": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p, _p]),
     "oc_kth_smallest": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p]),
     "oc_group_gate": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i64, _i64, _i32, _i32, ctypes.c_double, _i32, _p,
-                             _i64, _i64, _p, _p]),
+                             _i64, _i64, _p, _p, _p]),
     "oc_prefill_attention": (_i32, [ctypes.POINTER(OcPrefillParams), _p]),
     "oc_prefill_params_bytes": (ctypes.c_size_t, []),
     "oc_block_spectra": (_i32, [ctypes.POINTER(OcSpectraParams), _p]),

@@ -277,22 +277,20 @@ class OrthoCache_GQA_Attention:
         norms = nc.cache[:Hkv].unsqueeze(0)
         qh = X.row_norms(query, low_band=_LOW_BAND).view(B, Hq)
         # 1 = attend: complete tiles that pass the gate, and the partial last tile
-        keep, med = X.group_gate(qh, norms, Hkv, G, T, tiles, tau * TILE * d, N.OC_GROUP_MEDIAN, keep_polarity=True)
+        keep, _, dev = X.group_gate(qh, norms, Hkv, G, T, tiles, tau * TILE * d, N.OC_GROUP_MEDIAN,
+                                    keep_polarity=True, want_stats=True)
         kv = X.rows_layout(key.reshape(B * Hkv, Skv, d), value.reshape(B * Hkv, Skv, d), partial_tail=True)
         res = X.decode(kv, query.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0,
                        mode=N.OC_MODE_CACHED, out_dtype=query.dtype, tile_mask=keep.view(B * Hkv, -1))
-        dev = torch.stack([
-            (keep[:, :, :T] == 0).view(B, -1).sum(1, dtype=torch.int64).to(torch.float32),
-            med.amax(1).clamp(min=0.0),
-            norms[0, :, :T].amax().clamp(min=0.0).expand(B) if T > 0 else torch.zeros(
-                (B,), dtype=torch.float32, device=query.device),
-        ])
+        # dev (B, Hkv, 3), written by the gate kernel: evicted complete
+        # tiles, the group's q norm and the largest K norm per kv head,
+        # reduced over the heads (and clamped at 0) when folded
         stats, gov = self.stats, self.governor
 
         def fold(host):
             for b in range(B):
-                skipped = int(host[0, b])
-                _exhaust(stats, float(host[1, b]), float(host[2, b]))
+                skipped = int(host[b, :, 0].sum())
+                _exhaust(stats, float(host[b, :, 1].max().clamp(min=0.0)), float(host[b, :, 2].max().clamp(min=0.0)))
                 stats['decode_steps'] += 1
                 stats['decode_tiles_skipped'] += skipped
                 stats['decode_tiles_total'] += T * Hkv

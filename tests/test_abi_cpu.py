@@ -115,8 +115,8 @@ def test_hook_entry_point_argument_checks():
     assert b"low_band" in L.oc_last_error()
     assert L.oc_kth_smallest(256, 2, 5, 5, 5, 256, None) == N.OC_ERR_INVALID
     assert L.oc_kth_smallest(256, 2, 5, 4, 1, 256, None) == N.OC_ERR_INVALID
-    assert L.oc_group_gate(256, 1, 2, 4, 7, 256, 0, 8, 4, 4, 1.0, 0, 256, 8, 4, None, None) == N.OC_ERR_INVALID
-    assert L.oc_group_gate(256, 1, 2, 4, N.OC_GROUP_MAX, 256, 0, 8, 5, 4, 1.0, 0, 256, 8, 4, None,
+    assert L.oc_group_gate(256, 1, 2, 4, 7, 256, 0, 8, 4, 4, 1.0, 0, 256, 8, 4, None, None, None) == N.OC_ERR_INVALID
+    assert L.oc_group_gate(256, 1, 2, 4, N.OC_GROUP_MAX, 256, 0, 8, 5, 4, 1.0, 0, 256, 8, 4, None, None,
                            None) == N.OC_ERR_INVALID
 
 

@@ -117,18 +117,36 @@ def test_group_gate_vs_loops(reduce):
     for keep in (False, True):
         for shared in (False, True):
             kn_t = torch.from_numpy(kn[:1] if shared else kn).to(DEV)
-            mask, gn = X.group_gate(torch.from_numpy(qn).to(DEV), kn_t, Hkv, G, T, cols, tau_norm, mode,
-                                    keep_polarity=keep)
-            mask, gn = mask.cpu().numpy(), gn.cpu().numpy()
+            mask, gn, st = X.group_gate(torch.from_numpy(qn).to(DEV), kn_t, Hkv, G, T, cols, tau_norm, mode,
+                                        keep_polarity=keep, want_stats=True)
+            mask, gn, st = mask.cpu().numpy(), gn.cpu().numpy(), st.cpu().numpy()
             for b in range(B):
                 for h in range(Hkv):
                     grp = qn[b, h * G:(h + 1) * G]
                     want = grp.max() if reduce == "max" else np.sort(grp)[G // 2]
                     assert gn[b, h] == want
                     knr = kn[0 if shared else b, h]
+                    evs = [t < T and np.float32(want) * knr[t] <= np.float32(tau_norm) for t in range(cols)]
                     for t in range(cols):
-                        ev = t < T and np.float32(want) * knr[t] <= np.float32(tau_norm)
-                        assert mask[b, h, t] == (int(not ev) if keep else int(ev))
+                        assert mask[b, h, t] == (int(not evs[t]) if keep else int(evs[t]))
+                    # the hook's per-call statistics before their reductions
+                    assert st[b, h, 0] == sum(evs) and st[b, h, 1] == want and st[b, h, 2] == knr[:T].max()
+
+
+def test_group_gate_stats_edge_cases():
+    """The gate statistics with no complete tile (-inf K maximum) and with a
+    NaN K norm (NaN, as torch's amax gives)."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    qn = torch.ones((1, 4), device=DEV)
+    kn = torch.ones((1, 2, 8), device=DEV)
+    _, _, st = X.group_gate(qn, kn, 2, 2, 0, 1, 1.0, N.OC_GROUP_MAX, keep_polarity=True, want_stats=True)
+    st = st.cpu().numpy()
+    assert (st[0, :, 0] == 0).all() and np.isneginf(st[0, :, 2]).all()
+    kn[0, 1, 3] = float("nan")
+    _, _, st = X.group_gate(qn, kn, 2, 2, 8, 8, 1.0, N.OC_GROUP_MAX, keep_polarity=True, want_stats=True)
+    st = st.cpu().numpy()
+    assert st[0, 0, 2] == 1.0 and np.isnan(st[0, 1, 2])
 
 
 def _gap_tau(prods):
