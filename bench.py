@@ -424,6 +424,38 @@ def hook_measure(steps, warmup):
         if dt == torch.float32:
             line["cpu_baseline"] = _hook_cpu(q, k, v, Hq // Hkv)
         print(json.dumps(line), flush=True)
+    hook_decode_measure(steps, warmup)
+
+
+def hook_decode_measure(steps, warmup):
+    """One decode step of the patched attention (OrthoCache_GQA_Attention,
+    cached K band norms, q_len 1) on a Llama-3-8B layer: 32 / 8 heads,
+    head_dim 128, bfloat16, 4096 cached tokens, batch 1, with nothing and with
+    everything evicted; torch's SDPA decode of the same step beside it.  The
+    warmup is at least 300 calls: the clocks of a box that has just been idle
+    rise over the first few hundred."""
+    import torch
+    from orthocache_gpu.model_hook import OrthoCache_GQA_Attention
+    from orthocache_gpu.norm_cache import SpectralNormCache
+    g = torch.Generator(device="cuda").manual_seed(0)
+    B, Hq, Hkv, d, S = 1, 32, 8, 128, 4096
+    G = Hq // Hkv
+    q = torch.randn((B, Hq, S, d), device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(torch.bfloat16)
+    hook = OrthoCache_GQA_Attention(tau=0.0)
+    hook.norm_cache = SpectralNormCache(Hkv, S // 64 + 4, torch.device("cuda"))
+    hook.orthocache_attention(q, k, v, G)  # prefill: fills the norm cache
+    q1 = q[:, :, -1:].contiguous()
+    line = {"only": "hook", "kernel": "hook_decode_step", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+            "cached_tokens": S, "head_dim": d, "dtype": "bfloat16"}
+    for name, tau in (("us_none_evicted", 0.0), ("us_all_evicted", 1e30)):
+        hook.tau = tau
+        line[name] = round(_event_us(lambda: hook.orthocache_attention(q1, k, v, G), steps, max(warmup, 300)), 1)
+    kk, vv = k.repeat_interleave(G, 1), v.repeat_interleave(G, 1)
+    line["torch_sdpa_us"] = round(_event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q1, kk, vv),
+                                            steps, max(warmup, 300)), 1)
+    print(json.dumps(line), flush=True)
 
 
 def _hook_cpu(q, k, v, G):
