@@ -1214,6 +1214,180 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
   }
 }
 
+// ---- transposed matrix-core step (attend-every-tile loop, contiguous rows)
+//
+// S^T = K.q^T: with K as the A operand, lane 16r + x register i of c[tb]
+// holds the logit of head x for K row 4r + i of 16-token block tb, so each
+// head's online softmax is per lane (two cross-lane steps) and the
+// probabilities are already the B operand of O^T += V^T.P^T: no P round trip
+// through LDS.  For that, A-row a of the tile holds token kperm(a): within
+// each 32-token block, a = 16h + 4r + i holds token 8r + 4h + i, so the eight
+// probabilities a lane holds for block j are tokens 32j + 8kg .. + 7 in order,
+// the k index of the p.V instruction (V stays in token order).
+__device__ __forceinline__ int kperm(int a) {
+  return (a & ~31) + 8 * ((a >> 2) & 3) + 4 * ((a >> 4) & 1) + (a & 3);
+}
+
+struct MStateT {
+  float m;  // running max of the lane's head, base-2 units
+  float l;  // partial sum over the lane's tokens
+};
+
+// K rows of tile t in kperm order (one descriptor for the tile; rows at or
+// past n_tok read as zero through its range check)
+template <int DT, int D>
+__device__ __forceinline__ void load_k_mfma_t(const DecodeArgs& a, const RowInfo& ri, int row, int t, int lane,
+                                              uint32_t (&kb)[4][D / 32][4]) {
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+  const int tok0 = t * 64;
+  const int64_t ts = a.k_tok_stride;
+  const char* base = a.k + (int64_t)row * a.k_row_stride + tok0 * ts;
+  const int nbytes = (int)(min(ri.n_tok - tok0, 64) * ts);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, nbytes, 0x00020000);
+  const int cofs = F8 ? kg * (D / 4) : 16 * kg;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int voff = kperm(16 * tb + x) * (int)ts + cofs;
+#pragma unroll
+    for (int dc = 0; dc < (F8 ? D / 64 : D / 32); ++dc) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (F8 ? 16 : 64) * dc, 0, kStreamAux);
+      kb[tb][dc][0] = v[0];
+      kb[tb][dc][1] = v[1];
+      kb[tb][dc][2] = v[2];
+      kb[tb][dc][3] = v[3];
+    }
+  }
+}
+
+template <int DT, int D>
+__device__ __forceinline__ void tile_logits_t(const uint32_t (&aq)[D / 32][4], const uint32_t (&kb)[4][D / 32][4],
+                                              f32x4 (&c)[4]) {
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) {
+      uint32_t b[4];
+      k_operand<DT, D>(kb, tb, dc, b);
+      c[tb] = mfma_qk<MfmaT<DT>::value>(b, aq[dc], c[tb]);
+    }
+  }
+}
+
+// Online-softmax update of the lane's head from the tile's raw logits (c
+// becomes the probabilities times vmul); base-2 units, as tile_softmax_regs
+template <int D>
+__device__ __forceinline__ void tile_softmax_t(MStateT& ms, f32x4 (&accp)[D / 16], f32x4 (&c)[4], float lscale,
+                                               float vmul, int valid, int lane) {
+  const int r = lane >> 4;
+  const float lscale2 = lscale * 1.4426950408889634f;
+  if (valid >= 64) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[tb][i] *= lscale2;
+  } else {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[tb][i] = kperm(16 * tb + 4 * r + i) < valid ? c[tb][i] * lscale2 : -__builtin_inff();
+  }
+  float mt = -__builtin_inff();
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) mt = fmaxf(mt, fmaxf(fmaxf(c[tb][0], c[tb][1]), fmaxf(c[tb][2], c[tb][3])));
+  mt = fmaxf(mt, xpair<16>(mt));
+  mt = fmaxf(mt, xpair<32>(mt));
+  const float mn = fmaxf(ms.m, mt);
+  const float alpha = __builtin_amdgcn_exp2f(ms.m - mn);
+  ms.m = mn;
+  float ls = 0.f;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float pp = __builtin_amdgcn_exp2f(c[tb][i] - mn);
+      ls += pp;
+      c[tb][i] = pp;
+    }
+  ms.l = __builtin_fmaf(ms.l, alpha, ls);
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc) accp[nc] *= alpha;
+  }
+  if (vmul != 1.f) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) c[tb] *= vmul;
+  }
+}
+
+// O^T += V^T.P^T: A = V^T from the LDS tile (transposing reads, as
+// tile_pv_mfma's B operand), B = the lane's own probabilities of block j
+// (c[2j][0..3], c[2j + 1][0..3]: tokens 32j + 8kg .. + 7) as a 16-bit high
+// part plus the 16-bit rounding of the remainder; accp[nc] lane 16r + x
+// register i = output column 16nc + 4r + i of head x.
+template <int DT, int D>
+__device__ __forceinline__ void tile_pv_t(f32x4 (&accp)[D / 16], const f32x4 (&c)[4], const uint16_t* sv, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+#pragma unroll
+  for (int tb2 = 0; tb2 < 2; ++tb2) {
+    float pv[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pv[e] = c[2 * tb2][e];
+      pv[4 + e] = c[2 * tb2 + 1][e];
+    }
+    uint32_t phi[4], plo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (MfmaT<DT>::value == OC_BF16) {
+        const __bf16 h0 = (__bf16)pv[2 * e], h1 = (__bf16)pv[2 * e + 1];
+        const __bf16 l0 = (__bf16)(pv[2 * e] - (float)h0), l1 = (__bf16)(pv[2 * e + 1] - (float)h1);
+        phi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        plo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+      } else {
+        const _Float16 h0 = (_Float16)pv[2 * e], h1 = (_Float16)pv[2 * e + 1];
+        const _Float16 l0 = (_Float16)(pv[2 * e] - (float)h0), l1 = (_Float16)(pv[2 * e + 1] - (float)h1);
+        phi[e] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+        plo[e] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+      }
+    }
+    const int vrow = 32 * tb2 + 8 * kg + (x >> 2);
+    const int vx = v_xor<DT, D>(vrow) >> 1;
+    const uint16_t* rowp = sv + vrow * D + 4 * (x & 3);
+    const int vrow8 = 32 * tb2 + 8 * kg + (x >> 1);
+    const int vx8 = v_xor<DT, D>(vrow8);
+    const uint8_t* rowp8 = reinterpret_cast<const uint8_t*>(sv) + vrow8 * D + 8 * (x & 1);
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc) {
+      uint32_t va[4];
+      if constexpr (DT == OC_FP8_E4M3FN) {
+        typedef int i32x2 __attribute__((ext_vector_type(2)));
+        const i32x2 b8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * (nc ^ vx8)));
+        fp8x4_to_bf16((uint32_t)b8[0], va[0], va[1]);
+        fp8x4_to_bf16((uint32_t)b8[1], va[2], va[3]);
+      } else {
+        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vx)));
+        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vx)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
+        va[0] = w0[0];
+        va[1] = w0[1];
+        va[2] = w1[0];
+        va[3] = w1[1];
+      }
+      accp[nc] = mfma_qk<MfmaT<DT>::value>(va, phi, accp[nc]);
+      accp[nc] = mfma_qk<MfmaT<DT>::value>(va, plo, accp[nc]);
+    }
+  }
+}
+
 // Retain decision for tile t of a row in cached mode from its stored
 // energies; a partial tail tile is always retained.
 __device__ __forceinline__ bool cached_keep(const DecodeArgs& a, const RowInfo& ri, int t, float el, float eh,
@@ -1362,6 +1536,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     ms.m[i] = kM0;
     ms.l[i] = 0.f;
   }
+  // the transposed step: matrix cores, every listed tile attended, contiguous rows
+  constexpr bool kT = MQK && LOOP && !PAGED;
+  MStateT mst{kM0, 0.f};
   uint32_t aq[MQK ? D / 32 : 1][4];
   if constexpr (MQK) load_q_mfma<DT, D, GT>(sh_qp, lane, aq);
   float* sp = sh_p + wave * 64 * kPH;     // this wave's p[head][token] slot (MQK)
@@ -1465,7 +1642,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
     // a block id outside the pool (paged): raised once after the loop, so no
     // global atomic sits among the tile loads
     bool bad_page = false;
-    if constexpr (LOOP) {
+    if constexpr (kT) {
+      // cached or dense decode on contiguous rows: the transposed step
+      for (int t = next_tile(); t >= 0; t = next_tile()) {
+        const int valid = min(64, ri.n_tok - t * 64);
+        load_k_mfma_t<DT, D>(a, ri, row, t, lane, kb);
+        load_v_lds<DT, D, PAGED>(a, ri, row, t, lane, sv, TilePages{});
+        f32x4 c[4];
+        tile_logits_t<DT, D>(aq, kb, c);
+        tile_softmax_t<D>(mst, accp, c, lscale_of(t), tile_vmul(a, row, t), valid, lane);
+        // the V tile's direct-to-LDS loads (issued after K) have landed
+        __builtin_amdgcn_s_waitcnt(0);
+        tile_pv_t<DT, D>(accp, c, sv, lane);
+        ++kept;
+      }
+    } else if constexpr (LOOP) {
       // cached or dense decode (LOOP, fixed at launch: the same condition as
       // cached || gate == NONE): every listed tile is attended
       for (int t = next_tile(); t >= 0; t = next_tile()) {
@@ -1573,10 +1764,30 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   }
 
   // wave -> LDS: l summed over lanes, acc summed over the 4 token groups
+  float lsum_t = 0.f;
+  if constexpr (kT) {
+    // head x's state in lanes x, x + 16, x + 32, x + 48; its output
+    // columns 16nc + 4r + i in lane 16r + x, register i
+    lsum_t = mst.l + xpair<16>(mst.l);
+    lsum_t += xpair<32>(lsum_t);
+    float* ao = reinterpret_cast<float*>(sv);
+    const int x = lane & 15;
+    const int r = lane >> 4;
+    if (x < GT) {
+#pragma unroll
+      for (int nc = 0; nc < D / 16; ++nc)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ao[x * D + 16 * nc + 4 * r + i] = accp[nc][i];
+    }
+  }
 #pragma unroll
   for (int g = 0; g < GT; ++g) {
     float mg, lt;
-    if constexpr (MQK) {
+    if constexpr (kT) {
+      mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mst.m), g));
+      if (mg != kM0) mg *= 0.6931471805599453f;
+      lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum_t), g));
+    } else if constexpr (MQK) {
       // head g: register g % 4 of the lanes of row g / 4; the p.V result of
       // head g, column 16nc + x sits in lane 16 (g / 4) + x, register g % 4 of
       // accp[nc].  It goes to the wave's (now idle) V slot.
