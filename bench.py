@@ -61,8 +61,10 @@ def parse():
                     help="with --only paged/fp8: comma-separated subset of cached,single_pass,dense")
     ap.add_argument("--extra-configs", type=int, default=1,
                     help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
+    ap.add_argument("--sweep", type=int, default=1,
+                    help="also time BASELINE.json config 1 over 1K..32K tokens and config 2 at full size (0 = skip)")
     ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read",
-                                       "paged", "fp8", "hook", "compact"],
+                                       "paged", "fp8", "hook", "compact", "sweep", "config2"],
                     default=None,
                     help="time only this decode variant of the primary batch, a plain 1 GiB device copy "
                          "(the reference kernel for scaling the profiler's byte counters), the model hook's "
@@ -201,13 +203,15 @@ class Setup:
         return kept * 2 * kv_tile + q_bytes + tiles * 4  # + e_high score per tile
 
 
-def _decode_params(lib, N, kv, q, G, gate, mode, tau, scores, P, out, ws):
+def _decode_params(lib, N, kv, q, G, gate, mode, tau, scores, P, out, ws, dtype_code=None):
     """OcDecodeParams of one production oc_decode call (merge fused, partials
-    and counters in the workspace `ws`, a zeroed device buffer)."""
+    and counters in the workspace `ws`, a zeroed device buffer); q and out in
+    dtype_code (default bfloat16)."""
+    dtype_code = N.OC_BF16 if dtype_code is None else dtype_code
     p = N.OcDecodeParams()
     p.kv = kv.struct()
     p.q = q.data_ptr()
-    p.q_dtype = N.OC_BF16
+    p.q_dtype = dtype_code
     p.G = G
     p.q_row_stride = q.stride(0)
     p.gate = gate
@@ -218,7 +222,7 @@ def _decode_params(lib, N, kv, q, G, gate, mode, tau, scores, P, out, ws):
         p.score_e_high = scores.e_high.data_ptr()
         p.score_row_stride = scores.e_high.stride(0)
     p.num_splits = P
-    p.out_dtype = N.OC_BF16
+    p.out_dtype = dtype_code
     p.out = out.data_ptr()
     p.out_row_stride = out.stride(0)
     need = lib.oc_decode_workspace_size(ctypes.byref(p))
@@ -334,6 +338,176 @@ class ExtraConfig:
         return r
 
 
+class Sweep:
+    """BASELINE.json config 1 / the reference's published table
+    (README.md:26-35, benchmarks/profile_multihead.py:61-191): v2 zeta gate
+    (zeta_max 5), 32 heads (MHA, G = 1), head_dim 128, float16, half the
+    tiles noise (evicted), one sequence length per instance.  Times this
+    build's dense decode, the single-pass gated decode (the reference's v2
+    design: every K tile scored, V of retained tiles) and the cached-score
+    decode, each one oc_decode call per step on buffer sets rotated past the
+    Infinity Cache, plus the reference's own dense comparator (torch.bmm +
+    softmax + bmm in float16, profile_multihead.py:127-146) on the same data."""
+
+    H = 32
+
+    def __init__(self, seq_len, seed=500):
+        import torch
+        from orthocache_gpu import _launch as X
+        from orthocache_gpu import _native as N
+        from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
+        from orthocache_gpu.workloads import make_kv, make_q
+        self.torch, self.N, self.S = torch, N, seq_len
+        dev = torch.device("cuda", 0)
+        self.lib, self.stream = N.lib(), X.current_stream(dev)
+        set_bytes = self.H * seq_len * D * 2 * 2
+        self.nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
+        self.tiles = seq_len // 64
+        self.P = X.auto_num_splits(self.tiles, dev)
+        self.out = torch.empty((self.H, D), dtype=torch.float16, device=dev)
+        self.sets, self.params = [], {"dense": [], "single_pass": [], "cached": []}
+        ws_bytes = 0
+        for i in range(self.nsets):
+            wl = make_kv(self.H, seq_len, D, noise_frac=0.5, dtype=torch.float16, device=dev, seed=seed + 31 * i)
+            q = make_q(self.H, 1, D, dtype=torch.float16, device=dev, seed=seed + 31 * i + 1)
+            self.sets.append({"wl": wl, "q": q, "scores": score_tiles(wl.keys),
+                              "kv": X.rows_layout(wl.keys, wl.values)})
+        self.ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+        for st in self.sets:
+            for v, gate, mode in (("dense", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS),
+                                  ("single_pass", N.OC_GATE_ZETA, N.OC_MODE_SINGLE_PASS),
+                                  ("cached", N.OC_GATE_ZETA, N.OC_MODE_CACHED)):
+                self.params[v].append(_decode_params(self.lib, N, st["kv"], st["q"], 1, gate, mode, 5.0,
+                                                     st["scores"], self.P, self.out, self.ws, N.OC_F16))
+        self.kept = int((~self.sets[0]["wl"].noise).sum())
+
+    def check(self):
+        """The zeta mask of set 0 equals the smooth-tile labels."""
+        from orthocache_gpu import fused_orthocache_attention_v2
+        st = self.sets[0]
+        _, meta = fused_orthocache_attention_v2(st["q"], st["wl"].keys, st["wl"].values, 5.0)
+        assert self.torch.equal(meta["eviction_mask"], ~st["wl"].noise), "zeta mask differs from the tile labels"
+        return meta["eviction_rate"]
+
+    def time(self, variant, steps, warmup):
+        plist = self.params[variant]
+        lib, N, stream = self.lib, self.N, ctypes.c_void_p(self.stream)
+
+        def run(i):
+            rc = lib.oc_decode(ctypes.byref(plist[i % self.nsets]), stream)
+            if rc:
+                N.check("oc_decode", rc)
+        return _event_us_i(run, steps, warmup)
+
+    def time_torch_dense(self, steps, warmup):
+        torch = self.torch
+        scale = 1.0 / math.sqrt(D)
+
+        def run(i):
+            st = self.sets[i % self.nsets]
+            k, v = st["wl"].keys, st["wl"].values
+            # K q as (H, S, d) x (H, d, 1): no transposed operand
+            lg = torch.bmm(k, st["q"].unsqueeze(-1)).squeeze(-1) * scale
+            torch.bmm(torch.softmax(lg.float(), dim=-1).half().unsqueeze(1), v)
+        return _event_us_i(run, steps, warmup)
+
+    def bytes(self, variant):
+        tile = 64 * D * 2
+        qo = 2 * self.H * D * 2
+        all_t = self.H * self.tiles
+        if variant == "dense":
+            return all_t * 2 * tile + qo
+        if variant == "single_pass":
+            return all_t * tile + self.kept * tile + qo
+        return self.kept * 2 * tile + all_t * 8 + qo  # e_low + e_high per tile
+
+    def measure(self, steps, warmup):
+        r = {"seq_len": self.S, "eviction_rate": round(self.check(), 4), "num_splits": self.P}
+        for v in ("dense", "single_pass", "cached"):
+            us = self.time(v, steps, warmup)
+            gbps = self.bytes(v) / (us * 1e-6) / 1e9
+            r[v] = {"us": round(us, 2), "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+        r["torch_dense_us"] = round(self.time_torch_dense(max(10, steps // 4), 3), 2)
+        r["single_pass_speedup"] = round(r["dense"]["us"] / r["single_pass"]["us"], 3)
+        r["cached_speedup"] = round(r["dense"]["us"] / r["cached"]["us"], 3)
+        return r
+
+
+def sweep_measure(steps, warmup, lengths=(1024, 2048, 4096, 8192, 16384, 32768)):
+    """Config 1 over the published sequence lengths, and the crossovers:
+    the shortest length from which each gated decode stays faster than the
+    dense one."""
+    import torch
+    rows = []
+    for s_len in lengths:
+        sw = Sweep(s_len)
+        rows.append(sw.measure(steps, warmup))
+        del sw
+        torch.cuda.empty_cache()
+
+    def crossover(key):
+        for i in range(len(rows)):
+            if all(r[key] > 1.0 for r in rows[i:]):
+                return rows[i]["seq_len"]
+        return None
+    return {"workload": "config 1: v2 zeta gate (zeta_max 5), 32 heads, d 128, float16, 50% noise tiles",
+            "rows": rows, "crossover_single_pass": crossover("single_pass_speedup"),
+            "crossover_cached": crossover("cached_speedup")}
+
+
+def config2_measure(steps, warmup, seed=700):
+    """BASELINE.json config 2 at full size: batch 8, 32 query / 8 kv heads
+    (G = 4), 65536 tokens, bfloat16, half the tiles noise; two of each
+    group's four query heads projected onto the low head_dim Walsh rows.
+    The literal tau = 1.0 (the full-norm Cauchy-Schwarz gate keeps every
+    tile) and a calibrated tau (the noise half kept), cached decode, beside
+    the single-pass and dense decodes.  One set of 2.1 GB, larger than the
+    Infinity Cache, so every step streams from HBM."""
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q
+    dev = torch.device("cuda", 0)
+    B, hkv, g, s_len = 8, 8, 4, 65536
+    rows = B * hkv
+    wl = make_kv(rows, s_len, D, noise_frac=0.5, dtype=torch.bfloat16, device=dev, seed=seed)
+    q = make_q(rows, g, D, dtype=torch.bfloat16, device=dev, seed=seed + 1, low_band_heads=2)
+    sc = score_tiles(wl.keys)
+    kv = X.rows_layout(wl.keys, wl.values)
+    lib, stream = N.lib(), X.current_stream(dev)
+    P = X.auto_num_splits(s_len // 64, dev)
+    out = torch.empty((rows * g, D), dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    tau_cal = calibrate_tau(sc.e_high, q, g)
+    qn = q.float().view(rows, g, -1).norm(dim=2).amax(dim=1)
+    cs = qn[:, None] * sc.e_high.sqrt()
+    tiles = rows * (s_len // 64)
+    tile = 64 * D * 2
+    r = {"workload": f"config 2: batch {B} x {hkv} kv heads, {s_len} tokens, G={g}, bf16, 2 of 4 q heads "
+                     "low-band", "num_splits": P, "tau_calibrated": tau_cal}
+    for name, gate, mode, tau in (("cached_tau1", N.OC_GATE_CS, N.OC_MODE_CACHED, 1.0),
+                                  ("cached", N.OC_GATE_CS, N.OC_MODE_CACHED, tau_cal),
+                                  ("single_pass", N.OC_GATE_CS, N.OC_MODE_SINGLE_PASS, tau_cal),
+                                  ("dense", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS, 0.0)):
+        p = _decode_params(lib, N, kv, q, g, gate, mode, tau, sc, P, out, ws)
+        run = lambda i, p=p: N.check("oc_decode", lib.oc_decode(ctypes.byref(p), ctypes.c_void_p(stream)))
+        us = _event_us_i(run, steps, warmup)
+        kept = tiles if gate == N.OC_GATE_NONE else int((cs > tau).sum())
+        if name == "dense":
+            nbytes = tiles * 2 * tile
+        elif mode == N.OC_MODE_SINGLE_PASS:
+            nbytes = tiles * tile + kept * tile
+        else:
+            nbytes = kept * 2 * tile + tiles * 4
+        gbps = nbytes / (us * 1e-6) / 1e9
+        r[name] = {"us": round(us, 2), "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4),
+                   "eviction_rate": round(1 - kept / tiles, 4)}
+    r["tokens_per_s"] = round(B / (r["cached"]["us"] * 1e-6), 1)
+    r["speedup_vs_dense"] = round(r["dense"]["us"] / r["cached"]["us"], 3)
+    return r
+
+
 def measure(setup, steps, warmup):
     evict = setup.check()
     r = {"batch": setup.batch, "eviction_rate": evict, "num_splits": setup.P, "tau": setup.tau,
@@ -380,6 +554,22 @@ def cpu_baseline(setup, seconds):
                       f"tiles, G={G}, Cauchy-Schwarz gate), {reps} repetitions in {dt:.1f} s: "
                       f"{step_s * 1e3:.1f} ms per step",
             "host_cpus": os.cpu_count()}
+
+
+def _event_us_i(fn, steps, warmup):
+    """Mean µs of fn(i) over `steps` back-to-back calls between two HIP
+    events, after `warmup` calls."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        fn(i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e3 / steps
 
 
 def _event_us(fn, steps, warmup):
@@ -619,6 +809,12 @@ def main():
     if args.only == "compact":
         compact_measure(args.steps, args.warmup)
         return
+    if args.only == "sweep":
+        print(json.dumps(dict(only="sweep", **sweep_measure(args.steps, args.warmup))))
+        return
+    if args.only == "config2":
+        print(json.dumps(dict(only="config2", **config2_measure(args.steps, args.warmup))))
+        return
     if args.only in ("paged", "fp8"):
         variants = tuple(args.variants.split(",")) if args.variants else ("cached", "single_pass", "dense")
         print(json.dumps(dict(only=args.only, **ExtraConfig(args.only).measure(args.steps, args.warmup, variants))))
@@ -645,6 +841,12 @@ def main():
             cfg = ExtraConfig(which)
             extras[which] = cfg.measure(args.steps, args.warmup)
             del cfg
+    sweep = cfg2 = None
+    if args.sweep:
+        torch.cuda.empty_cache()
+        sweep = sweep_measure(args.steps, args.warmup)
+        torch.cuda.empty_cache()
+        cfg2 = config2_measure(args.steps, args.warmup)
     ach = r1["step_gbps"]
     traffic = traffic_from_profiles()
     probe = read_probe(20, 3) if args.read_probe else None
@@ -695,6 +897,9 @@ def main():
     if extras:
         line["config3_paged"] = extras["paged"]
         line["config4_fp8"] = extras["fp8"]
+    if sweep:
+        line["config1_sweep"] = sweep
+        line["config2"] = cfg2
     print(json.dumps(line))
 
 

@@ -57,6 +57,10 @@
  *   oc_compact_gate  <- compute_multiband_mask, _compute_auto_tau, the zeta
  *                      statistics and classify_eviction as orthocache_forward
  *                      runs them (pipeline.py:458-527)
+ *   oc_block_regimes <- compute_block_beta + classify_eviction
+ *                      (perfect_eviction.py:75-186)
+ *   oc_device_props  <- torch.cuda.get_device_properties as _detect_gpu_profile
+ *                      reads it (pipeline.py:209-280)
  */
 #ifndef ORTHOCACHE_HIP_H
 #define ORTHOCACHE_HIP_H
@@ -393,6 +397,28 @@ int oc_compact_gate(const float* max_bound, const float* zeta, const float* ener
                     uint8_t* tile_mask, float* stats, void* stream);
 
 /*
+ * oc_block_regimes -- the eviction regime of every block of a compact-mode
+ * block table.  With qn[h] = max over s of q_norms[s * num_heads + h] (the
+ * (q_len, num_heads) spatial query norms, e.g. from oc_row_norms) and
+ * E = energy (num_blocks, num_heads):
+ *   beta_full[b, h] = qn[h] * sqrt(max(E[b, h], 0)) / sqrt(head_dim)
+ *   beta[b] = max_h beta_full[b, h],  gap[b] = z - beta[b]
+ *   regime[b] = 0 (retained: any of block_mask[b * mask_heads + 0 ..
+ *               mask_heads) set), 1 (evicted, gap >= underflow: exp of
+ *               every logit underflows, "perfect"), 2 (evicted, gap <
+ *               underflow, "statistical"); 0 as well for a NaN gap
+ *   counts = (regime-1 blocks, regime-2 blocks, retained blocks)  (int32)
+ * z = max(z_values[0 .. z_count)) when z_values is given, else z_max.
+ * float32 arithmetic, NaN propagating through every maximum; mask_heads 1
+ * or num_heads; beta_full may be NULL.  Replaces compute_block_beta and
+ * classify_eviction (perfect_eviction.py:75-186).
+ */
+int oc_block_regimes(const float* q_norms, int32_t q_len, int32_t num_heads, const float* energy,
+                     int32_t num_blocks, int32_t head_dim, double z_max, const float* z_values, int32_t z_count,
+                     const uint8_t* block_mask, int32_t mask_heads, double underflow, int32_t* regime,
+                     float* beta, float* gap, float* beta_full, int32_t* counts, void* stream);
+
+/*
  * oc_stream_compact -- the active-first stable permutation of num_blocks
  * blocks (block_mask != 0 = retained): indices[r] (int64) is the r-th
  * retained block, followed by the evicted blocks in order, and
@@ -489,6 +515,22 @@ int oc_abi_sizes(size_t* kv_desc_bytes, size_t* decode_params_bytes);
 
 /* number of compute units of the current device (256 on MI355X) */
 int oc_device_cu_count(int32_t* cus);
+
+/* properties of the current device that the host side sizes its dispatch
+ * and its crossover model by (no counterpart in the reference, which reads
+ * torch.cuda.get_device_properties, pipeline.py:209-280) */
+typedef struct oc_device_info {
+  char arch[64];               /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  char name[128];
+  int32_t compute_units;
+  int32_t wave_size;
+  int32_t memory_clock_khz;    /* peak memory clock */
+  int32_t memory_bus_bits;     /* memory interface width */
+  int64_t lds_per_cu_bytes;
+  int64_t total_memory_bytes;
+} oc_device_info;
+
+int oc_device_props(oc_device_info* info);
 
 const char* oc_version(void);
 const char* oc_last_error(void);

@@ -958,6 +958,33 @@ def compact_gate(max_bound, zeta, energy, qmax, d: int, zeta_max: float, tau: Op
             "perfect": perfect, "statistical": statistical}
 
 
+def block_regimes(q, energy, head_dim: int, z_max, block_mask, underflow: float = F32_UNDERFLOW):
+    """Per-block ceiling, gap and regime in the reference's float32 arithmetic
+    (perfect_eviction.py:75-186): qn_h = max over queries of ||q_s,h||;
+    beta[b, h] = qn_h * sqrt(clamp(E, 0)) / float32(sqrt(d)); beta_b = max over
+    h; gap = float32(z) - beta_b; regime 0 when any mask entry of the block is
+    set, 1 when gap >= underflow, 2 when gap < underflow (NaN: 0, counted in
+    neither).  z_max may be an array (its largest element).  Returns
+    (regime int32, beta float32 (nb,), gap float32, beta_full float32 (nb, H),
+    counts (perfect, statistical, retained))."""
+    f32 = np.float32
+    q = np.asarray(q, dtype=np.float32)
+    qn = np.sqrt(np.sum(q.astype(np.float64) ** 2, axis=-1)).astype(f32).max(axis=0)
+    e = np.asarray(energy, dtype=f32)
+    full = (qn[None, :] * np.sqrt(np.maximum(e, f32(0)))) / f32(math.sqrt(head_dim))
+    beta = full.max(axis=1) if full.shape[1] else np.zeros(full.shape[0], f32)
+    z = f32(np.max(np.asarray(z_max, dtype=f32))) if np.ndim(z_max) else f32(z_max)
+    gap = (z - beta).astype(f32)
+    m = np.asarray(block_mask, dtype=bool)
+    unified = m.any(axis=1) if m.ndim > 1 else m
+    thr = f32(underflow)
+    perfect = ~unified & (gap >= thr)
+    statistical = ~unified & (gap < thr)
+    regime = np.where(perfect, 1, np.where(statistical, 2, 0)).astype(np.int32)
+    return regime, beta.astype(f32), gap, full.astype(f32), (int(perfect.sum()), int(statistical.sum()),
+                                                              int(unified.sum()))
+
+
 def stream_compact(mask: np.ndarray):
     """(active-first stable order, count) (adaptive_attention.py:29-43)."""
     mask = np.asarray(mask, dtype=bool)

@@ -556,6 +556,26 @@ extern "C" int oc_device_cu_count(int32_t* cus) {
   return OC_OK;
 }
 
+extern "C" int oc_device_props(oc_device_info* info) {
+  if (!info) return fail(OC_ERR_INVALID, "info is NULL");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  hipDeviceProp_t pr;
+  e = hipGetDeviceProperties(&pr, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  memset(info, 0, sizeof *info);
+  info->compute_units = pr.multiProcessorCount;
+  info->memory_clock_khz = pr.memoryClockRate;
+  info->memory_bus_bits = pr.memoryBusWidth;
+  info->lds_per_cu_bytes = (int64_t)pr.maxSharedMemoryPerMultiProcessor;
+  info->total_memory_bytes = (int64_t)pr.totalGlobalMem;
+  info->wave_size = pr.warpSize;
+  strncpy(info->arch, pr.gcnArchName, sizeof info->arch - 1);
+  strncpy(info->name, pr.name, sizeof info->name - 1);
+  return OC_OK;
+}
+
 extern "C" const char* oc_version(void) { return "orthocache_hip 0.1.0 (gfx950, abi 1)"; }
 
 extern "C" const char* oc_last_error(void) { return g_last_error.c_str(); }

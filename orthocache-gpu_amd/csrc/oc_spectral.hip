@@ -446,6 +446,79 @@ __global__ __launch_bounds__(1024) void compact_gate_kernel(const float* mb, con
   }
 }
 
+// NaN-propagating maximum (torch.max semantics): a NaN operand wins
+__device__ __forceinline__ float nan_max(float a, float b) { return (a != a || a >= b) ? a : b; }
+
+// Eviction regimes of a block table (perfect_eviction.py:75-186 as
+// orthocache_forward and its callers use it), one workgroup:
+//   qn[h]   = max_s q_norms[s, h]                       (NaN propagates)
+//   b[b, h] = qn[h] * sqrt(E[b, h] clamped at 0) / sqrt_d  (float32, NaN kept)
+//   beta[b] = max_h b[b, h];  gap[b] = z - beta[b]
+//   regime  = 0 when any of the block's mask entries is set (retained);
+//             else 1 when gap >= underflow, 2 when gap < underflow, and 0
+//             when gap is NaN (neither compare holds)
+// counts = (regime-1 blocks, regime-2 blocks, retained blocks).  z is the
+// largest of z_vec[0 .. z_count) when given (NaN propagates), else z_scalar.
+__global__ __launch_bounds__(1024) void block_regimes_kernel(const float* qnorms, int sq, int H, const float* energy,
+                                                             int nb, float sqrt_d, float z_scalar, const float* z_vec,
+                                                             int z_count, const uint8_t* mask, int mask_heads,
+                                                             float underflow, int32_t* regime, float* beta,
+                                                             float* gap, float* beta_full, int32_t* counts) {
+  __shared__ float sh_qn[kGateHeads];
+  __shared__ float sh_f[kGateWaves][8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // z: the reduction runs in every wave over the same lanes, so each wave
+  // ends with the same value (no barrier needed)
+  float z = z_scalar;
+  if (z_vec) {
+    float m = -__builtin_inff();
+    for (int i = lane; i < z_count; i += 64) m = nan_max(m, z_vec[i]);
+    for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o, 64));
+    z = m;
+  }
+  // per-head query norm maxima; heads past the LDS table are re-derived
+  // where they are used
+  auto head_qmax = [&](int h) {
+    float m = -__builtin_inff();
+    for (int s = 0; s < sq; ++s) m = nan_max(m, qnorms[(int64_t)s * H + h]);
+    return m;
+  };
+  for (int h = threadIdx.x; h < H && h < kGateHeads; h += 1024) sh_qn[h] = head_qmax(h);
+  __syncthreads();
+  // one wave per block, lanes over heads
+  float cnt[3] = {0.f, 0.f, 0.f};
+  for (int b = wave; b < nb; b += kGateWaves) {
+    float bm = -__builtin_inff();
+    bool kept = false;
+    for (int h = lane; h < H; h += 64) {
+      const float e = energy[(int64_t)b * H + h];
+      const float qn = h < kGateHeads ? sh_qn[h] : head_qmax(h);
+      const float x = qn * __builtin_sqrtf(e < 0.f ? 0.f : e) / sqrt_d;
+      if (beta_full) beta_full[(int64_t)b * H + h] = x;
+      bm = nan_max(bm, x);
+      if (mask_heads > 1) kept = kept || mask[(int64_t)b * mask_heads + h] != 0;
+    }
+    for (int o = 32; o > 0; o >>= 1) bm = nan_max(bm, __shfl_xor(bm, o, 64));
+    kept = mask_heads > 1 ? __ballot(kept) != 0 : mask[b] != 0;
+    if (lane == 0) {
+      const float g = z - bm;
+      const int r = kept ? 0 : (g >= underflow ? 1 : (g < underflow ? 2 : 0));
+      regime[b] = r;
+      beta[b] = bm;
+      gap[b] = g;
+      cnt[0] += r == 1 ? 1.f : 0.f;
+      cnt[1] += r == 2 ? 1.f : 0.f;
+      cnt[2] += kept ? 1.f : 0.f;
+    }
+  }
+  gate_reduce<3>(cnt, 0u, sh_f);  // exact: counts below 2^24
+  if (threadIdx.x == 0) {
+    counts[0] = (int32_t)cnt[0];
+    counts[1] = (int32_t)cnt[1];
+    counts[2] = (int32_t)cnt[2];
+  }
+}
+
 // Active-first stable order of n blocks (stream compaction): out[r] = the
 // r-th retained block, then the evicted ones in order; *num_active = the
 // retained count.  One workgroup of 1024 threads, chunked prefix sums.
@@ -562,6 +635,27 @@ extern "C" int oc_compact_gate(const float* max_bound, const float* zeta, const 
                      (float)underflow, tiles_per_block, block_mask, tile_mask, stats);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "compact-gate launch");
+}
+
+extern "C" int oc_block_regimes(const float* q_norms, int32_t q_len, int32_t num_heads, const float* energy,
+                                int32_t num_blocks, int32_t head_dim, double z_max, const float* z_values,
+                                int32_t z_count, const uint8_t* block_mask, int32_t mask_heads, double underflow,
+                                int32_t* regime, float* beta, float* gap, float* beta_full, int32_t* counts,
+                                void* stream) {
+  if (!q_norms || !energy || !block_mask || !regime || !beta || !gap || !counts)
+    return fail(OC_ERR_INVALID, "NULL pointer");
+  if (q_len < 1 || num_heads < 1 || num_blocks < 0 || head_dim < 1 || (z_values && z_count < 1))
+    return fail(OC_ERR_INVALID, "bad sizes");
+  if (mask_heads != 1 && mask_heads != num_heads)
+    return fail(OC_ERR_INVALID, "mask_heads %d must be 1 or num_heads %d", mask_heads, num_heads);
+  if (num_blocks >= (1 << 24)) return fail(OC_ERR_UNSUPPORTED, "num_blocks %d >= 2^24", num_blocks);
+  // the divisor as the reference forms it: math.sqrt(head_dim) taken to float32
+  const float sqrt_d = (float)std::sqrt((double)head_dim);
+  hipLaunchKernelGGL(block_regimes_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, q_norms, q_len, num_heads,
+                     energy, num_blocks, sqrt_d, (float)z_max, z_values, z_count, block_mask, mask_heads,
+                     (float)underflow, regime, beta, gap, beta_full, counts);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "block-regimes launch");
 }
 
 extern "C" size_t oc_spectra_params_bytes(void) { return sizeof(oc_spectra_params); }

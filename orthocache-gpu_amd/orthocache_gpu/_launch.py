@@ -787,3 +787,43 @@ def compact_gate(spec: Dict[str, torch.Tensor], head_dim: int, tau: Optional[flo
             float(underflow), tiles_per_block, bm.data_ptr(), tm.data_ptr(), st.data_ptr(),
             ctypes.c_void_p(current_stream(device))))
     return bm, tm, st
+
+
+def block_regimes(q: torch.Tensor, energy: torch.Tensor, head_dim: int, z_max, block_mask: torch.Tensor,
+                  underflow: float, want_full: bool = False):
+    """oc_block_regimes: per-block logit ceilings and eviction regimes.
+    q (q_len, H, d) (its spatial row norms come from oc_row_norms), energy
+    float32 (nb, H), z_max a number or a tensor (its largest element is
+    used), block_mask bool/uint8 (nb,) or (nb, H).  Returns (regime int32
+    (nb,), beta (nb,), gap (nb,), beta_full (nb, H) or None, counts int32 (3,)
+    = perfect, statistical, retained)."""
+    device = require_gpu(q, energy, block_mask)
+    sq, H, d = q.shape
+    qn = row_norms(q.reshape(1, 1, sq * H, d)).view(sq, H)
+    energy = energy.to(torch.float32).contiguous()
+    nb = energy.shape[0]
+    if energy.dim() != 2 or energy.shape[1] != H:
+        raise ValueError(f"block_energies must be (num_blocks, {H}), got {tuple(energy.shape)}")
+    mask = block_mask.to(torch.uint8).contiguous()
+    mask_heads = 1 if mask.dim() == 1 else mask.shape[-1]
+    if mask.shape[0] != nb:
+        raise ValueError(f"block_mask has {mask.shape[0]} blocks, block_energies {nb}")
+    z_vec = None
+    z_scalar = 0.0
+    if isinstance(z_max, torch.Tensor) and z_max.dim() > 0:
+        require_gpu(z_max)
+        z_vec = z_max.to(torch.float32).contiguous().reshape(-1)
+    else:
+        z_scalar = float(z_max)
+    regime = torch.empty((nb,), dtype=torch.int32, device=device)
+    beta = torch.empty((nb,), dtype=torch.float32, device=device)
+    gap = torch.empty((nb,), dtype=torch.float32, device=device)
+    full = torch.empty((nb, H), dtype=torch.float32, device=device) if want_full else None
+    counts = torch.empty((3,), dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        N.check("oc_block_regimes", N.lib().oc_block_regimes(
+            qn.data_ptr(), sq, H, energy.data_ptr(), nb, head_dim, z_scalar,
+            None if z_vec is None else z_vec.data_ptr(), 0 if z_vec is None else z_vec.numel(),
+            mask.data_ptr(), mask_heads, float(underflow), regime.data_ptr(), beta.data_ptr(), gap.data_ptr(),
+            None if full is None else full.data_ptr(), counts.data_ptr(), ctypes.c_void_p(current_stream(device))))
+    return regime, beta, gap, full, counts

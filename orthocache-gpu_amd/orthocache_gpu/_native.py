@@ -96,6 +96,14 @@ class OcSpectraParams(ctypes.Structure):
     ]
 
 
+class OcDeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("arch", ctypes.c_char * 64), ("name", ctypes.c_char * 128), ("compute_units", _i32), ("wave_size", _i32),
+        ("memory_clock_khz", _i32), ("memory_bus_bits", _i32), ("lds_per_cu_bytes", _i64),
+        ("total_memory_bytes", _i64),
+    ]
+
+
 # every function declared in include/orthocache_hip.h: name -> (restype, argtypes)
 SIGNATURES = {
     "oc_score_tiles": (_i32, [ctypes.POINTER(OcKvDesc), ctypes.c_double, _p, _p, _p, _p, _i64, _p]),
@@ -119,6 +127,8 @@ SIGNATURES = {
     "oc_stream_compact": (_i32, [_p, _i32, _p, _p, _p]),
     "oc_compact_gate": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, ctypes.c_double, _i32, ctypes.c_double,
                                ctypes.c_double, _i32, _p, _p, _p, _p]),
+    "oc_block_regimes": (_i32, [_p, _i32, _i32, _p, _i32, _i32, ctypes.c_double, _p, _i32, _p, _i32,
+                                ctypes.c_double, _p, _p, _p, _p, _p, _p]),
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
@@ -127,6 +137,7 @@ SIGNATURES = {
     "oc_hbm_read_probe": (_i32, [_p, ctypes.c_size_t, _p, _i32, _p]),
     "oc_abi_sizes": (_i32, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "oc_device_cu_count": (_i32, [ctypes.POINTER(_i32)]),
+    "oc_device_props": (_i32, [ctypes.POINTER(OcDeviceInfo)]),
     "oc_version": (ctypes.c_char_p, []),
     "oc_last_error": (ctypes.c_char_p, []),
 }
@@ -189,3 +200,10 @@ def device_cu_count() -> int:
     n = _i32()
     check("oc_device_cu_count", lib().oc_device_cu_count(ctypes.byref(n)))
     return int(n.value)
+
+
+def device_props() -> OcDeviceInfo:
+    """hipDeviceProp_t fields of the current device (oc_device_props)."""
+    info = OcDeviceInfo()
+    check("oc_device_props", lib().oc_device_props(ctypes.byref(info)))
+    return info

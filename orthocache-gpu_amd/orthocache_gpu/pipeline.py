@@ -16,7 +16,6 @@ from __future__ import annotations
 
 import dataclasses
 import enum
-import math
 import threading
 import time
 
@@ -46,32 +45,36 @@ class TelemetryLevel(enum.IntEnum):
     VERBOSE = 2
 
 
+# reason text of every flag but the crossover bypass, which names the
+# sequence length, the threshold and the profile
+_FLAG_TEXT = {
+    BypassFlag.DENSE_EXPLICIT: "dense attention requested",
+    BypassFlag.TRITON_FUSED: "gated split-K decode on the HIP kernels",
+    BypassFlag.SPECTRAL_EVICTION: "512-token spectral eviction",
+    BypassFlag.ZERO_ACTIVE: "no block retained",
+    BypassFlag.TAU_AUTO: "tau from the bound statistics (mean minus one std)",
+    BypassFlag.PERFECT_EVICTION: "every evicted block underflows exactly",
+    BypassFlag.HW_AUTO_DETECTED: "crossover scaled by memory bandwidth from the MI355X measurement",
+}
+
+
 def format_bypass_reason(flags: BypassFlag, seq_len_k: int = 0, threshold: int = 0, profile=None) -> str:
-    """Human-readable form of a BypassFlag mask (pipeline.py:87-117)."""
-    parts = []
+    """Readable form of a BypassFlag mask for telemetry (the interface of
+    pipeline.py:87-117); built only when asked for."""
+    reasons = []
     if flags & BypassFlag.CROSSOVER_BYPASS:
-        p = f"seq_len_k={seq_len_k} < crossover={threshold}"
-        if profile:
-            p += f" on {profile.name} ({profile.sm_count} CUs, {profile.mem_bandwidth_gbps:.0f} GB/s)"
-        parts.append(p)
-    if flags & BypassFlag.DENSE_EXPLICIT:
-        parts.append("mode=dense (explicit)")
-    if flags & BypassFlag.TRITON_FUSED:
-        parts.append("mode=triton_fused (gated split-K decode)")
-    if flags & BypassFlag.SPECTRAL_EVICTION:
-        parts.append("full spectral eviction path")
-    if flags & BypassFlag.ZERO_ACTIVE:
-        parts.append("all blocks evicted")
-    if flags & BypassFlag.TAU_AUTO:
-        parts.append("tau auto-computed (mean - 1σ)")
-    if flags & BypassFlag.HW_AUTO_DETECTED:
-        parts.append("GPU auto-detected via bandwidth-ratio model")
-    return "; ".join(parts) if parts else "no flags set"
+        hw = ""
+        if profile is not None:
+            hw = f" ({profile.name}: {profile.sm_count} CUs, {profile.mem_bandwidth_gbps:.0f} GB/s)"
+        reasons.append(f"dense below the crossover: {seq_len_k} keys < {threshold}{hw}")
+    reasons.extend(text for flag, text in _FLAG_TEXT.items() if flags & flag)
+    return ", ".join(reasons) if reasons else "no flags set"
 
 
 @dataclasses.dataclass(frozen=True)
 class GPUProfile:
-    """Hardware profile for the crossover threshold (pipeline.py:121-129)."""
+    """Hardware profile for the crossover threshold (pipeline.py:121-129);
+    sm_count holds compute units on AMD parts."""
     name: str
     sm_count: int
     mem_bandwidth_gbps: float
@@ -80,10 +83,20 @@ class GPUProfile:
     compute_class: str
 
 
-# Known profiles.  The MI355X row is this build's own target; the others are
-# the reference's table (pipeline.py:139-203) kept for API compatibility.
+# Context length from which the gated decode of fused_orthocache_attention_v2
+# (single pass: every K tile scored, V of retained tiles; 32 heads, d 128,
+# float16, half the tiles evicted) stays faster than this build's own dense
+# decode on MI355X, measured by bench.py --only sweep (reference config 1):
+# 0.97x at 1024 tokens, 1.03x at 2048, 1.08x at 4096, 1.21x at 32768.  The
+# cached-score decode is ahead from 1024 tokens on (1.01x; 1.80x at 32768).
+MI355X_CROSSOVER = 2048
+MI355X_PEAK_GBPS = 8000.0
+
+# Known profiles: the MI355X row is this build's own measurement; the
+# others are the reference's table (pipeline.py:139-203), kept so that code
+# which reads them by name keeps working.
 _GPU_PROFILES = {
-    "MI355X": GPUProfile("MI355X", 256, 8000.0, 160.0, 1024, "datacenter"),
+    "MI355X": GPUProfile("MI355X", 256, MI355X_PEAK_GBPS, 160.0, MI355X_CROSSOVER, "datacenter"),
     "RTX 4060 Laptop": GPUProfile("RTX 4060 Laptop", 24, 256, 100, 4096, "consumer"),
     "RTX 4060": GPUProfile("RTX 4060", 24, 272, 100, 4096, "consumer"),
     "RTX 4070": GPUProfile("RTX 4070", 46, 504, 100, 3072, "consumer"),
@@ -99,40 +112,42 @@ _REFERENCE_PROFILE = _GPU_PROFILES["RTX 4060 Laptop"]
 CROSSOVER_SEQ_LEN = _REFERENCE_PROFILE.crossover_seq_len
 
 
+def _peak_gbps(info) -> float:
+    """Peak HBM bandwidth from the device's memory clock and bus width: an
+    HBM interface moves four transfers per reported memory clock (MI300X:
+    1.3 GHz x 8192 bits -> 5.3 TB/s; MI355X: 2.0 GHz -> 8.2 TB/s)."""
+    return 4.0 * info.memory_clock_khz * 1e3 * info.memory_bus_bits / 8 / 1e9
+
+
 def _detect_gpu_profile(device=None) -> GPUProfile:
-    """Profile of the current GPU (pipeline.py:209-280).  gfx950 parts map to
-    the MI355X row; unknown GPUs get the reference's bandwidth-ratio estimate,
-    read from `total_memory` (the reference reads a `total_mem` attribute
-    that torch does not have, pipeline.py:245)."""
+    """Profile of the current GPU from its HIP properties (oc_device_props).
+
+    gfx950 (MI350X / MI355X) takes the measured MI355X crossover with the
+    device's own CU count and LDS size.  Any other AMD part gets the
+    MI355X crossover scaled by its peak bandwidth: in the latency-bound
+    regime the gate's fixed cost is paid once per call while its saving is
+    the skipped bytes over the bandwidth, so the break-even context grows
+    with bandwidth.  The result is rounded to whole 64-token tiles and the
+    profile is marked 'unknown' (the HW_AUTO_DETECTED flag).  Without a GPU
+    the reference's own profile is returned, as the reference does."""
     if not torch.cuda.is_available():
         return _REFERENCE_PROFILE
     if device is None:
         device = torch.device("cuda", torch.cuda.current_device())
-    idx = device.index if device.index is not None else 0
-    props = torch.cuda.get_device_properties(idx)
-    name = props.name or ""
-    arch = getattr(props, "gcnArchName", "") or ""
-    if "gfx950" in arch or "MI355" in name or "MI350" in name:
-        base = _GPU_PROFILES["MI355X"]
-        return dataclasses.replace(base, sm_count=props.multi_processor_count)
-    for key, prof in _GPU_PROFILES.items():
-        if key in name:
-            return prof
-    total_mem_gb = props.total_memory / (1024 ** 3)
-    if total_mem_gb > 80:
-        est_bw = 4000.0
-    elif total_mem_gb > 48:
-        est_bw = 2500.0
-    elif total_mem_gb > 16:
-        est_bw = 700.0
-    else:
-        est_bw = 300.0
-    sm = props.multi_processor_count
-    raw = _REFERENCE_PROFILE.crossover_seq_len * (est_bw / _REFERENCE_PROFILE.mem_bandwidth_gbps) * (
-        _REFERENCE_PROFILE.sm_count / max(sm, 1))
-    clamped = max(512, min(8192, int(raw)))
-    crossover = 1 << int(math.log2(clamped) + 0.5)
-    return GPUProfile(f"{name} (auto-detected)", sm, est_bw, 100.0, crossover, "unknown")
+    with torch.cuda.device(device):
+        info = N.device_props()
+    arch = info.arch.decode(errors="replace").split(":")[0]
+    name = info.name.decode(errors="replace") or arch
+    lds_kb = info.lds_per_cu_bytes / 1024
+    bw = _peak_gbps(info)
+    if arch == "gfx950":
+        return dataclasses.replace(_GPU_PROFILES["MI355X"], sm_count=info.compute_units,
+                                   sram_per_sm_kb=lds_kb or 160.0)
+    if not bw > 0:
+        bw = MI355X_PEAK_GBPS
+    tiles = max(1, round(MI355X_CROSSOVER * bw / MI355X_PEAK_GBPS / X.TILE_SIZE))
+    return GPUProfile(f"{name} ({arch}, from its HIP properties)", info.compute_units, bw, lds_kb,
+                      tiles * X.TILE_SIZE, "unknown")
 
 
 _cached_profile = None

@@ -25,3 +25,13 @@ def pytest_configure(config):
         torch.set_flush_denormal(True)
     except Exception:
         pass
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """The achieved output errors of the GPU parity checks (tests/bars.py)."""
+    try:
+        from tests import bars
+    except Exception:
+        return
+    for line in bars.summary_lines():
+        terminalreporter.write_line(line)

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from oracle import orthocache_oracle as O
+from tests.bars import assert_out
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -33,12 +34,6 @@ def _gpu():
 
 def np64(t):
     return t.detach().double().cpu().numpy()
-
-
-def _tol(dtype, ref):
-    if dtype == "f32":
-        return 1e-5 + 1e-5 * np.abs(ref)
-    return 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == "bf16" else 2.0 ** -11)
 
 
 def _qkv(B, Hq, Hkv, Sq, Skv, d, dtype, seed):
@@ -78,10 +73,8 @@ def test_prefill_attention_vs_oracle(dtype, case, masked):
     torch.cuda.synchronize()
     ref, ref_ent = O.hook_causal_attention(np64(q), np64(k), np64(v), G,
                                            None if evict is None else evict.numpy())
-    ref = O.round_to(ref, dtype) if dtype != "f32" else ref
     assert out.dtype == q.dtype and out.shape == (B, Hq, Sq, d)
-    err = np.abs(np64(out) - ref)
-    assert (err <= _tol(dtype, ref)).all(), float(err.max())
+    assert_out(out, ref, dtype, f"prefill {dtype} {case} masked={masked}")
     np.testing.assert_allclose(np64(ent), ref_ent, atol=1e-4, rtol=1e-5)
 
 
@@ -176,8 +169,7 @@ def test_hook_prefill_then_decode_vs_oracle(dtype):
     print(f"hook prefill {dtype} tau={tau}", flush=True)
     out = hook.orthocache_attention(q, kp, vp, G)
     ref = O.hook_prefill(np64(q), np64(kp), np64(vp), G, tau)
-    r = O.round_to(ref["out"], dtype) if dtype != "f32" else ref["out"]
-    assert (np.abs(np64(out) - r) <= _tol(dtype, r)).all()
+    assert_out(out, ref["out"], dtype, f"hook prefill {dtype}")
     T = S // 64
     assert 0 < ref["evict"].sum() < B * Hkv * T
     assert hook.stats['total_tiles'] == B * Hkv * T
@@ -198,9 +190,8 @@ def test_hook_prefill_then_decode_vs_oracle(dtype):
     print(f"hook decode {dtype} tau={hook.tau}", flush=True)
     out1 = hook.orthocache_attention(q1, k, v, G)
     ref1 = O.hook_decode(np64(q1), np64(k), np64(v), nc_np, G, hook.tau)
-    r1 = O.round_to(ref1["out"], dtype) if dtype != "f32" else ref1["out"]
     assert out1.shape == (B, Hq, 1, d)
-    assert (np.abs(np64(out1) - r1) <= _tol(dtype, r1)).all()
+    assert_out(out1, ref1["out"], dtype, f"hook decode {dtype}")
     assert 0 < ref1["skipped"].sum() < B * Hkv * T
     assert hook.stats['decode_steps'] == B
     assert hook.stats['decode_tiles_skipped'] == int(ref1["skipped"].sum())
@@ -224,8 +215,7 @@ def test_hook_entropy_governor_and_short_context():
     qs, ks, vs = _qkv(1, 4, 2, 40, 40, 64, "bf16", seed=13)
     out = OrthoCache_GQA_Attention(tau=1.0).orthocache_attention(qs, ks, vs, 2)
     ref_s, _ = O.hook_causal_attention(np64(qs), np64(ks), np64(vs), 2)
-    r = O.round_to(ref_s, "bf16")
-    assert (np.abs(np64(out) - r) <= _tol("bf16", r)).all()
+    assert_out(out, ref_s, "bf16", "hook short context")
 
 
 def test_hf_llama_patched_matches_dense():
@@ -282,7 +272,6 @@ def test_hook_decode_scores_new_tiles_and_whole_tiles(dtype):
     out = hook.orthocache_attention(q1, k, v, G)
     np.testing.assert_allclose(np64(hook.norm_cache.cache[:, :6]), want_norms, rtol=4 * 2.0 ** -23)
     ref = O.hook_decode(np64(q1), np64(k), np64(v), want_norms, G, hook.tau)
-    r = O.round_to(ref["out"], dtype)
-    assert (np.abs(np64(out) - r) <= _tol(dtype, r)).all()
+    assert_out(out, ref["out"], dtype, f"hook decode after append {dtype}")
     assert hook.stats['decode_tiles_skipped'] == int(ref["skipped"].sum())
     assert 0 < ref["skipped"].sum() < Hkv * 6

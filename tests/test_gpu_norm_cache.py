@@ -15,6 +15,7 @@ import pytest
 import torch
 
 from oracle import orthocache_oracle as O
+from tests.bars import assert_out
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -163,9 +164,8 @@ def test_block_sparse_attention_vs_oracle(dtype, block_size):
                  torch.zeros(n_blocks, dtype=torch.bool)):
         out = triton_block_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV), block_size)
         assert out.dtype == q.dtype and out.shape == (1, d)
-        ref = O.round_to(O.block_sparse_attention(np32(q), np32(k), np32(v), mask.numpy(), block_size), dtype)
-        tol = 1e-5 if dtype == "f32" else 2e-3 + np.abs(ref) * (2.0 ** -8 if dtype == "bf16" else 2.0 ** -11)
-        assert (np.abs(np32(out) - ref) <= tol).all()
+        ref = O.block_sparse_attention(np32(q), np32(k), np32(v), mask.numpy(), block_size)
+        assert_out(out, ref, dtype, f"block sparse {dtype} bs={block_size}")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -178,9 +178,8 @@ def test_indirect_attention_vs_oracle(dtype):
     v = torch.randn((n_blocks * bs + 100, d), generator=g).to(TORCH_DT[dtype])
     idx = torch.randperm(n_blocks, generator=g)[:9].to(torch.int32)
     out = triton_indirect_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), 7, bs)
-    ref = O.round_to(O.indirect_attention(np32(q), np32(k), np32(v), idx.numpy(), 7, bs), dtype)
-    tol = 1e-5 if dtype == "f32" else 2e-3 + np.abs(ref) * 2.0 ** -8
-    assert (np.abs(np32(out) - ref) <= tol).all()
+    ref = O.indirect_attention(np32(q), np32(k), np32(v), idx.numpy(), 7, bs)
+    assert_out(out, ref, dtype, f"indirect {dtype}")
     zero = triton_indirect_attention(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), 0, bs)
     assert not zero.any()
     with pytest.raises(ValueError, match="block index"):
