@@ -484,6 +484,26 @@ size_t oc_decode_workspace_size(const oc_decode_params* p);
 int oc_decode(const oc_decode_params* p, void* stream);
 
 /*
+ * oc_decode_static -- oc_decode that allocates nothing and takes no
+ * workspace: p->workspace / workspace_bytes are ignored, and the split
+ * partials and merge counters live in a static device array of
+ * oc_decode_static_scratch_bytes() bytes (16 MiB), one per GPU, held until
+ * the process ends.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  Same results as oc_decode.
+ * A call needing more than the array (oc_decode_workspace_size(p) > the
+ * scratch bytes) fails with OC_ERR_WORKSPACE.  Every call on a GPU shares
+ * its array: calls that overlap on one GPU (other streams or threads) race
+ * and must be serialised by the caller.  The first call on a device clears
+ * the merge counters with a small kernel on `stream`; every call leaves them
+ * zero.
+ */
+int oc_decode_static(const oc_decode_params* p, void* stream);
+
+/* bytes of the static device scratch of oc_decode_static */
+size_t oc_decode_static_scratch_bytes(void);
+
+/*
  * oc_lse_merge -- out[r, :] = merge over s of (m[r,s], l[r,s], acc[r,s,:]),
  * acc/max(l, 1e-9), written in out_dtype with row stride out_row_stride.
  */

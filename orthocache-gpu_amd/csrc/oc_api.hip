@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "oc_kernels.h"
@@ -362,7 +363,9 @@ extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   return n;
 }
 
-extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
+// oc_decode with the workspace (`ws`, `ws_bytes`) given separately from p,
+// so that oc_decode_static can bring its own.
+static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, void* stream) {
   if (!p) return fail(OC_ERR_INVALID, "params is NULL");
   DecodeArgs a;
   int rc = fill_kv(&p->kv, a);
@@ -412,9 +415,9 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   const size_t need = oc_decode_workspace_size(p);
   char* w = nullptr;
   if (need) {
-    if (!p->workspace || p->workspace_bytes < need)
-      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
-    w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
+    if (!ws || ws_bytes < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    w = (char*)(((uintptr_t)ws + 255) & ~(uintptr_t)255);
   }
   if (p->out) {
     a.counters = (int32_t*)w;
@@ -450,6 +453,71 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   if (!p->out || a.fuse) return OC_OK;
   return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, a.Pg, D, p->out, p->out_dtype,
                       p->out_row_stride, st);
+}
+
+extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
+  if (!p) return fail(OC_ERR_INVALID, "params is NULL");
+  return decode_impl(p, p->workspace, p->workspace_bytes, stream);
+}
+
+// ------------------------------------------------ oc_decode_static scratch
+//
+// The split partials and merge counters of oc_decode_static live in this
+// array: one copy per GPU, held until the process ends.  Its name is only a
+// host-side stand-in in host code; the device address comes from
+// hipGetSymbolAddress, once per device, and is what every kernel gets.
+static constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// Zeroes n 32-bit words (the merge counters at set-up): a fill kernel, not
+// hipMemsetAsync, so that a caller may capture the call in a graph.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+static constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The current device's scratch address; at the first call on a device its
+// merge counters are cleared on `st` (the array starts zeroed as well; the
+// clear makes that independent of the loader), after which every call
+// leaves them zero.
+static int scratch_of_device(hipStream_t st, char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(OC_ERR_UNSUPPORTED, "device index %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress");
+    const int64_t words = (int64_t)(kCounterBytes + 256) / 4;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, (uint32_t*)ptr, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "scratch clear launch");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = (char*)g_scratch_ptr[dev];
+  return OC_OK;
+}
+
+extern "C" size_t oc_decode_static_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int oc_decode_static(const oc_decode_params* p, void* stream) {
+  if (!p) return fail(OC_ERR_INVALID, "params is NULL");
+  const size_t need = oc_decode_workspace_size(p);
+  // the workspace is aligned up to 256 bytes inside; the array already is
+  if (need > kScratchBytes)
+    return fail(OC_ERR_WORKSPACE, "oc_decode_static: %zu bytes of split partials and counters needed, the static "
+                "scratch holds %zu (use oc_decode with a workspace)", need, kScratchBytes);
+  char* ptr = nullptr;
+  if (need) {
+    const int rc = scratch_of_device((hipStream_t)stream, &ptr);
+    if (rc) return rc;
+  }
+  return decode_impl(p, ptr, need ? kScratchBytes : 0, stream);
 }
 
 extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e_high, float* zeta,

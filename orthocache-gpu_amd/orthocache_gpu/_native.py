@@ -132,6 +132,8 @@ SIGNATURES = {
     "oc_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode_num_groups": (_i32, [ctypes.POINTER(OcDecodeParams)]),
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
+    "oc_decode_static": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
+    "oc_decode_static_scratch_bytes": (ctypes.c_size_t, []),
     "oc_lse_merge": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i32, _i64, _p]),
     "oc_dequant_fp8": (_i32, [_p, _i64, ctypes.c_float, _i32, _p, _p]),
     "oc_hbm_read_probe": (_i32, [_p, ctypes.c_size_t, _p, _i32, _p]),
