@@ -279,7 +279,7 @@ int oc_kth_smallest(const float* x, int64_t rows, int64_t n, int64_t row_stride,
  * OC_GROUP_MEDIAN), group_norms[b * num_kv_heads + h] = qn (if given), and
  * for t < mask_cols
  *   evict(t) = t < num_tiles && qn * k_norms[b * k_norms_stride_b + h * k_norms_stride_h + t]
- *              <= (float)tau_norm
+ *              <= tau_norm      (product and compare in float64)
  *   mask[b * mask_stride_b + h * mask_stride_h + t] = keep_polarity ? !evict(t) : evict(t)
  * (keep_polarity 0: 1 = evict, the prefill kernel's convention; 1: 1 =
  * attend, oc_decode's OC_GATE_MASK convention).  tau_norm = tau * 64 *

@@ -730,12 +730,15 @@ def entropy_tau(tau: float, alpha: float, rates, beta: float, h_median: float, e
 
 
 def hook_tile_norms(keys: np.ndarray) -> np.ndarray:
-    """||(W64 K_t)[48:64]||_F of every complete tile of (B, Hkv, S, d) keys,
-    float32 (B, Hkv, S // 64) (perplexity_eval.py:466-470)."""
+    """||(H64 K_t)[48:64]||_F of every complete tile of (B, Hkv, S, d) keys,
+    float32 (B, Hkv, S // 64) (perplexity_eval.py:466-470).  The hook's
+    Walsh matrix is its own, unnormalised Sylvester H64 with entries +-1
+    (generate_walsh_matrix, perplexity_eval.py:54-64), 8 x W64, so these
+    norms are 8x the SpectralNormCache band norms of the same tiles."""
     B, H, S, _ = keys.shape
     T = S // TILE_SIZE
     out = np.zeros((B, H, T), dtype=F32)
-    w = walsh_matrix()
+    w = walsh_matrix() * F32(8.0)  # exact: +-1/8 -> +-1
     for b in range(B):
         for h in range(H):
             for t in range(T):

@@ -627,7 +627,7 @@ __global__ __launch_bounds__(256) void kth_smallest_kernel(const float* x, int64
 // num_tiles and 0 up to mask_cols (keep_pol: 1 = attend instead).
 __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, int Hkv, int G, int reduce,
                                                          const float* kn, int64_t kn_sb, int64_t kn_sh,
-                                                         int num_tiles, int mask_cols, float tau_norm, int keep_pol,
+                                                         int num_tiles, int mask_cols, double tau_norm, int keep_pol,
                                                          uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out,
                                                          float* stats) {
   __shared__ float s_qn;
@@ -665,7 +665,10 @@ __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, 
   bool knan = false;
   for (int t = threadIdx.x; t < mask_cols; t += 256) {
     const bool full = t < num_tiles;
-    const bool ev = full && qn * knr[t] <= tau_norm;
+    // the reference compares (qn * kn) / (64 d) <= tau in float64 with
+    // float32 norms; 64 d is a power of two, so that is qn * kn <= tau * 64 d
+    // with an exact product (two float32 factors fit a double)
+    const bool ev = full && (double)qn * (double)knr[t] <= tau_norm;
     mr[t] = (ev != (keep_pol != 0)) ? 1 : 0;
     if (full) {
       nev += ev ? 1.f : 0.f;
@@ -817,7 +820,7 @@ extern "C" int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv
   if (wgs > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many heads");
   hipLaunchKernelGGL(group_gate_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, q_norms,
                      num_kv_heads, G, reduce, k_norms, k_norms_stride_b, k_norms_stride_h, num_tiles, mask_cols,
-                     (float)tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms, gate_stats);
+                     tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms, gate_stats);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "group-gate launch");
 }

@@ -16,7 +16,8 @@ head_dim) and k, v (batch, num_kv_heads, kv_len, head_dim):
   mask), which never reads an evicted tile's K or V.
 * otherwise the prefill branch (perplexity_eval.py:399-545): per q head the
   lower median over positions of ||q||_2, the max over the group, times the
-  tile's ||(W64 K_t)[48:64]||_F over 64 * head_dim, at or below tau evicts
+  tile's ||(H64 K_t)[48:64]||_F (the unnormalised Walsh matrix of the
+  reference's evaluation code) over 64 * head_dim, at or below tau evicts
   the tile for every query of the group; causal attention over the rest
   (oc_prefill_attention), the attention entropy when the governor reads
   it, and the band norms go to the norm cache.
@@ -53,6 +54,11 @@ from . import _native as N
 TILE = 64
 _HIGH_BAND = (48, 64)  # (tile_size * 3) // 4 .. tile_size (perplexity_eval.py:441-442)
 _LOW_BAND = 8          # _compute_q_high_norm's default (perplexity_eval.py:547)
+# The hook transforms with its own unnormalised Sylvester H64, entries +-1
+# (perplexity_eval.py:54-64), which is 8 x the W64 = H64 / 8 of the band-norm
+# kernel: every ||K_high||_F the hook forms (its gate, statistics and norm
+# cache) is 8x the kernel's.  A power-of-two scale, so exact.
+_HOOK_NORM_SCALE = 8.0
 
 
 class ResidualGovernor:
@@ -204,10 +210,10 @@ class OrthoCache_GQA_Attention:
         Hkv, Skv = key.shape[1], key.shape[2]
         T = Skv // TILE
         tau = self._tau()
-        # ||(W64 K_t)[48:64]||_F of every complete tile, (B, Hkv, T)
+        # ||(H64 K_t)[48:64]||_F of every complete tile, (B, Hkv, T)
         kn = torch.empty((B * Hkv, T), dtype=torch.float32, device=key.device)
         X.band_norms(X.rows_layout(key.reshape(B * Hkv, Skv, d), None), 0, T, _HIGH_BAND, kn)
-        kn = kn.view(B, Hkv, T)
+        kn = kn.view(B, Hkv, T).mul_(_HOOK_NORM_SCALE)
         # per q head: lower median over positions of ||q||_2; the group's max
         med = X.kth_smallest(X.row_norms(query).view(B * Hq, Sq), (Sq - 1) // 2).view(B, Hq)
         evict, qn = X.group_gate(med, kn, Hkv, G, T, T, tau * TILE * d, N.OC_GROUP_MAX)
@@ -273,7 +279,7 @@ class OrthoCache_GQA_Attention:
                              f"context ({Hkv} heads x {T} tiles)")
         if self.score_new_tiles and T > self._prefill_tiles:
             # the tiles completed since the prefill, scored from this call's K
-            nc.update_tiles(key[B - 1], self._prefill_tiles, T - self._prefill_tiles)
+            nc.update_tiles(key[B - 1], self._prefill_tiles, T - self._prefill_tiles, norm_scale=_HOOK_NORM_SCALE)
         norms = nc.cache[:Hkv].unsqueeze(0)
         qh = X.row_norms(query, low_band=_LOW_BAND).view(B, Hq)
         # 1 = attend: complete tiles that pass the gate, and the partial last tile

@@ -275,3 +275,20 @@ def test_hook_decode_scores_new_tiles_and_whole_tiles(dtype):
     assert_out(out, ref["out"], dtype, f"hook decode after append {dtype}")
     assert hook.stats['decode_tiles_skipped'] == int(ref["skipped"].sum())
     assert 0 < ref["skipped"].sum() < Hkv * 6
+
+
+def test_group_gate_compares_in_float64():
+    """The hook compares (qn * kn) / (64 d) <= tau in Python floats
+    (perplexity_eval.py:480-491, :639-645): qn = kn = 1 + 2^-23 has the exact
+    product 1 + 2^-22 + 2^-46, which float32 rounds down to 1 + 2^-22.  At
+    tau_norm = 1 + 2^-22 the reference keeps the tile (a float32 compare
+    would evict it); half of it is evicted either way."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    x = float(np.float32(1 + 2.0 ** -23))
+    qn = torch.tensor([[x]], dtype=torch.float32, device=DEV)             # (batch 1, 1 kv head x G 1)
+    kn = torch.tensor([[[x, x / 2]]], dtype=torch.float32, device=DEV)    # (1, 1 kv head, 2 tiles)
+    assert (x * x) / 8192.0 > (1 + 2.0 ** -22) / 8192.0                   # the reference's compare
+    for reduce in (N.OC_GROUP_MAX, N.OC_GROUP_MEDIAN):
+        mask, _ = X.group_gate(qn, kn, 1, 1, 2, 2, 1 + 2.0 ** -22, reduce)
+        assert mask.cpu().tolist() == [[[0, 1]]]

@@ -84,8 +84,12 @@ def test_update_prefill_and_append_path():
     # with lengths, a tile not yet complete is skipped
     c.update_tiles(k, 9, 1, context_lens=torch.tensor([9 * 64 + 10, 10 * 64], device=DEV))
     assert c.get_norm(0, 9) == 0.0 and c.get_norm(1, 9) == full.get_norm(1, 9)
+    # a multiple of the Walsh matrix scales the norms (exactly for powers of
+    # two); any other matrix is refused
+    c.update_prefill(0, 0, k[0, :64], w * 2, 48, 64)
+    assert c.get_norm(0, 0) == 2 * full.get_norm(0, 0)
     with pytest.raises(NotImplementedError):
-        c.update_prefill(0, 0, k[0, :64], w * 2, 48, 64)
+        c.update_prefill(0, 0, k[0, :64], w.flip(0), 48, 64)
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp8"])

@@ -93,12 +93,15 @@ def test_hook_tile_norms_closed_form_and_no_clamp():
         for t in range(2):
             kt = keys[0, h, 64 * t:64 * t + 64].astype(np.float64)
             g = kt[0:16] - kt[16:32] - kt[32:48] + kt[48:64]
-            np.testing.assert_allclose(kn[0, h, t], np.sqrt(0.25 * np.sum(g ** 2)), rtol=2e-6)
+            # rows 48..63 of the unnormalised H64: 16 sum ||g||^2 (64x the W64 band)
+            np.testing.assert_allclose(kn[0, h, t], np.sqrt(16.0 * np.sum(g ** 2)), rtol=2e-6)
+            # exactly 8x the normalised band norm (a power-of-two scale)
+            assert kn[0, h, t] == np.float32(8.0) * O.band_norm(keys[0, h, 64 * t:64 * t + 64], 48, 64)
     # a float32 sum of squares is 0 or >= 2^-149, so its root is 0 or above
     # 3e-23: the 1e-38 clamp of SpectralNormCache never changes a float32 norm
     tiny = np.zeros((1, 1, 64, 4), np.float32)
     tiny[0, 0, 0, 0] = 1e-18
-    assert O.hook_tile_norms(tiny)[0, 0, 0] == O.band_norm(tiny[0, 0], 48, 64) > 1e-38
+    assert O.hook_tile_norms(tiny)[0, 0, 0] == 8 * O.band_norm(tiny[0, 0], 48, 64) > 1e-38
 
 
 def test_hook_prefill_gate_extremes_and_stats():
