@@ -447,6 +447,23 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   if (a.num_rows == 0) return OC_OK;
   const int gt = heads_per_group(p->G);
   const int gchunks = (p->G + gt - 1) / gt;
+  // the barrier-free prologue (decode_fast): the transposed matrix-core step
+  // on contiguous rows (q of K's 16-bit type, bf16 for fp8 K), every query
+  // head of a row in one workgroup, q rows readable as 16-byte pieces,
+  // partials internal; a score-gated cached decode whose rows have at most
+  // 64 * kFastChunks tiles (their ranks split evenly over the row's
+  // workgroups), or a dense decode over more than one split per workgroup
+  {
+    const int dt = p->kv.dtype;
+    const bool mq = (dt == OC_BF16 && p->q_dtype == OC_BF16) || (dt == OC_F16 && p->q_dtype == OC_F16) ||
+                    (dt == OC_FP8_E4M3FN && p->q_dtype == OC_BF16);
+    const bool cached_gate = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
+    const bool q16 = aligned(p->q, 16) && (a.q_row_stride % 16) == 0;
+    a.fast = (mq && !a.paged && !a.flat && gchunks == 1 && q16 && p->kv.k_scale_mode != OC_KSCALE_Q_FOLD &&
+              !partials_given && !p->split_counts &&
+              ((cached_gate && a.bal && p->kv.num_tiles <= 64 * kFastChunks) ||
+               (p->gate == OC_GATE_NONE && a.spw > 1))) ? 1 : 0;
+  }
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
   if (e != hipSuccess) return hip_fail(e, "decode launch");

@@ -34,6 +34,8 @@ struct DecWaves {
 constexpr float kM0 = -1e9f;
 constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
 constexpr int kKeepLds = kMaxBalTiles / 8;  // keep flags staged in LDS (bytes of the bitmask array)
+constexpr int kFastChunks = 32;  // decode_fast: at most 64 * kFastChunks tiles per row
+constexpr int kFastBatch = 16;   // decode_fast: 64-tile chunks whose scores are in flight at once
 
 // Kernel arguments (byte strides).  Built by oc_api.hip from oc_decode_params.
 struct DecodeArgs {
@@ -87,6 +89,8 @@ struct DecodeArgs {
   // (flat_map) and its partials live at slots [first slot of r, + q_r)
   int32_t flat;
   int32_t flat_target;  // workgroups the flat layout aims at (slots = flat_target + num_rows)
+  // the barrier-free prologue of decode_fast (set by the host when it applies)
+  int32_t fast;
   int32_t* counters;
   char* out;
   int64_t out_stride;  // bytes between query-head rows of out
@@ -1135,6 +1139,9 @@ __device__ __forceinline__ void tile_energies_mfma(const uint32_t (&kb)[4][D / 3
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding (gfx9 encoding; export and LDS counts left at their maxima)
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+// s_waitcnt immediate: outstanding LDS / scalar-memory operations done, vector
+// memory operations left in flight
+constexpr int kLgkmOnly = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 
 // p.V on the matrix cores: D[head][d] += sum_token P[head][token] V[token][d]
 // per 32-token block and 16-column chunk.  A = P of head (lane & 15), tokens
@@ -1816,6 +1823,233 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   if (lane == 0) sh_cnt[wave] = kept;
 }
 
+// The attend-every-tile transposed step on contiguous rows with a
+// barrier-free prologue (a.fast): cached decode with a score gate (at most
+// 64 * kFastChunks tiles per row) or dense decode, q of the matrix-core type,
+// all G <= GT query heads of a row in one workgroup.  Every wave forms by
+// itself, from global memory: the matrix-core q operand, the row's q norms,
+// the row's retained-tile bitmask (lane c holds the bits of tiles 64c ..
+// 64c + 63, with their inclusive prefix counts over the lanes), the
+// workgroup's even share [r0, r1) of the row's retained tiles (dense: of its
+// tiles) and its first rank r0 + wave.  It issues that tile's K and V loads
+// before the workgroup's one barrier, which publishes the LDS counter the
+// later ranks are drawn from (a wave whose tiles arrived sooner takes more).
+// The wave's state goes to LDS as decode_body leaves it.
+template <int DT, int D, int GT>
+__device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg,
+                                            float (*sh_m)[GT], float (*sh_l)[GT], int* sh_cnt, uint16_t* sh_v) {
+  constexpr int kDW = DecWaves<DT, D>::value;
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
+  constexpr int QT = MfmaT<DT>::value;  // q's 16-bit type
+  static_assert(GT <= 16, "one q head per 16-lane group of the operand");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int x = lane & 15, kg = lane >> 4;
+  const bool cached = a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE;
+  const int T = ri.n_tiles;
+
+  // q operand (B of S^T = K.q^T): lane 16 kg + x holds q[head x] columns
+  // 32 dc + 8 kg .. + 8 (fp8 K: kg D / 4 + 8 dc ..), zero past G; one 16-byte
+  // load per instruction column block, straight from q
+  uint32_t aq[D / 32][4];
+  auto load_q = [&]() {
+    const char* qh = a.q + ((int64_t)row * a.G + x) * a.q_row_stride;
+#pragma unroll
+    for (int dc = 0; dc < D / 32; ++dc) {
+      const int e0 = F8 ? kg * (D / 4) + 8 * dc : 32 * dc + 8 * kg;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (x < a.G) v = *reinterpret_cast<const uint4*>(qh + 2 * e0);
+      aq[dc][0] = v.x;
+      aq[dc][1] = v.y;
+      aq[dc][2] = v.z;
+      aq[dc][3] = v.w;
+    }
+  };
+
+  // cached: the row's keep flags, lane c holding the bits of chunk c.  One
+  // copy of the pass per gate, with the gate's tests compiled in.  The first
+  // kFastBatch chunks' scores are requested before q, so that their latency
+  // overlaps q's; indices are clamped into the row and masked after.
+  const int nch = (T + 63) >> 6;
+  uint32_t wlo = 0u, whi = 0u;
+  auto score_pass = [&](auto gate_tag) {
+    constexpr int GATE = decltype(gate_tag)::value;
+    const int64_t so = (int64_t)row * a.sc_stride;
+    float el[kFastBatch], eh[kFastBatch];
+    auto load_scores = [&](int c0) {
+#pragma unroll
+      for (int k = 0; k < kFastBatch; ++k) {
+        const int t = min((c0 + k) * 64 + lane, T - 1);
+        el[k] = 0.f;
+        if constexpr (GATE == OC_GATE_MASK) {
+          eh[k] = a.tmask[(int64_t)row * a.tmask_stride + t] ? 1.f : 0.f;
+        } else {
+          eh[k] = a.sc_eh[so + t];
+          if constexpr (GATE == OC_GATE_ZETA) el[k] = a.sc_el[so + t];
+        }
+      }
+    };
+    load_scores(0);
+    load_q();
+    // max over the row's G heads of ||q_g||_2 (CS gate; norms below 1e-38
+    // count as 0): head x's squares summed over its four lane groups
+    float qmax = 0.f;
+    bool qnan = false;
+    if constexpr (GATE == OC_GATE_CS) {
+      float ss = 0.f;
+#pragma unroll
+      for (int dc = 0; dc < D / 32; ++dc)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float lo, hi;
+          unpack16x2<QT>(aq[dc][w], lo, hi);
+          ss = __builtin_fmaf(lo, lo, __builtin_fmaf(hi, hi, ss));
+        }
+      ss += xpair<16>(ss);
+      ss += xpair<32>(ss);
+      float qn = __builtin_sqrtf(ss);
+      if ((double)qn < 1e-38) qn = 0.f;
+      const bool head = x < a.G;
+      qnan = __ballot(head && __builtin_isnan(qn)) != 0;
+      float qv = head && !__builtin_isnan(qn) ? qn : 0.f;
+      qv = fmaxf(qv, xpair<8>(qv));
+      qv = fmaxf(qv, xpair<4>(qv));
+      qv = fmaxf(qv, xpair<2>(qv));
+      qv = fmaxf(qv, xpair<1>(qv));
+      qmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(qv)));
+    }
+    const bool keep_wr = a.keep_out && gidx == 0;
+    for (int c0 = 0; c0 < nch; c0 += kFastBatch) {
+      if (c0 > 0) load_scores(c0);
+#pragma unroll
+      for (int k = 0; k < kFastBatch; ++k) {
+        const int c = c0 + k;
+        if (c < nch) {
+          const int t = c * 64 + lane;
+          // cached_keep with the gate fixed: a partial last tile is kept
+          // (score gates), the mask byte decides (mask gate)
+          bool keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
+          if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
+          keep = keep && t < T;
+          const uint64_t m = __ballot(keep);
+          if (lane == c) {
+            wlo = (uint32_t)m;
+            whi = (uint32_t)(m >> 32);
+          }
+          // the keep flags, by the row's first workgroup (chunk c by wave c mod waves)
+          if (keep_wr && (c % kDW) == wave && t < T) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+        }
+      }
+    }
+  };
+  if (!cached) load_q();
+  else if (a.gate == OC_GATE_CS) score_pass(std::integral_constant<int, OC_GATE_CS>{});
+  else if (a.gate == OC_GATE_ZETA) score_pass(std::integral_constant<int, OC_GATE_ZETA>{});
+  else score_pass(std::integral_constant<int, OC_GATE_MASK>{});
+  const int cnt = __popc(wlo) + __popc(whi);
+  const int pre = wave_incl_scan(cnt);
+  const int total = cached ? __builtin_amdgcn_readlane(pre, 63) : T;
+  const int r0 = (int)((int64_t)total * gidx / npg);
+  const int r1 = (int)((int64_t)total * (gidx + 1) / npg);
+  // the tile of retained rank rb (cached) or tile rb (dense); wave-uniform
+  auto tile_of_rank = [&](int rb) -> int {
+    if (!cached) return rb;
+    const int lg = __popcll((unsigned long long)__ballot(pre <= rb));  // chunk holding rank rb
+    const int base = __builtin_amdgcn_readlane(pre, lg) - __builtin_amdgcn_readlane(cnt, lg);
+    const uint64_t bits = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)whi, lg) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)wlo, lg);
+    const int k = rb - base;
+    const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+    const bool hit = ((bits >> lane) & 1ull) && below == k;
+    return __builtin_amdgcn_readfirstlane(lg * 64 + __ffsll((unsigned long long)__ballot(hit)) - 1);
+  };
+  // A wave's step covers NT consecutive ranks.  NT = 2 for fp8 (two tiles
+  // fill the register and LDS footprint of one 16-bit tile) measured slower
+  // on 32 rows of 2048 fp8 tiles (110.6 us cached, 174.9 dense, against
+  // 104.0 and 166.6), so every type takes one tile per step.
+  constexpr int NT = 1;
+  // a tile's per-tile K and V scales (fp8) are requested before its K and V,
+  // so the wait for K covers them; without per-tile scales a valid word (q)
+  // is read and 1 selected, keeping the loads unconditional
+  const bool ks_tile = a.k_scale_mode == OC_KSCALE_TILE, vs_tile = a.v_scale_mode == OC_VSCALE_TILE;
+  const float* qword = reinterpret_cast<const float*>(a.q);
+  float ks_raw[NT], vs_raw[NT];
+  uint32_t kb[NT][4][D / 32][4];
+  int tt[NT];
+  uint16_t* sv = sh_v + wave * 64 * D;  // this wave's V slot: NT tiles of 64 * D elements
+  auto slot = [&](int i) { return sv + i * (64 * D * Elem<DT>::size / 2); };
+  // the tiles of ranks rb .. rb + NT - 1 (-1 past r1), their loads issued
+  auto fetch = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      tt[i] = rb + i < r1 ? tile_of_rank(rb + i) : -1;
+      if (tt[i] >= 0) {
+        ks_raw[i] = *(ks_tile ? a.k_scales + (int64_t)row * a.ks_stride + tt[i] : qword);
+        vs_raw[i] = *(vs_tile ? a.v_scales + (int64_t)row * a.vs_stride + tt[i] : qword);
+        load_k_mfma_t<DT, D>(a, ri, row, tt[i], lane, kb[i]);
+        load_v_lds<DT, D, false>(a, ri, row, tt[i], lane, slot(i), TilePages{});
+      }
+    }
+  };
+  MStateT mst{kM0, 0.f};
+  f32x4 accp[D / 16];
+#pragma unroll
+  for (int nc = 0; nc < D / 16; ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int kept = 0;
+  fetch(r0 + NT * wave);
+  // publish the LDS rank counter with a bare barrier after the counter's
+  // store has completed, so that the first tiles' K and V loads stay in
+  // flight across it (a fenced barrier, even an LDS-only one, waits for them:
+  // V is loaded straight into LDS).  The signal fences keep the compiler from
+  // moving LDS accesses across the barrier.
+  if (threadIdx.x == 0) sh_cnt[kDW] = NT * kDW;
+  __builtin_amdgcn_s_waitcnt(kLgkmOnly);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  while (tt[0] >= 0) {
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      if (tt[i] < 0) break;
+      const int valid = min(64, ri.n_tok - tt[i] * 64);
+      f32x4 c[4];
+      tile_logits_t<DT, D>(aq, kb[i], c);
+      tile_softmax_t<D>(mst, accp, c, a.scale * (ks_tile ? ks_raw[i] : 1.f), vs_tile ? vs_raw[i] : 1.f, valid, lane);
+      // the step's V tiles (direct-to-LDS loads, issued after K) have landed
+      if (i == 0) __builtin_amdgcn_s_waitcnt(0);
+      tile_pv_t<DT, D>(accp, c, slot(i), lane);
+      ++kept;
+    }
+    int xr = 0;
+    if (lane == 0) xr = atomicAdd(&sh_cnt[kDW], NT);
+    fetch(r0 + __builtin_amdgcn_readfirstlane(xr));
+  }
+
+  // wave -> LDS in decode_body's layout: head x's state in lanes x, x + 16,
+  // x + 32, x + 48; its output columns 16 nc + 4 r + i in lane 16 r + x,
+  // register i, to the wave's (now idle) V slot
+  float lsum = mst.l + xpair<16>(mst.l);
+  lsum += xpair<32>(lsum);
+  float* ao = reinterpret_cast<float*>(sv);
+  if (x < GT) {
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ao[x * D + 16 * nc + 4 * kg + i] = accp[nc][i];
+  }
+#pragma unroll
+  for (int g = 0; g < GT; ++g) {
+    float mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mst.m), g));
+    if (mg != kM0) mg *= 0.6931471805599453f;
+    const float lt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsum), g));
+    if (lane == 0) {
+      sh_m[wave][g] = mg;
+      sh_l[wave][g] = lt;
+    }
+  }
+  if (lane == 0) sh_cnt[wave] = kept;
+}
+
 // Fused split merge.  Every workgroup waits until its partial stores (agent
 // scope, written through to memory) are complete and takes a ticket on its
 // (row, chunk) counter; the workgroup that takes the last ticket resets the
@@ -2001,195 +2235,204 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_p[MQK ? kDW * 64 * (GT > 4 ? 8 : 4) : 1];  // per wave p[head][token] of the current tile (MQK)
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
-  // cached mode: fetch the scores before anything else (balanced: tiles
-  // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
-  // entry of the first chunk of the split list)
-  constexpr int kPreChunks = 4;
-  float pre_el[kPreChunks], pre_eh[kPreChunks];
-#pragma unroll
-  for (int k = 0; k < kPreChunks; ++k) pre_el[k] = pre_eh[k] = 0.f;
-  if (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) {
-#pragma unroll
-    for (int k = 0; k < kPreChunks; ++k) {
-      int t;
-      bool in;
-      if (a.bal) {
-        t = k * kDT + threadIdx.x;
-        in = t < ri.n_tiles;
-      } else {
-        t = tl.s + (lane / tl.w) * tl.P + lane % tl.w;
-        in = k == 0 && lane < tl.n && t < ri.n_tiles;
-      }
-      if (in) cached_scores(a, row, t, pre_el[k], pre_eh[k]);
+  bool fast_done = false;
+  if constexpr (MQK && LOOP && !PAGED) {
+    if (a.fast) {
+      decode_fast<DT, D, GT>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
+      fast_done = true;
     }
   }
+  if (!fast_done) {
+    // cached mode: fetch the scores before anything else (balanced: tiles
+    // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
+    // entry of the first chunk of the split list)
+    constexpr int kPreChunks = 4;
+    float pre_el[kPreChunks], pre_eh[kPreChunks];
+  #pragma unroll
+    for (int k = 0; k < kPreChunks; ++k) pre_el[k] = pre_eh[k] = 0.f;
+    if (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) {
+  #pragma unroll
+      for (int k = 0; k < kPreChunks; ++k) {
+        int t;
+        bool in;
+        if (a.bal) {
+          t = k * kDT + threadIdx.x;
+          in = t < ri.n_tiles;
+        } else {
+          t = tl.s + (lane / tl.w) * tl.P + lane % tl.w;
+          in = k == 0 && lane < tl.n && t < ri.n_tiles;
+        }
+        if (in) cached_scores(a, row, t, pre_el[k], pre_eh[k]);
+      }
+    }
 
-  // stage q of this chunk in LDS (float and packed 16-bit); q := round(q *
-  // k_scale) in q's dtype for the Q_FOLD mode (fused_eviction.py:619-621)
-  const int qes = a.q_dtype == OC_F32 ? 4 : 2;
-  float qss = 0.f;  // x0^2 + x1^2 of this thread's pair (head norms below)
-  for (int idx = threadIdx.x; idx < GT * D / 2; idx += kDT) {
-    const int e0 = 2 * idx;
-    const int g = e0 / D;
-    const int c = e0 - g * D;
-    float x0 = 0.f, x1 = 0.f;
-    if (g < g_active) {
-      const char* qp = a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride + (int64_t)c * qes;
-      x0 = load_scalar(qp, a.q_dtype);
-      x1 = load_scalar(qp + qes, a.q_dtype);
-      if (a.k_scale_mode == OC_KSCALE_Q_FOLD) {
-        x0 = round_to(x0 * a.k_scale, a.q_dtype);
-        x1 = round_to(x1 * a.k_scale, a.q_dtype);
-      }
-    }
-    sh_qf[e0] = x0;
-    sh_qf[e0 + 1] = x1;
-    qss = __builtin_fmaf(x1, x1, x0 * x0);
-    if constexpr (DOT2) {
-      // x0, x1 are exact in the 16-bit q dtype, so the narrowing is exact
-      uint32_t lo, hi;
-      if (MfmaT<DT>::value == OC_BF16) {
-        lo = __float_as_uint(x0) >> 16;
-        hi = __float_as_uint(x1) >> 16;
-      } else {
-        lo = __builtin_bit_cast(uint16_t, (_Float16)x0);
-        hi = __builtin_bit_cast(uint16_t, (_Float16)x1);
-      }
-      sh_qp[idx] = lo | (hi << 16);
-    }
-  }
-  // max_g ||q_g|| over all G query heads of the row (CS gate).  When all G
-  // heads are in this workgroup (and GT * D / 2 <= threads), the D / 2
-  // threads of a head (one wave at D = 128, half a wave at D = 64) add their
-  // pairs' squares right away; otherwise wave w forms the norms of heads w,
-  // w + 8, ... from LDS and global memory after the barrier.  The wave
-  // maxima are combined after the next barrier.
-  __shared__ float sh_qn[kDW];
-  __shared__ int sh_qnan[kDW];
-  if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
-  const bool fast_norms = a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
-  if (fast_norms) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float ss;
-    if constexpr (D == 128) {
-      ss = wave_sum(qss);
-    } else {
-      float lo, hi;
-      row_pair<16>(row16_sum(qss), lo, hi);
-      ss = lo + hi;  // the 32-lane half of this lane
-    }
-    float qn = __builtin_sqrtf(ss);
-    if ((double)qn < 1e-38) qn = 0.f;
-    const int hpw = 128 / D;  // heads per wave
-    float wmax = 0.f;
-    bool wnan = false;
-#pragma unroll
-    for (int h = 0; h < 128 / D; ++h) {
-      const int g = wave * hpw + h;
-      const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qn), h * (64 / hpw)));
-      if (g < a.G) {
-        if (__builtin_isnan(x)) wnan = true;
-        wmax = fmaxf(wmax, x);
-      }
-    }
-    if (lane == 0) {
-      sh_qn[wave] = wmax;
-      sh_qnan[wave] = wnan ? 1 : 0;
-    }
-  }
-  __syncthreads();
-  float qmax = 0.f;
-  bool qnan = false;
-  if (a.gate == OC_GATE_CS && !fast_norms) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float wmax = 0.f;
-    bool wnan = false;
-    for (int g = wave; g < a.G; g += kDW) {
-      float ss = 0.f;
-      if (lane < 16) {
-        const int gl = g - g0;
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-          const int col = (lane & 15) * (D / 16) + c;
-          float x;
-          if (gl >= 0 && gl < GT) {
-            x = sh_qf[gl * D + col];
-          } else {
-            x = load_scalar(a.q + (int64_t)(row * a.G + g) * a.q_row_stride + (int64_t)col * qes, a.q_dtype);
-            if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * a.k_scale, a.q_dtype);
-          }
-          ss = __builtin_fmaf(x, x, ss);
+    // stage q of this chunk in LDS (float and packed 16-bit); q := round(q *
+    // k_scale) in q's dtype for the Q_FOLD mode (fused_eviction.py:619-621)
+    const int qes = a.q_dtype == OC_F32 ? 4 : 2;
+    float qss = 0.f;  // x0^2 + x1^2 of this thread's pair (head norms below)
+    for (int idx = threadIdx.x; idx < GT * D / 2; idx += kDT) {
+      const int e0 = 2 * idx;
+      const int g = e0 / D;
+      const int c = e0 - g * D;
+      float x0 = 0.f, x1 = 0.f;
+      if (g < g_active) {
+        const char* qp = a.q + (int64_t)(row * a.G + g0 + g) * a.q_row_stride + (int64_t)c * qes;
+        x0 = load_scalar(qp, a.q_dtype);
+        x1 = load_scalar(qp + qes, a.q_dtype);
+        if (a.k_scale_mode == OC_KSCALE_Q_FOLD) {
+          x0 = round_to(x0 * a.k_scale, a.q_dtype);
+          x1 = round_to(x1 * a.k_scale, a.q_dtype);
         }
       }
-      float qn = __builtin_sqrtf(wave_sum(ss));
-      if ((double)qn < 1e-38) qn = 0.f;
-      if (__builtin_isnan(qn)) wnan = true;
-      wmax = fmaxf(wmax, qn);
+      sh_qf[e0] = x0;
+      sh_qf[e0 + 1] = x1;
+      qss = __builtin_fmaf(x1, x1, x0 * x0);
+      if constexpr (DOT2) {
+        // x0, x1 are exact in the 16-bit q dtype, so the narrowing is exact
+        uint32_t lo, hi;
+        if (MfmaT<DT>::value == OC_BF16) {
+          lo = __float_as_uint(x0) >> 16;
+          hi = __float_as_uint(x1) >> 16;
+        } else {
+          lo = __builtin_bit_cast(uint16_t, (_Float16)x0);
+          hi = __builtin_bit_cast(uint16_t, (_Float16)x1);
+        }
+        sh_qp[idx] = lo | (hi << 16);
+      }
     }
-    if (lane == 0) {
-      sh_qn[wave] = wmax;
-      sh_qnan[wave] = wnan ? 1 : 0;
+    // max_g ||q_g|| over all G query heads of the row (CS gate).  When all G
+    // heads are in this workgroup (and GT * D / 2 <= threads), the D / 2
+    // threads of a head (one wave at D = 128, half a wave at D = 64) add their
+    // pairs' squares right away; otherwise wave w forms the norms of heads w,
+    // w + 8, ... from LDS and global memory after the barrier.  The wave
+    // maxima are combined after the next barrier.
+    __shared__ float sh_qn[kDW];
+    __shared__ int sh_qnan[kDW];
+    if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
+    const bool fast_norms = a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
+    if (fast_norms) {
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      float ss;
+      if constexpr (D == 128) {
+        ss = wave_sum(qss);
+      } else {
+        float lo, hi;
+        row_pair<16>(row16_sum(qss), lo, hi);
+        ss = lo + hi;  // the 32-lane half of this lane
+      }
+      float qn = __builtin_sqrtf(ss);
+      if ((double)qn < 1e-38) qn = 0.f;
+      const int hpw = 128 / D;  // heads per wave
+      float wmax = 0.f;
+      bool wnan = false;
+  #pragma unroll
+      for (int h = 0; h < 128 / D; ++h) {
+        const int g = wave * hpw + h;
+        const float x = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qn), h * (64 / hpw)));
+        if (g < a.G) {
+          if (__builtin_isnan(x)) wnan = true;
+          wmax = fmaxf(wmax, x);
+        }
+      }
+      if (lane == 0) {
+        sh_qn[wave] = wmax;
+        sh_qnan[wave] = wnan ? 1 : 0;
+      }
     }
     __syncthreads();
-  }
-  if (a.gate == OC_GATE_CS) {
-#pragma unroll
-    for (int w = 0; w < kDW; ++w) {
-      qmax = fmaxf(qmax, sh_qn[w]);
-      qnan = qnan || sh_qnan[w] != 0;
+    float qmax = 0.f;
+    bool qnan = false;
+    if (a.gate == OC_GATE_CS && !fast_norms) {
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      float wmax = 0.f;
+      bool wnan = false;
+      for (int g = wave; g < a.G; g += kDW) {
+        float ss = 0.f;
+        if (lane < 16) {
+          const int gl = g - g0;
+  #pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+            const int col = (lane & 15) * (D / 16) + c;
+            float x;
+            if (gl >= 0 && gl < GT) {
+              x = sh_qf[gl * D + col];
+            } else {
+              x = load_scalar(a.q + (int64_t)(row * a.G + g) * a.q_row_stride + (int64_t)col * qes, a.q_dtype);
+              if (a.k_scale_mode == OC_KSCALE_Q_FOLD) x = round_to(x * a.k_scale, a.q_dtype);
+            }
+            ss = __builtin_fmaf(x, x, ss);
+          }
+        }
+        float qn = __builtin_sqrtf(wave_sum(ss));
+        if ((double)qn < 1e-38) qn = 0.f;
+        if (__builtin_isnan(qn)) wnan = true;
+        wmax = fmaxf(wmax, qn);
+      }
+      if (lane == 0) {
+        sh_qn[wave] = wmax;
+        sh_qnan[wave] = wnan ? 1 : 0;
+      }
+      __syncthreads();
     }
-  }
+    if (a.gate == OC_GATE_CS) {
+  #pragma unroll
+      for (int w = 0; w < kDW; ++w) {
+        qmax = fmaxf(qmax, sh_qn[w]);
+        qnan = qnan || sh_qnan[w] != 0;
+      }
+    }
 
-  // balanced cached decode: retained-tile bitmask of the whole row and its
-  // prefix counts, then this workgroup's even share [r0, r1) of the ranks
-  int r0 = 0, r1 = 0, wpre = 0;
-  if (a.bal) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nw = (ri.n_tiles + 63) / 64;
-#pragma unroll
-    for (int c = 0; c < kPreChunks * kDT; c += kDT) {
-      if (c < ri.n_tiles) {
+    // balanced cached decode: retained-tile bitmask of the whole row and its
+    // prefix counts, then this workgroup's even share [r0, r1) of the ranks
+    int r0 = 0, r1 = 0, wpre = 0;
+    if (a.bal) {
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      const int nw = (ri.n_tiles + 63) / 64;
+  #pragma unroll
+      for (int c = 0; c < kPreChunks * kDT; c += kDT) {
+        if (c < ri.n_tiles) {
+          const int t = c + threadIdx.x;
+          const bool keep = t < ri.n_tiles && cached_keep(a, ri, t, pre_el[c / kDT], pre_eh[c / kDT], qmax, qnan);
+          if (a.keep_out && t < ri.n_tiles && gidx == 0 && blockIdx.z == 0)
+            a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+          const uint64_t m = __ballot(keep);
+          const int wi = (c >> 6) + wave;
+          if (lane == 0 && wi < nw) sh_bits[wi] = m;
+        }
+      }
+      for (int c = kPreChunks * kDT; c < ri.n_tiles; c += kDT) {
         const int t = c + threadIdx.x;
-        const bool keep = t < ri.n_tiles && cached_keep(a, ri, t, pre_el[c / kDT], pre_eh[c / kDT], qmax, qnan);
-        if (a.keep_out && t < ri.n_tiles && gidx == 0 && blockIdx.z == 0)
+        const bool in = t < ri.n_tiles;
+        float el = 0.f, eh = 0.f;
+        if (in) cached_scores(a, row, t, el, eh);
+        const bool keep = in && cached_keep(a, ri, t, el, eh, qmax, qnan);
+        if (a.keep_out && in && gidx == 0 && blockIdx.z == 0)
           a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
         const uint64_t m = __ballot(keep);
         const int wi = (c >> 6) + wave;
         if (lane == 0 && wi < nw) sh_bits[wi] = m;
       }
+      // words nw .. (nw rounded up to 4) read as empty in the lookups below
+      if (threadIdx.x < 4 && nw + (int)threadIdx.x < ((nw + 3) & ~3)) sh_bits[nw + threadIdx.x] = 0;
+      __syncthreads();
+      // every wave: lane l counts the retained tiles of bitmask words
+      // 4l .. 4l+3; wpre = inclusive prefix of those counts over the lanes
+      int x = 0;
+  #pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int wi = 4 * lane + k;
+        x += wi < nw ? __popcll((unsigned long long)sh_bits[wi]) : 0;
+      }
+      wpre = wave_incl_scan(x);
+      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(wpre, 63);
+      r0 = (int)((uint64_t)total * gidx / (uint32_t)npg);
+      r1 = (int)((uint64_t)total * (gidx + 1) / (uint32_t)npg);
     }
-    for (int c = kPreChunks * kDT; c < ri.n_tiles; c += kDT) {
-      const int t = c + threadIdx.x;
-      const bool in = t < ri.n_tiles;
-      float el = 0.f, eh = 0.f;
-      if (in) cached_scores(a, row, t, el, eh);
-      const bool keep = in && cached_keep(a, ri, t, el, eh, qmax, qnan);
-      if (a.keep_out && in && gidx == 0 && blockIdx.z == 0)
-        a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
-      const uint64_t m = __ballot(keep);
-      const int wi = (c >> 6) + wave;
-      if (lane == 0 && wi < nw) sh_bits[wi] = m;
-    }
-    // words nw .. (nw rounded up to 4) read as empty in the lookups below
-    if (threadIdx.x < 4 && nw + (int)threadIdx.x < ((nw + 3) & ~3)) sh_bits[nw + threadIdx.x] = 0;
-    __syncthreads();
-    // every wave: lane l counts the retained tiles of bitmask words
-    // 4l .. 4l+3; wpre = inclusive prefix of those counts over the lanes
-    int x = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int wi = 4 * lane + k;
-      x += wi < nw ? __popcll((unsigned long long)sh_bits[wi]) : 0;
-    }
-    wpre = wave_incl_scan(x);
-    const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(wpre, 63);
-    r0 = (int)((uint64_t)total * gidx / (uint32_t)npg);
-    r1 = (int)((uint64_t)total * (gidx + 1) / (uint32_t)npg);
-  }
 
-  decode_body<DT, D, GT, DOT2, PAGED, MQK, LOOP>(a, ri, row, tl, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
-                                           pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v,
-                                           reinterpret_cast<uint8_t*>(sh_bits));
+    decode_body<DT, D, GT, DOT2, PAGED, MQK, LOOP>(a, ri, row, tl, g0, qmax, qnan, sh_qf, sh_qp, sh_m, sh_l, sh_acc, sh_cnt,
+                                             pre_el[0], pre_eh[0], sh_bits, wpre, r0, r1, sh_p, sh_v,
+                                             reinterpret_cast<uint8_t*>(sh_bits));
+  }
   __syncthreads();
   // matrix-core single pass: the keep flags staged in LDS in list order
   if (MQK && !LOOP && a.keep_out && blockIdx.z == 0) {
