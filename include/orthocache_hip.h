@@ -149,7 +149,9 @@ typedef struct oc_kv_desc {
   const float* k_scales;    /* (num_rows, >= num_tiles) for OC_KSCALE_TILE */
   int64_t k_scales_row_stride;
   int32_t v_scale_mode;     /* OC_VSCALE_* */
-  int32_t reserved0;
+  int32_t num_tokens;       /* lengths == NULL: tokens of every row, 1 .. num_tiles * 64
+                               (0 = num_tiles * 64); a partial last tile without a
+                               lengths array */
   const float* v_scales;
   int64_t v_scales_row_stride;
   int32_t* error_flag;      /* optional int32 set non-zero on a bad block id */
@@ -502,6 +504,53 @@ int oc_decode_static(const oc_decode_params* p, void* stream);
 
 /* bytes of the static device scratch of oc_decode_static */
 size_t oc_decode_static_scratch_bytes(void);
+
+/*
+ * oc_hook_decode -- the model hook's decode step (q_len 1, norm cache
+ * populated) in one call: for every batch element b and kv head h, the
+ * Walsh-subspace high norms of the group's G query rows (as oc_row_norms
+ * with low_band), their median qn (rank G/2), the gate
+ *   evict(t) = qn * k_norms[h * k_norms_stride + t] <= tau_norm   (float64)
+ * over the complete tiles t < kv_len / 64 (a partial last tile is always
+ * attended), then attention of the G heads over the retained tiles
+ * (oc_decode with OC_GATE_MASK, cached mode) written to out in `dtype`.
+ * Two launches (gate, decode).  Replaces the per-batch loop of the
+ * reference's decode branch (perplexity_eval.py:580-662): its per-head
+ * _compute_q_high_norm (:547-573), the median, the norm-cache lookups and
+ * compares, the -inf logit masking and the float32 softmax(q K^T) V.
+ * tau_norm = tau * 64 * head_dim.  k_norms (cached ||(H64 K_t)[48:64]||_F,
+ * float32, (num_kv_heads, >= kv_len / 64) with row stride k_norms_stride)
+ * is shared by the batch, as the reference's norm cache.  gate_stats
+ * (optional, float32 (batch * num_kv_heads, 3)) as oc_group_gate's.
+ * The workspace (oc_hook_decode_workspace_size bytes) must be zero before
+ * its first use and is left so; calls on one stream may share it.
+ */
+typedef struct oc_hook_decode_params {
+  const void* q;                 /* (batch * num_kv_heads * G, head_dim), row stride q_row_stride */
+  int64_t q_row_stride;          /* elements */
+  const void* k;                 /* rows (batch * num_kv_heads) of kv_len tokens */
+  const void* v;
+  int64_t k_row_stride, k_token_stride;  /* elements; head_dim contiguous */
+  int64_t v_row_stride, v_token_stride;
+  int32_t dtype;                 /* of q, K, V and out: OC_F32 / OC_F16 / OC_BF16 */
+  int32_t batch, num_kv_heads, G, head_dim, kv_len;
+  const float* k_norms;
+  int64_t k_norms_stride;        /* elements between kv heads */
+  double tau_norm;
+  int32_t low_band;              /* Walsh bands of q (the hook's 8) */
+  int32_t num_splits;            /* 0: min(#CU, max(1, T / 4), T) over T = ceil(kv_len / 64) tiles */
+  void* out;                     /* (batch * num_kv_heads * G, head_dim), row stride out_row_stride */
+  int64_t out_row_stride;
+  float* gate_stats;
+  void* workspace;
+  size_t workspace_bytes;
+} oc_hook_decode_params;
+
+size_t oc_hook_decode_workspace_size(const oc_hook_decode_params* p);
+int oc_hook_decode(const oc_hook_decode_params* p, void* stream);
+
+/* sizeof(oc_hook_decode_params) as compiled, for binding checks */
+size_t oc_hook_decode_params_bytes(void);
 
 /*
  * oc_lse_merge -- out[r, :] = merge over s of (m[r,s], l[r,s], acc[r,s,:]),

@@ -93,6 +93,9 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
   a.lengths = kv->lengths;
   a.num_rows = kv->num_rows;
   a.num_tiles = kv->num_tiles;
+  if (kv->num_tokens < 0 || (int64_t)kv->num_tokens > (int64_t)kv->num_tiles * 64)
+    return fail(OC_ERR_INVALID, "num_tokens %d outside 0..num_tiles * 64", kv->num_tokens);
+  a.row_tok = kv->lengths ? 0 : kv->num_tokens;
   a.k_scale_mode = kv->k_scale_mode;
   a.v_scale_mode = kv->v_scale_mode;
   a.k_scale = kv->k_scale;
@@ -363,9 +366,24 @@ extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   return n;
 }
 
+// The model hook's gate, fused into the decode's prologue (oc_hook_decode):
+// tile norms of kv head (row % rows), complete tiles, threshold, statistics.
+struct HookGate {
+  const float* norms;
+  int64_t stride;
+  int rows, full;
+  double tau;
+  float* stats;
+};
+// decode_impl's answer when a hook gate cannot be fused (the caller then
+// gates with its own kernel); no error message is recorded for it
+static constexpr int kHookNotFused = -1;
+
 // oc_decode with the workspace (`ws`, `ws_bytes`) given separately from p,
-// so that oc_decode_static can bring its own.
-static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, void* stream) {
+// so that oc_decode_static can bring its own; with `hk` the decode gates
+// with the hook's norms instead of p's gate (p's tile mask unused).
+static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, void* stream,
+                       const HookGate* hk = nullptr) {
   if (!p) return fail(OC_ERR_INVALID, "params is NULL");
   DecodeArgs a;
   int rc = fill_kv(&p->kv, a);
@@ -463,6 +481,16 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
               !partials_given && !p->split_counts &&
               ((cached_gate && a.bal && p->kv.num_tiles <= 64 * kFastChunks) ||
                (p->gate == OC_GATE_NONE && a.spw > 1))) ? 1 : 0;
+    if (hk) {
+      if (!a.fast || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
+      a.gate = kGateHook;
+      a.hk_norms = hk->norms;
+      a.hk_stride = hk->stride;
+      a.hk_rows = hk->rows;
+      a.hk_full = hk->full;
+      a.hk_tau = hk->tau;
+      a.hk_stats = hk->stats;
+    }
   }
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
@@ -476,6 +504,104 @@ extern "C" int oc_decode(const oc_decode_params* p, void* stream) {
   if (!p) return fail(OC_ERR_INVALID, "params is NULL");
   return decode_impl(p, p->workspace, p->workspace_bytes, stream);
 }
+
+// ------------------------------------------------ oc_hook_decode
+//
+// Workspace: [the decode's own workspace (merge counters first, so they stay
+// at the start whatever the shapes)] [mask: rows x T bytes], each part
+// 256-byte aligned.  A partial last tile is the descriptor's num_tokens (one
+// length for every row), so the decode keeps its contiguous-row layout.
+
+int oc_internal_hook_gate(const void* q, int32_t dtype, int64_t q_row_stride, int32_t batch, int32_t num_kv_heads,
+                          int32_t G, int32_t head_dim, int32_t low_band, const float* k_norms,
+                          int64_t k_norms_stride, int32_t num_tiles, int32_t mask_cols, double tau_norm,
+                          uint8_t* mask, int64_t mask_stride, float* gate_stats, void* stream);
+
+static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// The oc_decode parameters of a hook decode step (the mask pointer may be
+// null when only sizes are wanted).
+static int hook_to_decode(const oc_hook_decode_params* h, uint8_t* mask, oc_decode_params* d) {
+  if (!h) return fail(OC_ERR_INVALID, "params is NULL");
+  if (h->dtype != OC_F32 && h->dtype != OC_F16 && h->dtype != OC_BF16) return fail(OC_ERR_INVALID, "dtype %d", h->dtype);
+  if (h->batch < 0 || h->num_kv_heads < 0 || h->G < 1 || h->G > 64 || h->kv_len < 64)
+    return fail(OC_ERR_INVALID, "bad sizes (G in 1..64, kv_len >= 64)");
+  if (h->low_band < 1 || h->head_dim % h->low_band) return fail(OC_ERR_INVALID, "low_band %d", h->low_band);
+  const int64_t rows = (int64_t)h->batch * h->num_kv_heads;
+  if (rows > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many rows");
+  const int T = (h->kv_len + 63) / 64;
+  std::memset(d, 0, sizeof(*d));
+  d->kv.k = h->k;
+  d->kv.v = h->v;
+  d->kv.dtype = h->dtype;
+  d->kv.head_dim = h->head_dim;
+  d->kv.num_rows = (int32_t)rows;
+  d->kv.num_tiles = T;
+  d->kv.k_row_stride = h->k_row_stride;
+  d->kv.k_token_stride = h->k_token_stride;
+  d->kv.v_row_stride = h->v_row_stride;
+  d->kv.v_token_stride = h->v_token_stride;
+  d->kv.num_tokens = h->kv_len;
+  d->q = h->q;
+  d->q_dtype = h->dtype;
+  d->G = h->G;
+  d->q_row_stride = h->q_row_stride;
+  d->gate = OC_GATE_MASK;
+  d->mode = OC_MODE_CACHED;
+  if (h->num_splits > 0) {
+    d->num_splits = std::min(h->num_splits, T);
+  } else {
+    // about one workgroup per CU, two logical splits each (the retained
+    // tiles of a row are split evenly over its workgroups)
+    const int64_t wpr = std::max<int64_t>(1, std::min<int64_t>(device_cus() / std::max<int64_t>(rows, 1), T / 2));
+    d->num_splits = (int)(2 * wpr);
+    d->splits_per_group = 2;
+  }
+  d->out_dtype = h->dtype;
+  d->out = h->out;
+  d->out_row_stride = h->out_row_stride;
+  d->tile_mask = mask;
+  d->tile_mask_row_stride = T;
+  return OC_OK;
+}
+
+extern "C" size_t oc_hook_decode_workspace_size(const oc_hook_decode_params* p) {
+  oc_decode_params d;
+  if (hook_to_decode(p, nullptr, &d)) return 0;
+  d.out = (void*)1;  // sized as the call with an output
+  return round256(oc_decode_workspace_size(&d)) + round256((size_t)d.kv.num_rows * d.kv.num_tiles) + 256;
+}
+
+extern "C" int oc_hook_decode(const oc_hook_decode_params* p, void* stream) {
+  oc_decode_params d;
+  int rc = hook_to_decode(p, nullptr, &d);
+  if (rc) return rc;
+  if (!p->q || !p->k || !p->v || !p->out || !p->k_norms) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (d.kv.num_rows == 0) return OC_OK;
+  const size_t need = oc_hook_decode_workspace_size(p);
+  if (!p->workspace || p->workspace_bytes < need)
+    return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+  char* w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
+  d.out = p->out;
+  const size_t dec = round256(oc_decode_workspace_size(&d));
+  uint8_t* mask = (uint8_t*)(w + dec);
+  d.workspace = w;
+  d.workspace_bytes = dec;
+  d.tile_mask = mask;
+  if (p->low_band == 8 && (p->dtype == OC_BF16 || p->dtype == OC_F16)) {
+    // one launch: the gate runs in the decode's prologue
+    const HookGate hg{p->k_norms, p->k_norms_stride, p->num_kv_heads, p->kv_len / 64, p->tau_norm, p->gate_stats};
+    rc = decode_impl(&d, d.workspace, d.workspace_bytes, stream, &hg);
+    if (rc != kHookNotFused) return rc;
+  }
+  rc = oc_internal_hook_gate(p->q, p->dtype, p->q_row_stride, p->batch, p->num_kv_heads, p->G, p->head_dim,
+                             p->low_band, p->k_norms, p->k_norms_stride, p->kv_len / 64, d.kv.num_tiles, p->tau_norm,
+                             mask, d.kv.num_tiles, p->gate_stats, stream);
+  if (rc) return rc;
+  return decode_impl(&d, d.workspace, d.workspace_bytes, stream);
+}
+
+extern "C" size_t oc_hook_decode_params_bytes(void) { return sizeof(oc_hook_decode_params); }
 
 // ------------------------------------------------ oc_decode_static scratch
 //

@@ -34,6 +34,10 @@ struct DecWaves {
 constexpr float kM0 = -1e9f;
 constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
 constexpr int kKeepLds = kMaxBalTiles / 8;  // keep flags staged in LDS (bytes of the bitmask array)
+// decode_fast's gate of the model hook's decode step (internal, set by
+// oc_hook_decode): Walsh-subspace q norms, their group median and the cached
+// tile norms, compared in float64
+constexpr int kGateHook = 16;
 constexpr int kFastChunks = 32;  // decode_fast: at most 64 * kFastChunks tiles per row
 constexpr int kFastBatch = 16;   // decode_fast: 64-tile chunks whose scores are in flight at once
 
@@ -48,6 +52,15 @@ struct DecodeArgs {
   int64_t k_blk_stride, k_head_stride, v_blk_stride, v_head_stride;
   const int32_t* lengths;
   int32_t num_rows, num_tiles;
+  int32_t row_tok;  // tokens of every row without lengths (0: num_tiles * 64)
+  // kGateHook: tile norms of kv head (row % hk_rows) at hk_norms[h * hk_stride
+  // + t] for the hk_full complete tiles, threshold hk_tau, per-row
+  // statistics (evicted tiles, group norm, largest tile norm) to hk_stats
+  const float* hk_norms;
+  int64_t hk_stride;
+  int32_t hk_rows, hk_full;
+  double hk_tau;
+  float* hk_stats;
   int32_t k_scale_mode, v_scale_mode;
   float k_scale;
   int32_t q_dtype;
@@ -349,7 +362,7 @@ struct RowInfo {
 
 __device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) {
   RowInfo ri;
-  int n = a.num_tiles * 64;
+  int n = a.row_tok > 0 ? a.row_tok : a.num_tiles * 64;
   if (a.lengths) {
     const int len = a.lengths[row / a.rows_per_length];
     n = len < 0 ? 0 : (len < n ? len : n);
@@ -1433,7 +1446,7 @@ __device__ __forceinline__ TileList split_list(const DecodeArgs& a, const RowInf
 }
 
 __device__ __forceinline__ int row_tiles(const DecodeArgs& a, int r) {
-  int n = a.num_tiles * 64;
+  int n = a.row_tok > 0 ? a.row_tok : a.num_tiles * 64;
   if (a.lengths) {
     const int len = a.lengths[r / a.rows_per_length];
     n = len < 0 ? 0 : (len < n ? len : n);
@@ -1874,6 +1887,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   uint32_t wlo = 0u, whi = 0u;
   auto score_pass = [&](auto gate_tag) {
     constexpr int GATE = decltype(gate_tag)::value;
+    constexpr bool HOOK = GATE == kGateHook;
     const int64_t so = (int64_t)row * a.sc_stride;
     float el[kFastBatch], eh[kFastBatch];
     auto load_scores = [&](int c0) {
@@ -1881,7 +1895,10 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
       for (int k = 0; k < kFastBatch; ++k) {
         const int t = min((c0 + k) * 64 + lane, T - 1);
         el[k] = 0.f;
-        if constexpr (GATE == OC_GATE_MASK) {
+        if constexpr (HOOK) {
+          // the complete tiles' norms (a partial tail reads the last one's)
+          eh[k] = a.hk_norms[(int64_t)(row % a.hk_rows) * a.hk_stride + min(t, a.hk_full - 1)];
+        } else if constexpr (GATE == OC_GATE_MASK) {
           eh[k] = a.tmask[(int64_t)row * a.tmask_stride + t] ? 1.f : 0.f;
         } else {
           eh[k] = a.sc_eh[so + t];
@@ -1918,6 +1935,59 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
       qv = fmaxf(qv, xpair<1>(qv));
       qmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(qv)));
     }
+    float qn = 0.f;  // hook: the group's median Walsh-subspace norm
+    if constexpr (HOOK) {
+      static_assert(!F8, "the hook gate reads q in K's 16-bit layout");
+      // head x: ||q||^2 - sum_i S_i^2 / bs over the 8 blocks of bs = D / 8
+      // columns (S_i: block sums), from the lane's columns 32 dc + 8 kg .. +8
+      float ss = 0.f, sp[D / 32];
+#pragma unroll
+      for (int dc = 0; dc < D / 32; ++dc) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float lo, hi;
+          unpack16x2<QT>(aq[dc][w], lo, hi);
+          s += lo + hi;
+          ss = __builtin_fmaf(lo, lo, __builtin_fmaf(hi, hi, ss));
+        }
+        sp[dc] = s;
+      }
+      ss += xpair<16>(ss);
+      ss += xpair<32>(ss);
+      float lsq = 0.f;
+      if constexpr (D == 128) {
+        // block 2 dc + kg / 2: lane groups kg and kg ^ 1 hold its halves
+#pragma unroll
+        for (int dc = 0; dc < D / 32; ++dc) {
+          const float s = sp[dc] + xpair<16>(sp[dc]);
+          lsq = __builtin_fmaf(s, s, lsq);
+        }
+        lsq += xpair<32>(lsq);
+      } else {
+        // block 4 dc + kg: the lane's eight columns
+#pragma unroll
+        for (int dc = 0; dc < D / 32; ++dc) lsq = __builtin_fmaf(sp[dc], sp[dc], lsq);
+        lsq += xpair<16>(lsq);
+        lsq += xpair<32>(lsq);
+      }
+      float h2 = ss - lsq / (float)(D / 8);
+      h2 = h2 < 0.f ? 0.f : h2;
+      const float qh = __builtin_sqrtf(h2);
+      // the element of rank G / 2 of the G norms (ties by head index), as
+      // oc_group_gate's median
+      int below = 0;
+      for (int g = 0; g < a.G; ++g) {
+        const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qh), g));
+        below += (v < qh || (v == qh && g < x)) ? 1 : 0;
+      }
+      const uint64_t pick = __ballot(kg == 0 && x < a.G && below == a.G / 2);
+      // none when a NaN breaks the ranks: 0, as oc_group_gate
+      qn = pick ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qh), __ffsll((unsigned long long)pick) - 1))
+                : 0.f;
+    }
+    float nev = 0.f, kmax = -__builtin_inff();
+    bool knan = false;
     const bool keep_wr = a.keep_out && gidx == 0;
     for (int c0 = 0; c0 < nch; c0 += kFastBatch) {
       if (c0 > 0) load_scores(c0);
@@ -1928,9 +1998,21 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
           const int t = c * 64 + lane;
           // cached_keep with the gate fixed: a partial last tile is kept
           // (score gates), the mask byte decides (mask gate)
-          bool keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
-          if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
-          keep = keep && t < T;
+          bool keep;
+          if constexpr (HOOK) {
+            const bool full = t < a.hk_full;
+            const bool ev = full && (double)qn * (double)eh[k] <= a.hk_tau;
+            keep = !ev && t < T;
+            if (full) {
+              nev += ev ? 1.f : 0.f;
+              kmax = fmaxf(kmax, eh[k]);
+              knan = knan || __builtin_isnan(eh[k]);
+            }
+          } else {
+            keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
+            if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
+            keep = keep && t < T;
+          }
           const uint64_t m = __ballot(keep);
           if (lane == c) {
             wlo = (uint32_t)m;
@@ -1941,9 +2023,24 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
         }
       }
     }
+    if constexpr (HOOK) {
+      // the row's statistics, by wave 0 of its first workgroup (every wave
+      // holds them): evicted complete tiles, the group norm and the largest
+      // complete tile's norm (NaN if one is NaN, -inf if there are none)
+      nev = wave_sum(nev);
+      kmax = wave_max(kmax);
+      const bool wnan = __ballot(knan) != 0;
+      if (a.hk_stats && gidx == 0 && wave == 0 && lane == 0) {
+        float* o = a.hk_stats + (int64_t)row * 3;
+        o[0] = nev;
+        o[1] = qn;
+        o[2] = wnan ? __builtin_nanf("") : kmax;
+      }
+    }
   };
   if (!cached) load_q();
   else if (a.gate == OC_GATE_CS) score_pass(std::integral_constant<int, OC_GATE_CS>{});
+  else if (!F8 && a.gate == kGateHook) score_pass(std::integral_constant<int, F8 ? OC_GATE_CS : kGateHook>{});
   else if (a.gate == OC_GATE_ZETA) score_pass(std::integral_constant<int, OC_GATE_ZETA>{});
   else score_pass(std::integral_constant<int, OC_GATE_MASK>{});
   const int cnt = __popc(wlo) + __popc(whi);

@@ -540,24 +540,16 @@ __device__ __forceinline__ float pf_load_elem(const char* p, int dtype) {
   return (float)__builtin_bit_cast(_Float16, u);
 }
 
-// One wave per row of a 3-index view: ||row||_2, or with low_band > 0 its
+// ||row||_2 of one head_dim row by one wave, or with low_band > 0 its
 // Walsh-subspace high part sqrt(max(0, ||row||^2 - sum_i S_i^2 / bs)) (S_i:
-// sums of blocks of bs = d / low_band elements).
-__global__ __launch_bounds__(256) void row_norms_kernel(const char* x, int dtype, int64_t n0, int64_t n1,
-                                                        int64_t n2, int64_t s0, int64_t s1, int64_t s2, int d,
-                                                        int low_band, float* out) {
-  __shared__ float sh[4][1024];
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
-  if (r >= n0 * n1 * n2) return;
-  const int64_t i2 = r % n2, i1 = (r / n2) % n1, i0 = r / (n1 * n2);
-  const char* p = x + i0 * s0 + i1 * s1 + i2 * s2;
+// sums of blocks of bs = d / low_band elements).  shrow: d floats of LDS of
+// this wave.  The result is in every lane.
+__device__ float row_norm_wave(const char* p, int dtype, int d, int low_band, float* shrow, int lane) {
   const int es = dtype == OC_F32 ? 4 : 2;
   float ss = 0.f;
   for (int c = lane; c < d; c += 64) {
     const float v = pf_load_elem(p + (int64_t)c * es, dtype);
-    sh[wave][c] = v;
+    shrow[c] = v;
     ss = __builtin_fmaf(v, v, ss);
   }
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
@@ -569,7 +561,7 @@ __global__ __launch_bounds__(256) void row_norms_kernel(const char* x, int dtype
     float lo = 0.f;
     for (int i = lane; i < low_band; i += 64) {
       float s = 0.f;
-      for (int k = 0; k < bs; ++k) s += sh[wave][i * bs + k];
+      for (int k = 0; k < bs; ++k) s += shrow[i * bs + k];
       lo = __builtin_fmaf(s, s, lo);
     }
     for (int o = 32; o > 0; o >>= 1) lo += __shfl_xor(lo, o, 64);
@@ -577,7 +569,21 @@ __global__ __launch_bounds__(256) void row_norms_kernel(const char* x, int dtype
     ss = ss - lo;
     ss = ss < 0.f ? 0.f : ss;
   }
-  if (lane == 0) out[r] = __builtin_sqrtf(ss);
+  return __builtin_sqrtf(ss);
+}
+
+// One wave per row of a 3-index view (row_norm_wave).
+__global__ __launch_bounds__(256) void row_norms_kernel(const char* x, int dtype, int64_t n0, int64_t n1,
+                                                        int64_t n2, int64_t s0, int64_t s1, int64_t s2, int d,
+                                                        int low_band, float* out) {
+  __shared__ float sh[4][1024];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+  if (r >= n0 * n1 * n2) return;
+  const int64_t i2 = r % n2, i1 = (r / n2) % n1, i0 = r / (n1 * n2);
+  const float n = row_norm_wave(x + i0 * s0 + i1 * s1 + i2 * s2, dtype, d, low_band, sh[wave], lane);
+  if (lane == 0) out[r] = n;
 }
 
 // k-th smallest (0-based) of n non-negative floats per row by a radix
@@ -621,46 +627,35 @@ __global__ __launch_bounds__(256) void kth_smallest_kernel(const float* x, int64
   if (threadIdx.x == 0) out[blockIdx.x] = __uint_as_float(prefix);
 }
 
-// One workgroup per (batch, kv head): qn = max of the group's G per-head
-// norms (NaN-propagating) or the element of rank G/2 of their sorted order
-// (ties counted by index), then mask[t] = qn * kn[t] <= tau_norm for t <
-// num_tiles and 0 up to mask_cols (keep_pol: 1 = attend instead).
-__global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, int Hkv, int G, int reduce,
-                                                         const float* kn, int64_t kn_sb, int64_t kn_sh,
-                                                         int num_tiles, int mask_cols, double tau_norm, int keep_pol,
-                                                         uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out,
-                                                         float* stats) {
-  __shared__ float s_qn;
-  __shared__ float s_red[2][4];
-  const int bk = blockIdx.x;
-  const int b = bk / Hkv;
-  const int kv = bk % Hkv;
-  const float* qh = qn_heads + ((int64_t)b * Hkv + kv) * G;
-  if (threadIdx.x == 0) {
-    float qn = 0.f;
-    if (reduce == OC_GROUP_MAX) {
-      bool nan = false;
-      float best = -__builtin_inff();
-      for (int g = 0; g < G; ++g) {
-        nan = nan || __builtin_isnan(qh[g]);
-        best = qh[g] > best ? qh[g] : best;
-      }
-      qn = nan ? __builtin_nanf("") : best;
-    } else {
-      const int want = G / 2;
-      for (int g = 0; g < G; ++g) {
-        int below = 0;
-        for (int j = 0; j < G; ++j) below += (qh[j] < qh[g] || (qh[j] == qh[g] && j < g)) ? 1 : 0;
-        if (below == want) qn = qh[g];
-      }
+// The group norm of G per-head norms: their max (NaN-propagating) or the
+// element of rank G/2 of their sorted order (ties counted by index).
+__device__ float group_norm(const float* qh, int G, int reduce) {
+  if (reduce == OC_GROUP_MAX) {
+    bool nan = false;
+    float best = -__builtin_inff();
+    for (int g = 0; g < G; ++g) {
+      nan = nan || __builtin_isnan(qh[g]);
+      best = qh[g] > best ? qh[g] : best;
     }
-    s_qn = qn;
-    if (qn_out) qn_out[bk] = qn;
+    return nan ? __builtin_nanf("") : best;
   }
-  __syncthreads();
-  const float qn = s_qn;
-  const float* knr = kn + (int64_t)b * kn_sb + (int64_t)kv * kn_sh;
-  uint8_t* mr = mask + (int64_t)b * m_sb + (int64_t)kv * m_sh;
+  const int want = G / 2;
+  float qn = 0.f;
+  for (int g = 0; g < G; ++g) {
+    int below = 0;
+    for (int j = 0; j < G; ++j) below += (qh[j] < qh[g] || (qh[j] == qh[g] && j < g)) ? 1 : 0;
+    if (below == want) qn = qh[g];
+  }
+  return qn;
+}
+
+// The tile gate of one (batch, kv head) by a 256-thread workgroup:
+// mask[t] = qn * kn[t] <= tau_norm for t < num_tiles and 0 up to mask_cols
+// (keep_pol: 1 = attend instead); with stats, the evicted count, qn and the
+// largest kn of the complete tiles (NaN if any is NaN, -inf if none).
+__device__ void gate_tiles(float qn, const float* knr, int num_tiles, int mask_cols, double tau_norm, int keep_pol,
+                           uint8_t* mr, float* stats) {
+  __shared__ float s_red[2][4];
   float nev = 0.f, kmax = -__builtin_inff();
   bool knan = false;
   for (int t = threadIdx.x; t < mask_cols; t += 256) {
@@ -677,9 +672,7 @@ __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, 
     }
   }
   if (stats) {
-    // per (b, kv head): evicted complete tiles, the group norm and the
-    // largest K norm of the complete tiles (NaN if any is NaN, -inf if
-    // none), unclamped: the hook clamps after its reductions over heads
+    // unclamped: the hook clamps after its reductions over heads
     nev = wave_sum(nev);
     kmax = wave_max(kmax);
     const bool wnan = __ballot(knan) != 0;
@@ -690,14 +683,60 @@ __global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, 
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-      float* o = stats + (int64_t)bk * 3;
-      o[0] = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
-      o[1] = qn;
+      stats[0] = s_red[0][0] + s_red[0][1] + s_red[0][2] + s_red[0][3];
+      stats[1] = qn;
       float m = s_red[1][0];
       for (int i = 1; i < 4; ++i) m = (__builtin_isnan(m) || __builtin_isnan(s_red[1][i])) ? __builtin_nanf("") : fmaxf(m, s_red[1][i]);
-      o[2] = m;
+      stats[2] = m;
     }
   }
+}
+
+// One workgroup per (batch, kv head): qn = group_norm of the group's G
+// per-head norms, then gate_tiles.
+__global__ __launch_bounds__(256) void group_gate_kernel(const float* qn_heads, int Hkv, int G, int reduce,
+                                                         const float* kn, int64_t kn_sb, int64_t kn_sh,
+                                                         int num_tiles, int mask_cols, double tau_norm, int keep_pol,
+                                                         uint8_t* mask, int64_t m_sb, int64_t m_sh, float* qn_out,
+                                                         float* stats) {
+  __shared__ float s_qn;
+  const int bk = blockIdx.x;
+  const int b = bk / Hkv;
+  const int kv = bk % Hkv;
+  if (threadIdx.x == 0) {
+    const float qn = group_norm(qn_heads + ((int64_t)b * Hkv + kv) * G, G, reduce);
+    s_qn = qn;
+    if (qn_out) qn_out[bk] = qn;
+  }
+  __syncthreads();
+  gate_tiles(s_qn, kn + (int64_t)b * kn_sb + (int64_t)kv * kn_sh, num_tiles, mask_cols, tau_norm, keep_pol,
+             mask + (int64_t)b * m_sb + (int64_t)kv * m_sh, stats ? stats + (int64_t)bk * 3 : nullptr);
+}
+
+// The hook's decode gate in one launch: per (batch, kv head) the Walsh-
+// subspace high norms of the group's G query rows (row_norm_wave, four
+// waves), their median and the tile gate with the partial tail attended
+// (keep polarity).
+__global__ __launch_bounds__(256) void hook_gate_kernel(const char* q, int dtype, int64_t q_row_bytes, int Hkv, int G,
+                                                        int d, int low_band, const float* kn, int64_t kn_sh,
+                                                        int num_tiles, int mask_cols, double tau_norm, uint8_t* mask,
+                                                        int64_t m_sh, float* stats) {
+  __shared__ float sh[4][1024];
+  __shared__ float s_qh[64];
+  __shared__ float s_qn;
+  const int bk = blockIdx.x;
+  const int kv = bk % Hkv;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (int g = wave; g < G; g += 4) {
+    const float n = row_norm_wave(q + ((int64_t)bk * G + g) * q_row_bytes, dtype, d, low_band, sh[wave], lane);
+    if (lane == 0) s_qh[g] = n;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) s_qn = group_norm(s_qh, G, OC_GROUP_MEDIAN);
+  __syncthreads();
+  gate_tiles(s_qn, kn + (int64_t)kv * kn_sh, num_tiles, mask_cols, tau_norm, 1, mask + (int64_t)bk * m_sh,
+             stats ? stats + (int64_t)bk * 3 : nullptr);
 }
 
 bool pf_float_dtype(int dt) { return dt == OC_F32 || dt == OC_F16 || dt == OC_BF16; }
@@ -823,6 +862,21 @@ extern "C" int oc_group_gate(const float* q_norms, int32_t batch, int32_t num_kv
                      tau_norm, keep_polarity, mask, mask_stride_b, mask_stride_h, group_norms, gate_stats);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "group-gate launch");
+}
+
+// The hook decode's gate launch (oc_hook_decode); q_row_stride in elements.
+__attribute__((visibility("hidden"))) int oc_internal_hook_gate(
+    const void* q, int32_t dtype, int64_t q_row_stride, int32_t batch, int32_t num_kv_heads, int32_t G,
+    int32_t head_dim, int32_t low_band, const float* k_norms, int64_t k_norms_stride, int32_t num_tiles,
+    int32_t mask_cols, double tau_norm, uint8_t* mask, int64_t mask_stride, float* gate_stats, void* stream) {
+  const int64_t wgs = (int64_t)batch * num_kv_heads;
+  if (wgs == 0) return OC_OK;
+  const int es = dtype == OC_F32 ? 4 : 2;
+  hipLaunchKernelGGL(hook_gate_kernel, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, (const char*)q, dtype,
+                     q_row_stride * es, num_kv_heads, G, head_dim, low_band, k_norms, k_norms_stride, num_tiles,
+                     mask_cols, tau_norm, mask, mask_stride, gate_stats);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "hook-gate launch");
 }
 
 extern "C" size_t oc_prefill_params_bytes(void) { return sizeof(oc_prefill_params); }

@@ -116,6 +116,7 @@ class KVLayout:
     v_head_stride: int = 0
     lengths: Optional[torch.Tensor] = None
     rows_per_length: int = 1
+    num_tokens: int = 0  # tokens of every row without lengths (0: num_tiles * 64)
     k_scale_mode: int = N.OC_KSCALE_NONE
     k_scale: float = 1.0
     k_scales: Optional[torch.Tensor] = None
@@ -145,6 +146,7 @@ class KVLayout:
         d.k_block_stride, d.k_head_stride = self.k_block_stride, self.k_head_stride
         d.v_block_stride, d.v_head_stride = self.v_block_stride, self.v_head_stride
         d.lengths = _ptr(self.lengths)
+        d.num_tokens = self.num_tokens
         d.k_scale_mode = self.k_scale_mode
         d.k_scale = float(self.k_scale)
         d.k_scales = _ptr(self.k_scales)
@@ -159,7 +161,8 @@ class KVLayout:
 def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail: bool = False) -> KVLayout:
     """(rows, S, d) K/V views (last dimension contiguous, any other strides).
     The tiles are the S // 64 complete ones; with partial_tail a last
-    partial tile is included (as a row length of S)."""
+    partial tile is included (as the descriptor's num_tokens = S, one length
+    for every row)."""
     rows, s_len, d = keys.shape
     if values is not None and values.shape != keys.shape:
         raise ValueError(f"keys {tuple(keys.shape)} and values {tuple(values.shape)} must have the same shape")
@@ -174,8 +177,7 @@ def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail
         v_token_stride=0 if values is None else values.stride(1))
     if partial_tail and s_len % TILE_SIZE:
         kv.num_tiles += 1
-        kv.lengths = torch.full((1,), s_len, dtype=torch.int32, device=keys.device)
-        kv.rows_per_length = max(rows, 1)
+        kv.num_tokens = s_len
     return kv
 
 
@@ -438,6 +440,73 @@ def dequant_fp8(src: torch.Tensor, scale: float, out_dtype: torch.dtype) -> torc
             src.data_ptr(), n, float(scale), dtype_code(out_dtype, "out", allow_fp8=False), out.data_ptr(),
             ctypes.c_void_p(stream)))
     return out
+
+
+_HOOK_PARAMS: Dict[tuple, "N.OcHookDecodeParams"] = {}
+
+
+def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_norms: torch.Tensor, G: int,
+                tau_norm: float, low_band: int, want_stats: bool = True):
+    """oc_hook_decode: the model hook's decode step in one call.  query
+    (B, Hq, 1, d), key / value (B, Hkv, S, d) with a contiguous last
+    dimension, k_norms float32 (>= Hkv, >= S // 64) with contiguous rows
+    (shared by the batch).  Returns (out (B, Hq, 1, d) in query's dtype,
+    gate statistics float32 (B * Hkv, 3) or None).  The parameter block is
+    kept per shape and only its pointers and sizes are refreshed, so that
+    a decode step costs one library call on the host."""
+    B, Hq, _, d = query.shape
+    Hkv, S = key.shape[1], key.shape[2]
+    dt = query.dtype
+    if key.dtype != dt or value.dtype != dt:
+        key, value = key.to(dt), value.to(dt)
+    rows = []
+    for t in (key, value):
+        if t.stride(3) != 1 or (B > 1 and t.stride(0) != Hkv * t.stride(1)):
+            t = t.contiguous()
+        rows.append(t)
+    key, value = rows
+    if query.stride(3) != 1 or (B > 1 and query.stride(0) != Hq * query.stride(1)):
+        query = query.contiguous()
+    device = query.device
+    if not (device.type == "cuda" and key.device == device and value.device == device and k_norms.device == device):
+        require_gpu(query, key, value, k_norms)  # raises with the reason
+    if k_norms.dtype != torch.float32 or k_norms.stride(-1) != 1:
+        raise ValueError("k_norms must be float32 with contiguous rows")
+    skey = (device.index, dt, B, Hq, Hkv, d, key.stride(1), key.stride(2), value.stride(1), value.stride(2),
+            query.stride(1), k_norms.stride(0), low_band)
+    p = _HOOK_PARAMS.get(skey)
+    if p is None:
+        p = N.OcHookDecodeParams()
+        p.q_row_stride = query.stride(1)
+        p.k_row_stride, p.k_token_stride = key.stride(1), key.stride(2)
+        p.v_row_stride, p.v_token_stride = value.stride(1), value.stride(2)
+        p.dtype = dtype_code(dt, "q", allow_fp8=False)
+        p.batch, p.num_kv_heads, p.G, p.head_dim = B, Hkv, G, d
+        p.k_norms_stride = k_norms.stride(0)
+        p.low_band = low_band
+        p.num_splits = 0
+        p.out_row_stride = d
+        _HOOK_PARAMS[skey] = p
+    p.G = G
+    p.kv_len = S
+    p.tau_norm = tau_norm
+    p.q, p.k, p.v, p.k_norms = query.data_ptr(), key.data_ptr(), value.data_ptr(), k_norms.data_ptr()
+    out = torch.empty((B, Hq, 1, d), dtype=dt, device=device)
+    stats = torch.empty((B * Hkv, 3), dtype=torch.float32, device=device) if want_stats else None
+    p.out = out.data_ptr()
+    p.gate_stats = None if stats is None else stats.data_ptr()
+    lib = N.lib()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ws = workspace(device, stream, lib.oc_hook_decode_workspace_size(ctypes.byref(p)))
+    p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+    if device.index == torch.cuda.current_device():
+        rc = lib.oc_hook_decode(ctypes.byref(p), ctypes.c_void_p(stream))
+    else:
+        with torch.cuda.device(device):
+            rc = lib.oc_hook_decode(ctypes.byref(p), ctypes.c_void_p(stream))
+    if rc:
+        N.check("oc_hook_decode", rc)
+    return out, stats
 
 
 def decode_gate(q: torch.Tensor, norm_cache: torch.Tensor, tau_norm: float, num_tiles: int, G: int,

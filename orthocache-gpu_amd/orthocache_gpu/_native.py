@@ -50,7 +50,7 @@ class OcKvDesc(ctypes.Structure):
         ("lengths", _p),
         ("k_scale_mode", _i32), ("k_scale", ctypes.c_float),
         ("k_scales", _p), ("k_scales_row_stride", _i64),
-        ("v_scale_mode", _i32), ("reserved0", _i32),
+        ("v_scale_mode", _i32), ("num_tokens", _i32),
         ("v_scales", _p), ("v_scales_row_stride", _i64),
         ("error_flag", _p),
     ]
@@ -96,6 +96,18 @@ class OcSpectraParams(ctypes.Structure):
     ]
 
 
+class OcHookDecodeParams(ctypes.Structure):
+    _fields_ = [
+        ("q", _p), ("q_row_stride", _i64), ("k", _p), ("v", _p),
+        ("k_row_stride", _i64), ("k_token_stride", _i64), ("v_row_stride", _i64), ("v_token_stride", _i64),
+        ("dtype", _i32), ("batch", _i32), ("num_kv_heads", _i32), ("G", _i32), ("head_dim", _i32), ("kv_len", _i32),
+        ("k_norms", _p), ("k_norms_stride", _i64), ("tau_norm", ctypes.c_double),
+        ("low_band", _i32), ("num_splits", _i32),
+        ("out", _p), ("out_row_stride", _i64), ("gate_stats", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class OcDeviceInfo(ctypes.Structure):
     _fields_ = [
         ("arch", ctypes.c_char * 64), ("name", ctypes.c_char * 128), ("compute_units", _i32), ("wave_size", _i32),
@@ -134,6 +146,9 @@ SIGNATURES = {
     "oc_decode": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
     "oc_decode_static": (_i32, [ctypes.POINTER(OcDecodeParams), _p]),
     "oc_decode_static_scratch_bytes": (ctypes.c_size_t, []),
+    "oc_hook_decode": (_i32, [ctypes.POINTER(OcHookDecodeParams), _p]),
+    "oc_hook_decode_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcHookDecodeParams)]),
+    "oc_hook_decode_params_bytes": (ctypes.c_size_t, []),
     "oc_lse_merge": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i32, _i64, _p]),
     "oc_dequant_fp8": (_i32, [_p, _i64, ctypes.c_float, _i32, _p, _p]),
     "oc_hbm_read_probe": (_i32, [_p, ctypes.c_size_t, _p, _i32, _p]),
@@ -180,7 +195,8 @@ def lib():
                     "orthocache_gpu: struct layout mismatch between the binding and "
                     f"{LIB_PATH} ({kv_sz.value}/{p_sz.value} vs "
                     f"{ctypes.sizeof(OcKvDesc)}/{ctypes.sizeof(OcDecodeParams)} bytes)")
-            for fn, st in (("oc_prefill_params_bytes", OcPrefillParams), ("oc_spectra_params_bytes", OcSpectraParams)):
+            for fn, st in (("oc_prefill_params_bytes", OcPrefillParams), ("oc_spectra_params_bytes", OcSpectraParams),
+                           ("oc_hook_decode_params_bytes", OcHookDecodeParams)):
                 if getattr(handle, fn)() != ctypes.sizeof(st):
                     raise RuntimeError(f"orthocache_gpu: {st.__name__} layout mismatch between the binding and "
                                        f"{LIB_PATH}")

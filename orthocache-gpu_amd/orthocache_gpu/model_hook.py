@@ -45,6 +45,7 @@ from __future__ import annotations
 import math
 from typing import Optional
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -127,12 +128,15 @@ class _Stats(dict):
         if not self._pending or self._folding:
             return
         pending, self._pending = self._pending, []
-        host = torch.cat([d.reshape(-1).to(torch.float64) for _, d in pending]).cpu()
+        # one device concatenation (the values are float32), one transfer,
+        # then float64 numpy on the host: the folds index it per call, where
+        # numpy's scalar ops cost a fraction of torch's
+        host = torch.cat([d.reshape(-1) for _, d in pending]).cpu().numpy().astype(np.float64)
         self._folding = True
         try:
             i = 0
             for fn, d in pending:
-                fn(host[i:i + d.numel()].view(d.shape))
+                fn(host[i:i + d.numel()].reshape(tuple(d.shape)))
                 i += d.numel()
         finally:
             self._folding = False
@@ -235,15 +239,15 @@ class OrthoCache_GQA_Attention:
         def fold(host):
             for b in range(B):
                 evicted = int(host[0, b])
-                stats['total_tiles'] += Hkv * T
-                stats['evicted_tiles'] += evicted
+                _add(stats, 'total_tiles', Hkv * T)
+                _add(stats, 'evicted_tiles', evicted)
                 _exhaust(stats, float(host[1, b]), float(host[2, b]))
                 if gov is not None and Hkv * T > 0:
                     gov.report_layer(evicted / (Hkv * T))
                 if want_entropy:
                     gov.set_entropy(float(host[3, b]))
-                    stats['entropy'] = float(host[3, b])
-            stats['layers_processed'] += 1
+                    _dset(stats, 'entropy', float(host[3, b]))
+            _add(stats, 'layers_processed', 1)
         stats.defer(fold, dev)
         if gov is not None:
             stats.fold()
@@ -271,7 +275,6 @@ class OrthoCache_GQA_Attention:
         B, Hq, _, d = query.shape
         Hkv, Skv = key.shape[1], key.shape[2]
         T = Skv // TILE
-        tiles = (Skv + TILE - 1) // TILE
         tau = self._tau()
         nc = self.norm_cache
         if Hkv > nc.num_kv_heads or T > nc.max_tiles:
@@ -280,33 +283,31 @@ class OrthoCache_GQA_Attention:
         if self.score_new_tiles and T > self._prefill_tiles:
             # the tiles completed since the prefill, scored from this call's K
             nc.update_tiles(key[B - 1], self._prefill_tiles, T - self._prefill_tiles, norm_scale=_HOOK_NORM_SCALE)
-        norms = nc.cache[:Hkv].unsqueeze(0)
-        qh = X.row_norms(query, low_band=_LOW_BAND).view(B, Hq)
-        # 1 = attend: complete tiles that pass the gate, and the partial last tile
-        keep, _, dev = X.group_gate(qh, norms, Hkv, G, T, tiles, tau * TILE * d, N.OC_GROUP_MEDIAN,
-                                    keep_polarity=True, want_stats=True)
-        kv = X.rows_layout(key.reshape(B * Hkv, Skv, d), value.reshape(B * Hkv, Skv, d), partial_tail=True)
-        res = X.decode(kv, query.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0,
-                       mode=N.OC_MODE_CACHED, out_dtype=query.dtype, tile_mask=keep.view(B * Hkv, -1))
-        # dev (B, Hkv, 3), written by the gate kernel: evicted complete
+        # one library call: the Walsh-subspace q norms, their group medians,
+        # the gate over the complete tiles (the partial last tile attended)
+        # and the decode over the retained tiles
+        out, dev = X.hook_decode(query, key, value, nc.cache, G, tau * TILE * d, _LOW_BAND)
+        # dev (B * Hkv, 3), written by the gate kernel: evicted complete
         # tiles, the group's q norm and the largest K norm per kv head,
         # reduced over the heads (and clamped at 0) when folded
+        dev = dev.view(B, Hkv, 3)
         stats, gov = self.stats, self.governor
 
         def fold(host):
             for b in range(B):
-                skipped = int(host[b, :, 0].sum())
-                _exhaust(stats, float(host[b, :, 1].max().clamp(min=0.0)), float(host[b, :, 2].max().clamp(min=0.0)))
-                stats['decode_steps'] += 1
-                stats['decode_tiles_skipped'] += skipped
-                stats['decode_tiles_total'] += T * Hkv
+                hb = host[b]
+                skipped = int(hb[:, 0].sum())
+                _exhaust(stats, float(np.maximum(hb[:, 1].max(), 0.0)), float(np.maximum(hb[:, 2].max(), 0.0)))
+                _add(stats, 'decode_steps', 1)
+                _add(stats, 'decode_tiles_skipped', skipped)
+                _add(stats, 'decode_tiles_total', T * Hkv)
                 if gov is not None and T > 0:
                     gov.report_layer(skipped / (T * Hkv))
-            stats['layers_processed'] += 1
+            _add(stats, 'layers_processed', 1)
         stats.defer(fold, dev)
         if gov is not None:
             stats.fold()
-        return res.out.view(B, Hq, 1, d)
+        return out
 
     # ------------------------------------------------------------ dense
 
@@ -317,11 +318,20 @@ class OrthoCache_GQA_Attention:
         return out
 
 
+# plain dict access for the folds, which run inside _Stats.fold (the folding
+# accessors would only call it again)
+_dget, _dset = dict.__getitem__, dict.__setitem__
+
+
+def _add(stats, key: str, n) -> None:
+    _dset(stats, key, _dget(stats, key) + n)
+
+
 def _exhaust(stats, max_q: float, max_k: float) -> None:
     """The hallucination-exhaust entries of one batch element (perplexity_eval.py:506-510)."""
-    stats['hallucination_scores'].append(max_q / (max_k + 1e-10))
-    stats['q_search_intensity'].append(max_q)
-    stats['k_info_density'].append(max_k)
+    _dget(stats, 'hallucination_scores').append(max_q / (max_k + 1e-10))
+    _dget(stats, 'q_search_intensity').append(max_q)
+    _dget(stats, 'k_info_density').append(max_k)
 
 
 def _distinct_kv(query, key, value, G):

@@ -292,3 +292,47 @@ def test_group_gate_compares_in_float64():
     for reduce in (N.OC_GROUP_MAX, N.OC_GROUP_MEDIAN):
         mask, _ = X.group_gate(qn, kn, 1, 1, 2, 2, 1 + 2.0 ** -22, reduce)
         assert mask.cpu().tolist() == [[[0, 1]]]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("B,Hq,Hkv,d,S", [(2, 8, 2, 128, 333), (1, 16, 2, 64, 320), (3, 4, 4, 128, 65),
+                                         (1, 32, 8, 128, 4096)],
+                         ids=lambda x: str(x))
+def test_hook_decode_entry_point(dtype, B, Hq, Hkv, d, S):
+    """oc_hook_decode (one call: q Walsh-subspace norms, group medians, gate,
+    decode; one launch for 16-bit types, where the gate runs in the decode's
+    prologue, two for float32) against the oracle's decode branch and against
+    the same step composed from oc_row_norms, oc_group_gate and oc_decode:
+    gate decisions and counts identical, outputs within the bar.  K is a slice of a longer cache and q
+    the transposed view a decoder layer passes; S = 65 leaves one complete
+    tile and a one-token tail."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    G = Hq // Hkv
+    q, k, v = _qkv(B, Hq, Hkv, 1, S, d, dtype, seed=31 + S)
+    T = S // 64
+    g = torch.Generator().manual_seed(7)
+    norms = (torch.rand((Hkv, T + 3), generator=g) * 40 + 1).to(DEV)  # a norm cache with spare columns
+    probe = O.hook_decode(np64(q), np64(k), np64(v), np64(norms), G, tau=-1.0)
+    tau = _gap_tau(probe["qn"][:, :, None].astype(np.float64) * np64(norms)[None, :, :T] / (64 * d)) if T > 1 else 0.5
+    print(f"hook_decode entry {dtype} B={B} Hq={Hq} Hkv={Hkv} d={d} S={S} tau={tau}", flush=True)
+    out, stats = X.hook_decode(q, k, v, norms, G, tau * 64 * d, 8)
+    ref = O.hook_decode(np64(q), np64(k), np64(v), np64(norms), G, tau)
+    assert out.shape == (B, Hq, 1, d) and out.dtype == TD[dtype]
+    assert_out(out, ref["out"], dtype, f"oc_hook_decode {dtype} B={B} G={G} d={d} S={S}")
+    st = stats.view(B, Hkv, 3).cpu().numpy()
+    assert st[:, :, 0].sum(axis=1).tolist() == ref["skipped"].tolist()
+    np.testing.assert_allclose(st[:, :, 1], ref["qn"], rtol=8 * 2.0 ** -23)
+    # the composed path: the same kernels one by one
+    qh = X.row_norms(q, low_band=8).view(B, Hq)
+    keep, _, dev = X.group_gate(qh, norms[:Hkv].unsqueeze(0), Hkv, G, T, (S + 63) // 64, tau * 64 * d,
+                                N.OC_GROUP_MEDIAN, keep_polarity=True, want_stats=True)
+    # counts and tile norms exact; the group norm to float32 rounding (the
+    # one-launch path sums q's squares in another order)
+    dev = dev.view(B * Hkv, 3)
+    assert torch.equal(dev[:, 0], stats[:, 0]) and torch.equal(dev[:, 2], stats[:, 2])
+    torch.testing.assert_close(dev[:, 1], stats[:, 1], rtol=4 * 2.0 ** -23, atol=0)
+    kv = X.rows_layout(k.reshape(B * Hkv, S, d), v.reshape(B * Hkv, S, d), partial_tail=True)
+    res = X.decode(kv, q.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0, mode=N.OC_MODE_CACHED,
+                   out_dtype=q.dtype, tile_mask=keep.view(B * Hkv, -1))
+    assert_out(out.view(B * Hq, d), np64(res.out), dtype, f"oc_hook_decode vs composed {dtype}", ref_rounded=True)
