@@ -63,7 +63,7 @@ def parse():
                     help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
     ap.add_argument("--sweep", type=int, default=1,
                     help="also time BASELINE.json config 1 over 1K..32K tokens and config 2 at full size (0 = skip)")
-    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read",
+    ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read", "gather",
                                        "paged", "fp8", "hook", "compact", "sweep", "config2"],
                     default=None,
                     help="time only this decode variant of the primary batch, a plain 1 GiB device copy "
@@ -731,6 +731,57 @@ def compact_measure(steps, warmup):
                       "dense_forward_us": round(us_d, 1), "cpu_baseline": _compact_cpu(q, k, v, 2)}), flush=True)
 
 
+def gather_measure(steps, warmup):
+    """Read bandwidth of the decode's tile access patterns without its
+    arithmetic (oc_hbm_gather_probe; one step = one tile's K and V pieces in
+    flight per wave, 256 workgroups of 8 waves, K and V in two 2 GiB
+    regions so that every read comes from HBM): contiguous 16 KiB bf16 d128
+    tiles and 8 KiB fp8 tiles, all or half of them at random; and tiles of
+    four 4 KiB pages (16-token pages of bf16 d128) of a randomly permuted
+    pool, all or 40% of them.  Prints one line per pattern."""
+    import numpy as np
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    GiB = 1 << 30
+    buf = torch.empty(4 * GiB, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(256, dtype=torch.float32, device="cuda")
+    lib, stream = N.lib(), X.current_stream(buf.device)
+    rng = np.random.default_rng(0)
+
+    def run(name, offs, lps):
+        n, pps = offs.shape
+        assert offs.min() >= 0 and offs.max() + lps // pps * 1024 <= buf.numel()  # every piece inside the buffer
+        o = torch.from_numpy(np.ascontiguousarray(offs, dtype=np.int64)).to("cuda")
+
+        def fn():
+            N.check("oc_hbm_gather_probe", lib.oc_hbm_gather_probe(
+                ctypes.c_void_p(buf.data_ptr()), ctypes.c_void_p(o.data_ptr()), n, pps, lps,
+                ctypes.c_void_p(sink.data_ptr()), 256, ctypes.c_void_p(stream)))
+        us = _event_us(fn, steps, warmup)
+        nbytes = n * lps * 1024
+        gbps = nbytes / (us * 1e-6) / 1e9
+        print(json.dumps({"only": "gather", "pattern": name, "steps": n, "bytes": nbytes, "us": round(us, 1),
+                          "gbps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)}), flush=True)
+
+    for tile_kib, lps, label in ((16, 32, "bf16 d128 tiles (16 KiB K + 16 KiB V)"),
+                                 (8, 16, "fp8 d128 tiles (8 KiB K + 8 KiB V)")):
+        n_tiles = 2 * GiB // (tile_kib * 1024)
+        for frac in (1.0, 0.5):
+            idx = np.arange(n_tiles) if frac == 1.0 else np.nonzero(rng.random(n_tiles) < frac)[0]
+            offs = np.stack([idx * tile_kib * 1024, 2 * GiB + idx * tile_kib * 1024], axis=1)
+            run(f"{label}, {int(frac * 100)}% of the tiles", offs, lps)
+    pages = 2 * GiB // 4096
+    pk, pv = rng.permutation(pages), rng.permutation(pages)
+    n_tiles = pages // 4
+    for frac in (1.0, 0.4):
+        idx = np.arange(n_tiles) if frac == 1.0 else np.nonzero(rng.random(n_tiles) < frac)[0]
+        cols = [pk[4 * idx + j] * 4096 for j in range(4)] + [2 * GiB + pv[4 * idx + j] * 4096 for j in range(4)]
+        run(f"paged bf16 d128 tiles (4 + 4 random 4 KiB pages), {int(frac * 100)}% of the tiles",
+            np.stack(cols, axis=1), 32)
+    del buf
+
+
 def read_probe(steps, warmup, nbytes=2 << 30):
     """Achievable HBM read bandwidth: oc_hbm_read_probe (128-bit loads, four
     in flight per thread) over a 2 GiB buffer, best grid size."""
@@ -799,6 +850,9 @@ def main():
         us = t0.elapsed_time(t1) * 1e3 / args.steps
         print(json.dumps({"only": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "us_per_copy": us,
                           "gbps_read_plus_write": 2 * (1 << 30) / (us * 1e-6) / 1e9}))
+        return
+    if args.only == "gather":
+        gather_measure(args.steps, args.warmup)
         return
     if args.only == "read":
         print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))

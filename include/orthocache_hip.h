@@ -577,6 +577,18 @@ int oc_dequant_fp8(const void* src, int64_t n, float scale, int32_t out_dtype, v
  * next to the 8 TB/s peak. */
 int oc_hbm_read_probe(const void* src, size_t bytes, float* sink, int32_t blocks, void* stream);
 
+/* oc_hbm_gather_probe -- measurement aid with no counterpart in the
+ * reference: the decode's tile access pattern without its arithmetic.
+ * n_steps steps of pieces_per_step (1..8) pieces each, piece i of step s at
+ * byte offset piece_offsets[s * pieces_per_step + i] from base (1 KiB
+ * aligned), loads_per_step (16 or 32) KiB a step split evenly over its
+ * pieces; blocks 512-thread workgroups, each taking an even share of the
+ * steps, one step in flight per wave (non-temporal 128-bit loads).  Timed by
+ * bench.py to state the read bandwidth of the decode's patterns (contiguous
+ * 16-bit and fp8 tiles, 4 KiB pages) beside the decode's own. */
+int oc_hbm_gather_probe(const void* base, const int64_t* piece_offsets, int64_t n_steps, int32_t pieces_per_step,
+                        int32_t loads_per_step, float* sink, int32_t blocks, void* stream);
+
 /* sizeof(oc_kv_desc) and sizeof(oc_decode_params) as compiled into the
  * library, so that a binding can check its own struct layout (no
  * counterpart in the reference, which has no native ABI) */

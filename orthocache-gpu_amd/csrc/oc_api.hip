@@ -261,6 +261,66 @@ extern "C" int oc_hbm_read_probe(const void* src, size_t bytes, float* sink, int
   return e == hipSuccess ? OC_OK : hip_fail(e, "read probe launch");
 }
 
+// Gather probe: the decode's tile access pattern without its arithmetic.
+// Every step reads `pps` pieces of LPS / pps KiB each at the given byte
+// offsets (one 1 KiB load instruction per 16 bytes a lane, non-temporal,
+// the decode's cache policy), all of a step's loads in flight before any
+// is used, as the decode requests one tile's K and V.  Workgroup b takes
+// steps [b n / blocks, (b + 1) n / blocks), its 8 waves interleaved; the
+// offsets of a wave's next step are fetched while its current step's data
+// is in flight.
+template <int LPS>
+__global__ __launch_bounds__(512) void gather_probe_kernel(const char* __restrict__ base,
+                                                           const int64_t* __restrict__ offs, int64_t n_steps, int pps,
+                                                           float* sink) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t s1 = n_steps * (blockIdx.x + 1) / gridDim.x;
+  int64_t s = n_steps * blockIdx.x / gridDim.x + wave;
+  const int kib = LPS / pps;  // 1 KiB loads per piece
+  uint32_t acc = 0u;
+  int64_t o[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p) o[p] = (s < s1 && p < pps) ? offs[s * pps + p] : 0;
+  while (s < s1) {
+    v4u v[LPS];
+#pragma unroll
+    for (int i = 0; i < LPS; ++i) {
+      const int p = i / kib;
+      v[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const v4u*>(base + o[p < 8 ? p : 7] + (int64_t)(i - p * kib) * 1024 + lane * 16));
+    }
+    s += 8;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) o[p] = (s < s1 && p < pps) ? offs[s * pps + p] : 0;
+#pragma unroll
+    for (int i = 0; i < LPS; ++i) acc ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+  }
+  // a data-dependent store the compiler cannot remove keeps the loads live
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = 1.0f;
+}
+
+extern "C" int oc_hbm_gather_probe(const void* base, const int64_t* piece_offsets, int64_t n_steps,
+                                   int32_t pieces_per_step, int32_t loads_per_step, float* sink, int32_t blocks,
+                                   void* stream) {
+  if (!base || !piece_offsets || !sink) return fail(OC_ERR_INVALID, "NULL pointer");
+  if (pieces_per_step < 1 || pieces_per_step > 8 || n_steps < 0 || blocks < 1)
+    return fail(OC_ERR_INVALID, "bad sizes (1..8 pieces a step)");
+  if ((loads_per_step != 16 && loads_per_step != 32) || loads_per_step % pieces_per_step)
+    return fail(OC_ERR_INVALID, "loads_per_step must be 16 or 32 and a multiple of pieces_per_step");
+  if (n_steps == 0) return OC_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  if (loads_per_step == 16)
+    hipLaunchKernelGGL(gather_probe_kernel<16>, dim3(blocks), dim3(512), 0, st, (const char*)base, piece_offsets,
+                       n_steps, pieces_per_step, sink);
+  else
+    hipLaunchKernelGGL(gather_probe_kernel<32>, dim3(blocks), dim3(512), 0, st, (const char*)base, piece_offsets,
+                       n_steps, pieces_per_step, sink);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OC_OK : hip_fail(e, "gather probe launch");
+}
+
 extern "C" int oc_dequant_fp8(const void* src, int64_t n, float scale, int32_t out_dtype, void* dst, void* stream) {
   if (!src || !dst) return fail(OC_ERR_INVALID, "NULL pointer");
   if (out_dtype != OC_F32 && out_dtype != OC_F16 && out_dtype != OC_BF16)
@@ -466,21 +526,22 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   const int gt = heads_per_group(p->G);
   const int gchunks = (p->G + gt - 1) / gt;
   // the barrier-free prologue (decode_fast): the transposed matrix-core step
-  // on contiguous rows (q of K's 16-bit type, bf16 for fp8 K), every query
-  // head of a row in one workgroup, q rows readable as 16-byte pieces,
-  // partials internal; a score-gated cached decode whose rows have at most
-  // 64 * kFastChunks tiles (their ranks split evenly over the row's
-  // workgroups), or a dense decode over more than one split per workgroup
+  // on contiguous rows or pages of >= 16 tokens (q of K's 16-bit type, bf16
+  // for fp8 K), every query head of a row in one workgroup, q rows readable
+  // as 16-byte pieces, partials internal; a score-gated cached decode whose
+  // rows have at most 64 * kFastChunks tiles (their ranks split evenly over
+  // the row's workgroups), or a dense decode over more than one split per
+  // workgroup (or the flat layout of rows of different lengths)
   {
     const int dt = p->kv.dtype;
     const bool mq = (dt == OC_BF16 && p->q_dtype == OC_BF16) || (dt == OC_F16 && p->q_dtype == OC_F16) ||
                     (dt == OC_FP8_E4M3FN && p->q_dtype == OC_BF16);
     const bool cached_gate = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
     const bool q16 = aligned(p->q, 16) && (a.q_row_stride % 16) == 0;
-    a.fast = (mq && !a.paged && !a.flat && gchunks == 1 && q16 && p->kv.k_scale_mode != OC_KSCALE_Q_FOLD &&
-              !partials_given && !p->split_counts &&
+    a.fast = (mq && (!a.paged || a.bs_log2 >= 4) && gchunks == 1 && q16 &&
+              p->kv.k_scale_mode != OC_KSCALE_Q_FOLD && !partials_given && !p->split_counts &&
               ((cached_gate && a.bal && p->kv.num_tiles <= 64 * kFastChunks) ||
-               (p->gate == OC_GATE_NONE && a.spw > 1))) ? 1 : 0;
+               (p->gate == OC_GATE_NONE && (a.spw > 1 || a.flat)))) ? 1 : 0;
     if (hk) {
       if (!a.fast || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
       a.gate = kGateHook;

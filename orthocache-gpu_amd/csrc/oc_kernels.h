@@ -1281,6 +1281,43 @@ __device__ __forceinline__ void load_k_mfma_t(const DecodeArgs& a, const RowInfo
   }
 }
 
+// Paged K rows of tile t in kperm order (pages of >= 16 tokens, tile_pages'
+// ids).  The sixteen A-rows 16 tb .. +15 hold tokens of 16-token blocks
+// 2 (tb / 2) (lanes x < 8) and 2 (tb / 2) + 1 (x >= 8), each in one page, so
+// the loads are per-lane global loads (non-temporal) at the token's place in
+// its page; tokens past the block's valid count or of an invalid page read
+// as zero (their lanes load the pool's first row and drop it, so that every
+// load is unconditional and the compiler's wait counts stay exact).
+template <int DT, int D>
+__device__ __forceinline__ void load_k_mfma_t_paged(const DecodeArgs& a, const RowInfo& ri, int t, int lane,
+                                                    uint32_t (&kb)[4][D / 32][4], const TilePages& pg) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
+  const int x = lane & 15;
+  const int kg = lane >> 4;
+  const int64_t ts = a.k_tok_stride;
+  const int cofs = F8 ? kg * (D / 4) : 16 * kg;
+  const int bmask = (1 << a.bs_log2) - 1;
+  const int64_t head_off = (int64_t)ri.head * a.k_head_stride;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const int tok = kperm(16 * tb + x);
+    const int hi = x >> 3;  // block 2 (tb / 2) + hi
+    const int id = hi ? pg.id[2 * (tb >> 1) + 1] : pg.id[2 * (tb >> 1)];
+    const int n = hi ? pg.n[2 * (tb >> 1) + 1] : pg.n[2 * (tb >> 1)];
+    const bool ok = (tok & 15) < n;
+    const char* rp = page_row(a.k, a.k_blk_stride, head_off, ts, ok ? id : -1, t * 64 + tok, bmask) + cofs;
+#pragma unroll
+    for (int dc = 0; dc < (F8 ? D / 64 : D / 32); ++dc) {
+      const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(rp + (F8 ? 16 : 64) * dc));
+      kb[tb][dc][0] = ok ? v[0] : 0u;
+      kb[tb][dc][1] = ok ? v[1] : 0u;
+      kb[tb][dc][2] = ok ? v[2] : 0u;
+      kb[tb][dc][3] = ok ? v[3] : 0u;
+    }
+  }
+}
+
 template <int DT, int D>
 __device__ __forceinline__ void tile_logits_t(const uint32_t (&aq)[D / 32][4], const uint32_t (&kb)[4][D / 32][4],
                                               f32x4 (&c)[4]) {
@@ -1836,8 +1873,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
   if (lane == 0) sh_cnt[wave] = kept;
 }
 
-// The attend-every-tile transposed step on contiguous rows with a
-// barrier-free prologue (a.fast): cached decode with a score gate (at most
+// The attend-every-tile transposed step on contiguous rows, or on pages of
+// >= 16 tokens (block-table entries of a wave's next tile requested before
+// its current tile is computed), with a barrier-free prologue (a.fast):
+// cached decode with a score gate (at most
 // 64 * kFastChunks tiles per row) or dense decode, q of the matrix-core type,
 // all G <= GT query heads of a row in one workgroup.  Every wave forms by
 // itself, from global memory: the matrix-core q operand, the row's q norms,
@@ -1848,7 +1887,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // before the workgroup's one barrier, which publishes the LDS counter the
 // later ranks are drawn from (a wave whose tiles arrived sooner takes more).
 // The wave's state goes to LDS as decode_body leaves it.
-template <int DT, int D, int GT>
+template <int DT, int D, int GT, bool PAGED>
 __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg,
                                             float (*sh_m)[GT], float (*sh_l)[GT], int* sh_cnt, uint16_t* sh_v) {
   constexpr int kDW = DecWaves<DT, D>::value;
@@ -1882,7 +1921,9 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   // cached: the row's keep flags, lane c holding the bits of chunk c.  One
   // copy of the pass per gate, with the gate's tests compiled in.  The first
   // kFastBatch chunks' scores are requested before q, so that their latency
-  // overlaps q's; indices are clamped into the row and masked after.
+  // overlaps q's; indices are clamped into the row and masked after.  (All
+  // kFastChunks chunks in one batch, with uniform branches past the row,
+  // measured no faster on long rows and slower on short ones.)
   const int nch = (T + 63) >> 6;
   uint32_t wlo = 0u, whi = 0u;
   auto score_pass = [&](auto gate_tag) {
@@ -2060,32 +2101,53 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     const bool hit = ((bits >> lane) & 1ull) && below == k;
     return __builtin_amdgcn_readfirstlane(lg * 64 + __ffsll((unsigned long long)__ballot(hit)) - 1);
   };
-  // A wave's step covers NT consecutive ranks.  NT = 2 for fp8 (two tiles
-  // fill the register and LDS footprint of one 16-bit tile) measured slower
-  // on 32 rows of 2048 fp8 tiles (110.6 us cached, 174.9 dense, against
-  // 104.0 and 166.6), so every type takes one tile per step.
-  constexpr int NT = 1;
-  // a tile's per-tile K and V scales (fp8) are requested before its K and V,
+  // One tile per wave step.  (Two fp8 tiles per step, which fill the
+  // register and LDS footprint of one 16-bit tile, measured slower on 32 rows
+  // of 2048 fp8 tiles: 110.6 us cached and 174.9 dense against 104.0 and
+  // 166.6.)
+  // A tile's per-tile K and V scales (fp8) are requested before its K and V,
   // so the wait for K covers them; without per-tile scales a valid word (q)
-  // is read and 1 selected, keeping the loads unconditional
+  // is read and 1 selected, keeping the loads unconditional.
   const bool ks_tile = a.k_scale_mode == OC_KSCALE_TILE, vs_tile = a.v_scale_mode == OC_VSCALE_TILE;
   const float* qword = reinterpret_cast<const float*>(a.q);
-  float ks_raw[NT], vs_raw[NT];
-  uint32_t kb[NT][4][D / 32][4];
-  int tt[NT];
-  uint16_t* sv = sh_v + wave * 64 * D;  // this wave's V slot: NT tiles of 64 * D elements
-  auto slot = [&](int i) { return sv + i * (64 * D * Elem<DT>::size / 2); };
-  // the tiles of ranks rb .. rb + NT - 1 (-1 past r1), their loads issued
-  auto fetch = [&](int rb) {
+  float ks_raw = 1.f, vs_raw = 1.f;
+  uint32_t kb[4][D / 32][4];
+  uint16_t* sv = sh_v + wave * 64 * D;  // this wave's V slot
+  TilePages pg{};
+  bool bad_page = false;
+  // paged: the block-table entries of tile tt's four 16-token blocks, one
+  // unconditional vector load (lane j < 4: block j; blocks past the row read
+  // its last block's entry, unused), which the caller waits for
+  auto request_pages = [&](int tt) -> int {
+    if constexpr (PAGED) {
+      const int tok = min(tt * 64 + 16 * min(lane, 3), ri.n_tok - 1);
+      return a.bt[(int64_t)ri.seq * a.bt_stride + (tok >> a.bs_log2)];
+    }
+    return 0;
+  };
+  auto take_pages = [&](int tt, int ids) {
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      tt[i] = rb + i < r1 ? tile_of_rank(rb + i) : -1;
-      if (tt[i] >= 0) {
-        ks_raw[i] = *(ks_tile ? a.k_scales + (int64_t)row * a.ks_stride + tt[i] : qword);
-        vs_raw[i] = *(vs_tile ? a.v_scales + (int64_t)row * a.vs_stride + tt[i] : qword);
-        load_k_mfma_t<DT, D>(a, ri, row, tt[i], lane, kb[i]);
-        load_v_lds<DT, D, false>(a, ri, row, tt[i], lane, slot(i), TilePages{});
+    for (int tb = 0; tb < 4; ++tb) {
+      const int tok = tt * 64 + 16 * tb;
+      int n = min(max(ri.n_tok - tok, 0), 16);
+      int id = __builtin_amdgcn_readlane(ids, tb);
+      if (n > 0 && (id < 0 || id >= a.num_blocks)) {
+        bad_page = true;
+        n = 0;
       }
+      pg.id[tb] = n > 0 ? id : -1;
+      pg.n[tb] = n;
+    }
+  };
+  auto issue = [&](int tt) {
+    ks_raw = *(ks_tile ? a.k_scales + (int64_t)row * a.ks_stride + tt : qword);
+    vs_raw = *(vs_tile ? a.v_scales + (int64_t)row * a.vs_stride + tt : qword);
+    if constexpr (PAGED) {
+      load_k_mfma_t_paged<DT, D>(a, ri, tt, lane, kb, pg);
+      load_v_lds<DT, D, true>(a, ri, row, tt, lane, sv, pg);
+    } else {
+      load_k_mfma_t<DT, D>(a, ri, row, tt, lane, kb);
+      load_v_lds<DT, D, false>(a, ri, row, tt, lane, sv, TilePages{});
     }
   };
   MStateT mst{kM0, 0.f};
@@ -2093,34 +2155,59 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
 #pragma unroll
   for (int nc = 0; nc < D / 16; ++nc) accp[nc] = f32x4{0.f, 0.f, 0.f, 0.f};
   int kept = 0;
-  fetch(r0 + NT * wave);
+  int t = r0 + wave < r1 ? tile_of_rank(r0 + wave) : -1;
+  if (t >= 0) {
+    if constexpr (PAGED) {
+      const int ids = request_pages(t);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      take_pages(t, ids);
+    }
+    issue(t);
+  }
   // publish the LDS rank counter with a bare barrier after the counter's
-  // store has completed, so that the first tiles' K and V loads stay in
+  // store has completed, so that the first tile's K and V loads stay in
   // flight across it (a fenced barrier, even an LDS-only one, waits for them:
   // V is loaded straight into LDS).  The signal fences keep the compiler from
   // moving LDS accesses across the barrier.
-  if (threadIdx.x == 0) sh_cnt[kDW] = NT * kDW;
+  if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
   __builtin_amdgcn_s_waitcnt(kLgkmOnly);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  while (tt[0] >= 0) {
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      if (tt[i] < 0) break;
-      const int valid = min(64, ri.n_tok - tt[i] * 64);
-      f32x4 c[4];
-      tile_logits_t<DT, D>(aq, kb[i], c);
-      tile_softmax_t<D>(mst, accp, c, a.scale * (ks_tile ? ks_raw[i] : 1.f), vs_tile ? vs_raw[i] : 1.f, valid, lane);
-      // the step's V tiles (direct-to-LDS loads, issued after K) have landed
-      if (i == 0) __builtin_amdgcn_s_waitcnt(0);
-      tile_pv_t<DT, D>(accp, c, slot(i), lane);
-      ++kept;
+  while (t >= 0) {
+    // paged: the next rank is claimed first and its block-table entries
+    // requested, so that they arrive while this tile is computed
+    int tn = -1, ids = 0;
+    if constexpr (PAGED) {
+      int xr = 0;
+      if (lane == 0) xr = atomicAdd(&sh_cnt[kDW], 1);
+      const int rb = r0 + __builtin_amdgcn_readfirstlane(xr);
+      tn = rb < r1 ? tile_of_rank(rb) : -1;
+      if (tn >= 0) ids = request_pages(tn);
     }
-    int xr = 0;
-    if (lane == 0) xr = atomicAdd(&sh_cnt[kDW], NT);
-    fetch(r0 + __builtin_amdgcn_readfirstlane(xr));
+    const int valid = min(64, ri.n_tok - t * 64);
+    f32x4 c[4];
+    tile_logits_t<DT, D>(aq, kb, c);
+    tile_softmax_t<D>(mst, accp, c, a.scale * (ks_tile ? ks_raw : 1.f), vs_tile ? vs_raw : 1.f, valid, lane);
+    // the V tile's direct-to-LDS loads (issued after K) have landed; paged,
+    // the next tile's block-table load (issued last) may still be in flight
+    if (PAGED && tn >= 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(1));
+    else __builtin_amdgcn_s_waitcnt(0);
+    tile_pv_t<DT, D>(accp, c, sv, lane);
+    ++kept;
+    if constexpr (PAGED) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      if (tn >= 0) take_pages(tn, ids);
+    } else {
+      int xr = 0;
+      if (lane == 0) xr = atomicAdd(&sh_cnt[kDW], 1);
+      const int rb = r0 + __builtin_amdgcn_readfirstlane(xr);
+      tn = rb < r1 ? tile_of_rank(rb) : -1;
+    }
+    t = tn;
+    if (t >= 0) issue(t);
   }
+  if (PAGED && bad_page && a.error_flag && lane == 0) atomicOr(a.error_flag, 1);
 
   // wave -> LDS in decode_body's layout: head x's state in lanes x, x + 16,
   // x + 32, x + 48; its output columns 16 nc + 4 r + i in lane 16 r + x,
@@ -2333,9 +2420,9 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
   bool fast_done = false;
-  if constexpr (MQK && LOOP && !PAGED) {
+  if constexpr (MQK && LOOP) {
     if (a.fast) {
-      decode_fast<DT, D, GT>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
+      decode_fast<DT, D, GT, PAGED>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
       fast_done = true;
     }
   }

@@ -152,6 +152,7 @@ SIGNATURES = {
     "oc_lse_merge": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p, _i32, _i64, _p]),
     "oc_dequant_fp8": (_i32, [_p, _i64, ctypes.c_float, _i32, _p, _p]),
     "oc_hbm_read_probe": (_i32, [_p, ctypes.c_size_t, _p, _i32, _p]),
+    "oc_hbm_gather_probe": (_i32, [_p, _p, _i64, _i32, _i32, _p, _i32, _p]),
     "oc_abi_sizes": (_i32, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     "oc_device_cu_count": (_i32, [ctypes.POINTER(_i32)]),
     "oc_device_props": (_i32, [ctypes.POINTER(OcDeviceInfo)]),
