@@ -542,6 +542,9 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
               p->kv.k_scale_mode != OC_KSCALE_Q_FOLD && !partials_given && !p->split_counts &&
               ((cached_gate && a.bal && p->kv.num_tiles <= 64 * kFastChunks) ||
                (p->gate == OC_GATE_NONE && (a.spw > 1 || a.flat)))) ? 1 : 0;
+    // the flat layout runs several rounds of small workgroups: two 4-wave
+    // workgroups per CU, so that one's prologue overlaps the other's loop
+    a.fast_waves = a.flat ? 4 : 8;
     if (hk) {
       if (!a.fast || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
       a.gate = kGateHook;

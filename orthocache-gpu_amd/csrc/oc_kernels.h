@@ -102,8 +102,9 @@ struct DecodeArgs {
   // (flat_map) and its partials live at slots [first slot of r, + q_r)
   int32_t flat;
   int32_t flat_target;  // workgroups the flat layout aims at (slots = flat_target + num_rows)
-  // the barrier-free prologue of decode_fast (set by the host when it applies)
-  int32_t fast;
+  // the per-wave prologue of decode_fast_kernel (set by the host when it
+  // applies) and that kernel's waves per workgroup (4 or 8)
+  int32_t fast, fast_waves;
   int32_t* counters;
   char* out;
   int64_t out_stride;  // bytes between query-head rows of out
@@ -1887,10 +1888,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // before the workgroup's one barrier, which publishes the LDS counter the
 // later ranks are drawn from (a wave whose tiles arrived sooner takes more).
 // The wave's state goes to LDS as decode_body leaves it.
-template <int DT, int D, int GT, bool PAGED>
+template <int DT, int D, int GT, bool PAGED, int kDW>
 __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg,
                                             float (*sh_m)[GT], float (*sh_l)[GT], int* sh_cnt, uint16_t* sh_v) {
-  constexpr int kDW = DecWaves<DT, D>::value;
   constexpr bool F8 = DT == OC_FP8_E4M3FN;
   constexpr int QT = MfmaT<DT>::value;  // q's 16-bit type
   static_assert(GT <= 16, "one q head per 16-lane group of the operand");
@@ -2380,6 +2380,38 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
 // exactly one logical split's state.
 // Two waves per SIMD (<= 256 VGPRs) except for float32 K/V, whose raw K and
 // V tiles alone take 256 registers.
+// The kDW wave states of a workgroup merged into its split partial.  Partial
+// index of query head h in slot p of the row: pbase + h * hstride + p *
+// qstride ((row * G + h) * Pg + p, or with the flat layout (slot0 + p) * G +
+// h).  acc_of(w, g, c): wave w's accumulator of head g, column c.
+template <int D, int GT, int kDW, typename AccOf>
+__device__ __forceinline__ void write_partial(const DecodeArgs& a, int g0, int g_active, int gidx, int64_t pbase,
+                                              int hstride, int qstride, const float (*sh_m)[GT],
+                                              const float (*sh_l)[GT], AccOf acc_of) {
+  for (int idx = threadIdx.x; idx < g_active * D; idx += kDW * kWave) {
+    const int g = idx / D;
+    const int c = idx - g * D;
+    float mx = sh_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kDW; ++w) mx = fmaxf(mx, sh_m[w][g]);
+    float acc = 0.f, l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDW; ++w) {
+      const float e = __expf(sh_m[w][g] - mx);
+      acc = __builtin_fmaf(acc_of(w, g, c), e, acc);
+      l = __builtin_fmaf(sh_l[w][g], e, l);
+    }
+    const int64_t pidx = pbase + (int64_t)(g0 + g) * hstride + (int64_t)gidx * qstride;
+    // agent-scope stores write through this XCD's L2, so the fused merge
+    // (possibly on another XCD) reads them without a cache write-back
+    __hip_atomic_store(a.pacc + pidx * D + c, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c == 0) {
+      __hip_atomic_store(a.pm + pidx, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.pl + pidx, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK, bool LOOP>
 __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
     const DecodeArgs a) {
@@ -2419,14 +2451,7 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   __shared__ float sh_p[MQK ? kDW * 64 * (GT > 4 ? 8 : 4) : 1];  // per wave p[head][token] of the current tile (MQK)
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[MQK ? kDW * 64 * D : 8];  // per wave V tile (MQK)
 
-  bool fast_done = false;
-  if constexpr (MQK && LOOP) {
-    if (a.fast) {
-      decode_fast<DT, D, GT, PAGED>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
-      fast_done = true;
-    }
-  }
-  if (!fast_done) {
+  {
     // cached mode: fetch the scores before anything else (balanced: tiles
     // threadIdx.x + 256k of the first kPreChunks chunks; otherwise the lane's
     // entry of the first chunk of the split list)
@@ -2629,35 +2654,12 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
     }
   }
 
-  // merge the eight wave states into the split's partial.  Partial index of
-  // query head h in slot p of the row: (row * G + h) * Pg + p, or with the
-  // flat layout (slot0 + p) * G + h
   const int64_t pbase = a.flat ? (int64_t)slot0 * a.G : (int64_t)row * a.G * a.Pg;
   const int hstride = a.flat ? 1 : a.Pg;
   const int qstride = a.flat ? a.G : 1;
-  for (int idx = threadIdx.x; idx < g_active * D; idx += kDT) {
-    const int g = idx / D;
-    const int c = idx - g * D;
-    float mx = sh_m[0][g];
-#pragma unroll
-    for (int w = 1; w < kDW; ++w) mx = fmaxf(mx, sh_m[w][g]);
-    float acc = 0.f, l = 0.f;
-#pragma unroll
-    for (int w = 0; w < kDW; ++w) {
-      const float e = __expf(sh_m[w][g] - mx);
-      const float aw = MQK ? reinterpret_cast<const float*>(sh_v + w * 64 * D)[g * D + c] : sh_acc[MQK ? 0 : w][g][c];
-      acc = __builtin_fmaf(aw, e, acc);
-      l = __builtin_fmaf(sh_l[w][g], e, l);
-    }
-    const int64_t pidx = pbase + (int64_t)(g0 + g) * hstride + (int64_t)gidx * qstride;
-    // agent-scope stores write through this XCD's L2, so the fused merge
-    // (possibly on another XCD) reads them without a cache write-back
-    __hip_atomic_store(a.pacc + pidx * D + c, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (c == 0) {
-      __hip_atomic_store(a.pm + pidx, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.pl + pidx, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  write_partial<D, GT, kDW>(a, g0, g_active, gidx, pbase, hstride, qstride, sh_m, sh_l, [&](int w, int g, int c) {
+    return MQK ? reinterpret_cast<const float*>(sh_v + w * 64 * D)[g * D + c] : sh_acc[MQK ? 0 : w][g][c];
+  });
   if (a.split_counts && threadIdx.x == 0 && blockIdx.z == 0)
   {
     int n = 0;
@@ -2670,6 +2672,39 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
   float* sh_w = MQK ? reinterpret_cast<float*>(sh_v) : &sh_acc[0][0][0];
   float4* sh_red = MQK ? reinterpret_cast<float4*>(sh_v + kDW * 64 * D / 2) : sh_red_own;
   if (a.fuse) merge_if_last<D, GT, kDW>(a, row, g0, g_active, sh_w, &sh_l[0][0], sh_red, npg, pbase, hstride, qstride);
+}
+
+// The decode with the per-wave prologue (decode_fast; a.fast, set by the
+// host): kDW waves per workgroup, every query head of a row in one
+// workgroup (GT >= G).  kDW = 8 fills a CU with one workgroup; kDW = 4 (the
+// flat layout's many small workgroups) lets two share a CU, so that one's
+// prologue overlaps the other's tile loop.
+template <int DT, int D, int GT, bool PAGED, int kDW>
+__global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_fast_kernel(
+    const DecodeArgs a) {
+  const int g_active = min(GT, a.G);
+  int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0;
+  if (a.flat) {
+    __shared__ int sh_fm[2 * kDW + 8];
+    if (!flat_map<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0)) return;
+  }
+  const RowInfo ri = row_info(a, row);
+  __shared__ float sh_m[kDW][GT];
+  __shared__ float sh_l[kDW][GT];
+  __shared__ int sh_cnt[kDW + 1];
+  __shared__ __attribute__((aligned(16))) uint16_t sh_v[kDW * 64 * D];  // per wave V tile, then its state
+  decode_fast<DT, D, GT, PAGED, kDW>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
+  __syncthreads();
+  const int64_t pbase = a.flat ? (int64_t)slot0 * a.G : (int64_t)row * a.G * a.Pg;
+  const int hstride = a.flat ? 1 : a.Pg;
+  const int qstride = a.flat ? a.G : 1;
+  write_partial<D, GT, kDW>(a, 0, g_active, gidx, pbase, hstride, qstride, sh_m, sh_l, [&](int w, int g, int c) {
+    return reinterpret_cast<const float*>(sh_v + w * 64 * D)[g * D + c];
+  });
+  // merge scratch inside the (idle) V slots: GT * Pg weights, one float4 per thread
+  if (a.fuse)
+    merge_if_last<D, GT, kDW>(a, row, 0, g_active, reinterpret_cast<float*>(sh_v), &sh_l[0][0],
+                              reinterpret_cast<float4*>(sh_v + kDW * 64 * D / 2), npg, pbase, hstride, qstride);
 }
 
 // Tile scoring: one wave per (row, tile); block = 4 waves.
@@ -2814,8 +2849,26 @@ hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_band(const DecodeArgs& a, int head_dim, hipStream_t st);
 
+template <int DT, int HD, bool PG, int W>
+inline void launch_fast_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  const dim3 block(W * kWave);
+  switch (gt) {
+    case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 1, PG, W>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 2, PG, W>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 4, PG, W>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 8, PG, W>), grid, block, 0, st, a); break;
+  }
+}
+
 template <int DT, int HD, bool DOT2, bool PG, bool MQ, bool LOOP>
 inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  if constexpr (MQ && LOOP) {
+    if (a.fast) {
+      if (a.fast_waves == 4) launch_fast_gt<DT, HD, PG, 4>(a, gt, grid, st);
+      else launch_fast_gt<DT, HD, PG, 8>(a, gt, grid, st);
+      return;
+    }
+  }
   const dim3 block(DecWaves<DT, HD>::value * kWave);
   switch (gt) {
     case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
