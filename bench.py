@@ -57,6 +57,9 @@ def parse():
                     help="host seconds spent on the cpu_baseline sample (0 = skip)")
     ap.add_argument("--read-probe", type=int, default=1, help="also time the streaming-read probe (0 = skip)")
     ap.add_argument("--spw", type=int, default=0, help="logical splits per workgroup (0 = library default)")
+    ap.add_argument("--q-dtype", choices=["bf16", "f32"], default="bf16",
+                    help="q of the primary workload: f32 (the same values) runs q . k on the VALU path, for "
+                         "comparing its instruction mix with the matrix-core path's (with --only)")
     ap.add_argument("--variants", default="",
                     help="with --only paged/fp8: comma-separated subset of cached,single_pass,dense")
     ap.add_argument("--extra-configs", type=int, default=1,
@@ -76,7 +79,7 @@ class Setup:
     """Device buffers, cached scores and prebuilt C-ABI parameter blocks for
     one batch size."""
 
-    def __init__(self, batch, seed=0, spw=0):
+    def __init__(self, batch, seed=0, spw=0, q_dtype="bf16"):
         import torch
         from orthocache_gpu import _launch as X
         from orthocache_gpu import _native as N
@@ -96,6 +99,8 @@ class Setup:
         for i in range(self.nsets):
             wl = make_kv(self.rows, S, D, noise_frac=0.5, dtype=torch.bfloat16, device=dev, seed=seed + 17 * i)
             q = make_q(self.rows, G, D, dtype=torch.bfloat16, device=dev, seed=seed + 17 * i + 1)
+            if q_dtype == "f32":
+                q = q.float()  # the same values; q . k then runs on the VALU path
             sc = score_tiles(wl.keys)
             self.sets.append({"wl": wl, "q": q, "scores": sc})
         # one tau for all sets (the clusters are the same by construction)
@@ -119,7 +124,7 @@ class Setup:
         p = N.OcDecodeParams()
         p.kv = kv.struct()
         p.q = st["q"].data_ptr()
-        p.q_dtype = N.OC_BF16
+        p.q_dtype = N.OC_F32 if st["q"].dtype == self.torch.float32 else N.OC_BF16
         p.G = G
         p.q_row_stride = st["q"].stride(0)
         p.gate = N.OC_GATE_NONE if variant == "dense" else N.OC_GATE_CS
@@ -873,7 +878,7 @@ def main():
         variants = tuple(args.variants.split(",")) if args.variants else ("cached", "single_pass", "dense")
         print(json.dumps(dict(only=args.only, **ExtraConfig(args.only).measure(args.steps, args.warmup, variants))))
         return
-    primary = Setup(args.batch, spw=args.spw)
+    primary = Setup(args.batch, spw=args.spw, q_dtype=args.q_dtype)
     if args.only:
         v = args.only
         us = primary.time(v, args.steps, args.warmup)
