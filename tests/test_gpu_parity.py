@@ -605,6 +605,37 @@ def test_paged_bad_block_id_rejected(dtype):
         fused_orthocache_attention_paged(q, kc, kc, bt, 5.0)
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_paged_bad_block_id_rejected_matrix_core(bs):
+    """The same check on the matrix-core path with the per-wave prologue
+    (bf16, pages of >= 16 tokens, cached mode over rows of given lengths):
+    an id outside the pool, in a tile past the first, reads as zeros and
+    raises, and the valid table gives the oracle's output."""
+    from orthocache_gpu import fused_orthocache_attention_paged
+    from orthocache_gpu.triton_kernels.paged_eviction import score_paged_tiles
+    g = torch.Generator().manual_seed(5)
+    hkv, G, d, nb = 2, 2, 64, 32
+    blocks = 256 // bs
+    q = torch.randn(1, hkv * G, d, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(nb, hkv, bs, d, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(nb, hkv, bs, d, generator=g).to(torch.bfloat16).to(DEV)
+    bt = torch.randperm(nb, generator=g)[:blocks].to(torch.int32).view(1, -1).to(DEV)
+    lens = torch.tensor([250], dtype=torch.int32, device=DEV)
+    sc = score_paged_tiles(kc, bt, context_lens=lens)
+    out, _ = fused_orthocache_attention_paged(q, kc, vc, bt, 5.0, num_query_groups=G, tau=-1.0,
+                                              context_lens=lens, mode="cached", score_cache=sc)
+    k_rows = kc[bt[0].long()].permute(1, 0, 2, 3).reshape(hkv, -1, d)[:, :250]
+    v_rows = vc[bt[0].long()].permute(1, 0, 2, 3).reshape(hkv, -1, d)[:, :250]
+    ref = np.stack([O.dense_decode(np32(q[0, h * G:(h + 1) * G]), np.broadcast_to(np32(k_rows[h]), (G, 250, d)),
+                                   np.broadcast_to(np32(v_rows[h]), (G, 250, d))) for h in range(hkv)])
+    assert_out(out[0], ref.reshape(hkv * G, d), "bf16", f"paged matrix-core bs={bs}")
+    bad = bt.clone()
+    bad[0, blocks - 2] = nb + 7
+    with pytest.raises(ValueError, match="block id"):
+        fused_orthocache_attention_paged(q, kc, vc, bad, 5.0, num_query_groups=G, tau=-1.0, context_lens=lens,
+                                         mode="cached", score_cache=sc)
+
+
 # ---------------------------------------------------------------- full size properties
 
 @pytest.mark.parametrize("gate", ["cs", "zeta"])
