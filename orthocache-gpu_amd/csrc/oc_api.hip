@@ -395,11 +395,14 @@ static bool fused_merge(const oc_decode_params* p, int pg) {
 }
 
 // Rows of different lengths (a lengths array) are laid out flat: row r gets
-// workgroups in proportion to its tiles, about kFlatPerCU per CU in all
-// (flat_map in the kernel), with the merge fused.  Not with partials
-// requested (their layout is the per-split one), per-split counts, or a
-// cached decode too long for the in-LDS retained-tile bitmask.
-static constexpr int kFlatPerCU = 4;
+// workgroups in proportion to its tiles, about g_flat_per_cu per CU in all
+// (flat_map in the kernel; flat_map_lpt, long shares first, in the
+// per-wave-prologue kernel, with g_flat_pct percent of each row's tiles in
+// long shares and short shares 1 / g_flat_div as long), with the merge
+// fused.  Not with partials requested (their layout is the per-split one),
+// per-split counts, or a cached decode too long for the in-LDS retained-tile
+// bitmask.
+static int g_flat_per_cu = 4, g_flat_pct = 90, g_flat_div = 4;
 
 static bool flat_layout(const oc_decode_params* p) {
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
@@ -409,7 +412,24 @@ static bool flat_layout(const oc_decode_params* p) {
          fused_merge(p, 1);
 }
 
-static int flat_target() { return kFlatPerCU * device_cus(); }
+static int flat_target() { return g_flat_per_cu * device_cus(); }
+
+// partial slots of the flat layout: flat_map_lpt's bound, which also covers
+// flat_map's flat_target + rows
+static size_t flat_slots(const oc_decode_params* p) {
+  return (size_t)flat_lpt_slots(flat_target(), p->kv.num_rows, g_flat_pct, g_flat_div);
+}
+
+// Measurement hook (not declared in the public header): the flat layout's
+// workgroups per CU (1..16), percent of tiles in long shares (0..100) and
+// short-share divisor (1..16).  Returns 0, or -1 for values out of range.
+extern "C" int oc_internal_flat_tuning(int per_cu, int pct, int div) {
+  if (per_cu < 1 || per_cu > 16 || pct < 0 || pct > 100 || div < 1 || div > 16) return -1;
+  g_flat_per_cu = per_cu;
+  g_flat_pct = pct;
+  g_flat_div = div;
+  return 0;
+}
 
 extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   if (!p || p->num_splits <= 0 || p->G <= 0) return 0;
@@ -417,9 +437,8 @@ extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {
   if (partials_given && !p->out) return 0;
   size_t n = 256 + (p->out ? kCounterBytes : 0);
   if (flat_layout(p)) {
-    // one partial per (slot, query head); slots = target + rows
-    const size_t slots = (size_t)flat_target() + (size_t)p->kv.num_rows;
-    return n + slots * (size_t)p->G * (2 + (size_t)p->kv.head_dim) * sizeof(float);
+    // one partial per (slot, query head)
+    return n + flat_slots(p) * (size_t)p->G * (2 + (size_t)p->kv.head_dim) * sizeof(float);
   }
   const int pg = num_groups(p, choose_spw(p));
   if (!partials_given) n += partial_floats(p, pg) * sizeof(float);
@@ -486,6 +505,9 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   a.Pg = num_groups(p, a.spw);
   a.flat = flat_layout(p) ? 1 : 0;
   a.flat_target = flat_target();
+  a.flat_pct = g_flat_pct;
+  a.flat_div = g_flat_div;
+  a.flat_slots = a.flat ? (int)flat_slots(p) : 0;
   a.keep_out = p->keep_out;
   a.keep_stride = p->keep_row_stride;
   a.split_counts = p->split_counts;
@@ -507,7 +529,7 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
     a.pl = p->partial_l;
     a.pacc = p->partial_acc;
   } else {
-    const size_t rq = a.flat ? ((size_t)a.flat_target + p->kv.num_rows) * p->G : (size_t)p->kv.num_rows * p->G * a.Pg;
+    const size_t rq = a.flat ? flat_slots(p) * p->G : (size_t)p->kv.num_rows * p->G * a.Pg;
     a.pacc = (float*)w;
     a.pm = a.pacc + rq * D;
     a.pl = a.pm + rq;
@@ -546,7 +568,8 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
     // workgroups per CU, so that one's prologue overlaps the other's loop
     a.fast_waves = a.flat ? 4 : 8;
     if (hk) {
-      if (!a.fast || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
+      // the row statistics come from a pass over the whole row (not flat)
+      if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
       a.gate = kGateHook;
       a.hk_norms = hk->norms;
       a.hk_stride = hk->stride;

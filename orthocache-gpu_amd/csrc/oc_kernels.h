@@ -102,6 +102,10 @@ struct DecodeArgs {
   // (flat_map) and its partials live at slots [first slot of r, + q_r)
   int32_t flat;
   int32_t flat_target;  // workgroups the flat layout aims at (slots = flat_target + num_rows)
+  // decode_fast_kernel's flat layout (flat_map_lpt): percent of each row's
+  // tiles in long shares, the short shares' size divisor, and the slot
+  // bound (flat_lpt_slots) that sizes its grid and partials
+  int32_t flat_pct, flat_div, flat_slots;
   // the per-wave prologue of decode_fast_kernel (set by the host when it
   // applies) and that kernel's waves per workgroup (4 or 8)
   int32_t fast, fast_waves;
@@ -361,13 +365,19 @@ struct RowInfo {
   int seq, head;   // paged: sequence and kv head of the row
 };
 
-__device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) {
-  RowInfo ri;
+// tokens of row r: its length clamped to the row capacity
+__device__ __forceinline__ int row_tokens(const DecodeArgs& a, int r) {
   int n = a.row_tok > 0 ? a.row_tok : a.num_tiles * 64;
   if (a.lengths) {
-    const int len = a.lengths[row / a.rows_per_length];
+    const int len = a.lengths[r / a.rows_per_length];
     n = len < 0 ? 0 : (len < n ? len : n);
   }
+  return n;
+}
+
+// row info from the row's token count n (row_tokens)
+__device__ __forceinline__ RowInfo row_info_n(const DecodeArgs& a, int row, int n) {
+  RowInfo ri;
   ri.n_tok = n;
   ri.n_tiles = (n + 63) >> 6;
   if (a.paged) {
@@ -379,6 +389,8 @@ __device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) {
   }
   return ri;
 }
+
+__device__ __forceinline__ RowInfo row_info(const DecodeArgs& a, int row) { return row_info_n(a, row, row_tokens(a, row)); }
 
 // Cache policy of the K/V tile loads: non-temporal (the buffer instructions'
 // nt bit).  K and V are streamed once per decode step; on MI355X nt loads
@@ -1483,14 +1495,7 @@ __device__ __forceinline__ TileList split_list(const DecodeArgs& a, const RowInf
   return tl;
 }
 
-__device__ __forceinline__ int row_tiles(const DecodeArgs& a, int r) {
-  int n = a.row_tok > 0 ? a.row_tok : a.num_tiles * 64;
-  if (a.lengths) {
-    const int len = a.lengths[r / a.rows_per_length];
-    n = len < 0 ? 0 : (len < n ? len : n);
-  }
-  return (n + 63) >> 6;
-}
+__device__ __forceinline__ int row_tiles(const DecodeArgs& a, int r) { return (row_tokens(a, r) + 63) >> 6; }
 
 // Flat workgroup layout for rows of different lengths.  With N tiles in all
 // and n_max in the longest row, U = max(ceil(N / flat_target),
@@ -1555,6 +1560,157 @@ __device__ __forceinline__ bool flat_map(const DecodeArgs& a, int qcap, int* sh_
   g = sh_i[2 * kDW + 5];
   q = sh_i[2 * kDW + 6];
   slot0 = sh_i[2 * kDW + 7];
+  return row >= 0;
+}
+
+// Slots of flat_map_lpt's layout, a bound on its share count for w =
+// flat_target and `rows` rows: the long shares number at most w pct / 100 and
+// the short ones fewer than w (100 - pct) div / 100 + rows (div + 1).
+__host__ __device__ inline int flat_lpt_slots(int w, int rows, int pct, int div) {
+  return (int)((int64_t)w * pct / 100 + ((int64_t)w * (100 - pct) * div + 99) / 100 + (int64_t)rows * (div + 1) + 1);
+}
+
+// The flat layout of decode_fast_kernel, longest shares first.  With N
+// tiles in all, n_max in the longest row and W = flat_target, shares are
+// cut from U = max(ceil(N / W), ceil(n_max f / (qcap - div - 1)), 1) tiles,
+// f = (pct + (100 - pct) div) / 100.  Row r (n_r tiles) gets
+// b_r = floor(n_r pct / (100 U)) long shares, tiles [g U, (g + 1) U), and its
+// other L_r = n_r - b_r U tiles are cut into s_r = ceil(L_r / V) short shares
+// of about V = ceil(U / div) tiles (tiles b_r U + floor(L_r h / s_r) ..; an
+// empty row gets one empty share).  blockIdx.x numbers every row's long
+// shares, row after row, then every row's short shares, so the hardware
+// dispatches the long shares first and the short ones fill the end of the
+// step.  A workgroup gets its row, its share index g among the row's
+// q = b_r + s_r shares (its partials' slot, <= qcap), the row's first slot
+// and its tile range [b0, b1); false for the slots past the last share.
+// Three passes over the rows: totals, long-share count, lookup; the
+// lengths are read once (rows threadIdx.x + k kDT, k < 4, kept in
+// registers; the rows past those are read again in each pass).  ntok: the
+// row's tokens.  sh_i: 4 kDW + 9 ints of LDS.
+template <int kDW>
+__device__ __forceinline__ bool flat_map_lpt(const DecodeArgs& a, int qcap, int* sh_i, int& row, int& g, int& q,
+                                             int& slot0, int& b0, int& b1, int& ntok) {
+  constexpr int kDT = kDW * kWave;
+  constexpr int kKeep = 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int bid = blockIdx.x;
+  const int pct = a.flat_pct, div = a.flat_div;
+  int kept_tok[kKeep];
+#pragma unroll
+  for (int k = 0; k < kKeep; ++k) {
+    const int r = threadIdx.x + k * kDT;
+    kept_tok[k] = r < a.num_rows ? row_tokens(a, r) : 0;
+  }
+  // tokens of row r = threadIdx.x + k kDT (0 past the last row)
+  auto tokens = [&](int k, int r) -> int {
+    if (r >= a.num_rows) return 0;
+    if (k >= kKeep) return row_tokens(a, r);
+    int n = kept_tok[0];
+#pragma unroll
+    for (int j = 1; j < kKeep; ++j) n = k == j ? kept_tok[j] : n;
+    return n;
+  };
+  int sum = 0, mx = 0;
+  for (int k = 0, r = threadIdx.x; r < a.num_rows; r += kDT, ++k) {
+    const int n = (tokens(k, r) + 63) >> 6;
+    sum += n;
+    mx = max(mx, n);
+  }
+  sum = wave_incl_scan(sum);
+  mx = (int)wave_max((float)mx);  // exact: a row has < 2^24 tiles
+  if (threadIdx.x == 0) sh_i[4 * kDW + 4] = -1;
+  if (lane == 63) sh_i[wave] = sum;
+  if (lane == 0) sh_i[kDW + wave] = mx;
+  __syncthreads();
+  int total = 0, nmax = 0;
+#pragma unroll
+  for (int w = 0; w < kDW; ++w) {
+    total += sh_i[w];
+    nmax = max(nmax, sh_i[kDW + w]);
+  }
+  const int64_t f100 = pct + (int64_t)(100 - pct) * div;
+  const int ucap = (int)(((int64_t)nmax * f100 + 100LL * (qcap - div - 1) - 1) / (100LL * (qcap - div - 1)));
+  const int U = max(1, max((total + a.flat_target - 1) / a.flat_target, ucap));
+  const int V = (U + div - 1) / div;
+  auto cut = [&](int k, int r, int& nb, int& ns, int& n) {
+    n = (tokens(k, r) + 63) >> 6;
+    nb = (int)((int64_t)n * pct / (100LL * U));
+    ns = r < a.num_rows ? (n == 0 ? 1 : (n - nb * U + V - 1) / V) : 0;
+  };
+  // pass 2: the number of long shares
+  int nbs = 0;
+  for (int k = 0, r = threadIdx.x; r < a.num_rows; r += kDT, ++k) {
+    int nb, ns, n;
+    cut(k, r, nb, ns, n);
+    nbs += nb;
+  }
+  nbs = wave_incl_scan(nbs);
+  __syncthreads();  // sh_i[0 .. 2 kDW) is reused
+  if (lane == 63) sh_i[wave] = nbs;
+  __syncthreads();
+  int NB = 0;
+#pragma unroll
+  for (int w = 0; w < kDW; ++w) NB += sh_i[w];
+  // pass 3: this slot's share
+  int cb = 0, cs = 0, ca = 0;  // long, short and all shares of the rows before the chunk
+  for (int c = 0; c < a.num_rows; c += kDT) {
+    __syncthreads();  // sh_i[0 .. 3 kDW) is reused
+    const int r = c + threadIdx.x;
+    int nb, ns, n;
+    cut(c / kDT, r, nb, ns, n);
+    const int ib = wave_incl_scan(nb), is = wave_incl_scan(ns), ia = wave_incl_scan(nb + ns);
+    if (lane == 63) {
+      sh_i[wave] = ib;
+      sh_i[kDW + wave] = is;
+      sh_i[2 * kDW + wave] = ia;
+    }
+    __syncthreads();
+    int pb = cb, ps = cs, pa = ca, tb = 0, ts = 0, ta = 0;
+#pragma unroll
+    for (int w = 0; w < kDW; ++w) {
+      const int xb = sh_i[w], xs = sh_i[kDW + w], xa = sh_i[2 * kDW + w];
+      pb += w < wave ? xb : 0;
+      ps += w < wave ? xs : 0;
+      pa += w < wave ? xa : 0;
+      tb += xb;
+      ts += xs;
+      ta += xa;
+    }
+    const int fb = pb + ib - nb, fs = NB + ps + is - ns;  // first blockIdx of the row's long / short shares
+    int gi = -1, lo = 0, hi = 0;
+    if (nb > 0 && fb <= bid && bid < fb + nb) {
+      gi = bid - fb;
+      lo = gi * U;
+      hi = lo + U;
+    } else if (ns > 0 && fs <= bid && bid < fs + ns) {
+      const int h = bid - fs;
+      const int L = n - nb * U;
+      gi = nb + h;
+      lo = nb * U + (int)((int64_t)L * h / ns);
+      hi = nb * U + (int)((int64_t)L * (h + 1) / ns);
+    }
+    if (gi >= 0) {
+      sh_i[4 * kDW + 4] = r;
+      sh_i[4 * kDW + 5] = gi;
+      sh_i[4 * kDW + 6] = nb + ns;
+      sh_i[4 * kDW + 7] = pa + ia - nb - ns;
+      sh_i[3 * kDW] = lo;
+      sh_i[3 * kDW + 1] = hi;
+      sh_i[4 * kDW + 8] = tokens(c / kDT, r);
+    }
+    cb += tb;
+    cs += ts;
+    ca += ta;
+  }
+  __syncthreads();
+  row = sh_i[4 * kDW + 4];
+  g = sh_i[4 * kDW + 5];
+  q = sh_i[4 * kDW + 6];
+  slot0 = sh_i[4 * kDW + 7];
+  b0 = sh_i[3 * kDW];
+  b1 = sh_i[3 * kDW + 1];
+  ntok = sh_i[4 * kDW + 8];
   return row >= 0;
 }
 
@@ -1881,15 +2037,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // 64 * kFastChunks tiles per row) or dense decode, q of the matrix-core type,
 // all G <= GT query heads of a row in one workgroup.  Every wave forms by
 // itself, from global memory: the matrix-core q operand, the row's q norms,
-// the row's retained-tile bitmask (lane c holds the bits of tiles 64c ..
-// 64c + 63, with their inclusive prefix counts over the lanes), the
-// workgroup's even share [r0, r1) of the row's retained tiles (dense: of its
-// tiles) and its first rank r0 + wave.  It issues that tile's K and V loads
+// the retained-tile bitmask of the tile range [b0, b1) (lane c holds the
+// bits of tiles b0 + 64c .. + 63, with their inclusive prefix counts over the
+// lanes), the workgroup's even share [r0, r1) of the range's retained tiles
+// (dense: of its tiles; share gidx of npg) and its first rank r0 + wave.  It issues that tile's K and V loads
 // before the workgroup's one barrier, which publishes the LDS counter the
 // later ranks are drawn from (a wave whose tiles arrived sooner takes more).
 // The wave's state goes to LDS as decode_body leaves it.
 template <int DT, int D, int GT, bool PAGED, int kDW>
-__device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg,
+__device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg, int b0, int b1,
                                             float (*sh_m)[GT], float (*sh_l)[GT], int* sh_cnt, uint16_t* sh_v) {
   constexpr bool F8 = DT == OC_FP8_E4M3FN;
   constexpr int QT = MfmaT<DT>::value;  // q's 16-bit type
@@ -1898,7 +2054,6 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int x = lane & 15, kg = lane >> 4;
   const bool cached = a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE;
-  const int T = ri.n_tiles;
 
   // q operand (B of S^T = K.q^T): lane 16 kg + x holds q[head x] columns
   // 32 dc + 8 kg .. + 8 (fp8 K: kg D / 4 + 8 dc ..), zero past G; one 16-byte
@@ -1924,7 +2079,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   // overlaps q's; indices are clamped into the row and masked after.  (All
   // kFastChunks chunks in one batch, with uniform branches past the row,
   // measured no faster on long rows and slower on short ones.)
-  const int nch = (T + 63) >> 6;
+  const int nch = (b1 - b0 + 63) >> 6;
   uint32_t wlo = 0u, whi = 0u;
   auto score_pass = [&](auto gate_tag) {
     constexpr int GATE = decltype(gate_tag)::value;
@@ -1934,7 +2089,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     auto load_scores = [&](int c0) {
 #pragma unroll
       for (int k = 0; k < kFastBatch; ++k) {
-        const int t = min((c0 + k) * 64 + lane, T - 1);
+        const int t = min(b0 + (c0 + k) * 64 + lane, b1 - 1);  // b1 > b0 here
         el[k] = 0.f;
         if constexpr (HOOK) {
           // the complete tiles' norms (a partial tail reads the last one's)
@@ -1947,7 +2102,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
         }
       }
     };
-    load_scores(0);
+    if (nch > 0) load_scores(0);
     load_q();
     // max over the row's G heads of ||q_g||_2 (CS gate; norms below 1e-38
     // count as 0): head x's squares summed over its four lane groups
@@ -2036,14 +2191,14 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
       for (int k = 0; k < kFastBatch; ++k) {
         const int c = c0 + k;
         if (c < nch) {
-          const int t = c * 64 + lane;
+          const int t = b0 + c * 64 + lane;
           // cached_keep with the gate fixed: a partial last tile is kept
           // (score gates), the mask byte decides (mask gate)
           bool keep;
           if constexpr (HOOK) {
             const bool full = t < a.hk_full;
             const bool ev = full && (double)qn * (double)eh[k] <= a.hk_tau;
-            keep = !ev && t < T;
+            keep = !ev && t < b1;
             if (full) {
               nev += ev ? 1.f : 0.f;
               kmax = fmaxf(kmax, eh[k]);
@@ -2052,7 +2207,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
           } else {
             keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
             if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
-            keep = keep && t < T;
+            keep = keep && t < b1;
           }
           const uint64_t m = __ballot(keep);
           if (lane == c) {
@@ -2060,7 +2215,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
             whi = (uint32_t)(m >> 32);
           }
           // the keep flags, by the row's first workgroup (chunk c by wave c mod waves)
-          if (keep_wr && (c % kDW) == wave && t < T) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+          if (keep_wr && (c % kDW) == wave && t < b1) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
         }
       }
     }
@@ -2079,6 +2234,17 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
       }
     }
   };
+  // paged: the block-table entries of the range's first 16 tiles (lane 4 d
+  // + j: tile b0 + d, 16-token block j; tokens past the row read its last
+  // block's entry), requested with the scores, so that a wave whose first
+  // tile is among them needs no further round trip before its K and V
+  int spec_ids = 0;
+  if constexpr (PAGED) {
+    if (ri.n_tok > 0) {
+      const int tok = min(b0 * 64 + 16 * lane, ri.n_tok - 1);
+      spec_ids = a.bt[(int64_t)ri.seq * a.bt_stride + (tok >> a.bs_log2)];
+    }
+  }
   if (!cached) load_q();
   else if (a.gate == OC_GATE_CS) score_pass(std::integral_constant<int, OC_GATE_CS>{});
   else if (!F8 && a.gate == kGateHook) score_pass(std::integral_constant<int, F8 ? OC_GATE_CS : kGateHook>{});
@@ -2086,12 +2252,12 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   else score_pass(std::integral_constant<int, OC_GATE_MASK>{});
   const int cnt = __popc(wlo) + __popc(whi);
   const int pre = wave_incl_scan(cnt);
-  const int total = cached ? __builtin_amdgcn_readlane(pre, 63) : T;
+  const int total = cached ? __builtin_amdgcn_readlane(pre, 63) : b1 - b0;
   const int r0 = (int)((int64_t)total * gidx / npg);
   const int r1 = (int)((int64_t)total * (gidx + 1) / npg);
   // the tile of retained rank rb (cached) or tile rb (dense); wave-uniform
   auto tile_of_rank = [&](int rb) -> int {
-    if (!cached) return rb;
+    if (!cached) return b0 + rb;
     const int lg = __popcll((unsigned long long)__ballot(pre <= rb));  // chunk holding rank rb
     const int base = __builtin_amdgcn_readlane(pre, lg) - __builtin_amdgcn_readlane(cnt, lg);
     const uint64_t bits = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)whi, lg) << 32) |
@@ -2099,7 +2265,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     const int k = rb - base;
     const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
     const bool hit = ((bits >> lane) & 1ull) && below == k;
-    return __builtin_amdgcn_readfirstlane(lg * 64 + __ffsll((unsigned long long)__ballot(hit)) - 1);
+    return __builtin_amdgcn_readfirstlane(b0 + lg * 64 + __ffsll((unsigned long long)__ballot(hit)) - 1);
   };
   // One tile per wave step.  (Two fp8 tiles per step, which fill the
   // register and LDS footprint of one 16-bit tile, measured slower on 32 rows
@@ -2158,8 +2324,13 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   int t = r0 + wave < r1 ? tile_of_rank(r0 + wave) : -1;
   if (t >= 0) {
     if constexpr (PAGED) {
-      const int ids = request_pages(t);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      int ids;
+      if (t - b0 < 16) {
+        ids = __shfl(spec_ids, 4 * (t - b0) + (lane & 3));
+      } else {
+        ids = request_pages(t);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      }
       take_pages(t, ids);
     }
     issue(t);
@@ -2683,17 +2854,22 @@ template <int DT, int D, int GT, bool PAGED, int kDW>
 __global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_fast_kernel(
     const DecodeArgs a) {
   const int g_active = min(GT, a.G);
-  int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0;
+  int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0, b0 = 0, b1 = 0, ntok = 0;
   if (a.flat) {
-    __shared__ int sh_fm[2 * kDW + 8];
-    if (!flat_map<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0)) return;
+    __shared__ int sh_fm[4 * kDW + 9];
+    if (!flat_map_lpt<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0, b0, b1, ntok)) return;
   }
-  const RowInfo ri = row_info(a, row);
+  const RowInfo ri = a.flat ? row_info_n(a, row, ntok) : row_info(a, row);
+  if (!a.flat) b1 = ri.n_tiles;
   __shared__ float sh_m[kDW][GT];
   __shared__ float sh_l[kDW][GT];
   __shared__ int sh_cnt[kDW + 1];
   __shared__ __attribute__((aligned(16))) uint16_t sh_v[kDW * 64 * D];  // per wave V tile, then its state
-  decode_fast<DT, D, GT, PAGED, kDW>(a, ri, row, gidx, npg, sh_m, sh_l, sh_cnt, sh_v);
+  // flat: the share is the tile range [b0, b1), all of whose retained tiles
+  // the workgroup takes (one split of one); otherwise an even split of the
+  // row's retained ranks (dense: tiles) over its npg workgroups
+  decode_fast<DT, D, GT, PAGED, kDW>(a, ri, row, a.flat ? 0 : gidx, a.flat ? 1 : npg, b0, b1, sh_m, sh_l, sh_cnt,
+                                     sh_v);
   __syncthreads();
   const int64_t pbase = a.flat ? (int64_t)slot0 * a.G : (int64_t)row * a.G * a.Pg;
   const int hstride = a.flat ? 1 : a.Pg;
@@ -2925,7 +3101,8 @@ constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
-    const dim3 grid = a.flat ? dim3(a.flat_target + a.num_rows, 1, gchunks) : dim3(a.Pg, a.num_rows, gchunks); \
+    const dim3 grid = a.flat ? dim3(a.fast ? a.flat_slots : a.flat_target + a.num_rows, 1, gchunks)      \
+                             : dim3(a.Pg, a.num_rows, gchunks);                                   \
     if (kHasDot2<DT> && a.q_dtype == kDot2Q<DT>) {                                               \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \

@@ -11,6 +11,10 @@ checked against what the mathematics fixes (no GPU needed).
 2. flat_map (csrc/oc_kernels.h): rows of different lengths get
    max(1, ceil(n_r / U)) workgroups; every slot below the total must map to
    exactly one (row, share) and the shares must tile each row.
+3. flat_map_lpt (csrc/oc_kernels.h): the same for the long-shares-first
+   layout, whose share count must also stay within flat_lpt_slots (the grid
+   and partial slots the host allocates) and its per-row count within the
+   merge's bound.
 """
 
 import numpy as np
@@ -120,3 +124,95 @@ def test_flat_layout_covers_every_slot_once():
             for g in range(q[r]):
                 cover += range(n[r] * g // q[r], n[r] * (g + 1) // q[r])
             assert cover == list(range(n[r]))
+
+
+def _flat_lpt_slots(w, rows, pct, div):
+    """flat_lpt_slots (csrc/oc_kernels.h): the slot bound the host allocates"""
+    return w * pct // 100 + (w * (100 - pct) * div + 99) // 100 + rows * (div + 1) + 1
+
+
+def _flat_lpt_map(lens, tiles_max, target, qcap, pct, div, kdt=256, mistake=None):
+    """flat_map_lpt (csrc/oc_kernels.h) restated: for every blockIdx below the
+    share count, (row, share index, row's share count, row's first slot, b0,
+    b1), with pass 3's scan done chunk by chunk of kdt rows as the kernel does."""
+    n = [(min(max(l, 0), tiles_max * 64) + 63) // 64 for l in lens]
+    total, nmax = sum(n), max(n)
+    f100 = pct + (100 - pct) * div
+    ucap = -(-nmax * f100 // (100 * (qcap - div - 1)))
+    u = max(1, -(-total // target), ucap)
+    v = -(-u // div)
+
+    def cut(x):
+        nb = x * pct // (100 * u)
+        ns = 1 if x == 0 else -(-(x - nb * u) // v)
+        return nb, ns
+
+    big = sum(cut(x)[0] for x in n)
+    out = {}
+    cb = cs = ca = 0
+    for c in range(0, len(n), kdt):
+        chunk = [cut(x) for x in n[c:c + kdt]]
+        ib = np.cumsum([b for b, _ in chunk])
+        is_ = np.cumsum([s for _, s in chunk])
+        ia = np.cumsum([b + s for b, s in chunk])
+        for j, (nb, ns) in enumerate(chunk):
+            r = c + j
+            fb = cb + int(ib[j]) - nb
+            fs = (0 if mistake == "short_after_long" else big) + cs + int(is_[j]) - ns
+            slot0 = ca + int(ia[j]) - nb - ns
+            for g in range(nb):
+                out.setdefault(fb + g, []).append((r, g, nb + ns, slot0, g * u, (g + 1) * u))
+            L = n[r] - nb * u
+            for h in range(ns):
+                out.setdefault(fs + h, []).append((r, nb + h, nb + ns, slot0, nb * u + L * h // ns,
+                                                   nb * u + L * (h + 1) // ns))
+        cb += int(ib[-1])
+        cs += int(is_[-1])
+        ca += int(ia[-1])
+    return n, out, big
+
+
+def _flat_lpt_check(lens, t_max, target, qcap, pct, div, mistake=None):
+    n, out, big = _flat_lpt_map(lens, t_max, target, qcap, pct, div, mistake=mistake)
+    count = len(out)
+    assert all(len(v) == 1 for v in out.values())                # one share per slot
+    assert sorted(out) == list(range(count))                       # slots 0 .. count-1 all used
+    assert count <= _flat_lpt_slots(target, len(lens), pct, div)   # the grid the host launches
+    cover = {r: [] for r in range(len(n))}
+    slots = set()
+    for bid in range(count):
+        r, g, q, slot0, b0, b1 = out[bid][0]
+        assert q <= qcap                                          # the merge's LDS bound
+        assert 0 <= g < q and (slot0 + g) not in slots
+        slots.add(slot0 + g)
+        cover[r].append((g, b0, b1))
+    assert max(slots) < _flat_lpt_slots(target, len(lens), pct, div)
+    for r in range(len(n)):
+        parts = sorted(cover[r])
+        assert [g for g, _, _ in parts] == list(range(len(parts)))
+        tiles = [t for _, b0, b1 in parts for t in range(b0, b1)]
+        assert tiles == list(range(n[r]))                          # the shares tile the row in order
+    # long shares (U tiles) are numbered before every short one
+    longs = [out[b][0][5] - out[b][0][4] for b in range(big)]
+    assert len(set(longs)) <= 1
+
+
+def test_flat_lpt_layout_tiles_every_row_once():
+    rng = np.random.default_rng(2)
+    for _ in range(200):
+        rows = int(rng.integers(1, 700))
+        t_max = int(rng.integers(1, 3000))
+        lens = [int(rng.choice([0, rng.integers(0, t_max * 64 + 1), t_max * 64, rng.integers(0, 200)]))
+                for _ in range(rows)]
+        target, qcap = int(rng.choice([256, 512, 1024, 2048])), int(rng.choice([256, 512]))
+        pct, div = int(rng.choice([0, 50, 75, 90, 100])), int(rng.choice([1, 2, 4, 8, 16]))
+        _flat_lpt_check(lens, t_max, target, qcap, pct, div)
+
+
+def test_flat_lpt_layout_planted_mistake():
+    # numbering the short shares from 0 (forgetting the long shares before
+    # them) puts two shares on one slot
+    lens = [64 * 700, 64 * 300, 64 * 50]
+    _flat_lpt_check(lens, 700, 64, 512, 75, 4)
+    with pytest.raises(AssertionError):
+        _flat_lpt_check(lens, 700, 64, 512, 75, 4, mistake="short_after_long")
