@@ -103,6 +103,13 @@ extern "C" {
 #define OC_KSCALE_Q_FOLD 1   /* q := round_qdtype(float(q) * k_scale), k = float(k_elem)
                                 (fused_eviction.py:619-621, gqa_eviction.py:565-567) */
 #define OC_KSCALE_TILE 3     /* k = float(k_elem) * k_scales[row, tile]   (extension) */
+#define OC_KSCALE_DEQUANT 4  /* k = round_bf16(float(k_elem) * k_scale): the reference's
+                                k_cache.to(q.dtype) * k_scale (paged_eviction.py:354-357)
+                                done in-kernel, for fp8 K: by oc_score_tiles /
+                                oc_score_tile_range, and by oc_decode / oc_decode_static
+                                for bf16 q in cached or dense decodes that take the
+                                per-wave-prologue kernel (else OC_ERR_UNSUPPORTED);
+                                other entry points refuse it */
 
 /* V dequantisation */
 #define OC_VSCALE_NONE 0
@@ -128,7 +135,7 @@ extern "C" {
 typedef struct oc_kv_desc {
   const void* k;
   const void* v;
-  int32_t dtype;        /* OC_F32 .. OC_FP8_E4M3FN, same for K and V */
+  int32_t dtype;        /* OC_F32 .. OC_FP8_E4M3FN: K's, and V's unless v_dtype says otherwise */
   int32_t head_dim;     /* 64 or 128 */
   int32_t num_rows;
   int32_t num_tiles;    /* tiles per row (upper bound when lengths != NULL) */
@@ -155,6 +162,12 @@ typedef struct oc_kv_desc {
   const float* v_scales;
   int64_t v_scales_row_stride;
   int32_t* error_flag;      /* optional int32 set non-zero on a bad block id */
+  int32_t v_dtype;          /* 0: V has K's dtype; OC_BF16 with fp8 K: bf16 V read as it
+                               is (extension; the reference's fp8 caches pair an fp8 K
+                               with a wider V, test_fp8.py:43-57).  Entry points that
+                               read no V accept it; oc_decode / oc_decode_static take it
+                               for bf16 q in the per-wave-prologue kernel's cached and
+                               dense decodes, else OC_ERR_UNSUPPORTED */
 } oc_kv_desc;
 
 /*

@@ -33,50 +33,63 @@ static int elem_size(int dt) {
 static bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
 
 // Validates the KV descriptor and fills the layout part of DecodeArgs.
-static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
+// allow_dq: the entry point implements OC_KSCALE_DEQUANT (decode, scoring)
+static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
   if (!kv) return fail(OC_ERR_INVALID, "kv descriptor is NULL");
   const int es = elem_size(kv->dtype);
   if (!es) return fail(OC_ERR_INVALID, "unknown K/V dtype %d", kv->dtype);
+  // V's own element type: K's, or bf16 beside fp8 K
+  const bool v_bf16 = kv->v_dtype != 0 && kv->v_dtype != kv->dtype;
+  if (v_bf16 && (kv->dtype != OC_FP8_E4M3FN || kv->v_dtype != OC_BF16))
+    return fail(OC_ERR_UNSUPPORTED, "V dtype %d beside K dtype %d (a different V type is bf16 beside fp8 K only)",
+                kv->v_dtype, kv->dtype);
+  const int ves = v_bf16 ? 2 : es;
   if (kv->head_dim != 64 && kv->head_dim != 128)
     return fail(OC_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", kv->head_dim);
   if (kv->num_rows < 0 || kv->num_tiles < 0) return fail(OC_ERR_INVALID, "negative sizes");
   if (kv->num_rows > 65535) return fail(OC_ERR_UNSUPPORTED, "num_rows %d > 65535", kv->num_rows);
   if (!kv->k) return fail(OC_ERR_INVALID, "K pointer is NULL");
-  const int64_t lb = (int64_t)(kv->head_dim / 16) * es;  // bytes per lane per token row
-  const int64_t al = lb < 16 ? lb : 16;
-  auto chk = [&](int64_t stride_el, const char* what) -> int {
-    if ((stride_el * es) % al) return fail(OC_ERR_INVALID, "%s stride %lld not a multiple of %lld bytes",
-                                           what, (long long)stride_el, (long long)al);
+  // bytes per lane per token row, and the alignment of every K (V) offset
+  auto align_of = [&](int e) -> int64_t {
+    const int64_t lb = (int64_t)(kv->head_dim / 16) * e;
+    return lb < 16 ? lb : 16;
+  };
+  const int64_t al = align_of(es), val = align_of(ves);
+  auto chk = [&](int64_t stride_el, const char* what, bool is_v) -> int {
+    const int64_t e = is_v ? ves : es, x = is_v ? val : al;
+    if ((stride_el * e) % x) return fail(OC_ERR_INVALID, "%s stride %lld not a multiple of %lld bytes",
+                                         what, (long long)stride_el, (long long)x);
     return OC_OK;
   };
-  if (!aligned(kv->k, al) || (kv->v && !aligned(kv->v, al)))
-    return fail(OC_ERR_INVALID, "K/V base pointers must be %lld-byte aligned", (long long)al);
+  if (!aligned(kv->k, al) || (kv->v && !aligned(kv->v, val)))
+    return fail(OC_ERR_INVALID, "K/V base pointers must be %lld/%lld-byte aligned", (long long)al, (long long)val);
   int rc;
-  if ((rc = chk(kv->k_token_stride, "K token"))) return rc;
-  if (kv->k_token_stride * es * 64 >= ((int64_t)1 << 31) || kv->v_token_stride * es * 64 >= ((int64_t)1 << 31))
+  if ((rc = chk(kv->k_token_stride, "K token", false))) return rc;
+  if (kv->k_token_stride * es * 64 >= ((int64_t)1 << 31) || kv->v_token_stride * ves * 64 >= ((int64_t)1 << 31))
     return fail(OC_ERR_UNSUPPORTED, "token stride too large (64 tokens must span < 2 GiB)");
-  if ((rc = chk(kv->v_token_stride, "V token"))) return rc;
+  if ((rc = chk(kv->v_token_stride, "V token", true))) return rc;
   memset(&a, 0, sizeof a);
   a.k = (const char*)kv->k;
   a.v = (const char*)kv->v;
+  a.v_bf16 = v_bf16 ? 1 : 0;
   a.k_tok_stride = kv->k_token_stride * es;
-  a.v_tok_stride = kv->v_token_stride * es;
+  a.v_tok_stride = kv->v_token_stride * ves;
   a.paged = kv->paged ? 1 : 0;
   if (!a.paged) {
-    if ((rc = chk(kv->k_row_stride, "K row"))) return rc;
-    if ((rc = chk(kv->v_row_stride, "V row"))) return rc;
+    if ((rc = chk(kv->k_row_stride, "K row", false))) return rc;
+    if ((rc = chk(kv->v_row_stride, "V row", true))) return rc;
     a.k_row_stride = kv->k_row_stride * es;
-    a.v_row_stride = kv->v_row_stride * es;
+    a.v_row_stride = kv->v_row_stride * ves;
   } else {
     const int bs = kv->block_size;
     if (bs < 4 || (bs & (bs - 1))) return fail(OC_ERR_INVALID, "block_size %d must be a power of 2 >= 4", bs);
     if (kv->num_kv_heads <= 0 || kv->num_rows % kv->num_kv_heads)
       return fail(OC_ERR_INVALID, "num_rows %d not a multiple of num_kv_heads %d", kv->num_rows, kv->num_kv_heads);
     if (!kv->block_tables) return fail(OC_ERR_INVALID, "block_tables is NULL");
-    if ((rc = chk(kv->k_block_stride, "K block"))) return rc;
-    if ((rc = chk(kv->k_head_stride, "K head"))) return rc;
-    if ((rc = chk(kv->v_block_stride, "V block"))) return rc;
-    if ((rc = chk(kv->v_head_stride, "V head"))) return rc;
+    if ((rc = chk(kv->k_block_stride, "K block", false))) return rc;
+    if ((rc = chk(kv->k_head_stride, "K head", false))) return rc;
+    if ((rc = chk(kv->v_block_stride, "V block", true))) return rc;
+    if ((rc = chk(kv->v_head_stride, "V head", true))) return rc;
     int l2 = 0;
     while ((1 << l2) < bs) ++l2;
     a.bs_log2 = l2;
@@ -86,8 +99,8 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
     a.num_blocks = kv->num_blocks;
     a.k_blk_stride = kv->k_block_stride * es;
     a.k_head_stride = kv->k_head_stride * es;
-    a.v_blk_stride = kv->v_block_stride * es;
-    a.v_head_stride = kv->v_head_stride * es;
+    a.v_blk_stride = kv->v_block_stride * ves;
+    a.v_head_stride = kv->v_head_stride * ves;
   }
   a.rows_per_length = kv->rows_per_length > 0 ? kv->rows_per_length : 1;
   a.lengths = kv->lengths;
@@ -104,8 +117,14 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a) {
   a.v_scales = kv->v_scales;
   a.vs_stride = kv->v_scales_row_stride;
   a.error_flag = kv->error_flag;
-  if (a.k_scale_mode != OC_KSCALE_NONE && a.k_scale_mode != OC_KSCALE_Q_FOLD && a.k_scale_mode != OC_KSCALE_TILE)
+  if (a.k_scale_mode == OC_KSCALE_DEQUANT) {
+    if (!allow_dq)
+      return fail(OC_ERR_UNSUPPORTED, "k_scale_mode OC_KSCALE_DEQUANT is implemented by the decode and scoring only");
+    if (kv->dtype != OC_FP8_E4M3FN) return fail(OC_ERR_INVALID, "OC_KSCALE_DEQUANT needs fp8 K");
+  } else if (a.k_scale_mode != OC_KSCALE_NONE && a.k_scale_mode != OC_KSCALE_Q_FOLD &&
+             a.k_scale_mode != OC_KSCALE_TILE) {
     return fail(OC_ERR_INVALID, "k_scale_mode %d", a.k_scale_mode);
+  }
   if (a.k_scale_mode == OC_KSCALE_TILE && !a.k_scales) return fail(OC_ERR_INVALID, "k_scales is NULL");
   if (a.v_scale_mode == OC_VSCALE_TILE && !a.v_scales) return fail(OC_ERR_INVALID, "v_scales is NULL");
   if (a.v_scale_mode != OC_VSCALE_NONE && a.v_scale_mode != OC_VSCALE_TILE)
@@ -465,9 +484,12 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
                        const HookGate* hk = nullptr) {
   if (!p) return fail(OC_ERR_INVALID, "params is NULL");
   DecodeArgs a;
-  int rc = fill_kv(&p->kv, a);
+  int rc = fill_kv(&p->kv, a, true);
   if (rc) return rc;
   if (!p->kv.v) return fail(OC_ERR_INVALID, "V pointer is NULL");
+  // in-kernel dequantisation runs where fp8 K is widened for the matrix cores
+  if (a.k_scale_mode == OC_KSCALE_DEQUANT && (p->q_dtype != OC_BF16 || (a.paged && a.bs_log2 < 4)))
+    return fail(OC_ERR_UNSUPPORTED, "OC_KSCALE_DEQUANT needs bf16 q and contiguous rows or pages of >= 16 tokens");
   const int D = p->kv.head_dim;
   if (p->G < 1 || p->G > 64) return fail(OC_ERR_UNSUPPORTED, "G=%d outside 1..64", p->G);
   if (p->num_splits < 1 || p->num_splits > 8192) return fail(OC_ERR_INVALID, "num_splits %d outside 1..8192", p->num_splits);
@@ -567,6 +589,14 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
     // the flat layout runs several rounds of small workgroups: two 4-wave
     // workgroups per CU, so that one's prologue overlaps the other's loop
     a.fast_waves = a.flat ? 4 : 8;
+    // in-kernel K dequantisation and bf16 V beside fp8 K: in the
+    // per-wave-prologue kernel only
+    if (a.k_scale_mode == OC_KSCALE_DEQUANT && !a.fast)
+      return fail(OC_ERR_UNSUPPORTED, "OC_KSCALE_DEQUANT: the decode of this shape or mode does not dequantise "
+                                      "K itself (dequantise the pool, or decode cached / dense)");
+    if (a.v_bf16 && !a.fast)
+      return fail(OC_ERR_UNSUPPORTED, "bf16 V beside fp8 K: the decode of this shape or mode reads K and V in one "
+                                      "type (convert one of them, or decode cached / dense)");
     if (hk) {
       // the row statistics come from a pass over the whole row (not flat)
       if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
@@ -753,7 +783,7 @@ extern "C" int oc_decode_static(const oc_decode_params* p, void* stream) {
 extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e_high, float* zeta,
                               uint8_t* keep, int64_t out_row_stride, void* stream) {
   DecodeArgs a;
-  int rc = fill_kv(kv, a);
+  int rc = fill_kv(kv, a, true);
   if (rc) return rc;
   a.thr = zeta_max;
   a.o_el = e_low;
@@ -773,7 +803,7 @@ extern "C" int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int
                                    float* e_low, float* e_high, float* zeta, uint8_t* keep, int64_t out_row_stride,
                                    void* stream) {
   DecodeArgs a;
-  int rc = fill_kv(kv, a);
+  int rc = fill_kv(kv, a, true);
   if (rc) return rc;
   if (first_tile < 0 || count < 0 || (int64_t)first_tile + count > kv->num_tiles)
     return fail(OC_ERR_INVALID, "tile range [%d, %d) outside 0..%d", first_tile, first_tile + count, kv->num_tiles);

@@ -46,6 +46,7 @@ struct DecodeArgs {
   const char* k;
   const char* v;
   int64_t k_row_stride, k_tok_stride, v_row_stride, v_tok_stride;
+  int32_t v_bf16;  // fp8 K with bf16 V (decode_fast only; strides above in bytes)
   int32_t paged, bs_log2, nkv, rows_per_length;
   const int32_t* bt;
   int64_t bt_stride, num_blocks;
@@ -62,7 +63,7 @@ struct DecodeArgs {
   double hk_tau;
   float* hk_stats;
   int32_t k_scale_mode, v_scale_mode;
-  float k_scale;
+  float k_scale;  // OC_KSCALE_Q_FOLD and OC_KSCALE_DEQUANT
   int32_t q_dtype;
   const float* k_scales;
   int64_t ks_stride;
@@ -486,6 +487,9 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const RowInfo& ri
   }
 }
 
+// bf16 round to nearest even of a float32 (NaN stays NaN)
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+
 // Per-tile dequantisation scale: value = float(elem) * mul when `scaled`.
 struct Deq {
   float mul;
@@ -535,7 +539,9 @@ __device__ __forceinline__ void decode_tile(const uint32_t (&w)[16][Lay<DT, D>::
 // `mul` is the tile's dequantisation scale (1 when unscaled: exact).  The
 // multiply is unconditional: a branch here lets the compiler hoist the
 // element conversions of both arms and keep the whole tile live as floats.
-template <int DT, int D>
+// RND (OC_KSCALE_DEQUANT): each scaled element is rounded to bf16, as the
+// reference's k.to(bfloat16) * k_scale before its transform.
+template <int DT, int D, bool RND = false>
 __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D>::LW], const Deq& dq, int lane,
                                               float& e_low, float& e_high) {
   const float mul = dq.mul;
@@ -554,6 +560,10 @@ __device__ __forceinline__ void tile_energies(const uint32_t (&kw)[16][Lay<DT, D
     for (int c = 0; c < CPL; ++c) {
       fa[c] *= mul;
       fb[c] *= mul;
+      if constexpr (RND) {
+        fa[c] = __builtin_bit_cast(float, bf16_bits(fa[c]) << 16);
+        fb[c] = __builtin_bit_cast(float, bf16_bits(fb[c]) << 16);
+      }
     }
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -788,6 +798,28 @@ __device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t
   hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
+
+// OC_KSCALE_DEQUANT: four fp8 values -> bf16(float32(float(k) * s)), the
+// reference's k.to(bfloat16) * k_scale (a float32 product rounded once more to
+// bfloat16).  v_cvt_scalef32_pk_bf16_fp8 cannot do it: it applies only the
+// exponent of its scale operand (measured on the GPU over all 256 codes).
+__device__ __forceinline__ void fp8x4_to_bf16_scaled(uint32_t w, float sc, uint32_t& lo, uint32_t& hi) {
+  const auto p0 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const auto p1 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  lo = bf16_bits(p0[0] * sc) | (bf16_bits(p0[1] * sc) << 16);
+  hi = bf16_bits(p1[0] * sc) | (bf16_bits(p1[1] * sc) << 16);
+}
+
+// how K enters the matrix cores: fp8 widened exactly, or (OC_KSCALE_DEQUANT)
+// scaled and rounded to bf16
+struct KDq {
+  bool on;
+  float s;
+};
+__device__ __forceinline__ KDq k_dq(const DecodeArgs& a) {
+  return KDq{a.k_scale_mode == OC_KSCALE_DEQUANT, a.k_scale};
+}
+
 template <int DT>
 __device__ __forceinline__ f32x4 mfma_qk(const uint32_t (&aq)[4], const uint32_t (&bk)[4], f32x4 c) {
   const u32x4 av = {aq[0], aq[1], aq[2], aq[3]};
@@ -824,10 +856,16 @@ __device__ __forceinline__ void load_q_mfma(const uint32_t* sh_qp, int lane, uin
 // registers: kb[tb][dc] for 16-bit K; for fp8 K the lane's bytes 8*dc .. +8
 // of its D/4-byte row piece (words 2dc, 2dc + 1), widened to bf16.
 template <int DT, int D>
-__device__ __forceinline__ void k_operand(const uint32_t (&kb)[4][D / 32][4], int tb, int dc, uint32_t (&b)[4]) {
+__device__ __forceinline__ void k_operand(const uint32_t (&kb)[4][D / 32][4], int tb, int dc, uint32_t (&b)[4],
+                                          bool dq = false, float sc = 1.f) {
   if constexpr (DT == OC_FP8_E4M3FN) {
-    fp8x4_to_bf16(kb[tb][(2 * dc) >> 2][(2 * dc) & 3], b[0], b[1]);
-    fp8x4_to_bf16(kb[tb][(2 * dc + 1) >> 2][(2 * dc + 1) & 3], b[2], b[3]);
+    if (dq) {
+      fp8x4_to_bf16_scaled(kb[tb][(2 * dc) >> 2][(2 * dc) & 3], sc, b[0], b[1]);
+      fp8x4_to_bf16_scaled(kb[tb][(2 * dc + 1) >> 2][(2 * dc + 1) & 3], sc, b[2], b[3]);
+    } else {
+      fp8x4_to_bf16(kb[tb][(2 * dc) >> 2][(2 * dc) & 3], b[0], b[1]);
+      fp8x4_to_bf16(kb[tb][(2 * dc + 1) >> 2][(2 * dc + 1) & 3], b[2], b[3]);
+    }
   } else {
 #pragma unroll
     for (int w = 0; w < 4; ++w) b[w] = kb[tb][dc][w];
@@ -1333,17 +1371,21 @@ __device__ __forceinline__ void load_k_mfma_t_paged(const DecodeArgs& a, const R
 
 template <int DT, int D>
 __device__ __forceinline__ void tile_logits_t(const uint32_t (&aq)[D / 32][4], const uint32_t (&kb)[4][D / 32][4],
-                                              f32x4 (&c)[4]) {
+                                              f32x4 (&c)[4], KDq kd = KDq{false, 1.f}) {
+  auto run = [&](auto dq_tag) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tb = 0; tb < 4; ++tb) {
+      c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dc = 0; dc < D / 32; ++dc) {
-      uint32_t b[4];
-      k_operand<DT, D>(kb, tb, dc, b);
-      c[tb] = mfma_qk<MfmaT<DT>::value>(b, aq[dc], c[tb]);
+      for (int dc = 0; dc < D / 32; ++dc) {
+        uint32_t b[4];
+        k_operand<DT, D>(kb, tb, dc, b, decltype(dq_tag)::value, kd.s);
+        c[tb] = mfma_qk<MfmaT<DT>::value>(b, aq[dc], c[tb]);
+      }
     }
-  }
+  };
+  if (DT == OC_FP8_E4M3FN && kd.on) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // Online-softmax update of the lane's head from the tile's raw logits (c
@@ -2044,7 +2086,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 // before the workgroup's one barrier, which publishes the LDS counter the
 // later ranks are drawn from (a wave whose tiles arrived sooner takes more).
 // The wave's state goes to LDS as decode_body leaves it.
-template <int DT, int D, int GT, bool PAGED, int kDW>
+template <int DT, int D, int GT, bool PAGED, int kDW, int VT>
 __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg, int b0, int b1,
                                             float (*sh_m)[GT], float (*sh_l)[GT], int* sh_cnt, uint16_t* sh_v) {
   constexpr bool F8 = DT == OC_FP8_E4M3FN;
@@ -2310,10 +2352,10 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     vs_raw = *(vs_tile ? a.v_scales + (int64_t)row * a.vs_stride + tt : qword);
     if constexpr (PAGED) {
       load_k_mfma_t_paged<DT, D>(a, ri, tt, lane, kb, pg);
-      load_v_lds<DT, D, true>(a, ri, row, tt, lane, sv, pg);
+      load_v_lds<VT, D, true>(a, ri, row, tt, lane, sv, pg);
     } else {
       load_k_mfma_t<DT, D>(a, ri, row, tt, lane, kb);
-      load_v_lds<DT, D, false>(a, ri, row, tt, lane, sv, TilePages{});
+      load_v_lds<VT, D, false>(a, ri, row, tt, lane, sv, TilePages{});
     }
   };
   MStateT mst{kM0, 0.f};
@@ -2358,13 +2400,13 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     }
     const int valid = min(64, ri.n_tok - t * 64);
     f32x4 c[4];
-    tile_logits_t<DT, D>(aq, kb, c);
+    tile_logits_t<DT, D>(aq, kb, c, k_dq(a));
     tile_softmax_t<D>(mst, accp, c, a.scale * (ks_tile ? ks_raw : 1.f), vs_tile ? vs_raw : 1.f, valid, lane);
     // the V tile's direct-to-LDS loads (issued after K) have landed; paged,
     // the next tile's block-table load (issued last) may still be in flight
     if (PAGED && tn >= 0) __builtin_amdgcn_s_waitcnt(vmcnt_imm(1));
     else __builtin_amdgcn_s_waitcnt(0);
-    tile_pv_t<DT, D>(accp, c, sv, lane);
+    tile_pv_t<VT, D>(accp, c, sv, lane);
     ++kept;
     if constexpr (PAGED) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -2849,8 +2891,9 @@ __global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((am
 // host): kDW waves per workgroup, every query head of a row in one
 // workgroup (GT >= G).  kDW = 8 fills a CU with one workgroup; kDW = 4 (the
 // flat layout's many small workgroups) lets two share a CU, so that one's
-// prologue overlaps the other's tile loop.
-template <int DT, int D, int GT, bool PAGED, int kDW>
+// prologue overlaps the other's tile loop.  VT: V's element type (DT, or
+// bf16 V beside fp8 K).
+template <int DT, int D, int GT, bool PAGED, int kDW, int VT = DT>
 __global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_fast_kernel(
     const DecodeArgs a) {
   const int g_active = min(GT, a.G);
@@ -2868,7 +2911,7 @@ __global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(2))
   // flat: the share is the tile range [b0, b1), all of whose retained tiles
   // the workgroup takes (one split of one); otherwise an even split of the
   // row's retained ranks (dense: tiles) over its npg workgroups
-  decode_fast<DT, D, GT, PAGED, kDW>(a, ri, row, a.flat ? 0 : gidx, a.flat ? 1 : npg, b0, b1, sh_m, sh_l, sh_cnt,
+  decode_fast<DT, D, GT, PAGED, kDW, VT>(a, ri, row, a.flat ? 0 : gidx, a.flat ? 1 : npg, b0, b1, sh_m, sh_l, sh_cnt,
                                      sh_v);
   __syncthreads();
   const int64_t pbase = a.flat ? (int64_t)slot0 * a.G : (int64_t)row * a.G * a.Pg;
@@ -2899,7 +2942,11 @@ __global__ __launch_bounds__(kThreads) void score_kernel(const DecodeArgs a) {
   if ((t + 1) * 64 <= ri.n_tok) {
     uint32_t kw[16][L::LW];
     load_tile<DT, D, PAGED>(a, ri, row, t, false, lane, kw);
-    tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
+    if (DT == OC_FP8_E4M3FN && a.k_scale_mode == OC_KSCALE_DEQUANT) {
+      if constexpr (DT == OC_FP8_E4M3FN) tile_energies<DT, D, true>(kw, Deq{a.k_scale, true}, lane, el, eh);
+    } else {
+      tile_energies<DT, D>(kw, tile_kdeq(a, row, t), lane, el, eh);
+    }
     z = eh / (el + 1e-6f);
     keep = gate_keep(OC_GATE_ZETA, a.thr, el, eh, 0.f, false) ? 1 : 0;
   } else if (t < ri.n_tiles) {
@@ -3025,14 +3072,14 @@ hipError_t launch_fwht(const DecodeArgs& a, int head_dim, hipStream_t st);
 template <int DT>
 hipError_t launch_band(const DecodeArgs& a, int head_dim, hipStream_t st);
 
-template <int DT, int HD, bool PG, int W>
+template <int DT, int HD, bool PG, int W, int VT = DT>
 inline void launch_fast_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   const dim3 block(W * kWave);
   switch (gt) {
-    case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 1, PG, W>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 2, PG, W>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 4, PG, W>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 8, PG, W>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 1, PG, W, VT>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 2, PG, W, VT>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 4, PG, W, VT>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_fast_kernel<DT, HD, 8, PG, W, VT>), grid, block, 0, st, a); break;
   }
 }
 
@@ -3040,6 +3087,13 @@ template <int DT, int HD, bool DOT2, bool PG, bool MQ, bool LOOP>
 inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if constexpr (MQ && LOOP) {
     if (a.fast) {
+      if constexpr (DT == OC_FP8_E4M3FN) {
+        if (a.v_bf16) {
+          if (a.fast_waves == 4) launch_fast_gt<DT, HD, PG, 4, OC_BF16>(a, gt, grid, st);
+          else launch_fast_gt<DT, HD, PG, 8, OC_BF16>(a, gt, grid, st);
+          return;
+        }
+      }
       if (a.fast_waves == 4) launch_fast_gt<DT, HD, PG, 4>(a, gt, grid, st);
       else launch_fast_gt<DT, HD, PG, 8>(a, gt, grid, st);
       return;

@@ -130,7 +130,9 @@ class KVLayout:
         d.v = _ptr(self.v)
         d.dtype = dtype_code(self.k.dtype, "K")
         if self.v is not None and self.v.dtype != self.k.dtype:
-            raise TypeError(f"orthocache_gpu: K and V dtypes differ ({self.k.dtype} vs {self.v.dtype})")
+            if not (self.k.dtype == torch.float8_e4m3fn and self.v.dtype == torch.bfloat16):
+                raise TypeError(f"orthocache_gpu: K and V dtypes differ ({self.k.dtype} vs {self.v.dtype})")
+            d.v_dtype = N.OC_BF16  # read as it is by the decodes that take it
         d.head_dim = self.head_dim
         d.num_rows = self.num_rows
         d.num_tiles = self.num_tiles
@@ -181,15 +183,23 @@ def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail
     return kv
 
 
+def mixed_fp8k_bf16v(k: torch.Tensor, v: Optional[torch.Tensor]) -> bool:
+    """fp8 K beside bf16 V, which the per-wave-prologue decode reads as they are."""
+    return v is not None and k.dtype == torch.float8_e4m3fn and v.dtype == torch.bfloat16
+
+
 def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
-                 num_tiles: int) -> KVLayout:
-    """(num_blocks, num_kv_heads, block_size, d) caches + int32 block table."""
+                 num_tiles: int, *, keep_mixed: bool = False) -> KVLayout:
+    """(num_blocks, num_kv_heads, block_size, d) caches + int32 block table.
+    keep_mixed: an fp8 K beside a bf16 V is passed as it is (no conversion);
+    decodes that cannot read it fail with OC_ERR_UNSUPPORTED."""
     nb, hkv, bs, d = k_cache.shape
     if v_cache.shape != k_cache.shape:
         raise ValueError(f"k_cache {tuple(k_cache.shape)} and v_cache {tuple(v_cache.shape)} must have the same shape")
     if block_tables.dim() != 2:
         raise ValueError("block_tables must be 2-D (num_seqs, max_blocks)")
-    k_cache, v_cache = harmonize_kv(k_cache, v_cache)
+    if not (keep_mixed and mixed_fp8k_bf16v(k_cache, v_cache)):
+        k_cache, v_cache = harmonize_kv(k_cache, v_cache)
     k_cache = last_dim_ready(k_cache, d)
     v_cache = last_dim_ready(v_cache, d)
     if block_tables.dtype != torch.int32:

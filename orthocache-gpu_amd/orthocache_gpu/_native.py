@@ -26,7 +26,7 @@ OC_F32, OC_F16, OC_BF16, OC_FP8_E4M3FN = 0, 1, 2, 3
 # gates / modes / scale modes
 OC_GATE_NONE, OC_GATE_ZETA, OC_GATE_CS, OC_GATE_MASK = 0, 1, 2, 3
 OC_MODE_SINGLE_PASS, OC_MODE_CACHED = 0, 1
-OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE = 0, 1, 3
+OC_KSCALE_NONE, OC_KSCALE_Q_FOLD, OC_KSCALE_TILE, OC_KSCALE_DEQUANT = 0, 1, 3, 4
 OC_VSCALE_NONE, OC_VSCALE_TILE = 0, 1
 # q norm of the decode gate
 OC_QNORM_SPATIAL, OC_QNORM_WALSH_HIGH = 0, 1
@@ -53,6 +53,7 @@ class OcKvDesc(ctypes.Structure):
         ("v_scale_mode", _i32), ("num_tokens", _i32),
         ("v_scales", _p), ("v_scales_row_stride", _i64),
         ("error_flag", _p),
+        ("v_dtype", _i32),
     ]
 
 

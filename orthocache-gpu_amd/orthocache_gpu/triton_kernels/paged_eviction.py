@@ -86,26 +86,56 @@ def fused_orthocache_attention_paged(
         num_splits = _auto_num_splits(num_tiles, device)
 
     rows = num_seqs * num_kv_heads
+    # fp8 K with a scalar k_scale: the reference dequantises the pool,
+    # k_cache.to(q.dtype) * k_scale, and scales nothing after
+    # (paged_eviction.py:354-357).  With bf16 q, a cached decode on pages of
+    # >= 16 tokens does that rounding in-kernel as it widens K
+    # (OC_KSCALE_DEQUANT) and reads a bf16 V beside the fp8 K as it is: no
+    # copy of either pool.  Other shapes dequantise the pool first (bf16 q
+    # holds every fp8 value, so an unscaled K is only widened to V's type).
+    in_kernel = None
     if k_cache.dtype == torch.float8_e4m3fn and not isinstance(k_scale, torch.Tensor):
-        # reference semantics: k_cache.to(q.dtype) * k_scale in q's dtype, then
-        # no further scaling (paged_eviction.py:354-357)
-        k_cache = X.dequant_fp8(k_cache, float(k_scale), q.dtype)
+        ks = float(k_scale)
         k_scale = 1.0
-    kv = X.paged_layout(k_cache, v_cache, block_tables, num_tiles)
-    kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, device)
-    kv.v_scale_mode, kv.v_scales = X.vscale_mode(v_scale, rows, num_tiles, device)
+        if q.dtype == torch.bfloat16 and block_size >= 16 and mode == "cached":
+            in_kernel = ks
+        elif q.dtype != torch.bfloat16 or ks != 1.0:
+            k_cache = X.dequant_fp8(k_cache, ks, q.dtype)
+    vmode, vscales = X.vscale_mode(v_scale, rows, num_tiles, device)
+    lengths = None
     if context_lens is not None:
         if context_lens.numel() != num_seqs:
             raise ValueError(f"context_lens must have {num_seqs} entries")
-        kv.lengths = context_lens.to(device=device, dtype=torch.int32).clamp(
+        lengths = context_lens.to(device=device, dtype=torch.int32).clamp(
             min=0, max=max_blocks_per_seq * block_size).contiguous()
-    kv.error_flag = torch.zeros(1, dtype=torch.int32, device=device) if sync else None
+    error_flag = torch.zeros(1, dtype=torch.int32, device=device) if sync else None
     gate, thr = (N.OC_GATE_CS, tau) if tau is not None else (N.OC_GATE_ZETA, zeta_max)
     mode_c, scores = _mode_code(mode, score_cache)
     q2 = q.reshape(num_seqs * num_heads, head_dim)
     out2 = None if out is None else out.view(num_seqs * num_heads, head_dim)
-    res = X.decode(kv, q2, G, gate=gate, threshold=thr, mode=mode_c, scores=scores, num_splits=num_splits,
-                   out_dtype=input_dtype, want_keep=sync, out=out2)
+
+    def run(kc, dequant):
+        kv = X.paged_layout(kc, v_cache, block_tables, num_tiles, keep_mixed=dequant is not None)
+        kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, device)
+        if dequant is not None and dequant != 1.0:
+            kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_DEQUANT, dequant
+        kv.v_scale_mode, kv.v_scales = vmode, vscales
+        kv.lengths = lengths
+        kv.error_flag = error_flag
+        return kv, X.decode(kv, q2, G, gate=gate, threshold=thr, mode=mode_c, scores=scores,
+                            num_splits=num_splits, out_dtype=input_dtype, want_keep=sync, out=out2)
+
+    if in_kernel is None:
+        kv, res = run(k_cache, None)
+    else:
+        try:
+            kv, res = run(k_cache, in_kernel)
+        except N.OrthoCacheHIPError as e:
+            # a decode shape whose kernel neither dequantises K nor reads the
+            # two types: the library refused before launching anything
+            if e.code != N.OC_ERR_UNSUPPORTED:
+                raise
+            kv, res = run(X.dequant_fp8(k_cache, in_kernel, q.dtype) if in_kernel != 1.0 else k_cache, None)
     metadata: Dict[str, Any] = {
         "num_splits": num_splits,
         "num_tiles": num_tiles,
@@ -147,8 +177,19 @@ def score_paged_tiles(k_cache: torch.Tensor, block_tables: torch.Tensor, tile_si
         kv.lengths = context_lens.to(device=k_cache.device, dtype=torch.int32).clamp(
             min=0, max=maxb * bs).contiguous()
     if k_cache.dtype == torch.float8_e4m3fn and k_scale is not None and not isinstance(k_scale, torch.Tensor):
-        raise NotImplementedError("score an fp8 cache with per-tile k_scale tensors; scalar k_scale "
-                                  "needs the q-dtype rounding of the decode path")
+        # the decode's K: k_cache.to(q_dtype) * k_scale (paged_eviction.py:354-357)
+        ks = float(k_scale)
+        if q_dtype is None:
+            raise ValueError("an fp8 cache with a scalar k_scale needs q_dtype (the decode's query dtype)")
+        if q_dtype == torch.bfloat16:
+            if ks != 1.0:
+                kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_DEQUANT, ks  # rounded to bf16 in the kernel
+        else:
+            kd = X.dequant_fp8(k_cache, ks, q_dtype)
+            kv = X.paged_layout(kd, kd, block_tables, num_tiles)  # no V is read
+            if context_lens is not None:
+                kv.lengths = context_lens.to(device=k_cache.device, dtype=torch.int32).clamp(
+                    min=0, max=maxb * bs).contiguous()
     if isinstance(k_scale, torch.Tensor):
         kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, k_cache.device)
     e_low, e_high, zeta, keep = X.score_tiles(kv, 0.0)

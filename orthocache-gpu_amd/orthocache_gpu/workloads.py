@@ -179,7 +179,7 @@ def paged_pool(keys: torch.Tensor, values: torch.Tensor, num_kv_heads: int, bloc
     perm = torch.randperm(total, generator=g)
     bt = torch.full((b_count, max_blocks), -1, dtype=torch.int32)
     k_cache = torch.zeros((total, num_kv_heads, block_size, d), dtype=keys.dtype, device=keys.device)
-    v_cache = torch.zeros_like(k_cache)
+    v_cache = torch.zeros(k_cache.shape, dtype=values.dtype, device=values.device)
     pos = 0
     kr = keys.view(b_count, num_kv_heads, s_len, d)
     vr = values.view(b_count, num_kv_heads, s_len, d)
@@ -189,7 +189,7 @@ def paged_pool(keys: torch.Tensor, values: torch.Tensor, num_kv_heads: int, bloc
         bt[b, :need[b]] = ids.to(torch.int32)
         n_full = need[b] * block_size
         kb = torch.zeros((num_kv_heads, n_full, d), dtype=keys.dtype, device=keys.device)
-        vb = torch.zeros_like(kb)
+        vb = torch.zeros(kb.shape, dtype=values.dtype, device=values.device)
         take = min(n_full, s_len)
         kb[:, :take] = kr[b, :, :take]
         vb[:, :take] = vr[b, :, :take]

@@ -170,6 +170,65 @@ def test_golden_paged(name):
     assert_out(out, dec["out"], bar, name, ref_rounded=True)
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("gate", ["zeta", "cs"])
+@pytest.mark.parametrize("lens", [False, True])
+@pytest.mark.parametrize("vdt", ["bf16", "fp8"])
+def test_paged_fp8_k_in_kernel(bs, G, gate, lens, vdt, monkeypatch):
+    """fp8 K with a scalar k_scale and bf16 q, cached-score decode: the
+    scoring and the decode kernels round float(k) * k_scale to bf16 as they
+    widen K (OC_KSCALE_DEQUANT), the reference's k_cache.to(q.dtype) *
+    k_scale (paged_eviction.py:354-357), and a bf16 V beside the fp8 K is read
+    as it is: no copy of either pool.  The scores equal, bit for bit, those of
+    the pool dequantised beforehand; masks, counts and outputs match the
+    oracle on the dequantised values, as the copy path's do."""
+    from orthocache_gpu import fused_orthocache_attention_paged
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu.triton_kernels.paged_eviction import score_paged_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_q, paged_pool
+    B, hkv, tiles, d = 2, 2, 6, 128
+    ks = 0.37  # not a power of two: the rounding after the product matters
+    wl = _mixed(B * hkv, tiles, d, "f32", seed=bs + G)
+    k8 = (wl.keys / ks).to(torch.float8_e4m3fn)
+    kd = (k8.float() * ks).to(torch.bfloat16)  # the reference's dequantised K
+    vv = wl.values.to(TORCH_DT[vdt])
+    seq_lens = [tiles * 64 - 70, tiles * 64] if lens else [tiles * 64] * B
+    k8c, vc, bt = paged_pool(k8, vv, hkv, bs, seq_lens, seed=7)
+    kdc, _, _ = paged_pool(kd, vv, hkv, bs, seq_lens, seed=7)
+    k8c, vc, bt, kdc = k8c.to(DEV), vc.to(DEV), bt.to(DEV), kdc.to(DEV)
+    assert torch.equal(X.dequant_fp8(k8c, ks, torch.bfloat16), kdc)
+    q = make_q(B * hkv, G, d, seed=bs).to(DEV)
+    cl = torch.tensor(seq_lens, dtype=torch.int32, device=DEV) if lens else None
+    sc = score_paged_tiles(k8c, bt, k_scale=ks, q_dtype=torch.bfloat16, context_lens=cl)
+    sc_ref = score_paged_tiles(kdc, bt, context_lens=cl)
+    assert torch.equal(sc.e_low, sc_ref.e_low) and torch.equal(sc.e_high, sc_ref.e_high)
+    row_lens = [seq_lens[r // hkv] for r in range(B * hkv)]
+    live = (torch.arange(tiles, device=DEV)[None, :] * 64 + 64
+            <= torch.tensor(row_lens, device=DEV)[:, None]) if lens else None
+    thr = calibrate_tau(sc_ref.e_high, q, G, live) if gate == "cs" else 5.0
+    kw = dict(num_query_groups=G, mode="cached", context_lens=cl)
+    if gate == "cs":
+        kw["tau"] = thr
+    if not lens:
+        kw["num_splits"] = 256  # whole rows over many splits, several per workgroup
+    qb = q.view(B, hkv * G, d)
+    ref = O.decode_rows(np32(q), np32(kd), np32(vv), gate=gate, threshold=thr, G=G, lengths=row_lens)
+    out_copy, mc = fused_orthocache_attention_paged(qb, kdc, vc, bt, 5.0, k_scale=1.0, score_cache=sc_ref, **kw)
+    # the in-kernel path: no dequantised copy of K, no conversion of V
+    monkeypatch.setattr(X, "dequant_fp8", lambda *a, **k: pytest.fail("the K pool was dequantised"))
+    real_harmonize = X.harmonize_kv
+    monkeypatch.setattr(X, "harmonize_kv", lambda k, v: real_harmonize(k, v) if v is None or v.dtype == k.dtype
+                        else pytest.fail("K or V was converted"))
+    out, m = fused_orthocache_attention_paged(qb, k8c, vc, bt, 5.0, k_scale=ks, score_cache=sc, **kw)
+    for mm in (m, mc):
+        assert mm["tiles_retained"] == ref["retained"] and mm["tiles_evicted"] == ref["evicted"]
+    assert 0 < ref["retained"] and 0 < ref["evicted"]
+    what = f"paged fp8 K in-kernel bs={bs} G={G} {gate} lens={lens} V={vdt}"
+    assert_out(out.view(-1, d), ref["out"], "bf16", what)
+    assert_out(out_copy.view(-1, d), ref["out"], "bf16", what + " (copy path)")
+
+
 # ---------------------------------------------------------------- random vs oracle
 
 def _mixed(rows, tiles, d, dtype, seed, noise_frac=0.5):
