@@ -964,7 +964,7 @@ struct MState {
 // is a multiple of the bank line; the XOR gives them distinct bank slots
 // (each slot used twice) instead of one slot 16 times over.
 template <int DT, int D>
-__device__ __forceinline__ int v_xor(int r) {
+__host__ __device__ constexpr int v_xor(int r) {
   if constexpr (DT == OC_FP8_E4M3FN) {
     if constexpr (D == 128) return (r >> 1) & 7;
     else if constexpr (D == 64) return (r >> 2) & 3;
@@ -975,6 +975,35 @@ __device__ __forceinline__ int v_xor(int r) {
     else return 0;
   }
 }
+
+// Compile-time pin of v_xor: every chunk stays inside its row, and each
+// transposing read of tile_pv_t (16-bit: 16 rows x 32 bytes, rows 32 tb2 +
+// 8 kg + 4 h + m; fp8: 32 rows x 16 bytes, rows 32 tb2 + 8 kg + m) puts at
+// most two 16-byte pieces on any of the 16 bank slots of a 256-byte line.
+template <int DT, int D>
+constexpr bool v_xor_pin() {
+  constexpr bool F8 = DT == OC_FP8_E4M3FN;
+  constexpr int es = F8 ? 1 : 2, row_bytes = D * es, chunks = row_bytes / 16;
+  for (int r = 0; r < 64; ++r)
+    for (int c = 0; c < chunks; ++c)
+      if ((c ^ v_xor<DT, D>(r)) < 0 || (c ^ v_xor<DT, D>(r)) >= chunks) return false;
+  for (int tb2 = 0; tb2 < 2; ++tb2)
+    for (int nc = 0; nc < D / 16; ++nc)
+      for (int h = 0; h < (F8 ? 1 : 2); ++h) {
+        int use[16] = {};
+        for (int kg = 0; kg < 4; ++kg)
+          for (int m = 0; m < (F8 ? 8 : 4); ++m) {
+            const int r = F8 ? 32 * tb2 + 8 * kg + m : 32 * tb2 + 8 * kg + 4 * h + m;
+            const int o = F8 ? 16 * (nc ^ v_xor<DT, D>(r)) : 32 * (nc ^ (v_xor<DT, D>(r) >> 1));
+            for (int piece = 0; piece < (F8 ? 16 : 32); piece += 16)
+              if (++use[((r * row_bytes + o + piece) % 256) / 16] > 2) return false;
+          }
+      }
+  return true;
+}
+static_assert(v_xor_pin<OC_BF16, 128>() && v_xor_pin<OC_BF16, 64>() && v_xor_pin<OC_FP8_E4M3FN, 128>() &&
+                  v_xor_pin<OC_FP8_E4M3FN, 64>(),
+              "v_xor: a transposing V read uses a bank slot more than twice, or a chunk leaves its row");
 
 // 16 bytes per lane from a buffer straight to LDS (non-temporal): lane i's
 // bytes land at dst + 16 i (dst wave-uniform)
@@ -1295,9 +1324,27 @@ __device__ __forceinline__ void tile_pv_mfma(f32x4 (&accp)[D / 16], const float*
 // each 32-token block, a = 16h + 4r + i holds token 8r + 4h + i, so the eight
 // probabilities a lane holds for block j are tokens 32j + 8kg .. + 7 in order,
 // the k index of the p.V instruction (V stays in token order).
-__device__ __forceinline__ int kperm(int a) {
+__host__ __device__ constexpr int kperm(int a) {
   return (a & ~31) + 8 * ((a >> 2) & 3) + 4 * ((a >> 4) & 1) + (a & 3);
 }
+
+// Compile-time pin of kperm: a permutation of the tile's 64 rows under which
+// lane group kg's registers c[2j][i], c[2j + 1][i] (A rows 32j + 4kg + i and
+// 32j + 16 + 4kg + i) hold tokens 32j + 8kg .. + 7 in order.
+constexpr bool kperm_pin() {
+  bool seen[64] = {};
+  for (int a = 0; a < 64; ++a) {
+    const int t = kperm(a);
+    if (t < 0 || t >= 64 || seen[t]) return false;
+    seen[t] = true;
+  }
+  for (int j = 0; j < 2; ++j)
+    for (int kg = 0; kg < 4; ++kg)
+      for (int e = 0; e < 8; ++e)
+        if (kperm(32 * j + 16 * (e >> 2) + 4 * kg + (e & 3)) != 32 * j + 8 * kg + e) return false;
+  return true;
+}
+static_assert(kperm_pin(), "kperm: the transposed step's K row order no longer matches the p.V operand");
 
 struct MStateT {
   float m;  // running max of the lane's head, base-2 units

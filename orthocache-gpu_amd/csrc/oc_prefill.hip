@@ -457,17 +457,25 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
     if (t < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, t, tid, stage_k(0), stage_v(0));
     __builtin_amdgcn_s_waitcnt(0);
     int s = 0;
+    // one tile: the next one requested into the other stage, this one
+    // computed.  The stages are restrict parameters, so the compiler knows
+    // that the direct-to-LDS loads into one do not write what is read from
+    // the other, and issues no wait for them before the reads.
+    auto step = [&](int tn, char* __restrict__ nk, char* __restrict__ nv, const char* __restrict__ ck,
+                    const char* __restrict__ cv) {
+      if (tn < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, tn, tid, nk, nv);
+      if (t < tend) {
+        f32x4 c[4];
+        pf_logits<DT, D>(q, ck, lane, c);
+        pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
+        pf_pv<DT, D>(accp, c, cv, lane);
+      }
+    };
     while (t < wg_tend) {
       // stage s is complete; every wave is done with the tile before (stage s ^ 1)
       __syncthreads();
       const int tn = next_kept(t + 1);
-      if (tn < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, tn, tid, stage_k(1 - s), stage_v(1 - s));
-      if (t < tend) {
-        f32x4 c[4];
-        pf_logits<DT, D>(q, stage_k(s), lane, c);
-        pf_softmax<D, ENT>(st, accp, c, scale2, nvis, t * 64, t * 64 + 64 <= nvis_w, lane);
-        pf_pv<DT, D>(accp, c, stage_v(s), lane);
-      }
+      step(tn, stage_k(1 - s), stage_v(1 - s), stage_k(s), stage_v(s));
       __builtin_amdgcn_s_waitcnt(0);
       s = 1 - s;
       t = tn;
