@@ -405,15 +405,24 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // XCD-aware order: consecutive workgroups go to different XCDs, so work
-  // item w is placed so that items w, w+1, .. run on one XCD; items walk the
-  // query blocks from the last (longest causal window) to the first, heads
-  // fastest, so the G heads of one kv group share an XCD's L2.
-  const int nb = gridDim.x;
+  // XCD-aware order: workgroup i runs on XCD i % 8.  Each XCD takes a
+  // contiguous eighth of the (batch, head) pairs -- whole kv groups or equal
+  // parts of one, whose K/V tiles then stay in that XCD's L2 -- over every
+  // query block, dispatched from the last block (longest causal window) to
+  // the first, heads fastest.  So every XCD gets the same mix of window
+  // lengths, longest first.  (Without eight equal parts: the same order over
+  // the whole grid.)
+  const int nbh = a.B * a.Hq;
   const int i = blockIdx.x;
-  const int w = (nb % 8 == 0) ? (i % 8) * (nb / 8) + i / 8 : i;
-  const int bh = w % (a.B * a.Hq);
-  const int qb = a.qblocks - 1 - w / (a.B * a.Hq);
+  int bh, qb;
+  if (nbh % 8 == 0) {
+    const int hpx = nbh / 8, j = i / 8;
+    bh = (i % 8) * hpx + j % hpx;
+    qb = a.qblocks - 1 - j / hpx;
+  } else {
+    bh = i % nbh;
+    qb = a.qblocks - 1 - i / nbh;
+  }
   const int b = bh / a.Hq;
   const int h = bh % a.Hq;
   const int kv = h / a.G;
