@@ -408,8 +408,12 @@ static constexpr size_t kCounterBytes = 64 << 10;
 // The split merge runs inside the decode kernel when the counters and the
 // merge weights (GT * Pg floats in the kernel's 4 * GT * D wave-merge LDS)
 // fit; otherwise merge_kernel runs after it.
+static int gchunks_of(const oc_decode_params* p) {
+  return (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
+}
+
 static bool fused_merge(const oc_decode_params* p, int pg) {
-  const int gchunks = (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
+  const int gchunks = gchunks_of(p);
   return p->out && (size_t)p->kv.num_rows * gchunks * sizeof(int32_t) <= kCounterBytes && pg <= 4 * p->kv.head_dim;
 }
 
@@ -544,6 +548,11 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   if (p->out) {
     a.counters = (int32_t*)w;
     w += kCounterBytes;
+    // one 128-byte line per (row, chunk) counter where they fit: the tickets
+    // of different rows then do not queue on one line
+    const int64_t nctr = (int64_t)p->kv.num_rows * gchunks_of(p);
+    a.ctr_stride = 32;
+    while (a.ctr_stride > 1 && nctr * a.ctr_stride * (int64_t)sizeof(int32_t) > (int64_t)kCounterBytes) a.ctr_stride >>= 1;
   }
   if (partials_given) {
     if (!aligned(p->partial_acc, 16)) return fail(OC_ERR_INVALID, "partial_acc must be 16-byte aligned");

@@ -47,6 +47,7 @@ struct DecodeArgs {
   const char* v;
   int64_t k_row_stride, k_tok_stride, v_row_stride, v_tok_stride;
   int32_t v_bf16;  // fp8 K with bf16 V (decode_fast only; strides above in bytes)
+  int32_t ctr_stride;  // int32 words between the fused merge's (row, chunk) counters
   int32_t paged, bs_log2, nkv, rows_per_length;
   const int32_t* bt;
   int64_t bt_stride, num_blocks;
@@ -2511,7 +2512,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
-    int* ctr = a.counters + (int64_t)row * gridDim.z + blockIdx.z;
+    int* ctr = a.counters + ((int64_t)row * gridDim.z + blockIdx.z) * a.ctr_stride;
     const int done = atomicAdd(ctr, 1) + 1;
     sh_last = done == Pg;
     if (done == Pg) atomicExch(ctr, 0);
