@@ -233,7 +233,15 @@ def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def current_stream(device: torch.device) -> int:
+    """The handle of torch's current stream on device (the raw query skips
+    building a Stream object: about 0.3 against 1.9 us per call)."""
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -456,7 +464,8 @@ _HOOK_PARAMS: Dict[tuple, "N.OcHookDecodeParams"] = {}
 
 
 def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_norms: torch.Tensor, G: int,
-                tau_norm: float, low_band: int, want_stats: bool = True):
+                tau_norm: float, low_band: int, want_stats: bool = True,
+                stats_out: Optional[torch.Tensor] = None):
     """oc_hook_decode: the model hook's decode step in one call.  query
     (B, Hq, 1, d), key / value (B, Hkv, S, d) with a contiguous last
     dimension, k_norms float32 (>= Hkv, >= S // 64) with contiguous rows
@@ -502,11 +511,14 @@ def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_n
     p.tau_norm = tau_norm
     p.q, p.k, p.v, p.k_norms = query.data_ptr(), key.data_ptr(), value.data_ptr(), k_norms.data_ptr()
     out = torch.empty((B, Hq, 1, d), dtype=dt, device=device)
-    stats = torch.empty((B * Hkv, 3), dtype=torch.float32, device=device) if want_stats else None
+    if stats_out is not None:  # the caller's contiguous float32 (B * Hkv, 3) values, any view of them
+        stats = stats_out
+    else:
+        stats = torch.empty((B * Hkv, 3), dtype=torch.float32, device=device) if want_stats else None
     p.out = out.data_ptr()
     p.gate_stats = None if stats is None else stats.data_ptr()
     lib = N.lib()
-    stream = torch.cuda.current_stream(device).cuda_stream
+    stream = current_stream(device)
     ws = workspace(device, stream, lib.oc_hook_decode_workspace_size(ctypes.byref(p)))
     p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
     if device.index == torch.cuda.current_device():

@@ -116,11 +116,36 @@ class _Stats(dict):
         super().__init__(*args, **kw)
         self._pending = []
         self._folding = False
+        self._rings = {}  # (device, shape): views of a (_MAX_PENDING,) + shape float32 device ring
+        self._ring_next = 0
+
+    def ring_rows(self, device: torch.device, shape: tuple) -> torch.Tensor:
+        """float32 device values of one call, of the given shape, to be
+        deferred: a slot of a ring that is free again once the pending calls
+        are folded (at most _MAX_PENDING of them), so that a call allocates
+        nothing.  The slots' views are made once."""
+        if self._ring_next >= self._MAX_PENDING:
+            # (only after calls that failed before deferring) no pending call
+            # holds a row once the pending calls are folded
+            self.fold()
+            self._ring_next = 0
+        key = (device, shape)
+        views = self._rings.get(key)
+        if views is None:
+            ring = torch.empty((self._MAX_PENDING,) + tuple(shape), dtype=torch.float32, device=device)
+            views = self._rings[key] = list(ring.unbind(0))
+        slot = self._ring_next
+        self._ring_next += 1
+        return views[slot]
 
     _MAX_PENDING = 256  # calls held before a fold (bounds the device tensors kept alive)
 
-    def defer(self, fold, dev: torch.Tensor) -> None:
-        self._pending.append((fold, dev))
+    def defer(self, fold, dev: torch.Tensor, run=None) -> None:
+        """fold(host) folds one call's values (dev as a float64 array of its
+        shape).  run = (key, fold_many): consecutive calls with equal keys
+        fold together, fold_many(host of shape (n,) + dev.shape) standing for
+        their n folds in call order."""
+        self._pending.append((fold, dev, run))
         if len(self._pending) >= self._MAX_PENDING:
             self.fold()
 
@@ -128,16 +153,27 @@ class _Stats(dict):
         if not self._pending or self._folding:
             return
         pending, self._pending = self._pending, []
+        self._ring_next = 0  # the transfer below completes every pending call's writes
         # one device concatenation (the values are float32), one transfer,
         # then float64 numpy on the host: the folds index it per call, where
         # numpy's scalar ops cost a fraction of torch's
-        host = torch.cat([d.reshape(-1) for _, d in pending]).cpu().numpy().astype(np.float64)
+        host = torch.cat([d.reshape(-1) for _, d, _ in pending]).cpu().numpy().astype(np.float64)
         self._folding = True
         try:
-            i = 0
-            for fn, d in pending:
-                fn(host[i:i + d.numel()].reshape(tuple(d.shape)))
-                i += d.numel()
+            i = j = 0
+            while j < len(pending):
+                fn, d, run = pending[j]
+                k = j + 1
+                if run is not None:
+                    while k < len(pending) and pending[k][2] is not None and pending[k][2][0] == run[0]:
+                        k += 1
+                n, size = k - j, d.numel()
+                if n > 1:
+                    run[1](host[i:i + n * size].reshape((n,) + tuple(d.shape)))
+                else:
+                    fn(host[i:i + size].reshape(tuple(d.shape)))
+                i += n * size
+                j = k
         finally:
             self._folding = False
 
@@ -286,25 +322,16 @@ class OrthoCache_GQA_Attention:
         # one library call: the Walsh-subspace q norms, their group medians,
         # the gate over the complete tiles (the partial last tile attended)
         # and the decode over the retained tiles
-        out, dev = X.hook_decode(query, key, value, nc.cache, G, tau * TILE * d, _LOW_BAND)
-        # dev (B * Hkv, 3), written by the gate kernel: evicted complete
+        out, dev = X.hook_decode(query, key, value, nc.cache, G, tau * TILE * d, _LOW_BAND,
+                                 stats_out=self.stats.ring_rows(query.device, (B, Hkv, 3)))
+        # dev (B, Hkv, 3), written by the gate kernel: evicted complete
         # tiles, the group's q norm and the largest K norm per kv head,
         # reduced over the heads (and clamped at 0) when folded
-        dev = dev.view(B, Hkv, 3)
         stats, gov = self.stats, self.governor
 
-        def fold(host):
-            for b in range(B):
-                hb = host[b]
-                skipped = int(hb[:, 0].sum())
-                _exhaust(stats, float(np.maximum(hb[:, 1].max(), 0.0)), float(np.maximum(hb[:, 2].max(), 0.0)))
-                _add(stats, 'decode_steps', 1)
-                _add(stats, 'decode_tiles_skipped', skipped)
-                _add(stats, 'decode_tiles_total', T * Hkv)
-                if gov is not None and T > 0:
-                    gov.report_layer(skipped / (T * Hkv))
-            _add(stats, 'layers_processed', 1)
-        stats.defer(fold, dev)
+        fold, fold_many = _decode_folds(stats, gov, B, Hkv, T)
+        # without a governor, runs of decode calls of one shape fold together
+        stats.defer(fold, dev, None if gov is not None else (("decode", B, Hkv, T), fold_many))
         if gov is not None:
             stats.fold()
         return out
@@ -332,6 +359,39 @@ def _exhaust(stats, max_q: float, max_k: float) -> None:
     _dget(stats, 'hallucination_scores').append(max_q / (max_k + 1e-10))
     _dget(stats, 'q_search_intensity').append(max_q)
     _dget(stats, 'k_info_density').append(max_k)
+
+
+def _decode_folds(stats, gov, B: int, Hkv: int, T: int):
+    """The folds of a decode call's statistics (B, Hkv, 3): evicted complete
+    tiles, the group's q norm and the largest K norm per (batch, kv head)
+    (perplexity_eval.py:653-671).  fold(host) folds one call; fold_many(host)
+    n calls (n, B, Hkv, 3) at once, entries in call order, batch element
+    fastest, with the same float64 values."""
+
+    def fold(host):
+        for b in range(B):
+            hb = host[b]
+            skipped = int(hb[:, 0].sum())
+            _exhaust(stats, float(np.maximum(hb[:, 1].max(), 0.0)), float(np.maximum(hb[:, 2].max(), 0.0)))
+            _add(stats, 'decode_steps', 1)
+            _add(stats, 'decode_tiles_skipped', skipped)
+            _add(stats, 'decode_tiles_total', T * Hkv)
+            if gov is not None and T > 0:
+                gov.report_layer(skipped / (T * Hkv))
+        _add(stats, 'layers_processed', 1)
+
+    def fold_many(host):
+        mq = np.maximum(host[..., 1].max(axis=2), 0.0).ravel()
+        mk = np.maximum(host[..., 2].max(axis=2), 0.0).ravel()
+        _dget(stats, 'hallucination_scores').extend((mq / (mk + 1e-10)).tolist())
+        _dget(stats, 'q_search_intensity').extend(mq.tolist())
+        _dget(stats, 'k_info_density').extend(mk.tolist())
+        _add(stats, 'decode_steps', mq.size)
+        _add(stats, 'decode_tiles_skipped', int(host[..., 0].sum(axis=2).astype(np.int64).sum()))
+        _add(stats, 'decode_tiles_total', T * Hkv * mq.size)
+        _add(stats, 'layers_processed', host.shape[0])
+
+    return fold, fold_many
 
 
 def _distinct_kv(query, key, value, G):

@@ -103,3 +103,59 @@ def test_stats_fold_lazily_in_call_order():
         st.defer(make(i), torch.tensor([1.0]))
     assert len(st._pending) < 256
     assert dict.__getitem__(st, 'layers_processed') >= 3 + 256
+
+
+def test_decode_stats_fold_together_as_one_by_one():
+    """Runs of decode calls of one shape fold in one numpy pass; the lists and
+    counters equal those of folding each call alone (NaN, negative and zero
+    norms included), and a call of another shape or kind ends the run."""
+    import numpy as np
+    from orthocache_gpu.model_hook import _decode_folds, _empty_stats
+    rng = np.random.default_rng(3)
+    B, Hkv, T = 2, 4, 9
+    devs = []
+    for i in range(7):
+        x = rng.standard_normal((B, Hkv, 3)).astype(np.float32)
+        x[..., 0] = rng.integers(0, T + 1, (B, Hkv))
+        if i == 2:
+            x[1, 2, 1] = np.nan
+        if i == 4:
+            x[0, :, 2] = -1.0
+        devs.append(torch.from_numpy(x))
+    one, many = _empty_stats(), _empty_stats()
+    other = torch.zeros((B, Hkv + 1, 3))
+    order = list(range(4)) + ["other"] + list(range(4, 7))
+    for st, batched in ((one, False), (many, True)):
+        for i in order:
+            if i == "other":
+                f, fm = _decode_folds(st, None, B, Hkv + 1, T)
+                st.defer(f, other, (("decode", B, Hkv + 1, T), fm) if batched else None)
+                continue
+            f, fm = _decode_folds(st, None, B, Hkv, T)
+            st.defer(f, devs[i], (("decode", B, Hkv, T), fm) if batched else None)
+    a, b = dict(one.items()), dict(many.items())
+    for key in a:
+        if isinstance(a[key], list):
+            assert len(a[key]) == len(b[key]) and all(
+                (x == y) or (x != x and y != y) for x, y in zip(a[key], b[key])), key
+            assert all(type(y) is float for y in b[key]), key
+        else:
+            assert a[key] == b[key], key
+    assert a['decode_steps'] == 8 * B and a['layers_processed'] == 8
+
+
+def test_stats_ring_rows_reused_after_fold():
+    """A decode call's statistics rows come from a ring of _MAX_PENDING rows
+    per shape; a fold frees them, and rows taken without a deferred call (a
+    call that failed) never run past the ring."""
+    from orthocache_gpu.model_hook import _empty_stats
+    st = _empty_stats()
+    n = st._MAX_PENDING
+    rows = [st.ring_rows(torch.device("cpu"), (2, 2, 3)) for _ in range(3)]
+    assert all(r.shape == (2, 2, 3) and r.is_contiguous() for r in rows)
+    assert rows[0].data_ptr() != rows[1].data_ptr()
+    st.defer(lambda h: None, rows[0])
+    _ = st['layers_processed']  # a read folds: the ring starts over
+    assert st.ring_rows(torch.device("cpu"), (2, 2, 3)).data_ptr() == rows[0].data_ptr()
+    for _ in range(3 * n):  # rows taken, nothing deferred
+        st.ring_rows(torch.device("cpu"), (2, 2, 3))
