@@ -342,9 +342,18 @@ typedef struct oc_prefill_params {
   int32_t tile_mask_cols;         /* >= kv_len / 64 */
   float scale;                    /* logit scale, 1/sqrt(head_dim) in the hook */
   float* entropy;                 /* (batch, num_q_heads, q_len) or NULL */
+  void* workspace;                /* optional (extension): when the call's workgroups fit in one round,
+                                     the longest causal windows run as two workgroups each, one of which
+                                     merges the two states; NULL: one workgroup per query block */
+  size_t workspace_bytes;         /* >= oc_prefill_workspace_size(p); its first 64 KiB hold counters that
+                                     are zero before the first call (every call leaves them zero) */
 } oc_prefill_params;
 
 int oc_prefill_attention(const oc_prefill_params* p, void* stream);
+
+/* bytes of workspace that lets oc_prefill_attention split the longest causal
+ * windows (0: this call would not split).  No reference counterpart. */
+size_t oc_prefill_workspace_size(const oc_prefill_params* p);
 
 /* sizeof(oc_prefill_params) as compiled, for binding checks */
 size_t oc_prefill_params_bytes(void);

@@ -14,6 +14,7 @@
 // in that XCD's L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 
 #include "oc_kernels.h"
@@ -26,6 +27,8 @@ namespace {
 constexpr int kPfWaves = 8;
 constexpr int kPfRows = 16 * kPfWaves;  // query positions per workgroup
 constexpr int kPfThreads = kPfWaves * kWave;
+// work items of a call that splits its longest causal windows (beyond: no split)
+constexpr int kPfMaxItems = 512;
 // -(1e-10) * ln(1e-10): what one zero probability adds to the entropy of a
 // softmax row whose probabilities are clamped to >= 1e-10 before the log
 constexpr float kZeroPTerm = 2.302585093e-9f;
@@ -46,6 +49,15 @@ struct PrefillArgs {
   float* entropy;  // (B, Hq, Sq) or null
   int32_t qblocks;
   int32_t dtype;
+  // split windows (nitems > 0): work item e is query block items[e] >> 2,
+  // part items[e] & 3 (0: its whole window; 1, 2: the first and second half
+  // of its tiles).  Blocks >= q0 are split: (block, head) pair k of them keeps
+  // the two halves' per-lane states at part + (2 k + half) * 512 * (4 + D/4)
+  // floats and its ticket at ctr[k * ctr_stride].
+  int32_t nitems, q0, ctr_stride;
+  float* part;
+  int32_t* ctr;
+  uint16_t items[kPfMaxItems];
 };
 
 // Online-softmax state in the transposed layout: lane 16r + x works on
@@ -397,7 +409,7 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
   }
 }
 
-template <int DT, int D, bool ENT>
+template <int DT, int D, bool ENT, bool SPLIT>
 __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 4))) void prefill_kernel(
     const PrefillArgs a) {
   using L = PfTile<DT, D>;
@@ -412,16 +424,22 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
   // the first, heads fastest.  So every XCD gets the same mix of window
   // lengths, longest first.  (Without eight equal parts: the same order over
   // the whole grid.)
+  // With split windows the items come from the host's table, longest first.
   const int nbh = a.B * a.Hq;
   const int i = blockIdx.x;
-  int bh, qb;
+  int bh, e;
   if (nbh % 8 == 0) {
     const int hpx = nbh / 8, j = i / 8;
     bh = (i % 8) * hpx + j % hpx;
-    qb = a.qblocks - 1 - j / hpx;
+    e = j / hpx;
   } else {
     bh = i % nbh;
-    qb = a.qblocks - 1 - i / nbh;
+    e = i / nbh;
+  }
+  int qb = a.qblocks - 1 - e, part = 0;
+  if constexpr (SPLIT) {
+    qb = a.items[e] >> 2;
+    part = a.items[e] & 3;
   }
   const int b = bh / a.Hq;
   const int h = bh % a.Hq;
@@ -440,6 +458,10 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
   // this wave's tiles, and the workgroup's (its last query's window)
   const int tend = pos0 < a.Sq ? (min(max(min(pos0 + 15, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64 : 0;
   const int wg_tend = (min(max(min(qb * kPfRows + kPfRows - 1, a.Sq - 1) + off + 1, 0), a.Skv) + 63) / 64;
+  // this item's tiles: the window, or one half of it
+  const int tsplit = (wg_tend + 1) / 2;
+  const int t_lo = part == 2 ? tsplit : 0;
+  const int t_hi = part == 1 ? tsplit : wg_tend;
 
   PfQ<DT, D> q;
   pf_load_q<DT, D>(a, a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh, pos0, lane, q);
@@ -447,7 +469,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
   const char* vh = a.v + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh;
   const uint8_t* mrow = a.mask ? a.mask + (int64_t)b * a.m_sb + (int64_t)kv * a.m_sh : nullptr;
   auto next_kept = [&](int t) {  // first retained tile >= t (uniform over the workgroup)
-    while (t < wg_tend && mrow && t < a.T && mrow[t]) ++t;
+    while (t < t_hi && mrow && t < a.T && mrow[t]) ++t;
     return t;
   };
 
@@ -458,12 +480,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
 
   auto stage_k = [&](int s) { return sh + s * 2 * L::KV; };
   auto stage_v = [&](int s) { return sh + s * 2 * L::KV + L::KV; };
-  int t = next_kept(0);
+  int t = next_kept(t_lo);
   if constexpr (L::STAGES == 2) {
     // two stages: the next tile goes straight to the other stage while this
     // one is used; each wave waits for its own loads before the barrier
     // that opens the stage to the workgroup
-    if (t < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, t, tid, stage_k(0), stage_v(0));
+    if (t < t_hi) pf_fetch_lds<DT, D>(a, kh, vh, t, tid, stage_k(0), stage_v(0));
     __builtin_amdgcn_s_waitcnt(0);
     int s = 0;
     // one tile: the next one requested into the other stage, this one
@@ -472,7 +494,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
     // the other, and issues no wait for them before the reads.
     auto step = [&](int tn, char* __restrict__ nk, char* __restrict__ nv, const char* __restrict__ ck,
                     const char* __restrict__ cv) {
-      if (tn < wg_tend) pf_fetch_lds<DT, D>(a, kh, vh, tn, tid, nk, nv);
+      if (tn < t_hi) pf_fetch_lds<DT, D>(a, kh, vh, tn, tid, nk, nv);
       if (t < tend) {
         f32x4 c[4];
         pf_logits<DT, D>(q, ck, lane, c);
@@ -480,7 +502,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
         pf_pv<DT, D>(accp, c, cv, lane);
       }
     };
-    while (t < wg_tend) {
+    while (t < t_hi) {
       // stage s is complete; every wave is done with the tile before (stage s ^ 1)
       __syncthreads();
       const int tn = next_kept(t + 1);
@@ -493,14 +515,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
     // one stage (float32, head_dim 128): the next tile waits in registers
     // and is written to the stage once every wave is done with it
     PfStage<DT, D> reg;
-    if (t < wg_tend) {
+    if (t < t_hi) {
       pf_fetch<DT, D>(a, kh, vh, t, tid, reg);
       pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
     }
-    while (t < wg_tend) {
+    while (t < t_hi) {
       __syncthreads();  // the stage is complete
       const int tn = next_kept(t + 1);
-      if (tn < wg_tend) pf_fetch<DT, D>(a, kh, vh, tn, tid, reg);  // in flight during this tile
+      if (tn < t_hi) pf_fetch<DT, D>(a, kh, vh, tn, tid, reg);  // in flight during this tile
       if (t < tend) {
         f32x4 c[4];
         pf_logits<DT, D>(q, stage_k(0), lane, c);
@@ -508,9 +530,60 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
         pf_pv<DT, D>(accp, c, stage_v(0), lane);
       }
       __syncthreads();  // the stage is free again
-      if (tn < wg_tend) pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
+      if (tn < t_hi) pf_stash<DT, D>(reg, tid, stage_k(0), stage_v(0));
       t = tn;
     }
+  }
+
+  if (SPLIT && part != 0) {
+    // one half of a split window: this workgroup's per-lane state goes out
+    // (agent-scope stores, written through to memory), then a ticket; the
+    // workgroup that takes the second ticket merges the other half's state
+    // into its own, in the order first half, second half whichever it is,
+    // and writes the output.  Per lane: m, l, e, n, then the accumulators.
+    constexpr int NF = 4 + D / 4;
+    const int64_t k = (int64_t)(qb - a.q0) * nbh + bh;
+    float* mine = a.part + (2 * k + part - 1) * NF * kPfThreads + tid;
+    auto put = [&](int f, float v) {
+      __hip_atomic_store(mine + f * kPfThreads, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    put(0, st.m);
+    put(1, st.l);
+    put(2, st.e);
+    put(3, __int_as_float(st.n));
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) put(4 + 4 * nc + u, accp[nc][u]);
+    __shared__ int sh_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are acknowledged
+    __syncthreads();
+    if (tid == 0) {
+      int* c = a.ctr + k * a.ctr_stride;
+      const int done = atomicAdd(c, 1) + 1;
+      sh_last = done == 2;
+      if (done == 2) atomicExch(c, 0);
+    }
+    __syncthreads();
+    if (!sh_last) return;
+    const float* other = a.part + (2 * k + 2 - part) * NF * kPfThreads + tid;
+    auto get = [&](int f) { return __hip_atomic_load(other + f * kPfThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    const float m2 = get(0), l2 = get(1), e2 = get(2);
+    const int n2 = __float_as_int(get(3));
+    const float mm = fmaxf(st.m, m2);
+    const float w1 = __builtin_amdgcn_exp2f(st.m - mm), w2 = __builtin_amdgcn_exp2f(m2 - mm);
+    // (first half's w, value; second half's w, value)
+    auto mix = [&](float own, float oth) {
+      return part == 1 ? __builtin_fmaf(own, w1, oth * w2) : __builtin_fmaf(oth, w2, own * w1);
+    };
+    st.l = mix(st.l, l2);
+    st.e = mix(st.e, e2);
+    st.n += n2;
+    st.m = mm;
+#pragma unroll
+    for (int nc = 0; nc < D / 16; ++nc)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) accp[nc][u] = mix(accp[nc][u], get(4 + 4 * nc + u));
   }
 
   // sums over the query's four lanes, then out = acc / max(l, 1e-9): lane
@@ -760,10 +833,14 @@ bool pf_float_dtype(int dt) { return dt == OC_F32 || dt == OC_F16 || dt == OC_BF
 
 template <int DT, int D>
 int launch_prefill(const PrefillArgs& a, hipStream_t s, unsigned blocks) {
-  if (a.entropy)
-    hipLaunchKernelGGL((prefill_kernel<DT, D, true>), dim3(blocks), dim3(kPfThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((prefill_kernel<DT, D, false>), dim3(blocks), dim3(kPfThreads), 0, s, a);
+  const dim3 grid(blocks), block(kPfThreads);
+  if (a.nitems) {
+    if (a.entropy) hipLaunchKernelGGL((prefill_kernel<DT, D, true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<DT, D, false, true>), grid, block, 0, s, a);
+  } else {
+    if (a.entropy) hipLaunchKernelGGL((prefill_kernel<DT, D, true, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_kernel<DT, D, false, false>), grid, block, 0, s, a);
+  }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "prefill launch");
 }
@@ -771,6 +848,99 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s, unsigned blocks) {
 template <int DT>
 int launch_prefill_d(const PrefillArgs& a, int d, hipStream_t s, unsigned blocks) {
   return d == 64 ? launch_prefill<DT, 64>(a, s, blocks) : launch_prefill<DT, 128>(a, s, blocks);
+}
+
+// Workgroups of prefill_kernel<DT, D> that one CU holds at once (the
+// entropy variant's budget is the same), times the device's CUs.
+template <int DT, int D>
+int pf_slots_t() {
+  static int per_cu[64] = {0};
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!per_cu[dev]) {
+    int n = 0, c = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<DT, D, false, false>, kPfThreads, 0) !=
+        hipSuccess)
+      n = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) c = 0;
+    per_cu[dev] = n > 0 ? n : -1;
+    cus[dev] = c;
+  }
+  return per_cu[dev] > 0 ? per_cu[dev] * cus[dev] : 0;
+}
+
+int pf_slots(int dtype, int d) {
+  switch (dtype) {
+    case OC_F32: return d == 64 ? pf_slots_t<OC_F32, 64>() : pf_slots_t<OC_F32, 128>();
+    case OC_F16: return d == 64 ? pf_slots_t<OC_F16, 64>() : pf_slots_t<OC_F16, 128>();
+    default: return d == 64 ? pf_slots_t<OC_BF16, 64>() : pf_slots_t<OC_BF16, 128>();
+  }
+}
+
+constexpr size_t kPfCounterBytes = 64 << 10;
+
+// The split of a call's longest causal windows: when the call's workgroups
+// fit on the device at once (one round) and no tiles are evicted, its time
+// is the longest window's;
+// blocks whose window is over half the longest (and at least 4 tiles) then
+// run as two workgroups of half the tiles each.  Items are ordered longest
+// first (ties: later block first, first half first).  False: no split.
+struct PfPlan {
+  int nitems = 0, q0 = 0, ctr_stride = 1;
+  size_t part_bytes = 0;
+  uint16_t items[kPfMaxItems];
+};
+
+bool pf_plan(const oc_prefill_params* p, PfPlan* pl) {
+  // with evicted tiles the windows' work shrinks and the merge's fixed cost
+  // no longer pays (half the tiles evicted, TinyLlama layer, bfloat16: 43
+  // unsplit against 47 us split; float32 even)
+  if (p->tile_mask) return false;
+  const int qblocks = (p->q_len + kPfRows - 1) / kPfRows;
+  const int64_t nbh = (int64_t)p->batch * p->num_q_heads;
+  if (qblocks < 1 || nbh < 1) return false;
+  const int slots = pf_slots(p->dtype, p->head_dim);
+  if (slots <= 0 || nbh * qblocks > slots) return false;
+  const int off = p->kv_len - p->q_len;
+  auto window = [&](int qb) {
+    return (std::min(std::max(std::min(qb * kPfRows + kPfRows - 1, p->q_len - 1) + off + 1, 0), p->kv_len) + 63) / 64;
+  };
+  const int wmax = window(qblocks - 1);
+  int q0 = 0;
+  while (q0 < qblocks && (2 * window(q0) <= wmax || window(q0) < 4)) ++q0;
+  const int nsplit = qblocks - q0;
+  if (nsplit == 0 || qblocks + nsplit > kPfMaxItems) return false;
+  const int64_t npairs = (int64_t)nsplit * nbh;
+  if (npairs * (int64_t)sizeof(int32_t) > (int64_t)kPfCounterBytes) return false;
+  pl->ctr_stride = 32;
+  while (pl->ctr_stride > 1 && npairs * pl->ctr_stride * (int64_t)sizeof(int32_t) > (int64_t)kPfCounterBytes)
+    pl->ctr_stride >>= 1;
+  pl->q0 = q0;
+  pl->part_bytes = (size_t)npairs * 2 * (4 + p->head_dim / 4) * kPfThreads * sizeof(float);
+  struct Item {
+    int len, qb, part;
+  };
+  Item it[kPfMaxItems];
+  int n = 0;
+  for (int qb = 0; qb < qblocks; ++qb) {
+    const int w = window(qb);
+    if (qb >= q0) {
+      const int ts = (w + 1) / 2;
+      it[n++] = {ts, qb, 1};
+      it[n++] = {w - ts, qb, 2};
+    } else {
+      it[n++] = {w, qb, 0};
+    }
+  }
+  std::stable_sort(it, it + n, [](const Item& x, const Item& y) {
+    if (x.len != y.len) return x.len > y.len;
+    if (x.qb != y.qb) return x.qb > y.qb;
+    return x.part < y.part;
+  });
+  for (int e = 0; e < n; ++e) pl->items[e] = (uint16_t)((it[e].qb << 2) | it[e].part);
+  pl->nitems = n;
+  return true;
 }
 
 }  // namespace
@@ -821,7 +991,24 @@ extern "C" int oc_prefill_attention(const oc_prefill_params* p, void* stream) {
   a.entropy = p->entropy;
   a.qblocks = (p->q_len + kPfRows - 1) / kPfRows;
   a.dtype = p->dtype;
-  const int64_t blocks = (int64_t)a.qblocks * a.B * a.Hq;
+  int64_t items = a.qblocks;
+  if (p->workspace) {
+    PfPlan pl;
+    if (pf_plan(p, &pl)) {
+      const size_t need = kPfCounterBytes + pl.part_bytes + 256;
+      if (p->workspace_bytes < need)
+        return fail(OC_ERR_WORKSPACE, "prefill workspace of %zu bytes needed, %zu given", need, p->workspace_bytes);
+      char* w = (char*)(((uintptr_t)p->workspace + 255) & ~(uintptr_t)255);
+      a.ctr = (int32_t*)w;
+      a.part = (float*)(w + kPfCounterBytes);
+      a.nitems = pl.nitems;
+      a.q0 = pl.q0;
+      a.ctr_stride = pl.ctr_stride;
+      std::copy(pl.items, pl.items + pl.nitems, a.items);
+      items = pl.nitems;
+    }
+  }
+  const int64_t blocks = items * a.B * a.Hq;
   if (blocks > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "too many query blocks");
   const hipStream_t s = (hipStream_t)stream;
   switch (p->dtype) {
@@ -829,6 +1016,14 @@ extern "C" int oc_prefill_attention(const oc_prefill_params* p, void* stream) {
     case OC_F16: return launch_prefill_d<OC_F16>(a, p->head_dim, s, (unsigned)blocks);
     default: return launch_prefill_d<OC_BF16>(a, p->head_dim, s, (unsigned)blocks);
   }
+}
+
+extern "C" size_t oc_prefill_workspace_size(const oc_prefill_params* p) {
+  if (!p || !pf_float_dtype(p->dtype) || (p->head_dim != 64 && p->head_dim != 128) || p->batch <= 0 ||
+      p->num_q_heads <= 0 || p->q_len <= 0 || p->kv_len < 0)
+    return 0;
+  PfPlan pl;
+  return pf_plan(p, &pl) ? kPfCounterBytes + pl.part_bytes + 256 : 0;
 }
 
 extern "C" int oc_row_norms(const void* x, int32_t dtype, int64_t n0, int64_t n1, int64_t n2, int64_t stride0,

@@ -744,13 +744,15 @@ def group_gate(q_norms: torch.Tensor, k_norms: torch.Tensor, num_kv_heads: int, 
 
 
 def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, tile_mask: Optional[torch.Tensor] = None,
-                      scale: Optional[float] = None, want_entropy: bool = False
+                      scale: Optional[float] = None, want_entropy: bool = False, split: bool = True
                       ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """oc_prefill_attention: causal GQA attention of q (B, Hq, Sq, d) over k, v
     (B, Hkv, Skv, d) (last dimensions contiguous, other strides free),
     skipping the tiles whose tile_mask (B, Hkv, >= Skv // 64) byte is set.
     Returns (out (B, Hq, Sq, d) in q's dtype, entropy float32 (B, Hq, Sq) or
-    None)."""
+    None).  split: let the library run the longest causal windows as two
+    workgroups each when the call fits the device in one round (it then uses
+    the stream's workspace)."""
     device = require_gpu(q, k, v)
     if q.dim() != 4 or k.dim() != 4 or v.shape != k.shape:
         raise ValueError(f"q (B, Hq, Sq, d) and k, v (B, Hkv, Skv, d) expected, got {tuple(q.shape)}, "
@@ -781,8 +783,14 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, tile
     p.scale = float(scale) if scale is not None else 1.0 / (d ** 0.5)
     p.entropy = _ptr(ent)
     with torch.cuda.device(device):
-        N.check("oc_prefill_attention", N.lib().oc_prefill_attention(
-            ctypes.byref(p), ctypes.c_void_p(current_stream(device))))
+        lib = N.lib()
+        stream = current_stream(device)
+        # a workspace lets the longest causal windows split over two workgroups
+        nws = lib.oc_prefill_workspace_size(ctypes.byref(p)) if split else 0
+        if nws:
+            ws = workspace(device, stream, nws)
+            p.workspace, p.workspace_bytes = ws.data_ptr(), ws.numel()
+        N.check("oc_prefill_attention", lib.oc_prefill_attention(ctypes.byref(p), ctypes.c_void_p(stream)))
     return out, ent
 
 

@@ -84,6 +84,7 @@ class OcPrefillParams(ctypes.Structure):
         ("tile_mask", _p), ("tile_mask_stride_b", _i64), ("tile_mask_stride_h", _i64),
         ("tile_mask_cols", _i32), ("scale", ctypes.c_float),
         ("entropy", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -134,6 +135,7 @@ SIGNATURES = {
     "oc_group_gate": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _i64, _i64, _i32, _i32, ctypes.c_double, _i32, _p,
                              _i64, _i64, _p, _p, _p]),
     "oc_prefill_attention": (_i32, [ctypes.POINTER(OcPrefillParams), _p]),
+    "oc_prefill_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(OcPrefillParams)]),
     "oc_prefill_params_bytes": (ctypes.c_size_t, []),
     "oc_block_spectra": (_i32, [ctypes.POINTER(OcSpectraParams), _p]),
     "oc_spectra_params_bytes": (ctypes.c_size_t, []),

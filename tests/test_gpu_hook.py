@@ -78,6 +78,46 @@ def test_prefill_attention_vs_oracle(dtype, case, masked):
     np.testing.assert_allclose(np64(ent), ref_ent, atol=1e-4, rtol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("masked", [False, True])
+def test_prefill_split_windows_vs_oracle(dtype, d, masked):
+    """A call whose workgroups fit the device in one round, with no tiles
+    evicted, runs its longest causal windows as two workgroups each (the
+    second to finish merges the two halves' states); output and entropy match
+    the oracle as the unsplit call's do, and the library asked for a
+    workspace (so it did split).  A masked call does not split."""
+    import ctypes
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    B, Hq, Hkv, S = 1, 8, 2, 1000  # 8 query blocks, windows of 2..16 tiles
+    G = Hq // Hkv
+    q, k, v = _qkv(B, Hq, Hkv, S, S, d, dtype, seed=d + (7 if masked else 0))
+    evict, tm = None, None
+    if masked:
+        evict = torch.rand((B, Hkv, S // 64), generator=torch.Generator().manual_seed(5)) < 0.4
+        tm = evict.to(torch.uint8).to(DEV)
+    p = N.OcPrefillParams()
+    p.dtype, p.batch, p.num_q_heads, p.num_kv_heads = X.dtype_code(q.dtype, "q"), B, Hq, Hkv
+    p.q_len, p.kv_len, p.head_dim = S, S, d
+    if masked:
+        p.tile_mask, p.tile_mask_cols = tm.data_ptr(), S // 64
+    # a mask turns the split off (its merge does not pay with tiles evicted)
+    assert (N.lib().oc_prefill_workspace_size(ctypes.byref(p)) > 0) == (not masked)
+    print(f"prefill split {dtype} d={d} masked={masked}", flush=True)
+    out, ent = X.prefill_attention(q, k, v, tile_mask=tm, want_entropy=True)
+    out1, ent1 = X.prefill_attention(q, k, v, tile_mask=tm, want_entropy=True, split=False)
+    torch.cuda.synchronize()
+    ref, ref_ent = O.hook_causal_attention(np64(q), np64(k), np64(v), G,
+                                           None if evict is None else evict.numpy())
+    for o, e, what in ((out, ent, "split"), (out1, ent1, "one workgroup per block")):
+        assert_out(o, ref, dtype, f"prefill {what} {dtype} d={d} masked={masked}")
+        np.testing.assert_allclose(np64(e), ref_ent, atol=1e-4, rtol=1e-5)
+    # a second call reuses the workspace (its tickets were left at zero)
+    out2, ent2 = X.prefill_attention(q, k, v, tile_mask=tm, want_entropy=True)
+    assert torch.equal(out2, out) and torch.equal(ent2, ent)
+
+
 def test_row_norms_and_selection():
     from orthocache_gpu import _launch as X
     g = torch.Generator().manual_seed(4)
