@@ -608,10 +608,14 @@ def hook_measure(steps, warmup):
         v = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)
         ev = (torch.rand((B, Hkv, S // 64), device="cuda", generator=g) < 0.5).to(torch.uint8)
         flops = B * Hq * (S * (S + 1) / 2) * 4 * d
-        us = _event_us(lambda: X.prefill_attention(q, k, v), steps, warmup)
-        us_ev = _event_us(lambda: X.prefill_attention(q, k, v, tile_mask=ev), steps, warmup)
+        # at least 50 warmup and 100 timed calls each: the clocks still rise
+        # over the first tens of calls of a shape (Llama-3-8B layer, bf16: 280,
+        # 250, then 237 us over consecutive 30-call windows)
+        n, w = max(steps, 100), max(warmup, 50)
+        us = _event_us(lambda: X.prefill_attention(q, k, v), n, w)
+        us_ev = _event_us(lambda: X.prefill_attention(q, k, v, tile_mask=ev), n, w)
         sdpa = _event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
-                                                                                  enable_gqa=True), steps, warmup)
+                                                                                  enable_gqa=True), n, w)
         line = {"only": "hook", "kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
                 "tokens": S, "head_dim": d, "dtype": str(dt).replace("torch.", ""),
                 "us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
