@@ -91,13 +91,15 @@ def fused_orthocache_attention_paged(
     # (paged_eviction.py:354-357).  With bf16 q, a cached decode on pages of
     # >= 16 tokens does that rounding in-kernel as it widens K
     # (OC_KSCALE_DEQUANT) and reads a bf16 V beside the fp8 K as it is: no
-    # copy of either pool.  Other shapes dequantise the pool first (bf16 q
-    # holds every fp8 value, so an unscaled K is only widened to V's type).
+    # copy of either pool.  Other shapes (and V of another type) dequantise
+    # the pool first (bf16 q holds every fp8 value, so an unscaled K is only
+    # widened to V's type).
     in_kernel = None
     if k_cache.dtype == torch.float8_e4m3fn and not isinstance(k_scale, torch.Tensor):
         ks = float(k_scale)
         k_scale = 1.0
-        if q.dtype == torch.bfloat16 and block_size >= 16 and mode == "cached":
+        if (q.dtype == torch.bfloat16 and block_size >= 16 and mode == "cached"
+                and v_cache.dtype in (torch.float8_e4m3fn, torch.bfloat16)):
             in_kernel = ks
         elif q.dtype != torch.bfloat16 or ks != 1.0:
             k_cache = X.dequant_fp8(k_cache, ks, q.dtype)

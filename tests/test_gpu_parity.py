@@ -229,6 +229,29 @@ def test_paged_fp8_k_in_kernel(bs, G, gate, lens, vdt, monkeypatch):
     assert_out(out_copy.view(-1, d), ref["out"], "bf16", what + " (copy path)")
 
 
+def test_paged_fp8_k_beside_f16_v_dequantises_the_pool():
+    """fp8 K with a scalar k_scale beside a V of neither K's type nor bf16
+    (float16), bf16 q, cached decode: the wrapper dequantises the pool, as
+    the reference does, instead of asking for the in-kernel form."""
+    from orthocache_gpu import fused_orthocache_attention_paged
+    from orthocache_gpu.triton_kernels.paged_eviction import score_paged_tiles
+    from orthocache_gpu.workloads import make_q, paged_pool
+    B, hkv, tiles, d, bs, ks = 2, 2, 4, 128, 16, 0.37
+    wl = _mixed(B * hkv, tiles, d, "f32", seed=11)
+    k8 = (wl.keys / ks).to(torch.float8_e4m3fn)
+    kd = (k8.float() * ks).to(torch.bfloat16)
+    vv = wl.values.to(torch.float16)
+    k8c, vc, bt = paged_pool(k8, vv, hkv, bs, [tiles * 64] * B, seed=2)
+    k8c, vc, bt = k8c.to(DEV), vc.to(DEV), bt.to(DEV)
+    q = make_q(B * hkv, 1, d, seed=3).to(DEV)
+    sc = score_paged_tiles(k8c, bt, k_scale=ks, q_dtype=torch.bfloat16)
+    out, m = fused_orthocache_attention_paged(q.view(B, hkv, d), k8c, vc, bt, 5.0, k_scale=ks, mode="cached",
+                                              score_cache=sc)
+    ref = O.decode_rows(np32(q), np32(kd), np32(vv), gate="zeta", threshold=5.0, G=1)
+    assert m["tiles_retained"] == ref["retained"]
+    assert_out(out.view(-1, d), ref["out"], "bf16", "paged fp8 K beside f16 V")
+
+
 # ---------------------------------------------------------------- random vs oracle
 
 def _mixed(rows, tiles, d, dtype, seed, noise_frac=0.5):
