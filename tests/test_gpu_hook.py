@@ -118,6 +118,34 @@ def test_prefill_split_windows_vs_oracle(dtype, d, masked):
     assert torch.equal(out2, out) and torch.equal(ent2, ent)
 
 
+SPLIT_CASES = [  # B, Hq, Hkv, Sq, Skv, d: calls that split their longest windows
+    (2, 4, 4, 300, 700, 64),    # chunk of queries at the end of a longer context, G = 1
+    (1, 16, 2, 513, 513, 128),  # G = 8, a partial last query block and tile
+    (1, 8, 1, 37, 2000, 64),    # one query block, a 32-tile window
+    (2, 8, 2, 640, 640, 128),   # five query blocks per head
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_prefill_split_shapes_vs_oracle(dtype, case):
+    import ctypes
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    B, Hq, Hkv, Sq, Skv, d = case
+    q, k, v = _qkv(B, Hq, Hkv, Sq, Skv, d, dtype, seed=sum(case) + 1)
+    p = N.OcPrefillParams()
+    p.dtype, p.batch, p.num_q_heads, p.num_kv_heads = X.dtype_code(q.dtype, "q"), B, Hq, Hkv
+    p.q_len, p.kv_len, p.head_dim = Sq, Skv, d
+    assert N.lib().oc_prefill_workspace_size(ctypes.byref(p)) > 0
+    print(f"prefill split {dtype} {case}", flush=True)
+    out, ent = X.prefill_attention(q, k, v, want_entropy=True)
+    torch.cuda.synchronize()
+    ref, ref_ent = O.hook_causal_attention(np64(q), np64(k), np64(v), Hq // Hkv, None)
+    assert_out(out, ref, dtype, f"prefill split {dtype} {case}")
+    np.testing.assert_allclose(np64(ent), ref_ent, atol=1e-4, rtol=1e-5)
+
+
 def test_row_norms_and_selection():
     from orthocache_gpu import _launch as X
     g = torch.Generator().manual_seed(4)
