@@ -839,7 +839,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (--gpus {args.gpus} requested): this build has no multi-GPU "
-              "path; see DESIGN.md for how the decode would shard.", file=sys.stderr)
+              "path (the decode would shard by kv heads, or by sequence with its split partials merged by "
+              "oc_lse_merge after an all-gather).", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
