@@ -27,9 +27,14 @@ constexpr int kWaves = 4;  // scoring / transform kernels: one tile per wave
 constexpr int kThreads = kWave * kWaves;
 // Decode kernel workgroup: 8 waves (one workgroup per CU at two waves per
 // SIMD) except float32 K/V at head_dim 128, which runs one wave per SIMD.
-template <int DT, int D>
+// waves of a decode_kernel workgroup: 8 (two per SIMD, <= 256 registers
+// each), or 4 at one per SIMD (512 registers) where 256 do not hold a
+// wave's state: float32 K/V at head_dim 128 (the raw K and V tile alone take
+// 256), and the VALU path at head_dim 128 with two or more heads per
+// workgroup (its tile words, heads' accumulators and states)
+template <int DT, int D, bool MQK = true, int GT = 1>
 struct DecWaves {
-  static constexpr int value = (DT == OC_F32 && D == 128) ? 4 : 8;
+  static constexpr int value = (D == 128 && (DT == OC_F32 || (!MQK && GT >= 2))) ? 4 : 8;
 };
 constexpr float kM0 = -1e9f;
 constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
@@ -1814,7 +1819,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
                                             const uint64_t* sh_bits, int wpre, int r0, int r1, float* sh_p,
                                             uint16_t* sh_v, uint8_t* sh_keep) {
   constexpr int CPL = D / 16;
-  constexpr int kDW = DecWaves<DT, D>::value;
+  constexpr int kDW = DecWaves<DT, D, MQK, GT>::value;
   constexpr int kPH = GT > 4 ? 8 : 4;  // heads per P slot row block (MQK)
   using L = Lay<DT, D>;
   const int lane = threadIdx.x & 63;
@@ -2674,9 +2679,9 @@ __device__ __forceinline__ void write_partial(const DecodeArgs& a, int g0, int g
 }
 
 template <int DT, int D, int GT, bool DOT2, bool PAGED, bool MQK, bool LOOP>
-__global__ __launch_bounds__((DecWaves<DT, D>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DT == OC_F32 && D == 128 ? 1 : 2))) void decode_kernel(
+__global__ __launch_bounds__((DecWaves<DT, D, MQK, GT>::value * kWave)) __attribute__((amdgpu_waves_per_eu(DecWaves<DT, D, MQK, GT>::value == 4 ? 1 : 2))) void decode_kernel(
     const DecodeArgs a) {
-  constexpr int kDW = DecWaves<DT, D>::value;
+  constexpr int kDW = DecWaves<DT, D, MQK, GT>::value;
   constexpr int kDT = kDW * kWave;
   const int lane = threadIdx.x & 63;
   const int g0 = blockIdx.z * GT;
@@ -3147,12 +3152,12 @@ inline void launch_decode_gt(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
       return;
     }
   }
-  const dim3 block(DecWaves<DT, HD>::value * kWave);
+  auto block = [](int w) { return dim3(w * kWave); };
   switch (gt) {
-    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ, LOOP>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_kernel<DT, HD, 1, DOT2, PG, MQ, LOOP>), grid, block(DecWaves<DT, HD, MQ, 1>::value), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<DT, HD, 2, DOT2, PG, MQ, LOOP>), grid, block(DecWaves<DT, HD, MQ, 2>::value), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<DT, HD, 4, DOT2, PG, MQ, LOOP>), grid, block(DecWaves<DT, HD, MQ, 4>::value), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<DT, HD, 8, DOT2, PG, MQ, LOOP>), grid, block(DecWaves<DT, HD, MQ, 8>::value), 0, st, a); break;
   }
 }
 
