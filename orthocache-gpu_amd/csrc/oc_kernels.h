@@ -2689,15 +2689,25 @@ __global__ __launch_bounds__((DecWaves<DT, D, MQK, GT>::value * kWave)) __attrib
   // the row, this workgroup's index among the row's workgroups, their
   // number and (flat layout) the row's first partial slot
   int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0;
+  // flat layout: single pass and dense take tile-range shares, longest
+  // first (flat_map_lpt); a cached decode splits each row's retained ranks
+  // over its workgroups (a.bal) on flat_map's layout
+  const bool lpt = a.flat && !a.bal;
+  int fb0 = 0, fb1 = 0, fntok = 0;
   if (a.flat) {
-    __shared__ int sh_fm[2 * kDW + 8];
-    if (!flat_map<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0)) return;
+    __shared__ int sh_fm[4 * kDW + 9];
+    if (lpt ? !flat_map_lpt<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0, fb0, fb1, fntok)
+            : !flat_map<kDW>(a, 4 * D, sh_fm, row, gidx, npg, slot0))
+      return;
   }
-  const RowInfo ri = row_info(a, row);
+  const RowInfo ri = lpt ? row_info_n(a, row, fntok) : row_info(a, row);
   TileList tl;
-  if (a.flat) {
-    // a contiguous share of the row's tiles (single pass, dense); cached
-    // mode splits the retained ranks instead (a.bal)
+  if (lpt) {
+    tl.s = fb0;
+    tl.n = fb1 - fb0;
+    tl.w = tl.P = 1;
+  } else if (a.flat) {
+    // a contiguous share of the row's tiles (unused by the balanced split)
     tl.s = (int)((int64_t)ri.n_tiles * gidx / npg);
     tl.n = (int)((int64_t)ri.n_tiles * (gidx + 1) / npg) - tl.s;
     tl.w = tl.P = 1;
@@ -3208,7 +3218,7 @@ constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
   template <>                                                                                     \
   hipError_t launch_decode<DT>(const DecodeArgs& a, int head_dim, int gt, int gchunks,            \
                                hipStream_t st) {                                                  \
-    const dim3 grid = a.flat ? dim3(a.fast ? a.flat_slots : a.flat_target + a.num_rows, 1, gchunks)      \
+    const dim3 grid = a.flat ? dim3(a.fast || !a.bal ? a.flat_slots : a.flat_target + a.num_rows, 1, gchunks)      \
                              : dim3(a.Pg, a.num_rows, gchunks);                                   \
     if (kHasDot2<DT> && a.q_dtype == kDot2Q<DT>) {                                               \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
