@@ -16,7 +16,7 @@ import torch
 from . import _launch as X
 from . import _native as N
 
-BS = 512
+BS = 512  # the default block size (the block_size arguments below override it per call)
 _Q_CHUNK = 64  # query rows per decode call (the kernel's group limit)
 
 
@@ -32,8 +32,6 @@ def orthocache_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.
     """q (seq_q, num_heads, head_dim), k_cache / v_cache (seq_k, num_heads,
     head_dim), block_mask (num_blocks,) bool, True = keep.  Returns (output
     (seq_q, num_heads, head_dim) bfloat16, stats) (adaptive_attention.py:159-215)."""
-    global BS
-    BS = block_size
     device = X.require_gpu(q, k_cache, v_cache)
     seq_k = k_cache.shape[0]
     nb = block_mask.shape[0]
@@ -79,8 +77,6 @@ def orthocache_attention_batched(q: torch.Tensor, k_cache: torch.Tensor, v_cache
     """q (batch, seq_q, heads, d), k_cache / v_cache (batch, seq_k, heads, d),
     one block_mask (num_blocks,) shared by the batch.  Returns (bfloat16
     (batch, seq_q, heads, d), stats) (adaptive_attention.py:246-294)."""
-    global BS
-    BS = block_size
     device = X.require_gpu(q, k_cache, v_cache)
     seq_k = k_cache.shape[1]
     nb = block_mask.shape[0]
