@@ -535,6 +535,49 @@ def test_variable_lengths_flat_layout(gate, mode, dtype, G, paged):
     assert_out(res.out, ref["out"], dtype, f"flat {gate} {mode} {dtype} G={G} paged={paged}")
 
 
+MANY_ROW_CASES = [("cs", "cached", "bf16", 4, False), ("cs", "single_pass", "bf16", 4, False),
+                  ("none", "single_pass", "bf16", 1, False), ("zeta", "cached", "f32", 2, False),
+                  ("cs", "cached", "bf16", 4, True), ("cs", "single_pass", "bf16", 2, True)]
+
+
+@pytest.mark.parametrize("gate,mode,dtype,G,paged", MANY_ROW_CASES)
+def test_flat_layout_many_rows(gate, mode, dtype, G, paged):
+    """2100 rows of random lengths (0..256 tokens, empty and partial-tile rows
+    among them): more rows than a workgroup keeps in registers while it cuts
+    the flat layout (1024 with 4-wave, 2048 with 8-wave workgroups), so the
+    rows past those are read again in every pass; most rows get a single
+    short share.  Outputs and masks against the oracle."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import calibrate_tau, make_q, paged_pool
+    rows, T, d = 2100, 4, 64
+    rng = np.random.default_rng(77)
+    lens = rng.integers(0, T * 64 + 1, size=rows)
+    lens[:40:3] = 0
+    lens[1:60:4] = T * 64
+    lens = [int(v) for v in lens]
+    wl = _mixed(rows, T, d, dtype, seed=78)
+    q = make_q(rows, G, d, dtype=TORCH_DT[dtype], seed=79)
+    el, eh, _, _ = X.score_tiles(X.rows_layout(wl.keys.to(DEV), None))
+    if paged:
+        kc, vc, bt = paged_pool(wl.keys, wl.values, 1, 16, lens, seed=80)
+        kv = X.paged_layout(kc.to(DEV), vc.to(DEV), bt.to(DEV), T)
+    else:
+        kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    gcode = {"none": N.OC_GATE_NONE, "zeta": N.OC_GATE_ZETA, "cs": N.OC_GATE_CS}[gate]
+    thr = {"cs": calibrate_tau(eh, q.to(DEV), G) if gate == "cs" else 0.0, "zeta": 5.0, "none": 0.0}[gate]
+    res = X.decode(kv, q.to(DEV), G, gate=gcode, threshold=thr,
+                   mode=N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS, scores=(el, eh),
+                   out_dtype=torch.float32, want_keep=True)
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate=gate, threshold=thr, G=G, lengths=lens)
+    if gate != "none":
+        assert np.array_equal(res.keep[:, :T].cpu().numpy().astype(bool), ref["keep"])
+    # float32 output: the short rows' outputs are single V values (up to ~3.6),
+    # where a 16-bit output's rounding alone would exceed the bar
+    assert_out(res.out, ref["out"], dtype, f"many rows {gate} {mode} {dtype} G={G} paged={paged}")
+
+
 @pytest.mark.parametrize("block_size", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("dtype,d", [("f32", 64), ("bf16", 128)])
 def test_paged_equals_contiguous(block_size, dtype, d):

@@ -172,8 +172,8 @@ def _flat_lpt_map(lens, tiles_max, target, qcap, pct, div, kdt=256, mistake=None
     return n, out, big
 
 
-def _flat_lpt_check(lens, t_max, target, qcap, pct, div, mistake=None):
-    n, out, big = _flat_lpt_map(lens, t_max, target, qcap, pct, div, mistake=mistake)
+def _flat_lpt_check(lens, t_max, target, qcap, pct, div, mistake=None, kdt=256):
+    n, out, big = _flat_lpt_map(lens, t_max, target, qcap, pct, div, kdt=kdt, mistake=mistake)
     count = len(out)
     assert all(len(v) == 1 for v in out.values())                # one share per slot
     assert sorted(out) == list(range(count))                       # slots 0 .. count-1 all used
@@ -216,3 +216,14 @@ def test_flat_lpt_layout_planted_mistake():
     _flat_lpt_check(lens, 700, 64, 512, 75, 4)
     with pytest.raises(AssertionError):
         _flat_lpt_check(lens, 700, 64, 512, 75, 4, mistake="short_after_long")
+
+
+def test_flat_lpt_layout_many_rows():
+    # more rows than the kernel's 4-wave (1024) or 8-wave (2048) workgroups
+    # keep in registers, scanned chunk by chunk; most rows get one short share
+    rng = np.random.default_rng(3)
+    lens = [int(v) for v in rng.integers(0, 257, size=2100)]
+    lens[:40:3] = [0] * len(lens[:40:3])
+    for kdt in (256, 512):
+        for qcap in (256, 512):
+            _flat_lpt_check(lens, 4, 1024, qcap, 90, 4, kdt=kdt)
