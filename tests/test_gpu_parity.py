@@ -473,6 +473,40 @@ def test_single_pass_long_split_list(gate):
     assert_out(out, ref, "bf16", f"single split {gate}")
 
 
+@pytest.mark.parametrize("tiles,gate", [(3000, "cs"), (16500, "cs"), (16500, "zeta")])
+def test_cached_decode_long_rows(tiles, gate):
+    """Cached decode of rows longer than the per-wave-prologue kernel takes
+    (2048 tiles) and, at 16,500 tiles, longer than the in-LDS retained-tile
+    bitmask of the balanced layout (16,384): the general kernel's paths for
+    such rows, with a length that cuts the last tile.  Keep flags and output
+    against the oracle."""
+    import orthocache_gpu._launch as X
+    import orthocache_gpu._native as N
+    from orthocache_gpu.workloads import calibrate_tau, make_q
+    G, d = 4, 64
+    wl = _mixed(2, tiles, d, "bf16", seed=tiles + 1)
+    q = make_q(2, G, d, dtype=torch.bfloat16, seed=tiles + 2)
+    lens = torch.tensor([tiles * 64 - 5, 2100 * 64 + 10], dtype=torch.int32)
+    kv = X.rows_layout(wl.keys.to(DEV), wl.values.to(DEV))
+    kv.lengths = lens.to(DEV)
+    el, eh, _, _ = X.score_tiles(kv, want_zeta=False, want_keep=False)
+    if gate == "cs":
+        thr, gcode = calibrate_tau(eh, q.to(DEV), G), N.OC_GATE_CS
+    else:
+        thr, gcode = 5.0, N.OC_GATE_ZETA
+    res = X.decode(kv, q.to(DEV), G, gate=gcode, threshold=thr, mode=N.OC_MODE_CACHED, scores=(el, eh),
+                   out_dtype=torch.float32, want_keep=True)
+    torch.cuda.synchronize()
+    ref = O.decode_rows(np32(q), np32(wl.keys), np32(wl.values), gate=gate, threshold=thr, G=G,
+                        lengths=lens.tolist())
+    got_keep = res.keep.cpu().numpy().astype(bool)
+    for r, n in enumerate(lens.tolist()):
+        nt = (n + 63) // 64
+        assert np.array_equal(got_keep[r, :nt], ref["keep"][r, :nt]), f"row {r}"
+    assert 0 < int(ref["keep"].sum()) < ref["keep"].size
+    assert_out(res.out, ref["out"], "bf16", f"long rows {tiles} {gate}")
+
+
 def test_auto_num_splits_on_device():
     from orthocache_gpu import fused_orthocache_attention_v2
     cus = torch.cuda.get_device_properties(0).multi_processor_count
