@@ -418,14 +418,24 @@ static bool fused_merge(const oc_decode_params* p, int pg) {
 }
 
 // Rows of different lengths (a lengths array) are laid out flat: row r gets
-// workgroups in proportion to its tiles, about g_flat_per_cu per CU in all
+// workgroups in proportion to its tiles, about per_cu per CU in all
 // (flat_map in the kernel; flat_map_lpt, long shares first, in the
-// per-wave-prologue kernel, with g_flat_pct percent of each row's tiles in
-// long shares and short shares 1 / g_flat_div as long), with the merge
-// fused.  Not with partials requested (their layout is the per-split one),
-// per-split counts, or a cached decode too long for the in-LDS retained-tile
-// bitmask.
-static int g_flat_per_cu = 4, g_flat_pct = 90, g_flat_div = 4;
+// per-wave-prologue kernel and the single-pass and dense decodes, with pct
+// percent of each row's tiles in long shares and short shares 1 / div as
+// long), with the merge fused.  Not with partials requested (their layout is
+// the per-split one), per-split counts, or a cached decode too long for the
+// in-LDS retained-tile bitmask.  A single-pass gated decode scores every tile
+// inside its loop, and runs best with fewer, longer shares (config 3: 437-441
+// us at 2 per CU and 95%, against 451-468 at 4 and 90%, where the cached and
+// dense decodes are fastest).
+struct FlatCfg {
+  int per_cu, pct, div;
+};
+static FlatCfg g_flat = {4, 90, 4}, g_flat_sp = {2, 95, 4};
+
+static FlatCfg flat_cfg(const oc_decode_params* p) {
+  return p->mode == OC_MODE_SINGLE_PASS && p->gate != OC_GATE_NONE ? g_flat_sp : g_flat;
+}
 
 static bool flat_layout(const oc_decode_params* p) {
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
@@ -435,22 +445,22 @@ static bool flat_layout(const oc_decode_params* p) {
          fused_merge(p, 1);
 }
 
-static int flat_target() { return g_flat_per_cu * device_cus(); }
+static int flat_target(const oc_decode_params* p) { return flat_cfg(p).per_cu * device_cus(); }
 
 // partial slots of the flat layout: flat_map_lpt's bound, which also covers
 // flat_map's flat_target + rows
 static size_t flat_slots(const oc_decode_params* p) {
-  return (size_t)flat_lpt_slots(flat_target(), p->kv.num_rows, g_flat_pct, g_flat_div);
+  const FlatCfg c = flat_cfg(p);
+  return (size_t)flat_lpt_slots(flat_target(p), p->kv.num_rows, c.pct, c.div);
 }
 
 // Measurement hook (not declared in the public header): the flat layout's
 // workgroups per CU (1..16), percent of tiles in long shares (0..100) and
-// short-share divisor (1..16).  Returns 0, or -1 for values out of range.
+// short-share divisor (1..16), for every mode.  Returns 0, or -1 for values
+// out of range.
 extern "C" int oc_internal_flat_tuning(int per_cu, int pct, int div) {
   if (per_cu < 1 || per_cu > 16 || pct < 0 || pct > 100 || div < 1 || div > 16) return -1;
-  g_flat_per_cu = per_cu;
-  g_flat_pct = pct;
-  g_flat_div = div;
+  g_flat = g_flat_sp = FlatCfg{per_cu, pct, div};
   return 0;
 }
 
@@ -530,9 +540,9 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   a.spw = choose_spw(p);
   a.Pg = num_groups(p, a.spw);
   a.flat = flat_layout(p) ? 1 : 0;
-  a.flat_target = flat_target();
-  a.flat_pct = g_flat_pct;
-  a.flat_div = g_flat_div;
+  a.flat_target = flat_target(p);
+  a.flat_pct = flat_cfg(p).pct;
+  a.flat_div = flat_cfg(p).div;
   a.flat_slots = a.flat ? (int)flat_slots(p) : 0;
   a.keep_out = p->keep_out;
   a.keep_stride = p->keep_row_stride;

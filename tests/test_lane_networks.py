@@ -205,7 +205,7 @@ def test_flat_lpt_layout_tiles_every_row_once():
         lens = [int(rng.choice([0, rng.integers(0, t_max * 64 + 1), t_max * 64, rng.integers(0, 200)]))
                 for _ in range(rows)]
         target, qcap = int(rng.choice([256, 512, 1024, 2048])), int(rng.choice([256, 512]))
-        pct, div = int(rng.choice([0, 50, 75, 90, 100])), int(rng.choice([1, 2, 4, 8, 16]))
+        pct, div = int(rng.choice([0, 50, 75, 90, 95, 100])), int(rng.choice([1, 2, 4, 8, 16]))
         _flat_lpt_check(lens, t_max, target, qcap, pct, div)
 
 
