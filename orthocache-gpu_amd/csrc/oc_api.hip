@@ -431,10 +431,10 @@ static bool fused_merge(const oc_decode_params* p, int pg) {
 struct FlatCfg {
   int per_cu, pct, div;
 };
-static FlatCfg g_flat = {4, 90, 4}, g_flat_sp = {2, 95, 4};
+static constexpr FlatCfg kFlat = {4, 90, 4}, kFlatSinglePass = {2, 95, 4};
 
 static FlatCfg flat_cfg(const oc_decode_params* p) {
-  return p->mode == OC_MODE_SINGLE_PASS && p->gate != OC_GATE_NONE ? g_flat_sp : g_flat;
+  return p->mode == OC_MODE_SINGLE_PASS && p->gate != OC_GATE_NONE ? kFlatSinglePass : kFlat;
 }
 
 static bool flat_layout(const oc_decode_params* p) {
@@ -452,16 +452,6 @@ static int flat_target(const oc_decode_params* p) { return flat_cfg(p).per_cu * 
 static size_t flat_slots(const oc_decode_params* p) {
   const FlatCfg c = flat_cfg(p);
   return (size_t)flat_lpt_slots(flat_target(p), p->kv.num_rows, c.pct, c.div);
-}
-
-// Measurement hook (not declared in the public header): the flat layout's
-// workgroups per CU (1..16), percent of tiles in long shares (0..100) and
-// short-share divisor (1..16), for every mode.  Returns 0, or -1 for values
-// out of range.
-extern "C" int oc_internal_flat_tuning(int per_cu, int pct, int div) {
-  if (per_cu < 1 || per_cu > 16 || pct < 0 || pct > 100 || div < 1 || div > 16) return -1;
-  g_flat = g_flat_sp = FlatCfg{per_cu, pct, div};
-  return 0;
 }
 
 extern "C" size_t oc_decode_workspace_size(const oc_decode_params* p) {

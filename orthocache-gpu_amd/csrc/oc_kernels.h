@@ -2605,14 +2605,26 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
       acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
       acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
     }
-#pragma unroll 16
-    for (int q = sl + PF * NSLICE; q < Pg; q += NSLICE) {
-      const float4 x = ld4(q);
-      const float w = wg[q];
-      acc.x = __builtin_fmaf(x.x, w, acc.x);
-      acc.y = __builtin_fmaf(x.y, w, acc.y);
-      acc.z = __builtin_fmaf(x.z, w, acc.z);
-      acc.w = __builtin_fmaf(x.w, w, acc.w);
+    // the rest in rounds of RB independent loads (the same order of
+    // additions as one partial at a time)
+    constexpr int RB = 16;
+#pragma unroll 1
+    for (int q0 = sl + PF * NSLICE; q0 < Pg; q0 += RB * NSLICE) {
+      float4 x[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int q = q0 + i * NSLICE;
+        x[i] = q < Pg ? ld4(q) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int q = q0 + i * NSLICE;
+        const float w = q < Pg ? wg[q] : 0.f;
+        acc.x = __builtin_fmaf(x[i].x, w, acc.x);
+        acc.y = __builtin_fmaf(x[i].y, w, acc.y);
+        acc.z = __builtin_fmaf(x[i].z, w, acc.z);
+        acc.w = __builtin_fmaf(x[i].w, w, acc.w);
+      }
     }
   }
   sh_red[threadIdx.x] = acc;

@@ -80,7 +80,7 @@ struct PfState {
 template <int D, bool ENT>
 __device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f32x4 (&c)[4], float scale2, int nvis,
                                            int tok0, bool full, int lane) {
-  const int r = lane >> 4;
+  (void)lane;  // lane / 16 (the row group r) is formed from the thread index below
   float mt = -__builtin_inff();
   if (full) {
 #pragma unroll
@@ -92,11 +92,17 @@ __device__ __forceinline__ void pf_softmax(PfState& st, f32x4 (&acc)[D / 16], f3
         mt = fmaxf(mt, v);
       }
   } else {
+    // 4 r formed here from the thread index (lane = threadIdx.x mod 64; the
+    // empty asm keeps the compiler from keeping it in a register across the
+    // tile loop, where the bfloat16 entropy kernels would spill it)
+    int tx = threadIdx.x;
+    asm volatile("" : "+v"(tx));
+    const int r4 = (tx >> 2) & 12;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = tok0 + 16 * tb + 4 * r + i < nvis ? c[tb][i] * scale2 : -__builtin_inff();
+        const float v = tok0 + 16 * tb + r4 + i < nvis ? c[tb][i] * scale2 : -__builtin_inff();
         c[tb][i] = v;
         mt = fmaxf(mt, v);
       }
@@ -555,6 +561,16 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
     for (int nc = 0; nc < D / 16; ++nc)
 #pragma unroll
       for (int u = 0; u < 4; ++u) put(4 + 4 * nc + u, accp[nc][u]);
+    // The hand-off below relies on gfx950's cache behaviour rather than on a
+    // release / acquire pair of the HIP memory model, as the decode's fused
+    // merge does: an agent-scope store is written through this XCD's L2
+    // (sc1), its vmcnt acknowledgement comes back once memory holds it, and
+    // an agent-scope load in the other workgroup (sc1) is served from memory,
+    // not from a stale line of that XCD's L2.  So once every thread's stores
+    // are acknowledged and the barrier has passed, the ticket can be taken
+    // relaxed.  The formal pair (release on the ticket: an L2 write-back of
+    // the whole XCD; acquire in the merging workgroup: an L2 invalidate)
+    // costs more than the merge it protects.
     __shared__ int sh_last;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are acknowledged
     __syncthreads();
@@ -592,8 +608,15 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
   l += xpair<16>(l);
   l += xpair<32>(l);
   const float inv = 1.f / fmaxf(l, 1e-9f);
-  if (qpos < a.Sq) {
-    char* orow = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qpos * a.o_ss;
+  // this lane's query again, formed from the thread index after the loop
+  // instead of kept in a register across it (the empty asm keeps the
+  // compiler from reusing the value from before the loop): that register
+  // would be the one spilled to scratch in the bfloat16 entropy kernels
+  int tid_late = tid;
+  asm volatile("" : "+v"(tid_late));
+  const int qpos_o = pos0 + (tid_late & 15);
+  if (qpos_o < a.Sq) {
+    char* orow = a.out + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qpos_o * a.o_ss;
 #pragma unroll
     for (int nc = 0; nc < D / 16; ++nc) {
       const int col = 16 * nc + 4 * r;
@@ -610,13 +633,13 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(DT =
     float e = st.e;
     e += xpair<16>(e);
     e += xpair<32>(e);
-    if (qpos < a.Sq && r == 0) {
+    if (qpos_o < a.Sq && r == 0) {
       // H = -sum p ln p with p = e^(s - m) / l: m + ln l - (sum e^(s-m) s) / l,
       // plus the clamp term of the probabilities that are exactly zero
       const float hz = (float)(a.Skv - st.n) * kZeroPTerm;
       constexpr float kLn2 = 0.6931471805599453f;
       const float H = l > 0.f ? kLn2 * (st.m - e / l) + logf(l) + hz : (float)a.Skv * kZeroPTerm;
-      a.entropy[((int64_t)b * a.Hq + h) * a.Sq + qpos] = H;
+      a.entropy[((int64_t)b * a.Hq + h) * a.Sq + qpos_o] = H;
     }
   }
 }

@@ -8,6 +8,7 @@ computation on the path runs in liborthocache_hip.
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 from typing import Dict, Optional, Tuple
 
@@ -460,7 +461,9 @@ def dequant_fp8(src: torch.Tensor, scale: float, out_dtype: torch.dtype) -> torc
     return out
 
 
-_HOOK_PARAMS: Dict[tuple, "N.OcHookDecodeParams"] = {}
+# the parameter blocks of hook_decode, per thread (a block's pointers are
+# rewritten on every call, so two threads must not share one)
+_HOOK_TLS = threading.local()
 
 
 def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_norms: torch.Tensor, G: int,
@@ -477,7 +480,13 @@ def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_n
     Hkv, S = key.shape[1], key.shape[2]
     dt = query.dtype
     if key.dtype != dt or value.dtype != dt:
-        key, value = key.to(dt), value.to(dt)
+        # the reference decodes from query.float(), key.float(), value.float()
+        # (perplexity_eval.py:590-592): with mixed types every operand is
+        # widened to float32 (exact for float16 / bfloat16), the decode runs in
+        # float32, and the output is rounded once to the query's type
+        out, stats = hook_decode(query.float(), key.float(), value.float(), k_norms, G, tau_norm, low_band,
+                                 want_stats, stats_out)
+        return out.to(dt), stats
     rows = []
     for t in (key, value):
         if t.stride(3) != 1 or (B > 1 and t.stride(0) != Hkv * t.stride(1)):
@@ -493,7 +502,10 @@ def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_n
         raise ValueError("k_norms must be float32 with contiguous rows")
     skey = (device.index, dt, B, Hq, Hkv, d, key.stride(1), key.stride(2), value.stride(1), value.stride(2),
             query.stride(1), k_norms.stride(0), low_band)
-    p = _HOOK_PARAMS.get(skey)
+    cache = getattr(_HOOK_TLS, "params", None)
+    if cache is None:
+        cache = _HOOK_TLS.params = {}
+    p = cache.get(skey)
     if p is None:
         p = N.OcHookDecodeParams()
         p.q_row_stride = query.stride(1)
@@ -505,7 +517,7 @@ def hook_decode(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, k_n
         p.low_band = low_band
         p.num_splits = 0
         p.out_row_stride = d
-        _HOOK_PARAMS[skey] = p
+        cache[skey] = p
     p.G = G
     p.kv_len = S
     p.tau_norm = tau_norm

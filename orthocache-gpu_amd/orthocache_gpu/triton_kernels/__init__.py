@@ -8,7 +8,7 @@ points run the decode kernel with a given tile mask.
 
 from .fwht_fused_prototype import (  # noqa: F401
     TILE_SIZE, BAND_DC_64, BAND_LOW_64, BAND_MID_64, BAND_HIGH_64,
-    generate_walsh_matrix, triton_fwht_eviction, score_tiles, fwht_tiles, TileScores,
+    generate_walsh_matrix, triton_fwht_eviction, score_tiles, fwht_tiles, TileScores, print_kernel_metadata,
 )
 from .fused_eviction import fused_orthocache_attention, fused_orthocache_attention_v2  # noqa: F401
 from .gqa_eviction import fused_orthocache_attention_v3_gqa  # noqa: F401
@@ -24,6 +24,7 @@ __all__ = [
     "score_tiles",
     "fwht_tiles",
     "TileScores",
+    "print_kernel_metadata",
     "fused_orthocache_attention",
     "fused_orthocache_attention_v2",
     "fused_orthocache_attention_v3_gqa",

@@ -158,3 +158,15 @@ def fwht_tiles(keys: torch.Tensor) -> torch.Tensor:
     kv = X.rows_layout(keys, None)
     out = X.fwht_tiles(kv)
     return out[0] if squeeze else out
+
+
+def print_kernel_metadata(match: str = "score_kernel"):
+    """Print the compiled kernels' LDS use, registers, scratch and spills
+    (fwht_fused_prototype.py:329-385).  The reference triggers Triton's JIT
+    and reads its metadata for the FWHT kernel; here every kernel is built
+    ahead of time, so the figures are read from the gfx950 code objects of
+    liborthocache_hip.so (no launch, no GPU needed).  `match` selects kernels
+    by a substring of their demangled names: the tile-scoring kernels by
+    default, '' for all.  Returns the printed rows."""
+    from ..kernel_metadata import print_kernel_metadata as _print
+    return _print(match)

@@ -182,6 +182,17 @@ def test_pipeline_host_logic():
     if not torch.cuda.is_available():
         assert get_hardware_profile().name == "RTX 4060 Laptop"
     assert "crossover" in format_bypass_reason(BypassFlag.CROSSOVER_BYPASS, 100, 4096)
+    # the reference's telemetry strings, order and separator (pipeline.py:87-117)
+    assert format_bypass_reason(BypassFlag.NONE) == "no flags set"
+    assert format_bypass_reason(BypassFlag.CROSSOVER_BYPASS, 100, 4096) == "seq_len_k=100 < crossover=4096"
+    assert (format_bypass_reason(BypassFlag.CROSSOVER_BYPASS, 512, 2048, _GPU_PROFILES["MI355X"])
+            == "seq_len_k=512 < crossover=2048 on MI355X (256 CUs, 8000 GB/s)")
+    allf = BypassFlag(0xFF)
+    assert format_bypass_reason(allf, 1, 2).split("; ") == [
+        "seq_len_k=1 < crossover=2", "mode=dense (explicit)", "mode=triton_fused (God Kernel)",
+        "full spectral eviction path", "all blocks evicted", "tau auto-computed (mean - 1σ)",
+        "GPU auto-detected via bandwidth-ratio model"]
+    assert format_bypass_reason(BypassFlag.PERFECT_EVICTION) == "no flags set"
     assert TelemetryLevel.SILENT < TelemetryLevel.FLAGS < TelemetryLevel.VERBOSE
     q = torch.randn(1, 2, 64)
     k = torch.randn(1024, 2, 64)

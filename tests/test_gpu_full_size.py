@@ -15,10 +15,14 @@
   - with tau = 1.0 nothing is evicted;
   - the cached and single-pass decodes agree;
   - the output equals a float64 softmax over the retained tokens.
+* Configs 0 (v1, one head, 4096 tokens, float32) and 1 (v2, 32 heads,
+  float16, 1K / 4K / 32K tokens, bench.py's own parameter blocks) at their
+  stated sizes against the oracle: masks bit-exact, outputs within the bar.
 * The stand-alone oc_lse_merge against the oracle's sequential merge
   (fused_eviction.py:316-373) and against the decode's fused merge.
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -190,6 +194,72 @@ def test_bench_batch1_step():
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("recipe", ["tokens", "literal"])
+@pytest.mark.parametrize("mode", ["single_pass", "cached"])
+def test_config0_full_size_vs_oracle(recipe, mode):
+    """Config 0 as stated: v1 on q (1, 128) and K, V (4096, 128) float32,
+    seed 0, zeta_max 5.0 (fused_eviction.py:698-800, CPU body :460-549).
+    `tokens` builds the half-smooth / half-noise tiles along the token axis
+    (the reference benchmark's construction), `literal` with the Walsh rows
+    along head_dim (the config text read literally).  Mask bit-exact with
+    the oracle, output within the float32 bar."""
+    from orthocache_gpu import fused_orthocache_attention, score_tiles
+    from orthocache_gpu.workloads import make_kv, make_kv_literal, make_q
+    if recipe == "tokens":
+        wl = make_kv(1, 4096, 128, noise_frac=0.5, dtype=torch.float32, seed=0)
+        k, v = wl.keys[0], wl.values[0]
+    else:
+        k, _ = make_kv_literal(1, 4096, 128, dtype=torch.float32, seed=0)
+        k = k[0]
+        v = torch.randn((4096, 128), generator=torch.Generator().manual_seed(1))
+    q = make_q(1, 1, 128, dtype=torch.float32, seed=2)
+    ref, rmeta = O.fused_v1(np32(q), np32(k), np32(v), 5.0, return_mask=True)
+    kd, vd = k.to(DEV), v.to(DEV)
+    sc = score_tiles(kd.unsqueeze(0)) if mode == "cached" else None
+    out, meta = fused_orthocache_attention(q.to(DEV), kd, vd, 5.0, return_mask=True, mode=mode, score_cache=sc)
+    assert np.array_equal(meta["eviction_mask"].cpu().numpy(), rmeta["eviction_mask"]), recipe
+    assert meta["tiles_retained"] == rmeta["tiles_retained"] and meta["tiles_evicted"] == rmeta["tiles_evicted"]
+    if recipe == "tokens":
+        assert rmeta["tiles_evicted"] == 32  # half of the 64 tiles are noise
+    assert_out(out, ref, "f32", f"config 0 full size {recipe} {mode}")
+
+
+@pytest.mark.parametrize("seq_len", [1024, 4096, 32768])
+def test_config1_full_size_vs_oracle(seq_len):
+    """Config 1 as stated and as bench.py times it (its Sweep parameter
+    blocks, buffer set 0): v2, 32 heads, float16 q/K/V, zeta_max 5.0, over
+    1K, 4K and 32K tokens (fused_eviction.py:573-691, CPU body :380-457).
+    Dense, single-pass and cached decodes: masks bit-exact with the oracle,
+    outputs within the float16 bar."""
+    import bench
+    sw = bench.Sweep(seq_len)
+    try:
+        s0 = sw.sets[0]
+        q, k, v = s0["q"], s0["wl"].keys, s0["wl"].values
+        print(f"config 1 full size S={seq_len}: oracle", flush=True)
+        ref, rmeta, rmask = O.fused_v2(np32(q), np32(k), np32(v), 5.0)
+        assert np.array_equal(rmask, ~s0["wl"].noise.cpu().numpy())
+        for variant in ("single_pass", "cached"):
+            rc = sw.lib.oc_decode(ctypes.byref(sw.params[variant][0]), ctypes.c_void_p(sw.stream))
+            assert rc == 0
+            torch.cuda.synchronize()
+            assert_out(sw.out, ref, "f16", f"config 1 full size S={seq_len} {variant} (bench parameters)")
+        # the drop-in API on the same inputs: its eviction mask
+        from orthocache_gpu import fused_orthocache_attention_v2
+        out, meta = fused_orthocache_attention_v2(q, k, v, 5.0)
+        assert np.array_equal(meta["eviction_mask"].cpu().numpy(), rmask)
+        assert meta["tiles_evicted"] == rmeta["tiles_evicted"]
+        assert_out(out, ref, "f16", f"config 1 full size S={seq_len} v2 API")
+        rc = sw.lib.oc_decode(ctypes.byref(sw.params["dense"][0]), ctypes.c_void_p(sw.stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        dense = O.dense_decode(np32(q), np32(k), np32(v))
+        assert_out(sw.out, dense, "f16", f"config 1 full size S={seq_len} dense (bench parameters)")
+    finally:
+        del sw
+        torch.cuda.empty_cache()
+
+
 def test_config2_full_size():
     """Batch 8 x 8 kv heads x 65536 tokens, bf16, G = 4 (two low-band query
     heads per group): calibrated tau (cached and single pass) and the
@@ -304,6 +374,13 @@ def test_lse_merge_standalone_vs_oracle(rows, P, d, out_dtype):
     w = np.exp(m.astype(np.float64) - m.max(axis=1, keepdims=True))
     exact = (w[..., None] * acc).sum(axis=1) / np.maximum((w * l).sum(axis=1), 1e-9)[:, None]
     assert_out(got, exact, bar, f"lse_merge rows={rows} P={P} d={d} vs exact")
+    if out_dtype != torch.float32:
+        # the same merge before the output's 16-bit rounding: float32 out
+        # against exact arithmetic at the float32 bar, so that the 16-bit
+        # figure above is the output rounding alone
+        got32 = X.lse_merge(torch.from_numpy(m).to(DEV), torch.from_numpy(l).to(DEV), torch.from_numpy(acc).to(DEV),
+                            out_dtype=torch.float32)
+        assert_out(got32, exact, "f32", f"lse_merge rows={rows} P={P} d={d} vs exact, before {bar} rounding")
     if P <= 512:
         # the oracle's sequential float32 merge accumulates one rounding per
         # split; over thousands of splits that alone nears the float32 bar

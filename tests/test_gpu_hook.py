@@ -404,3 +404,31 @@ def test_hook_decode_entry_point(dtype, B, Hq, Hkv, d, S):
     res = X.decode(kv, q.reshape(B * Hq, d), G, gate=N.OC_GATE_MASK, threshold=0.0, mode=N.OC_MODE_CACHED,
                    out_dtype=q.dtype, tile_mask=keep.view(B * Hkv, -1))
     assert_out(out.view(B * Hq, d), np64(res.out), dtype, f"oc_hook_decode vs composed {dtype}", ref_rounded=True)
+
+
+@pytest.mark.parametrize("qd,kd", [("bf16", "f32"), ("f16", "f32"), ("f32", "bf16"), ("bf16", "f16")])
+def test_hook_decode_mixed_dtypes(qd, kd):
+    """A cache whose type differs from the query's: the reference decodes
+    from query.float(), key.float(), value.float() (perplexity_eval.py:
+    590-592) and rounds once to the query's type.  oc_hook_decode widens
+    every operand to float32 (exact) and rounds the output once, so the
+    result equals the oracle on the float32 values of the stored operands
+    within the query type's bar, and equals the all-float32 call rounded."""
+    from orthocache_gpu import _launch as X
+    B, Hq, Hkv, d, S = 2, 8, 2, 128, 333
+    G = Hq // Hkv
+    q, _, _ = _qkv(B, Hq, Hkv, 1, S, d, qd, seed=51)
+    _, k, v = _qkv(B, Hq, Hkv, 1, S, d, kd, seed=52)
+    T = S // 64
+    g = torch.Generator().manual_seed(9)
+    norms = (torch.rand((Hkv, T), generator=g) * 40 + 1).to(DEV)
+    probe = O.hook_decode(np64(q), np64(k), np64(v), np64(norms), G, tau=-1.0)
+    tau = _gap_tau(probe["qn"][:, :, None].astype(np.float64) * np64(norms)[None, :, :T] / (64 * d))
+    print(f"hook_decode mixed q {qd} kv {kd}", flush=True)
+    out, stats = X.hook_decode(q, k, v, norms, G, tau * 64 * d, 8)
+    assert out.dtype == TD[qd]
+    ref = O.hook_decode(np64(q), np64(k), np64(v), np64(norms), G, tau)
+    assert_out(out, ref["out"], qd, f"oc_hook_decode mixed q {qd} kv {kd}")
+    assert stats.view(B, Hkv, 3)[:, :, 0].sum(dim=1).cpu().tolist() == ref["skipped"].tolist()
+    o32, _ = X.hook_decode(q.float(), k.float(), v.float(), norms, G, tau * 64 * d, 8)
+    assert torch.equal(out, o32.to(TD[qd]))
