@@ -25,6 +25,13 @@ is one launch of the decode kernel (the split merge runs inside it), so the
 roofline figure is the step's algorithmic bytes over the step time.  The
 partials-only call (no merge) is timed as well.
 
+The same JSON line carries the secondary measurements: batch 1
+configs 1 (the reference's published 1K..32K table), 2, 3 and 4 at full size;
+the reference's single-head 32K float32 fusion profile (single_head); the
+model hook's prefill kernel on four layer shapes and its decode step
+(hook_prefill, hook_decode); and orthocache_forward(mode='compact')
+(compact) -- each with its roofline fraction.
+
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 
@@ -62,12 +69,15 @@ def parse():
                          "comparing its instruction mix with the matrix-core path's (with --only)")
     ap.add_argument("--variants", default="",
                     help="with --only paged/fp8: comma-separated subset of cached,single_pass,dense")
+    ap.add_argument("--hook", type=int, default=1,
+                    help="also time the model hook's prefill and decode step and the compact forward (0 = skip)")
     ap.add_argument("--extra-configs", type=int, default=1,
                     help="also time BASELINE.json configs 3 (paged) and 4 (fp8) at full size (0 = skip)")
     ap.add_argument("--sweep", type=int, default=1,
                     help="also time BASELINE.json config 1 over 1K..32K tokens and config 2 at full size (0 = skip)")
     ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read", "gather",
-                                       "paged", "fp8", "hook", "compact", "sweep", "config2"],
+                                       "paged", "fp8", "hook", "compact", "sweep", "config2",
+                                       "single_head"],
                     default=None,
                     help="time only this decode variant of the primary batch, a plain 1 GiB device copy "
                          "(the reference kernel for scaling the profiler's byte counters), the model hook's "
@@ -513,6 +523,88 @@ def config2_measure(steps, warmup, seed=700):
     return r
 
 
+def single_head_measure(steps, warmup, seq_len=32768, seed=42):
+    """The reference's single-head fusion profile at 32K, 50% eviction
+    (benchmarks/profile_fusion.py:121-441; results/fusion_profiling_results.json,
+    rows "Dense 32768", "Fused OrthoCache (V1) 32768 0.5", "Split-K OrthoCache
+    32768 0.5", "Unfused OrthoCache 32768 0.5"): q (1, 128), K / V (32768, 128)
+    float32; half the 64-token tiles smooth (W64 C, C on sequency rows 0..7
+    with 2 N(0, 1) coefficients), half noise (0.1 N(0, 1)), shuffled
+    (profile_fusion.py:150-180); zeta_max midway between the two clusters.
+    Timed: this build's dense decode (gate none), the single-pass zeta decode
+    that both fused_orthocache_attention (v1) and fused_orthocache_attention_v2
+    on one head launch, the cached-score decode, the unfused pair (the
+    tile-scoring kernel, then torch attention over the retained tokens,
+    profile_fusion.py:231-278) and torch's dense decode (:207-228).  24 buffer
+    sets (768 MB) rotate past the Infinity Cache.  float32 K/V take the VALU
+    path (no 16-bit q for the matrix cores)."""
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles, triton_fwht_eviction
+    from orthocache_gpu.workloads import walsh64
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    T = seq_len // 64
+    w = walsh64(dev)
+    nsets = 24
+    lib, stream = N.lib(), X.current_stream(dev)
+    P = X.auto_num_splits(T, dev)
+    out = torch.empty((1, D), dtype=torch.float32, device=dev)
+    ws = torch.zeros(16 << 20, dtype=torch.uint8, device=dev)
+    sets, params = [], {"dense": [], "single_pass": [], "cached": []}
+    for i in range(nsets):
+        noise = torch.randperm(T, generator=g, device="cuda") < T // 2
+        c = torch.zeros((T, 64, D), device="cuda")
+        c[:, :8] = 2.0 * torch.randn((T, 8, D), generator=g, device="cuda")
+        k = torch.where(noise[:, None, None], 0.1 * torch.randn((T, 64, D), generator=g, device="cuda"),
+                        torch.matmul(w, c)).reshape(1, seq_len, D).contiguous()
+        v = torch.randn((1, seq_len, D), generator=g, device="cuda")
+        q = torch.randn((1, D), generator=g, device="cuda")
+        sc = score_tiles(k)
+        z = sc.e_high / (sc.e_low + 1e-6)
+        zmax = 0.5 * (float(z[~noise[None]].max()) + float(z[noise[None]].min()))
+        kv = X.rows_layout(k, v)
+        sets.append({"k": k, "v": v, "q": q, "sc": sc, "zmax": zmax, "kv": kv, "noise": noise})
+        for name, gate, mode in (("dense", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS),
+                                 ("single_pass", N.OC_GATE_ZETA, N.OC_MODE_SINGLE_PASS),
+                                 ("cached", N.OC_GATE_ZETA, N.OC_MODE_CACHED)):
+            params[name].append(_decode_params(lib, N, kv, q, 1, gate, mode, zmax, sc, P, out, ws, N.OC_F32))
+        del c
+    s0 = sets[0]
+    mask, _ = triton_fwht_eviction(s0["k"][0], s0["zmax"])
+    assert torch.equal(mask, ~s0["noise"]), "zeta mask differs from the tile labels"
+    kept = int(mask.sum())
+    tile = 64 * D * 4
+    nbytes = {"dense": 2 * T * tile, "single_pass": T * tile + kept * tile, "cached": 2 * kept * tile + T * 8}
+    r = {"workload": f"single head, q (1, {D}), K/V ({seq_len}, {D}) float32, "
+                     f"{1 - kept / T:.0%} of the tiles evicted (zeta gate)", "num_splits": P,
+         "eviction_rate": round(1 - kept / T, 4)}
+    for name, plist in params.items():
+        run = lambda i, plist=plist: N.check("oc_decode", lib.oc_decode(ctypes.byref(plist[i % nsets]),
+                                                                       ctypes.c_void_p(stream)))
+        us = _event_us_i(run, steps, warmup)
+        gbps = nbytes[name] / (us * 1e-6) / 1e9
+        r[name] = {"us": round(us, 2), "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+    scale = 1.0 / math.sqrt(D)
+
+    def unfused(i):
+        st = sets[i % nsets]
+        m, _ = triton_fwht_eviction(st["k"][0], st["zmax"])
+        tok = m.repeat_interleave(64)
+        kk, vv = st["k"][0][tok], st["v"][0][tok]
+        torch.softmax((st["q"] @ kk.T) * scale, dim=-1) @ vv
+
+    def torch_dense(i):
+        st = sets[i % nsets]
+        torch.softmax((st["q"] @ st["k"][0].T) * scale, dim=-1) @ st["v"][0]
+    r["unfused_us"] = round(_event_us_i(unfused, max(10, steps // 4), 3), 2)
+    r["torch_dense_us"] = round(_event_us_i(torch_dense, steps, warmup), 2)
+    r["speedup_vs_dense"] = {k: round(r["dense"]["us"] / r[k]["us"], 3) for k in ("single_pass", "cached")}
+    r["reference_rtx4060_ms"] = {"dense": 0.122, "fused_v1": 2.036, "split_k": 0.171, "unfused": 0.707}
+    return r
+
+
 def measure(setup, steps, warmup):
     evict = setup.check()
     r = {"batch": setup.batch, "eviction_rate": evict, "num_splits": setup.P, "tau": setup.tau,
@@ -591,16 +683,22 @@ def _event_us(fn, steps, warmup):
     return t0.elapsed_time(t1) * 1e3 / steps
 
 
+MFMA_PEAK_TFLOPS = {"float32": 157.3, "bfloat16": 2500.0, "float16": 2500.0}  # MI355X dense peaks
+
+
 def hook_measure(steps, warmup):
     """The model hook's causal prefill attention kernel (oc_prefill_attention)
     at a TinyLlama-1.1B layer (32 q / 4 kv heads, head_dim 64, float32 as the
     reference's evaluation runs it, and bfloat16) and a Llama-3-8B layer (32 / 8,
     head_dim 128, bfloat16 and float16), 2048 / 4096 tokens, without eviction and with half
     of the tiles evicted; torch's SDPA (causal, GQA) timed beside it.  FLOPs
-    are 4 * head_dim per (query, attended key)."""
+    are 4 * head_dim per (query, attended key); mfma_frac is the achieved
+    rate over MI355X's dense matrix-core peak for the dtype (float32: the
+    vector peak).  Returns one dict per shape, then the decode step's."""
     import torch
     from orthocache_gpu import _launch as X
     g = torch.Generator(device="cuda").manual_seed(0)
+    lines = []
     for B, Hq, Hkv, S, d, dt in ((1, 32, 4, 2048, 64, torch.float32), (1, 32, 4, 2048, 64, torch.bfloat16),
                                  (1, 32, 8, 4096, 128, torch.bfloat16), (1, 32, 8, 4096, 128, torch.float16)):
         q = torch.randn((B, Hq, S, d), device="cuda", generator=g).to(dt)
@@ -608,22 +706,32 @@ def hook_measure(steps, warmup):
         v = torch.randn((B, Hkv, S, d), device="cuda", generator=g).to(dt)
         ev = (torch.rand((B, Hkv, S // 64), device="cuda", generator=g) < 0.5).to(torch.uint8)
         flops = B * Hq * (S * (S + 1) / 2) * 4 * d
-        # at least 50 warmup and 100 timed calls each: the clocks still rise
+        # at least 50 warmup and 100 timed calls each, and every variant timed
+        # twice in turn (the second round reported): the clocks still rise
         # over the first tens of calls of a shape (Llama-3-8B layer, bf16: 280,
-        # 250, then 237 us over consecutive 30-call windows)
+        # 250, then 237 us over consecutive 30-call windows), and SDPA timed
+        # first or cold read 71 against 162 us on the same layer
         n, w = max(steps, 100), max(warmup, 50)
-        us = _event_us(lambda: X.prefill_attention(q, k, v), n, w)
-        us_ev = _event_us(lambda: X.prefill_attention(q, k, v, tile_mask=ev), n, w)
-        sdpa = _event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
-                                                                                  enable_gqa=True), n, w)
-        line = {"only": "hook", "kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
-                "tokens": S, "head_dim": d, "dtype": str(dt).replace("torch.", ""),
-                "us": round(us, 1), "tflops": round(flops / us / 1e6, 1),
-                "us_half_evicted": round(us_ev, 1), "torch_sdpa_us": round(sdpa, 1)}
+        fns = {"us": lambda: X.prefill_attention(q, k, v),
+               "us_half_evicted": lambda: X.prefill_attention(q, k, v, tile_mask=ev),
+               "torch_sdpa_us": lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                                                         enable_gqa=True)}
+        got = {}
+        for _ in range(2):
+            for name, fn in fns.items():
+                got[name] = _event_us(fn, n, w)
+        dts = str(dt).replace("torch.", "")
+        tf = flops / got["us"] / 1e6
+        line = {"kernel": "prefill_attention", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+                "tokens": S, "head_dim": d, "dtype": dts,
+                "us": round(got["us"], 1), "tflops": round(tf, 1),
+                "mfma_frac": round(tf / MFMA_PEAK_TFLOPS[dts], 4),
+                "us_half_evicted": round(got["us_half_evicted"], 1), "torch_sdpa_us": round(got["torch_sdpa_us"], 1)}
         if dt == torch.float32:
             line["cpu_baseline"] = _hook_cpu(q, k, v, Hq // Hkv)
-        print(json.dumps(line), flush=True)
-    hook_decode_measure(steps, warmup)
+        lines.append(line)
+    lines.append(hook_decode_measure(steps, warmup))
+    return lines
 
 
 def hook_decode_measure(steps, warmup):
@@ -647,7 +755,7 @@ def hook_decode_measure(steps, warmup):
     hook.norm_cache = SpectralNormCache(Hkv, S // 64 + 4, torch.device("cuda"))
     hook.orthocache_attention(q, k, v, G)  # prefill: fills the norm cache
     q1 = q[:, :, -1:].contiguous()
-    line = {"only": "hook", "kernel": "hook_decode_step", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+    line = {"kernel": "hook_decode_step", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
             "cached_tokens": S, "head_dim": d, "dtype": "bfloat16"}
     for name, tau in (("us_none_evicted", 0.0), ("us_all_evicted", 1e30)):
         hook.tau = tau
@@ -656,7 +764,13 @@ def hook_decode_measure(steps, warmup):
     kk, vv = k.repeat_interleave(G, 1), v.repeat_interleave(G, 1)
     line["torch_sdpa_us"] = round(_event_us(lambda: torch.nn.functional.scaled_dot_product_attention(q1, kk, vv),
                                             max(steps, 300), max(warmup, 300)), 1)
-    print(json.dumps(line), flush=True)
+    # HBM bytes of the step when nothing is evicted: K and V of every cached
+    # token (the norm cache and q are a few KB)
+    kv_bytes = 2 * B * Hkv * S * d * 2
+    gbps = kv_bytes / (line["us_none_evicted"] * 1e-6) / 1e9
+    line["kv_bytes"] = kv_bytes
+    line["roofline_frac_none_evicted"] = round(gbps / HBM_PEAK_GBPS, 4)
+    return line
 
 
 def _hook_cpu(q, k, v, G):
@@ -735,11 +849,13 @@ def compact_measure(steps, warmup):
     us_c = _event_us(lambda: orthocache_forward(q, *kv(), mode="compact", tau=-1e30), steps, warmup)
     us_d = _event_us(lambda: orthocache_forward(q, *kv(), mode="dense"), steps, warmup)
     kb = S * H * d * 2
-    print(json.dumps({"only": "compact", "tokens": S, "heads": H, "head_dim": d, "dtype": "bfloat16",
-                      "eviction_rate": meta["eviction_rate"], "block_spectrum_us": round(us_spec, 1),
-                      "block_spectrum_gbps": round(kb / us_spec / 1e3, 1), "compact_gate_us": round(us_gate, 1),
-                      "masked_attention_us": round(us_attn, 1), "compact_forward_us": round(us_c, 1),
-                      "dense_forward_us": round(us_d, 1), "cpu_baseline": _compact_cpu(q, k, v, 2)}), flush=True)
+    return {"tokens": S, "heads": H, "head_dim": d, "dtype": "bfloat16",
+            "eviction_rate": meta["eviction_rate"], "block_spectrum_us": round(us_spec, 1),
+            "block_spectrum_gbps": round(kb / us_spec / 1e3, 1),
+            "block_spectrum_roofline_frac": round(kb / us_spec / 1e3 / HBM_PEAK_GBPS, 4),
+            "compact_gate_us": round(us_gate, 1), "masked_attention_us": round(us_attn, 1),
+            "compact_forward_us": round(us_c, 1), "dense_forward_us": round(us_d, 1),
+            "cpu_baseline": _compact_cpu(q, k, v, 2)}
 
 
 def gather_measure(steps, warmup):
@@ -873,10 +989,14 @@ def main():
         print(json.dumps(dict(only="read", **read_probe(args.steps, args.warmup))))
         return
     if args.only == "hook":
-        hook_measure(args.steps, args.warmup)
+        for line in hook_measure(args.steps, args.warmup):
+            print(json.dumps(dict(only="hook", **line)), flush=True)
         return
     if args.only == "compact":
-        compact_measure(args.steps, args.warmup)
+        print(json.dumps(dict(only="compact", **compact_measure(args.steps, args.warmup))))
+        return
+    if args.only == "single_head":
+        print(json.dumps(dict(only="single_head", **single_head_measure(args.steps, args.warmup))))
         return
     if args.only == "sweep":
         print(json.dumps(dict(only="sweep", **sweep_measure(args.steps, args.warmup))))
@@ -916,12 +1036,20 @@ def main():
             cfg = ExtraConfig(which)
             extras[which] = cfg.measure(s_steps, s_warm)
             del cfg
-    sweep = cfg2 = None
+    sweep = cfg2 = single = None
     if args.sweep:
         torch.cuda.empty_cache()
         sweep = sweep_measure(s_steps, s_warm)
         torch.cuda.empty_cache()
         cfg2 = config2_measure(s_steps, s_warm)
+        torch.cuda.empty_cache()
+        single = single_head_measure(s_steps, s_warm)
+    hook = compact = None
+    if args.hook:
+        torch.cuda.empty_cache()
+        hook = hook_measure(args.steps, args.warmup)
+        torch.cuda.empty_cache()
+        compact = compact_measure(s_steps, s_warm)
     ach = r1["step_gbps"]
     traffic = traffic_from_profiles()
     probe = read_probe(20, 3) if args.read_probe else None
@@ -975,6 +1103,11 @@ def main():
     if sweep:
         line["config1_sweep"] = sweep
         line["config2"] = cfg2
+        line["single_head"] = single
+    if hook:
+        line["hook_prefill"] = hook[:-1]
+        line["hook_decode"] = hook[-1]
+        line["compact"] = compact
     if extra or extras or sweep:
         line["secondary_steps"], line["secondary_warmup"] = s_steps, s_warm
     print(json.dumps(line))

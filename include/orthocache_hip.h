@@ -136,7 +136,7 @@ typedef struct oc_kv_desc {
   const void* k;
   const void* v;
   int32_t dtype;        /* OC_F32 .. OC_FP8_E4M3FN: K's, and V's unless v_dtype says otherwise */
-  int32_t head_dim;     /* 64 or 128 */
+  int32_t head_dim;     /* a power of two <= 512 (64 and 128: the tuned kernels) */
   int32_t num_rows;
   int32_t num_tiles;    /* tiles per row (upper bound when lengths != NULL) */
   int64_t k_row_stride, k_token_stride;
@@ -168,6 +168,13 @@ typedef struct oc_kv_desc {
                                read no V accept it; oc_decode / oc_decode_static take it
                                for bf16 q in the per-wave-prologue kernel's cached and
                                dense decodes, else OC_ERR_UNSUPPORTED */
+  int32_t tile_size;        /* tokens per spectral tile: 0 (= 64) or a power of two <= 256
+                               (fused_eviction.py:610, gqa_eviction.py:552,
+                               paged_eviction.py:346: any power of two; the bands stay
+                               the Walsh rows [1, 8) and [32, 64) clipped to the tile).
+                               Tiles other than 64 tokens, and head_dim other than 64
+                               and 128, run the portable kernels (oc_generic.hip);
+                               num_tiles and num_tokens count these tiles. */
 } oc_kv_desc;
 
 /*
@@ -469,7 +476,10 @@ typedef struct oc_decode_params {
   int32_t splits_per_group; /* logical splits per workgroup (0 = choose); the
                                partial states are per group of splits */
   int32_t out_dtype;        /* OC_F32 / OC_F16 / OC_BF16 */
-  int32_t reserved1;
+  int32_t portable;         /* 1: run the portable kernels whatever the shape (they
+                               take every shape; for testing them against the tuned
+                               kernels on the same inputs); 0: the tuned kernels where
+                               they apply */
   void* out;                /* (num_rows * G, head_dim) */
   int64_t out_row_stride;
   uint8_t* keep_out;        /* optional (num_rows, num_tiles): 1 = retained */

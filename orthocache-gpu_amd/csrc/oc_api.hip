@@ -11,6 +11,7 @@
 #include <mutex>
 #include <string>
 
+#include "oc_generic.h"
 #include "oc_kernels.h"
 #include "oc_status.h"
 #include "orthocache_hip.h"
@@ -44,13 +45,18 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
     return fail(OC_ERR_UNSUPPORTED, "V dtype %d beside K dtype %d (a different V type is bf16 beside fp8 K only)",
                 kv->v_dtype, kv->dtype);
   const int ves = v_bf16 ? 2 : es;
-  if (kv->head_dim != 64 && kv->head_dim != 128)
-    return fail(OC_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", kv->head_dim);
+  const int ts = kv->tile_size > 0 ? kv->tile_size : 64;
+  if (kv->tile_size < 0 || !generic_supported(kv->head_dim, ts))
+    return fail(OC_ERR_UNSUPPORTED, "head_dim %d with %d-token tiles not supported (powers of two, head_dim <= 512, "
+                "tile_size <= 256)", kv->head_dim, ts);
+  const bool tuned = !generic_shape(kv->head_dim, ts);
   if (kv->num_rows < 0 || kv->num_tiles < 0) return fail(OC_ERR_INVALID, "negative sizes");
   if (kv->num_rows > 65535) return fail(OC_ERR_UNSUPPORTED, "num_rows %d > 65535", kv->num_rows);
   if (!kv->k) return fail(OC_ERR_INVALID, "K pointer is NULL");
   // bytes per lane per token row, and the alignment of every K (V) offset
+  // (the portable kernels read element by element: element alignment)
   auto align_of = [&](int e) -> int64_t {
+    if (!tuned) return e;
     const int64_t lb = (int64_t)(kv->head_dim / 16) * e;
     return lb < 16 ? lb : 16;
   };
@@ -65,8 +71,8 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
     return fail(OC_ERR_INVALID, "K/V base pointers must be %lld/%lld-byte aligned", (long long)al, (long long)val);
   int rc;
   if ((rc = chk(kv->k_token_stride, "K token", false))) return rc;
-  if (kv->k_token_stride * es * 64 >= ((int64_t)1 << 31) || kv->v_token_stride * ves * 64 >= ((int64_t)1 << 31))
-    return fail(OC_ERR_UNSUPPORTED, "token stride too large (64 tokens must span < 2 GiB)");
+  if (kv->k_token_stride * es * ts >= ((int64_t)1 << 31) || kv->v_token_stride * ves * ts >= ((int64_t)1 << 31))
+    return fail(OC_ERR_UNSUPPORTED, "token stride too large (a tile must span < 2 GiB)");
   if ((rc = chk(kv->v_token_stride, "V token", true))) return rc;
   memset(&a, 0, sizeof a);
   a.k = (const char*)kv->k;
@@ -106,8 +112,10 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
   a.lengths = kv->lengths;
   a.num_rows = kv->num_rows;
   a.num_tiles = kv->num_tiles;
-  if (kv->num_tokens < 0 || (int64_t)kv->num_tokens > (int64_t)kv->num_tiles * 64)
-    return fail(OC_ERR_INVALID, "num_tokens %d outside 0..num_tiles * 64", kv->num_tokens);
+  if (kv->num_tokens < 0 || (int64_t)kv->num_tokens > (int64_t)kv->num_tiles * ts)
+    return fail(OC_ERR_INVALID, "num_tokens %d outside 0..num_tiles * tile_size", kv->num_tokens);
+  if ((int64_t)kv->num_tiles * ts > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "rows longer than 2^31 tokens");
+  a.ts = ts;
   a.row_tok = kv->lengths ? 0 : kv->num_tokens;
   a.k_scale_mode = kv->k_scale_mode;
   a.v_scale_mode = kv->v_scale_mode;
@@ -437,7 +445,15 @@ static FlatCfg flat_cfg(const oc_decode_params* p) {
   return p->mode == OC_MODE_SINGLE_PASS && p->gate != OC_GATE_NONE ? kFlatSinglePass : kFlat;
 }
 
+// The portable kernels (oc_generic.hip): head_dim other than 64 / 128, tiles
+// other than 64 tokens, or asked for (p->portable).  They write one partial
+// per split group and merge_kernel combines them.
+static bool portable_path(const oc_decode_params* p) {
+  return p->portable == 1 || generic_shape(p->kv.head_dim, p->kv.tile_size > 0 ? p->kv.tile_size : 64);
+}
+
 static bool flat_layout(const oc_decode_params* p) {
+  if (portable_path(p)) return false;
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
   const bool cached = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
   return p->kv.lengths && p->out && !partials_given && !p->split_counts && p->splits_per_group != 1 &&
@@ -492,7 +508,7 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   if (rc) return rc;
   if (!p->kv.v) return fail(OC_ERR_INVALID, "V pointer is NULL");
   // in-kernel dequantisation runs where fp8 K is widened for the matrix cores
-  if (a.k_scale_mode == OC_KSCALE_DEQUANT && (p->q_dtype != OC_BF16 || (a.paged && a.bs_log2 < 4)))
+  if (a.k_scale_mode == OC_KSCALE_DEQUANT && !portable_path(p) && (p->q_dtype != OC_BF16 || (a.paged && a.bs_log2 < 4)))
     return fail(OC_ERR_UNSUPPORTED, "OC_KSCALE_DEQUANT needs bf16 q and contiguous rows or pages of >= 16 tokens");
   const int D = p->kv.head_dim;
   if (p->G < 1 || p->G > 64) return fail(OC_ERR_UNSUPPORTED, "G=%d outside 1..64", p->G);
@@ -566,11 +582,13 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
     a.pl = a.pm + rq;
   }
   const int oes = p->out_dtype == OC_F32 ? 4 : 2;
-  a.fuse = (a.flat || fused_merge(p, a.Pg)) ? 1 : 0;
+  const bool portable = portable_path(p);
+  if (p->portable != 0 && p->portable != 1) return fail(OC_ERR_INVALID, "portable %d (0 or 1)", p->portable);
+  a.fuse = !portable && (a.flat || fused_merge(p, a.Pg)) ? 1 : 0;
   // split the retained tiles of a row evenly over its workgroups (cached
   // mode); with one split per workgroup each partial stays the state of
   // exactly one logical split {s + kP}
-  a.bal = (p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && (a.spw > 1 || a.flat) &&
+  a.bal = (!portable && p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && (a.spw > 1 || a.flat) &&
            p->kv.num_tiles <= kMaxBalTiles) ? 1 : 0;
   a.out = (char*)p->out;
   a.out_dtype = p->out_dtype;
@@ -578,6 +596,18 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   if (a.num_rows == 0) return OC_OK;
   const int gt = heads_per_group(p->G);
   const int gchunks = (p->G + gt - 1) / gt;
+  if (portable) {
+    // every gate, mode, scale mode and layout, in float32 on the VALU; the
+    // model hook's fused gate is not (its caller then gates with its own
+    // kernel and decodes with the mask gate)
+    if (hk) return kHookNotFused;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = gen_launch_decode(p->kv.dtype, a, D, gt, gchunks, st);
+    if (e != hipSuccess) return hip_fail(e, "portable decode launch");
+    if (!p->out) return OC_OK;
+    return launch_merge(a.pm, a.pl, a.pacc, p->kv.num_rows * p->G, a.Pg, D, p->out, p->out_dtype,
+                        p->out_row_stride, st);
+  }
   // the barrier-free prologue (decode_fast): the transposed matrix-core step
   // on contiguous rows or pages of >= 16 tokens (q of K's 16-bit type, bf16
   // for fp8 K), every query head of a row in one workgroup, q rows readable
@@ -804,7 +834,8 @@ extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_lo
   a.t0 = 0;
   a.tcnt = kv->num_tiles;
   if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
-  const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  const hipError_t e = generic_shape(kv->head_dim, a.ts) ? gen_launch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream)
+                                                         : dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
   return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
 }
 
@@ -826,7 +857,8 @@ extern "C" int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int
   a.t0 = first_tile;
   a.tcnt = count;
   if ((int64_t)kv->num_rows * count == 0) return OC_OK;
-  const hipError_t e = dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+  const hipError_t e = generic_shape(kv->head_dim, a.ts) ? gen_launch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream)
+                                                         : dispatch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
   return e == hipSuccess ? OC_OK : hip_fail(e, "score launch");
 }
 
@@ -836,6 +868,8 @@ extern "C" int oc_band_norms(const oc_kv_desc* kv, int32_t first_tile, int32_t c
   DecodeArgs a;
   int rc = fill_kv(kv, a);
   if (rc) return rc;
+  if (generic_shape(kv->head_dim, a.ts))
+    return fail(OC_ERR_UNSUPPORTED, "band norms take head_dim 64 or 128 with 64-token tiles");
   if (!out) return fail(OC_ERR_INVALID, "out is NULL");
   if (first_tile < 0 || count < 0 || (int64_t)first_tile + count > kv->num_tiles)
     return fail(OC_ERR_INVALID, "tile range [%d, %d) outside 0..%d", first_tile, first_tile + count, kv->num_tiles);
@@ -861,6 +895,12 @@ extern "C" int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream) {
   a.lengths = nullptr;
   a.o_fwht = out;
   if ((int64_t)kv->num_rows * kv->num_tiles == 0) return OC_OK;
+  if (generic_shape(kv->head_dim, a.ts)) {
+    a.t0 = 0;
+    a.tcnt = kv->num_tiles;
+    const hipError_t e = gen_launch_score(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
+    return e == hipSuccess ? OC_OK : hip_fail(e, "fwht launch");
+  }
   const hipError_t e = dispatch_fwht(kv->dtype, a, kv->head_dim, (hipStream_t)stream);
   return e == hipSuccess ? OC_OK : hip_fail(e, "fwht launch");
 }

@@ -59,7 +59,8 @@ struct DecodeArgs {
   int64_t k_blk_stride, k_head_stride, v_blk_stride, v_head_stride;
   const int32_t* lengths;
   int32_t num_rows, num_tiles;
-  int32_t row_tok;  // tokens of every row without lengths (0: num_tiles * 64)
+  int32_t row_tok;  // tokens of every row without lengths (0: num_tiles * ts)
+  int32_t ts;       // tokens per tile (64 in every kernel of this file; any power of two in oc_generic.hip)
   // kGateHook: tile norms of kv head (row % hk_rows) at hk_norms[h * hk_stride
   // + t] for the hk_full complete tiles, threshold hk_tau, per-row
   // statistics (evicted tiles, group norm, largest tile norm) to hk_stats

@@ -59,7 +59,25 @@ def _aligned(t: torch.Tensor, nbytes: int) -> bool:
 
 
 def _kv_align(head_dim: int, es: int) -> int:
+    """Byte alignment the kernels need of every K / V offset: the tuned
+    kernels' per-lane vector width at head_dim 64 / 128, one element for the
+    portable kernels (other head dims)."""
+    if head_dim not in (64, 128):
+        return es
     return min(16, (head_dim // 16) * es)
+
+
+def tuned_shape(head_dim: int, tile_size: int) -> bool:
+    """head_dim 64 or 128 with 64-token tiles: the tuned kernels' shapes
+    (every other power-of-two shape runs the portable kernels)."""
+    return tile_size == TILE_SIZE and head_dim in (64, 128)
+
+
+def check_tile_size(tile_size: int) -> None:
+    """The reference takes any power-of-two tile size (fused_eviction.py:610);
+    the portable kernels take up to 256 tokens."""
+    if tile_size > 256:
+        raise NotImplementedError(f"tiles of at most 256 tokens are supported, got {tile_size}")
 
 
 _WIDTH = {torch.float8_e4m3fn: 1, torch.float16: 2, torch.bfloat16: 2, torch.float32: 4}
@@ -117,7 +135,8 @@ class KVLayout:
     v_head_stride: int = 0
     lengths: Optional[torch.Tensor] = None
     rows_per_length: int = 1
-    num_tokens: int = 0  # tokens of every row without lengths (0: num_tiles * 64)
+    num_tokens: int = 0  # tokens of every row without lengths (0: num_tiles * tile_size)
+    tile_size: int = TILE_SIZE
     k_scale_mode: int = N.OC_KSCALE_NONE
     k_scale: float = 1.0
     k_scales: Optional[torch.Tensor] = None
@@ -158,12 +177,14 @@ class KVLayout:
         d.v_scales = _ptr(self.v_scales)
         d.v_scales_row_stride = 0 if self.v_scales is None else self.v_scales.stride(0)
         d.error_flag = _ptr(self.error_flag)
+        d.tile_size = 0 if self.tile_size == TILE_SIZE else self.tile_size
         return d
 
 
-def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail: bool = False) -> KVLayout:
+def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail: bool = False,
+                tile_size: int = TILE_SIZE) -> KVLayout:
     """(rows, S, d) K/V views (last dimension contiguous, any other strides).
-    The tiles are the S // 64 complete ones; with partial_tail a last
+    The tiles are the S // tile_size complete ones; with partial_tail a last
     partial tile is included (as the descriptor's num_tokens = S, one length
     for every row)."""
     rows, s_len, d = keys.shape
@@ -174,11 +195,11 @@ def rows_layout(keys: torch.Tensor, values: Optional[torch.Tensor], partial_tail
     if values is not None:
         values = last_dim_ready(values, d)
     kv = KVLayout(
-        k=keys, v=values, head_dim=d, num_rows=rows, num_tiles=s_len // TILE_SIZE,
+        k=keys, v=values, head_dim=d, num_rows=rows, num_tiles=s_len // tile_size,
         k_row_stride=keys.stride(0), k_token_stride=keys.stride(1),
         v_row_stride=0 if values is None else values.stride(0),
-        v_token_stride=0 if values is None else values.stride(1))
-    if partial_tail and s_len % TILE_SIZE:
+        v_token_stride=0 if values is None else values.stride(1), tile_size=tile_size)
+    if partial_tail and s_len % tile_size:
         kv.num_tiles += 1
         kv.num_tokens = s_len
     return kv
@@ -190,7 +211,7 @@ def mixed_fp8k_bf16v(k: torch.Tensor, v: Optional[torch.Tensor]) -> bool:
 
 
 def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
-                 num_tiles: int, *, keep_mixed: bool = False) -> KVLayout:
+                 num_tiles: int, *, keep_mixed: bool = False, tile_size: int = TILE_SIZE) -> KVLayout:
     """(num_blocks, num_kv_heads, block_size, d) caches + int32 block table.
     keep_mixed: an fp8 K beside a bf16 V is passed as it is (no conversion);
     decodes that cannot read it fail with OC_ERR_UNSUPPORTED."""
@@ -213,7 +234,7 @@ def paged_layout(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: tor
         paged=True, block_size=bs, num_kv_heads=hkv, block_tables=block_tables, num_blocks=nb,
         k_block_stride=k_cache.stride(0), k_head_stride=k_cache.stride(1),
         v_block_stride=v_cache.stride(0), v_head_stride=v_cache.stride(1),
-        rows_per_length=hkv)
+        rows_per_length=hkv, tile_size=tile_size)
 
 
 # ---------------------------------------------------------------- workspace
@@ -280,11 +301,12 @@ def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float
            scores: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, num_splits: Optional[int] = None,
            out_dtype: torch.dtype, want_keep: bool = False, want_partials: bool = False,
            out: Optional[torch.Tensor] = None, splits_per_group: Optional[int] = None,
-           tile_mask: Optional[torch.Tensor] = None) -> DecodeResult:
+           tile_mask: Optional[torch.Tensor] = None, portable: int = 0) -> DecodeResult:
     """One oc_decode call.  q is (rows*G, d) with a contiguous last dimension.
     With want_partials the per-split partial states (one workgroup per
     logical split) are returned as (m, l, acc) of shapes (rows*G, P) and
-    (rows*G, P, d)."""
+    (rows*G, P, d).  portable = 1 runs the portable kernels whatever the
+    shape (they take every shape; the tuned ones run where they apply)."""
     device = require_gpu(q, kv.k, kv.v)
     d = kv.head_dim
     if q.stride(-1) != 1:
@@ -323,6 +345,7 @@ def decode(kv: KVLayout, q: torch.Tensor, G: int, *, gate: int, threshold: float
         p.score_row_stride = e_high.stride(0)
     p.num_splits = P
     p.splits_per_group = 1 if want_partials else (splits_per_group or 0)
+    p.portable = portable
     p.out_dtype = dtype_code(out.dtype, "out", allow_fp8=False)
     p.out = out.data_ptr()
     p.out_row_stride = out.stride(0)
@@ -419,9 +442,9 @@ def band_norms(kv: KVLayout, first_tile: int, count: int, band: Tuple[int, int],
 
 
 def fwht_tiles(kv: KVLayout) -> torch.Tensor:
-    """oc_fwht_tiles: (rows, T, 64, d) float32 spectra X = W64 @ K_tile."""
+    """oc_fwht_tiles: (rows, T, TS, d) float32 spectra X = W_TS @ K_tile."""
     device = require_gpu(kv.k)
-    out = torch.empty((kv.num_rows, kv.num_tiles, TILE_SIZE, kv.head_dim), dtype=torch.float32, device=device)
+    out = torch.empty((kv.num_rows, kv.num_tiles, kv.tile_size, kv.head_dim), dtype=torch.float32, device=device)
     desc = kv.struct()
     stream = current_stream(device)
     with torch.cuda.device(device):

@@ -53,7 +53,7 @@ class OcKvDesc(ctypes.Structure):
         ("v_scale_mode", _i32), ("num_tokens", _i32),
         ("v_scales", _p), ("v_scales_row_stride", _i64),
         ("error_flag", _p),
-        ("v_dtype", _i32),
+        ("v_dtype", _i32), ("tile_size", _i32),
     ]
 
 
@@ -63,7 +63,7 @@ class OcDecodeParams(ctypes.Structure):
         ("q", _p), ("q_dtype", _i32), ("G", _i32), ("q_row_stride", _i64),
         ("gate", _i32), ("mode", _i32), ("threshold", ctypes.c_double),
         ("score_e_low", _p), ("score_e_high", _p), ("score_row_stride", _i64),
-        ("num_splits", _i32), ("splits_per_group", _i32), ("out_dtype", _i32), ("reserved1", _i32),
+        ("num_splits", _i32), ("splits_per_group", _i32), ("out_dtype", _i32), ("portable", _i32),
         ("out", _p), ("out_row_stride", _i64),
         ("keep_out", _p), ("keep_row_stride", _i64),
         ("split_counts", _p),

@@ -41,16 +41,22 @@ def _check_common(head_dim: int, tile_size: int, seq_len: int, num_tiles: int) -
 
 
 def _tile_size_supported(tile_size: int) -> None:
-    if tile_size != TILE_SIZE:
-        raise NotImplementedError(f"the HIP kernels implement {TILE_SIZE}-token tiles only, got {tile_size}")
+    """Powers of two up to 256 tokens (the reference takes any power of two,
+    fused_eviction.py:610; 64 runs the tuned kernels, the others the
+    portable ones)."""
+    X.check_tile_size(tile_size)
 
 
-def _mode_code(mode: str, score_cache) -> Tuple[int, Optional[Tuple[torch.Tensor, torch.Tensor]]]:
+def _mode_code(mode: str, score_cache, tile_size: int = TILE_SIZE
+               ) -> Tuple[int, Optional[Tuple[torch.Tensor, torch.Tensor]]]:
     if mode == "single_pass":
         return N.OC_MODE_SINGLE_PASS, None
     if mode == "cached":
         if score_cache is None:
             raise ValueError("mode='cached' needs score_cache= (see fwht_fused_prototype.score_tiles)")
+        cache_ts = getattr(score_cache, "tile_size", tile_size)
+        if cache_ts != tile_size:
+            raise ValueError(f"score_cache holds scores of {cache_ts}-token tiles, the decode uses {tile_size}")
         pair = score_cache.as_pair() if hasattr(score_cache, "as_pair") else tuple(score_cache)
         return N.OC_MODE_CACHED, (pair[0].float(), pair[1].float())
     raise ValueError(f"mode must be 'single_pass' or 'cached', got {mode!r}")
@@ -91,10 +97,10 @@ def fused_orthocache_attention_v2(
     if num_splits is None:
         num_splits = _auto_num_splits(num_tiles, device)
 
-    kv = X.rows_layout(keys, values)
+    kv = X.rows_layout(keys, values, tile_size=tile_size)
     kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, num_heads, num_tiles, device)
     kv.v_scale_mode, kv.v_scales = X.vscale_mode(v_scale, num_heads, num_tiles, device)
-    mode_c, scores = _mode_code(mode, score_cache)
+    mode_c, scores = _mode_code(mode, score_cache, tile_size)
     res = X.decode(kv, q, 1, gate=N.OC_GATE_ZETA, threshold=zeta_max, mode=mode_c, scores=scores,
                    num_splits=num_splits, out_dtype=input_dtype, want_keep=sync,
                    want_partials=return_partials, out=out)
@@ -144,10 +150,10 @@ def fused_orthocache_attention(
     input_dtype = q.dtype
     device = X.require_gpu(q, keys, values)
 
-    kv = X.rows_layout(keys.unsqueeze(0), values.unsqueeze(0))
+    kv = X.rows_layout(keys.unsqueeze(0), values.unsqueeze(0), tile_size=tile_size)
     kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, 1, num_tiles, device)
     kv.v_scale_mode, kv.v_scales = X.vscale_mode(v_scale, 1, num_tiles, device)
-    mode_c, scores = _mode_code(mode, score_cache)
+    mode_c, scores = _mode_code(mode, score_cache, tile_size)
     if scores is not None:
         scores = (scores[0].reshape(1, -1), scores[1].reshape(1, -1))
     res = X.decode(kv, q, 1, gate=N.OC_GATE_ZETA, threshold=zeta_max, mode=mode_c, scores=scores,

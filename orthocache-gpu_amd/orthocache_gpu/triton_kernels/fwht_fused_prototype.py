@@ -41,8 +41,7 @@ def _check_tiles(keys: torch.Tensor, tile_size: int) -> int:
     num_tiles = num_tokens // tile_size
     assert num_tokens == num_tiles * tile_size, (
         f"seq_len {num_tokens} not divisible by tile_size {tile_size}")
-    if tile_size != TILE_SIZE:
-        raise NotImplementedError(f"the HIP kernels implement {TILE_SIZE}-token tiles only, got {tile_size}")
+    X.check_tile_size(tile_size)
     return num_tiles
 
 
@@ -61,15 +60,16 @@ def triton_fwht_eviction(
     """
     num_tiles = _check_tiles(keys, tile_size)
     X.require_gpu(keys)
-    kv = X.rows_layout(keys.unsqueeze(0), None)
+    kv = X.rows_layout(keys.unsqueeze(0), None, tile_size=tile_size)
     kv.num_tiles = num_tiles
     _, _, zeta, keep = X.score_tiles(kv, zeta_max, want_zeta=return_zeta, want_keep=True)
     mask = keep[0, :num_tiles].bool()
     return mask, (zeta[0, :num_tiles] if return_zeta else None)
 
 
-def score_tiles(keys: torch.Tensor, zeta_max: float = 0.0, k_scale=None):
-    """Band energies of every 64-token tile of (rows, S, d) keys (or (S, d)).
+def score_tiles(keys: torch.Tensor, zeta_max: float = 0.0, k_scale=None, *, tile_size: int = TILE_SIZE):
+    """Band energies of every tile (64 tokens, or `tile_size`) of (rows, S, d)
+    keys (or (S, d)).
 
     Returns a TileScores with e_low, e_high, zeta (rows, T) float32 and keep
     (rows, T) bool for zeta_max.  These are the cached scores that the
@@ -83,14 +83,15 @@ def score_tiles(keys: torch.Tensor, zeta_max: float = 0.0, k_scale=None):
         keys = keys.unsqueeze(0)
     assert keys.ndim == 3, f"keys must be (rows, S, d) or (S, d), got {tuple(keys.shape)}"
     X.require_gpu(keys)
-    kv = X.rows_layout(keys, None)
+    X.check_tile_size(tile_size)
+    kv = X.rows_layout(keys, None, tile_size=tile_size)
     if k_scale is not None:
         kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, kv.num_rows, kv.num_tiles, keys.device)
         if kv.k_scale_mode != X.N.OC_KSCALE_TILE:
             kv.k_scale_mode, kv.k_scale = X.N.OC_KSCALE_NONE, 1.0
     e_low, e_high, zeta, keep = X.score_tiles(kv, zeta_max)
     return TileScores(e_low[:, :kv.num_tiles], e_high[:, :kv.num_tiles], zeta[:, :kv.num_tiles],
-                      keep[:, :kv.num_tiles].bool(), zeta_max=zeta_max)
+                      keep[:, :kv.num_tiles].bool(), zeta_max=zeta_max, tile_size=tile_size)
 
 
 class TileScores:
@@ -102,18 +103,21 @@ class TileScores:
     `update(keys, t)` (one small launch), so no step re-reads a whole K
     cache to keep its scores current."""
 
-    def __init__(self, e_low, e_high, zeta=None, keep=None, zeta_max: float = 0.0):
+    def __init__(self, e_low, e_high, zeta=None, keep=None, zeta_max: float = 0.0, tile_size: int = TILE_SIZE):
         self.e_low, self.e_high, self.zeta, self.keep = e_low, e_high, zeta, keep
         self.zeta_max = zeta_max
+        self.tile_size = tile_size  # tokens per tile the scores were formed over
 
     def as_pair(self):
         return self.e_low, self.e_high
 
     @classmethod
-    def allocate(cls, rows: int, max_tiles: int, device, zeta_max: float = 0.0) -> "TileScores":
+    def allocate(cls, rows: int, max_tiles: int, device, zeta_max: float = 0.0,
+                 tile_size: int = TILE_SIZE) -> "TileScores":
         """Zeroed (rows, max_tiles) score tensors to fill with `update`."""
         z = lambda dt: torch.zeros((rows, max_tiles), dtype=dt, device=device)
-        return cls(z(torch.float32), z(torch.float32), z(torch.float32), z(torch.bool), zeta_max=zeta_max)
+        return cls(z(torch.float32), z(torch.float32), z(torch.float32), z(torch.bool), zeta_max=zeta_max,
+                   tile_size=tile_size)
 
     def update(self, keys: torch.Tensor, first_tile: int, count: int = 1, *, block_tables=None,
                context_lens=None, k_scale=None) -> "TileScores":
@@ -128,12 +132,13 @@ class TileScores:
         if block_tables is not None:
             X.require_gpu(keys, block_tables)
             nb, hkv, bs, d = keys.shape
-            kv = X.paged_layout(keys, keys, block_tables, -(-(block_tables.shape[1] * bs) // TILE_SIZE))
+            ts = self.tile_size
+            kv = X.paged_layout(keys, keys, block_tables, -(-(block_tables.shape[1] * bs) // ts), tile_size=ts)
         else:
             squeeze = keys.ndim == 2
             keys = keys.unsqueeze(0) if squeeze else keys
             X.require_gpu(keys)
-            kv = X.rows_layout(keys, None)
+            kv = X.rows_layout(keys, None, tile_size=self.tile_size)
         if first_tile + count > kv.num_tiles:
             raise ValueError(f"keys hold {kv.num_tiles} tiles, tiles up to {first_tile + count} requested")
         if kv.num_rows > self.e_high.shape[0]:
@@ -148,14 +153,16 @@ class TileScores:
         return self
 
 
-def fwht_tiles(keys: torch.Tensor) -> torch.Tensor:
-    """The full transform X = W64 @ K_tile of every tile of (S, d) or
-    (rows, S, d) keys, float32 (rows, T, 64, d) (or (T, 64, d))."""
+def fwht_tiles(keys: torch.Tensor, *, tile_size: int = TILE_SIZE) -> torch.Tensor:
+    """The full transform X = W_TS @ K_tile of every tile of (S, d) or
+    (rows, S, d) keys, float32 (rows, T, TS, d) (or (T, TS, d)); TS = 64 or
+    `tile_size`."""
     squeeze = keys.ndim == 2
     if squeeze:
         keys = keys.unsqueeze(0)
     X.require_gpu(keys)
-    kv = X.rows_layout(keys, None)
+    X.check_tile_size(tile_size)
+    kv = X.rows_layout(keys, None, tile_size=tile_size)
     out = X.fwht_tiles(kv)
     return out[0] if squeeze else out
 

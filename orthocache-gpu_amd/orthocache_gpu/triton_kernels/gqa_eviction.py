@@ -70,7 +70,7 @@ def fused_orthocache_attention_v3_gqa(
     if num_splits is None:
         num_splits = _auto_num_splits_gqa(num_tiles, device)
 
-    kv = X.rows_layout(keys, values)
+    kv = X.rows_layout(keys, values, tile_size=tile_size)
     kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, num_kv_heads, num_tiles, device)
     kv.v_scale_mode, kv.v_scales = X.vscale_mode(v_scale, num_kv_heads, num_tiles, device)
     if context_lens is not None:
@@ -78,7 +78,7 @@ def fused_orthocache_attention_v3_gqa(
         kv.rows_per_length = 1
         if kv.lengths.numel() != num_kv_heads:
             raise ValueError(f"context_lens must have one entry per kv head ({num_kv_heads})")
-    mode_c, scores = _mode_code(mode, score_cache)
+    mode_c, scores = _mode_code(mode, score_cache, tile_size)
     res = X.decode(kv, q, G, gate=N.OC_GATE_CS, threshold=tau, mode=mode_c, scores=scores,
                    num_splits=num_splits, out_dtype=input_dtype, want_keep=sync,
                    want_partials=return_partials, out=out)

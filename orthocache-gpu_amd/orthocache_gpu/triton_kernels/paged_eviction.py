@@ -112,12 +112,12 @@ def fused_orthocache_attention_paged(
             min=0, max=max_blocks_per_seq * block_size).contiguous()
     error_flag = torch.zeros(1, dtype=torch.int32, device=device) if sync else None
     gate, thr = (N.OC_GATE_CS, tau) if tau is not None else (N.OC_GATE_ZETA, zeta_max)
-    mode_c, scores = _mode_code(mode, score_cache)
+    mode_c, scores = _mode_code(mode, score_cache, tile_size)
     q2 = q.reshape(num_seqs * num_heads, head_dim)
     out2 = None if out is None else out.view(num_seqs * num_heads, head_dim)
 
     def run(kc, dequant):
-        kv = X.paged_layout(kc, v_cache, block_tables, num_tiles, keep_mixed=dequant is not None)
+        kv = X.paged_layout(kc, v_cache, block_tables, num_tiles, keep_mixed=dequant is not None, tile_size=tile_size)
         kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, device)
         if dequant is not None and dequant != 1.0:
             kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_DEQUANT, dequant
@@ -173,7 +173,7 @@ def score_paged_tiles(k_cache: torch.Tensor, block_tables: torch.Tensor, tile_si
     nb, hkv, bs, d = k_cache.shape
     maxb = block_tables.shape[1]
     num_tiles = (maxb * bs) // tile_size if context_lens is None else -(-(maxb * bs) // tile_size)
-    kv = X.paged_layout(k_cache, k_cache, block_tables, num_tiles)
+    kv = X.paged_layout(k_cache, k_cache, block_tables, num_tiles, tile_size=tile_size)
     rows = block_tables.shape[0] * hkv
     if context_lens is not None:
         kv.lengths = context_lens.to(device=k_cache.device, dtype=torch.int32).clamp(
@@ -188,11 +188,11 @@ def score_paged_tiles(k_cache: torch.Tensor, block_tables: torch.Tensor, tile_si
                 kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_DEQUANT, ks  # rounded to bf16 in the kernel
         else:
             kd = X.dequant_fp8(k_cache, ks, q_dtype)
-            kv = X.paged_layout(kd, kd, block_tables, num_tiles)  # no V is read
+            kv = X.paged_layout(kd, kd, block_tables, num_tiles, tile_size=tile_size)  # no V is read
             if context_lens is not None:
                 kv.lengths = context_lens.to(device=k_cache.device, dtype=torch.int32).clamp(
                     min=0, max=maxb * bs).contiguous()
     if isinstance(k_scale, torch.Tensor):
         kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(k_scale, rows, num_tiles, k_cache.device)
     e_low, e_high, zeta, keep = X.score_tiles(kv, 0.0)
-    return TileScores(e_low[:, :num_tiles], e_high[:, :num_tiles], zeta[:, :num_tiles])
+    return TileScores(e_low[:, :num_tiles], e_high[:, :num_tiles], zeta[:, :num_tiles], tile_size=tile_size)
