@@ -28,9 +28,10 @@ partials-only call (no merge) is timed as well.
 The same JSON line carries the secondary measurements: batch 1
 configs 1 (the reference's published 1K..32K table), 2, 3 and 4 at full size;
 the reference's single-head 32K float32 fusion profile (single_head); the
-model hook's prefill kernel on four layer shapes and its decode step
-(hook_prefill, hook_decode); and orthocache_forward(mode='compact')
-(compact) -- each with its roofline fraction.
+portable kernels at head_dim 256 (portable); the model hook's prefill kernel
+on four layer shapes and its decode step (hook_prefill, hook_decode); and
+orthocache_forward(mode='compact') (compact) -- each with its roofline
+fraction.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -77,7 +78,7 @@ def parse():
                     help="also time BASELINE.json config 1 over 1K..32K tokens and config 2 at full size (0 = skip)")
     ap.add_argument("--only", choices=["cached", "cached_partials", "single_pass", "dense", "copy", "read", "gather",
                                        "paged", "fp8", "hook", "compact", "sweep", "config2",
-                                       "single_head"],
+                                       "single_head", "portable"],
                     default=None,
                     help="time only this decode variant of the primary batch, a plain 1 GiB device copy "
                          "(the reference kernel for scaling the profiler's byte counters), the model hook's "
@@ -605,6 +606,64 @@ def single_head_measure(steps, warmup, seq_len=32768, seed=42):
     return r
 
 
+def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
+    """The portable kernels (head dims other than 64 / 128, tiles other than
+    64 tokens) on a head_dim-256 GQA decode: 8 kv rows x 32768 tokens, G = 4,
+    bfloat16, half the tiles noise, the Cauchy-Schwarz gate at a calibrated
+    tau (cached and single pass) beside the dense decode, and the same at
+    head_dim 128 forced onto the portable kernels next to the tuned ones.
+    Buffer sets rotate past the Infinity Cache."""
+    import torch
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
+    from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q
+    dev = torch.device("cuda", 0)
+    rows, g = 8, 4
+    lib, stream = N.lib(), X.current_stream(dev)
+    r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16, 50% noise tiles, Cauchy-Schwarz gate"}
+    for d, portable in ((head_dim, 0), (128, 1), (128, 0)):
+        set_bytes = rows * seq_len * d * 2 * 2
+        nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
+        T = seq_len // 64
+        P = X.auto_num_splits(T, dev)
+        out = torch.empty((rows * g, d), dtype=torch.bfloat16, device=dev)
+        ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+        params = {"cached": [], "single_pass": [], "dense": []}
+        keep_alive = []
+        tau = None
+        for i in range(nsets):
+            wl = make_kv(rows, seq_len, d, noise_frac=0.5, dtype=torch.bfloat16, device=dev, seed=seed + 13 * i)
+            q = make_q(rows, g, d, dtype=torch.bfloat16, device=dev, seed=seed + 13 * i + 1)
+            sc = score_tiles(wl.keys)
+            if tau is None:
+                tau = calibrate_tau(sc.e_high, q, g)
+            kv = X.rows_layout(wl.keys, wl.values)
+            keep_alive.append((wl, q, sc, kv))
+            for name, gate, mode in (("cached", N.OC_GATE_CS, N.OC_MODE_CACHED),
+                                     ("single_pass", N.OC_GATE_CS, N.OC_MODE_SINGLE_PASS),
+                                     ("dense", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS)):
+                p = _decode_params(lib, N, kv, q, g, gate, mode, tau, sc, P, out, ws)
+                p.portable = portable
+                params[name].append(p)
+        tile = 64 * d * 2
+        tiles = rows * T
+        kept = tiles // 2
+        nbytes = {"cached": 2 * kept * tile + tiles * 4, "single_pass": tiles * tile + kept * tile,
+                  "dense": 2 * tiles * tile}
+        key = f"d{d}" + ("_portable" if portable else ("_tuned" if d in (64, 128) else "_portable"))
+        r[key] = {}
+        for name, plist in params.items():
+            run = lambda i, plist=plist: N.check("oc_decode", lib.oc_decode(ctypes.byref(plist[i % nsets]),
+                                                                           ctypes.c_void_p(stream)))
+            us = _event_us_i(run, steps, warmup)
+            gbps = nbytes[name] / (us * 1e-6) / 1e9
+            r[key][name] = {"us": round(us, 2), "gbps": round(gbps, 1), "roofline_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+        del keep_alive, params
+        torch.cuda.empty_cache()
+    return r
+
+
 def measure(setup, steps, warmup):
     evict = setup.check()
     r = {"batch": setup.batch, "eviction_rate": evict, "num_splits": setup.P, "tau": setup.tau,
@@ -998,6 +1057,9 @@ def main():
     if args.only == "single_head":
         print(json.dumps(dict(only="single_head", **single_head_measure(args.steps, args.warmup))))
         return
+    if args.only == "portable":
+        print(json.dumps(dict(only="portable", **portable_measure(args.steps, args.warmup))))
+        return
     if args.only == "sweep":
         print(json.dumps(dict(only="sweep", **sweep_measure(args.steps, args.warmup))))
         return
@@ -1036,7 +1098,7 @@ def main():
             cfg = ExtraConfig(which)
             extras[which] = cfg.measure(s_steps, s_warm)
             del cfg
-    sweep = cfg2 = single = None
+    sweep = cfg2 = single = portable = None
     if args.sweep:
         torch.cuda.empty_cache()
         sweep = sweep_measure(s_steps, s_warm)
@@ -1044,6 +1106,8 @@ def main():
         cfg2 = config2_measure(s_steps, s_warm)
         torch.cuda.empty_cache()
         single = single_head_measure(s_steps, s_warm)
+        torch.cuda.empty_cache()
+        portable = portable_measure(max(50, args.steps // 4), max(10, args.warmup))
     hook = compact = None
     if args.hook:
         torch.cuda.empty_cache()
@@ -1104,6 +1168,7 @@ def main():
         line["config1_sweep"] = sweep
         line["config2"] = cfg2
         line["single_head"] = single
+        line["portable"] = portable
     if hook:
         line["hook_prefill"] = hook[:-1]
         line["hook_decode"] = hook[-1]

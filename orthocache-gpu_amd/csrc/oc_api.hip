@@ -116,6 +116,16 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
     return fail(OC_ERR_INVALID, "num_tokens %d outside 0..num_tiles * tile_size", kv->num_tokens);
   if ((int64_t)kv->num_tiles * ts > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "rows longer than 2^31 tokens");
   a.ts = ts;
+  // the portable kernels' 16-byte staging: every K / V offset and row chunk
+  // 16-byte aligned (the tuned kernels' own checks are above)
+  {
+    auto a16 = [](int64_t bytes) { return bytes % 16 == 0; };
+    bool vec = !tuned && aligned(kv->k, 16) && (!kv->v || aligned(kv->v, 16)) && a16(a.k_tok_stride) &&
+               a16(a.v_tok_stride);
+    if (a.paged) vec = vec && a16(a.k_blk_stride) && a16(a.k_head_stride) && a16(a.v_blk_stride) && a16(a.v_head_stride);
+    else vec = vec && a16(a.k_row_stride) && a16(a.v_row_stride);
+    a.gen_vec = vec ? 1 : 0;
+  }
   a.row_tok = kv->lengths ? 0 : kv->num_tokens;
   a.k_scale_mode = kv->k_scale_mode;
   a.v_scale_mode = kv->v_scale_mode;
@@ -386,8 +396,13 @@ static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 
 // bitmask) and the merge tail twice and leave its own imbalance (config 4,
 // 32 rows of 2048 tiles: 512 workgroups took 121 us cached and 162 us single
 // pass, 256 take 115 and 147).
+static bool portable_path(const oc_decode_params* p);
+
 static int choose_spw(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
+  // the portable kernels: one split per workgroup (several workgroups per
+  // CU hide each other's staging round trips)
+  if (portable_path(p)) return 1;
   const int P = p->num_splits;
   const int64_t cus = device_cus();
   const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G));

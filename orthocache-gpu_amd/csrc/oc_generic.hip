@@ -91,33 +91,49 @@ __device__ __forceinline__ void gen_row_offsets(const DecodeArgs& a, int row, in
   voff[j] = vo;
 }
 
-// The dequantised K value of one element (float(elem), times the tile's
-// scale, or rounded to bf16 after the scalar scale for OC_KSCALE_DEQUANT)
-template <int DT>
-__device__ __forceinline__ float gen_kval(const DecodeArgs& a, const char* p, float ks) {
-  const float x = gen_elem<DT>(p);
-  if (a.k_scale_mode == OC_KSCALE_TILE) return x * ks;
-  if (a.k_scale_mode == OC_KSCALE_DEQUANT) return round_bf16(x * a.k_scale);
-  return x;
-}
-
 // Stage columns [c0, c0 + cw) of the tile's rows into s[tt * sp + c]
 // (zeros for rows without an offset).  vmul: V's tile scale (V staging) or
-// 1; ks: K's tile scale (K staging).
+// 1; ks: K's tile scale (K staging).  With a.gen_vec (every row offset and
+// the column chunk 16-byte aligned, set by the host) each thread moves
+// 16-byte pieces; otherwise one element at a time.
 template <int DT, bool ISK>
 __device__ __forceinline__ void gen_stage(const DecodeArgs& a, const char* base, const int64_t* off, int c0, int cw,
                                           int sp, float* s, float ks, float vmul) {
   constexpr int es = Elem<DT>::size;
+  constexpr int EP = 16 / es;  // elements per 16-byte piece
+  auto val = [&](float x) {
+    if constexpr (ISK) {
+      if (a.k_scale_mode == OC_KSCALE_TILE) return x * ks;
+      if (a.k_scale_mode == OC_KSCALE_DEQUANT) return round_bf16(x * a.k_scale);
+      return x;
+    } else {
+      return x * vmul;
+    }
+  };
+  if (a.gen_vec && cw >= EP) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const int ppr = cw / EP;  // pieces per row
+    const int pl = __builtin_ctz((unsigned)ppr);
+    const int n = a.ts * ppr;
+    for (int e = threadIdx.x; e < n; e += kGenThreads) {
+      const int tt = e >> pl, pc = e & (ppr - 1);
+      const int64_t o = off[tt];
+      v4u w = v4u{0u, 0u, 0u, 0u};
+      if (o >= 0) w = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base + o + (int64_t)(c0 + pc * EP) * es));
+      const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
+      float* dst = s + tt * sp + pc * EP;
+#pragma unroll
+      for (int i = 0; i < EP; ++i) dst[i] = o >= 0 ? val(elem<DT>(ww, i)) : 0.f;
+    }
+    return;
+  }
   const int n = a.ts * cw;
   const int cl = __builtin_ctz((unsigned)cw);
   for (int e = threadIdx.x; e < n; e += kGenThreads) {
     const int tt = e >> cl, c = e & (cw - 1);
     const int64_t o = off[tt];
     float x = 0.f;
-    if (o >= 0) {
-      const char* p = base + o + (int64_t)(c0 + c) * es;
-      x = ISK ? gen_kval<DT>(a, p, ks) : gen_elem<DT>(p) * vmul;
-    }
+    if (o >= 0) x = val(gen_elem<DT>(base + o + (int64_t)(c0 + c) * es));
     s[tt * sp + c] = x;
   }
 }

@@ -61,6 +61,7 @@ struct DecodeArgs {
   int32_t num_rows, num_tiles;
   int32_t row_tok;  // tokens of every row without lengths (0: num_tiles * ts)
   int32_t ts;       // tokens per tile (64 in every kernel of this file; any power of two in oc_generic.hip)
+  int32_t gen_vec;  // oc_generic.hip: K and V rows are read in 16-byte pieces (offsets 16-byte aligned)
   // kGateHook: tile norms of kv head (row % hk_rows) at hk_norms[h * hk_stride
   // + t] for the hk_full complete tiles, threshold hk_tau, per-row
   // statistics (evicted tiles, group norm, largest tile norm) to hk_stats
