@@ -117,10 +117,11 @@ static int fill_kv(const oc_kv_desc* kv, DecodeArgs& a, bool allow_dq = false) {
   if ((int64_t)kv->num_tiles * ts > 0x7FFFFFFF) return fail(OC_ERR_UNSUPPORTED, "rows longer than 2^31 tokens");
   a.ts = ts;
   // the portable kernels' 16-byte staging: every K / V offset and row chunk
-  // 16-byte aligned (the tuned kernels' own checks are above)
+  // 16-byte aligned (also set for the tuned shapes, which a caller can send
+  // to the portable kernels with the params' portable flag)
   {
     auto a16 = [](int64_t bytes) { return bytes % 16 == 0; };
-    bool vec = !tuned && aligned(kv->k, 16) && (!kv->v || aligned(kv->v, 16)) && a16(a.k_tok_stride) &&
+    bool vec = aligned(kv->k, 16) && (!kv->v || aligned(kv->v, 16)) && a16(a.k_tok_stride) &&
                a16(a.v_tok_stride);
     if (a.paged) vec = vec && a16(a.k_blk_stride) && a16(a.k_head_stride) && a16(a.v_blk_stride) && a16(a.v_head_stride);
     else vec = vec && a16(a.k_row_stride) && a16(a.v_row_stride);
@@ -206,12 +207,17 @@ __device__ __forceinline__ float block_reduce(float x, bool is_max, float* red) 
   return x;
 }
 
-// One workgroup per query-head row: out = sum_s e^(m_s-M) acc_s / max(sum_s e^(m_s-M) l_s, 1e-9)
+// out = sum_s e^(m_s-M) acc_s / max(sum_s e^(m_s-M) l_s, 1e-9) per query-head
+// row.  grid = (rows, ceil(D / 64)): workgroup (r, cb) forms the weights of
+// row r and merges columns 64 cb .. + 63, wave w summing the partials
+// s = w, w + 4, ... (eight loads in flight per lane), the four wave sums
+// added in wave order.
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ m, const float* __restrict__ l,
                                                     const float* __restrict__ acc, int P, int D, char* out,
                                                     int out_dtype, int64_t out_row_stride) {
   extern __shared__ float sw[];
   __shared__ float red[4];
+  __shared__ float part[4][64];
   const int64_t r = blockIdx.x;
   const float* mr = m + r * P;
   const float* lr = l + r * P;
@@ -227,20 +233,34 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ m,
   ls = block_reduce(ls, false, red);  // contains the barrier that publishes sw
   const float inv_l = fmaxf(ls, 1e-9f);
   const int es = out_dtype == OC_F32 ? 4 : 2;
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.y * 64 + lane;
+  float x = 0.f;
+  if (c < D) {
     const float* ap = acc + r * P * D + c;
-    float x = 0.f;
-    for (int s = 0; s < P; ++s) x = __builtin_fmaf(ap[(int64_t)s * D], sw[s], x);
-    store_scalar(out + r * out_row_stride + (int64_t)c * es, out_dtype, x / inv_l);
+    int s = wave;
+    for (; s + 28 < P; s += 32) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = ap[(int64_t)(s + 4 * i) * D];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x = __builtin_fmaf(v[i], sw[s + 4 * i], x);
+    }
+    for (; s < P; s += 4) x = __builtin_fmaf(ap[(int64_t)s * D], sw[s], x);
   }
+  part[wave][lane] = x;
+  __syncthreads();
+  if (wave == 0 && c < D)
+    store_scalar(out + r * out_row_stride + (int64_t)c * es, out_dtype,
+                 (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]) / inv_l);
 }
 
 static int launch_merge(const float* m, const float* l, const float* acc, int rows, int P, int D, void* out,
                         int out_dtype, int64_t out_row_stride_el, hipStream_t st) {
   if (rows == 0) return OC_OK;
   const int es = out_dtype == OC_F32 ? 4 : 2;
-  hipLaunchKernelGGL(merge_kernel, dim3(rows), dim3(256), (size_t)P * sizeof(float), st, m, l, acc, P, D,
-                     (char*)out, out_dtype, out_row_stride_el * es);
+  hipLaunchKernelGGL(merge_kernel, dim3(rows, (D + 63) / 64), dim3(256), (size_t)P * sizeof(float), st, m, l, acc, P,
+                     D, (char*)out, out_dtype, out_row_stride_el * es);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? OC_OK : hip_fail(e, "merge launch");
 }
