@@ -198,6 +198,48 @@ __device__ __forceinline__ void gen_bands(const float* s, int ts, int cw, int sp
   }
 }
 
+// Band energies of a staged 64-token, 128-column chunk (unscaled, this
+// thread's share) with the transform's butterflies (those of gen_fwht, in
+// its stage order) in registers.  Thread tid works on column tid mod 128:
+// stages 1..8 (row bits 0..3) on its two 16-row blocks 32 h and 32 h + 16
+// (h = tid / 128), stored back; after one barrier, stages 16 and 32 as
+// 4-point butterflies of rows (q, q + 16, q + 32, q + 48) for its eight
+// q = 8 h .. 8 h + 7, summing X[q]^2 over q = 1..7 and X[q + 32]^2,
+// X[q + 48]^2.  sk is left changed.
+__device__ __forceinline__ void gen_bands_64x128(float* sk, float& el, float& eh) {
+  constexpr int spd = 132;  // gen_pitch(128): constant LDS offsets
+  const int c = threadIdx.x & 127, h = threadIdx.x >> 7;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    float* col = sk + (32 * h + 16 * blk) * spd + c;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = col[i * spd];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (!(i & (1 << st))) {
+          const float a = x[i], b = x[i + (1 << st)];
+          x[i] = a + b;
+          x[i + (1 << st)] = a - b;
+        }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) col[i * spd] = x[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int q = 8 * h + i;
+    const float y0 = sk[q * spd + c], y1 = sk[(q + 16) * spd + c];
+    const float y2 = sk[(q + 32) * spd + c], y3 = sk[(q + 48) * spd + c];
+    const float a = y0 + y1, b = y0 - y1, d = y2 + y3, e = y2 - y3;
+    if (q >= 1 && q < 8) el = __builtin_fmaf(a + d, a + d, el);
+    eh = __builtin_fmaf(a - d, a - d, eh);
+    eh = __builtin_fmaf(b - e, b - e, eh);
+  }
+}
+
 __device__ __forceinline__ float gen_block_sum(float x, float* red) {
   x = wave_sum(x);
   const int w = threadIdx.x >> 6;
@@ -268,7 +310,8 @@ __global__ __launch_bounds__(kGenThreads) void gen_score_kernel(const DecodeArgs
   }
 }
 
-// Row pitch (floats) of a staged decode chunk: cw + 4 keeps every row
+// Row pitch (floats) of a staged decode chunk (gen_bands_64x128 assumes 132
+// for 128 columns): cw + 4 keeps every row
 // 16-byte aligned for 128-bit LDS reads and puts the rows' starts 4 banks
 // apart; chunks narrower than 4 columns (head_dim 1 or 2) use cw + 1.
 __host__ __device__ __forceinline__ int gen_pitch(int cw) { return (cw & 3) ? cw + 1 : cw + 4; }
@@ -517,8 +560,12 @@ void gen_decode_kernel(const DecodeArgs a, int D, int GT, int cw) {
           }
           if (sp_gate) {
             __syncthreads();
-            gen_fwht(sk, TS, cw, spd);
-            gen_bands(sk, TS, cw, spd, el, eh);
+            if (TS == 64 && cw == 128) {
+              gen_bands_64x128(sk, el, eh);
+            } else {
+              gen_fwht(sk, TS, cw, spd);
+              gen_bands(sk, TS, cw, spd, el, eh);
+            }
           }
           __syncthreads();
         }
