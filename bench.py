@@ -27,11 +27,11 @@ partials-only call (no merge) is timed as well.
 
 The same JSON line carries the secondary measurements: batch 1
 configs 1 (the reference's published 1K..32K table), 2, 3 and 4 at full size;
-the reference's single-head 32K float32 fusion profile (single_head); the
-portable kernels at head_dim 256 (portable); the model hook's prefill kernel
-on four layer shapes and its decode step (hook_prefill, hook_decode); and
-orthocache_forward(mode='compact') (compact) -- each with its roofline
-fraction.
+the reference's single-head 32K float32 fusion profile (single_head);
+head_dim 256 on the library's routing and on the portable kernels
+(portable); the model hook's prefill kernel on four layer shapes and its
+decode step (hook_prefill, hook_decode); and orthocache_forward(mode='compact')
+(compact) -- each with its roofline fraction.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -607,12 +607,15 @@ def single_head_measure(steps, warmup, seq_len=32768, seed=42):
 
 
 def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
-    """The portable kernels (head dims other than 64 / 128, tiles other than
-    64 tokens) on a head_dim-256 GQA decode: 8 kv rows x 32768 tokens, G = 4,
-    bfloat16, half the tiles noise, the Cauchy-Schwarz gate at a calibrated
-    tau (cached and single pass) beside the dense decode, and the same at
-    head_dim 128 forced onto the portable kernels next to the tuned ones.
-    Buffer sets rotate past the Infinity Cache."""
+    """head_dim 256 (a power of two the reference accepts beyond the
+    benchmark configurations): 8 kv rows x 32768 tokens, G = 4, bfloat16,
+    half the tiles noise, the Cauchy-Schwarz gate at a calibrated tau (cached
+    and single pass) beside the dense decode.  "d256": the library's own
+    routing (cached and dense on the per-wave-prologue matrix-core kernel,
+    the single pass on the portable kernels); "d256_portable": every variant
+    forced onto the portable kernels; the same at head_dim 128 forced
+    portable next to the tuned kernels.  Buffer sets rotate past the Infinity
+    Cache."""
     import torch
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
@@ -622,7 +625,7 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     rows, g = 8, 4
     lib, stream = N.lib(), X.current_stream(dev)
     r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16, 50% noise tiles, Cauchy-Schwarz gate"}
-    for d, portable in ((head_dim, 0), (128, 1), (128, 0)):
+    for d, portable in ((head_dim, 0), (head_dim, 1), (128, 1), (128, 0)):
         set_bytes = rows * seq_len * d * 2 * 2
         nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
         T = seq_len // 64
@@ -651,7 +654,7 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
         kept = tiles // 2
         nbytes = {"cached": 2 * kept * tile + tiles * 4, "single_pass": tiles * tile + kept * tile,
                   "dense": 2 * tiles * tile}
-        key = f"d{d}" + ("_portable" if portable else ("_tuned" if d in (64, 128) else "_portable"))
+        key = f"d{d}" + ("_portable" if portable else ("_tuned" if d in (64, 128) else ""))
         r[key] = {}
         for name, plist in params.items():
             run = lambda i, plist=plist: N.check("oc_decode", lib.oc_decode(ctypes.byref(plist[i % nsets]),

@@ -418,16 +418,22 @@ static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 
 // pass, 256 take 115 and 147).
 static bool portable_path(const oc_decode_params* p);
 
-static int choose_spw(const oc_decode_params* p) {
+// splits per workgroup of the tuned kernels
+static int choose_spw_tuned(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
-  // the portable kernels: one split per workgroup (several workgroups per
-  // CU hide each other's staging round trips)
-  if (portable_path(p)) return 1;
   const int P = p->num_splits;
   const int64_t cus = device_cus();
   const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G));
   const int64_t spw = (P * groups + cus - 1) / cus;
   return (int)std::max<int64_t>(1, std::min<int64_t>(spw, P));
+}
+
+static int choose_spw(const oc_decode_params* p) {
+  if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
+  // the portable kernels: one split per workgroup (several workgroups per
+  // CU hide each other's staging round trips)
+  if (portable_path(p)) return 1;
+  return choose_spw_tuned(p);
 }
 
 static int num_groups(const oc_decode_params* p, int spw) { return (p->num_splits + spw - 1) / spw; }
@@ -483,12 +489,50 @@ static FlatCfg flat_cfg(const oc_decode_params* p) {
 // The portable kernels (oc_generic.hip): head_dim other than 64 / 128, tiles
 // other than 64 tokens, or asked for (p->portable).  They write one partial
 // per split group and merge_kernel combines them.
+static bool flat_layout_tuned(const oc_decode_params* p);
+
+// head_dim 256 with 64-token tiles on the per-wave-prologue kernel
+// (decode_fast_kernel<DT, 256, GT <= 4, PG, 4 waves>): bf16 or f16 K/V with q
+// of K's type, at most 4 query heads per kv row, contiguous rows or pages of
+// >= 16 tokens, 16-byte aligned q, K, V and strides, no q-folded scale,
+// partials internal; a cached decode with a score or mask gate on rows of at
+// most 64 * kFastChunks tiles, or a dense decode; several splits per
+// workgroup or rows of different lengths (the conditions under which
+// decode_impl sets a.fast).  Every other head_dim-256 decode runs on the
+// portable kernels.
+static bool wide_fast(const oc_decode_params* p) {
+  const oc_kv_desc& kv = p->kv;
+  const int ts = kv.tile_size > 0 ? kv.tile_size : 64;
+  if (p->portable != 0 || kv.head_dim != 256 || ts != 64) return false;
+  const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16);
+  if (!mq || (kv.v_dtype != 0 && kv.v_dtype != kv.dtype) || p->G < 1 || p->G > 4) return false;
+  if (kv.paged && kv.block_size < 16) return false;
+  if (kv.k_scale_mode == OC_KSCALE_Q_FOLD || kv.k_scale_mode == OC_KSCALE_DEQUANT) return false;
+  if ((p->partial_m && p->partial_l && p->partial_acc) || p->split_counts) return false;
+  auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
+  if (!aligned(p->q, 16) || !a16(p->q_row_stride) || !aligned(kv.k, 16) || !aligned(kv.v, 16) ||
+      !a16(kv.k_token_stride) || !a16(kv.v_token_stride))
+    return false;
+  if (kv.paged ? !(a16(kv.k_block_stride) && a16(kv.k_head_stride) && a16(kv.v_block_stride) &&
+                   a16(kv.v_head_stride))
+               : !(a16(kv.k_row_stride) && a16(kv.v_row_stride)))
+    return false;
+  const bool cached_gate = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
+  if (!(cached_gate && kv.num_tiles <= 64 * kFastChunks) && p->gate != OC_GATE_NONE) return false;
+  return choose_spw_tuned(p) > 1 || flat_layout_tuned(p);
+}
+
 static bool portable_path(const oc_decode_params* p) {
-  return p->portable == 1 || generic_shape(p->kv.head_dim, p->kv.tile_size > 0 ? p->kv.tile_size : 64);
+  return (p->portable == 1 || generic_shape(p->kv.head_dim, p->kv.tile_size > 0 ? p->kv.tile_size : 64)) &&
+         !wide_fast(p);
 }
 
 static bool flat_layout(const oc_decode_params* p) {
   if (portable_path(p)) return false;
+  return flat_layout_tuned(p);
+}
+
+static bool flat_layout_tuned(const oc_decode_params* p) {
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
   const bool cached = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
   return p->kv.lengths && p->out && !partials_given && !p->split_counts && p->splits_per_group != 1 &&
@@ -673,7 +717,7 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
                                       "type (convert one of them, or decode cached / dense)");
     if (hk) {
       // the row statistics come from a pass over the whole row (not flat)
-      if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1) return kHookNotFused;
+      if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1 || D > 128) return kHookNotFused;
       a.gate = kGateHook;
       a.hk_norms = hk->norms;
       a.hk_stride = hk->stride;
@@ -683,6 +727,9 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
       a.hk_stats = hk->stats;
     }
   }
+  // head_dim 256 reaches here only through wide_fast, whose conditions are
+  // a.fast's
+  if (D == 256 && !a.fast) return fail(OC_ERR_UNSUPPORTED, "head_dim 256 decode routing (internal)");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
   if (e != hipSuccess) return hip_fail(e, "decode launch");

@@ -978,7 +978,8 @@ __host__ __device__ constexpr int v_xor(int r) {
     else if constexpr (D == 64) return (r >> 2) & 3;
     else return 0;
   } else {
-    if constexpr (D == 128) return 2 * ((r & 3) + 4 * ((r >> 3) & 1));
+    // 128 and 256 (512-byte rows: the same pairs of rows share a bank line)
+    if constexpr (D == 128 || D == 256) return 2 * ((r & 3) + 4 * ((r >> 3) & 1));
     else if constexpr (D == 64) return 2 * (((r & 3) >> 1) + 2 * ((r >> 3) & 1));
     else return 0;
   }
@@ -1009,7 +1010,8 @@ constexpr bool v_xor_pin() {
       }
   return true;
 }
-static_assert(v_xor_pin<OC_BF16, 128>() && v_xor_pin<OC_BF16, 64>() && v_xor_pin<OC_FP8_E4M3FN, 128>() &&
+static_assert(v_xor_pin<OC_BF16, 256>() && v_xor_pin<OC_BF16, 128>() && v_xor_pin<OC_BF16, 64>() &&
+                  v_xor_pin<OC_FP8_E4M3FN, 128>() &&
                   v_xor_pin<OC_FP8_E4M3FN, 64>(),
               "v_xor: a transposing V read uses a bank slot more than twice, or a chunk leaves its row");
 
@@ -2344,7 +2346,8 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   }
   if (!cached) load_q();
   else if (a.gate == OC_GATE_CS) score_pass(std::integral_constant<int, OC_GATE_CS>{});
-  else if (!F8 && a.gate == kGateHook) score_pass(std::integral_constant<int, F8 ? OC_GATE_CS : kGateHook>{});
+  else if (!F8 && D <= 128 && a.gate == kGateHook)
+    score_pass(std::integral_constant<int, (F8 || D > 128) ? OC_GATE_CS : kGateHook>{});
   else if (a.gate == OC_GATE_ZETA) score_pass(std::integral_constant<int, OC_GATE_ZETA>{});
   else score_pass(std::integral_constant<int, OC_GATE_MASK>{});
   const int cnt = __popc(wlo) + __popc(whi);
@@ -2971,7 +2974,10 @@ __global__ __launch_bounds__((DecWaves<DT, D, MQK, GT>::value * kWave)) __attrib
 // prologue overlaps the other's tile loop.  VT: V's element type (DT, or
 // bf16 V beside fp8 K).
 template <int DT, int D, int GT, bool PAGED, int kDW, int VT = DT>
-__global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(2))) void decode_fast_kernel(
+// Two waves per SIMD (<= 256 registers) at head_dim 64 and 128; at head_dim
+// 256 (4-wave workgroups, a 32 KiB V slot per wave) one wave per SIMD: the K
+// tile alone takes 128 registers and the accumulators 64.
+__global__ __launch_bounds__(kDW * kWave) __attribute__((amdgpu_waves_per_eu(D >= 256 ? 1 : 2))) void decode_fast_kernel(
     const DecodeArgs a) {
   const int g_active = min(GT, a.G);
   int row = blockIdx.y, gidx = blockIdx.x, npg = a.Pg, slot0 = 0, b0 = 0, b1 = 0, ntok = 0;
@@ -3217,8 +3223,30 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
   else launch_decode_gt<DT, HD, VDOT2, false, false, false>(a, gt, grid, st);
 }
 
+// head_dim 256: only the per-wave-prologue kernel, 16-bit K/V with q of K's
+// type, at most 4 query heads per workgroup (the fused merge gives each of
+// its 256 threads one column quad of one head); the host routes every other
+// head_dim-256 decode to the portable kernels
+template <int DT>
+inline void launch_fast256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  if constexpr (DT == OC_BF16 || DT == OC_F16) {
+    const dim3 block(4 * kWave);
+    auto go = [&](auto pg) {
+      constexpr bool PG = decltype(pg)::value;
+      switch (gt) {
+        case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, DT>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, DT>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, DT>), grid, block, 0, st, a); break;
+      }
+    };
+    if (a.paged) go(std::true_type{});
+    else go(std::false_type{});
+  }
+}
+
 #define OC_DECODE_CASES(DT, DOT2)                                 \
-  if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
+  if (head_dim == 256) launch_fast256<DT>(a, gt, grid, st);       \
+  else if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
   else launch_decode_hd<DT, 64, DOT2>(a, gt, grid, st);
 
 // q . k on 16-bit operands (matrix cores, or v_dot2 on the VALU path) when

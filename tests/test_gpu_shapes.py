@@ -352,3 +352,116 @@ def test_portable_switch_matches_tuned_kernels(gate, mode):
     assert torch.equal(keeps[0], keeps[1])
     assert torch.equal(keeps[0][:, :40].bool(), wl.noise if gate == "cs" else ~wl.noise)
     assert_out(outs[1], np32(outs[0]), "f32", f"portable vs tuned {gate} {mode}")
+
+
+# ------------------------------------------------ head_dim 256, tuned kernel
+
+def _d256_case(rows, T, G, dt, seed):
+    k, noise = mixed(rows, T, 256, 64, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    v = torch.randn(rows, T * 64, 256, generator=g)
+    q = torch.randn(rows * G, 256, generator=g)
+    kd, vd, qd = (x.to(TORCH_DT[dt]).to(DEV) for x in (k, v, q))
+    return kd, vd, qd, noise
+
+
+def _cs_tau(qd, kd, noise, G):
+    rows = kd.shape[0]
+    _, _, _, eh = O.fwht_scores(np32(kd).reshape(-1, 256), 0.0)
+    eh = eh.reshape(rows, -1)
+    qn = np.array([O.q_norms(np32(qd)[r * G:(r + 1) * G]).max() for r in range(rows)])
+    b = qn[:, None] * np.sqrt(eh)
+    return float(0.5 * (b[~noise.numpy()].max() + b[noise.numpy()].min()))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("G", [1, 2, 3, 4])
+@pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none"])
+def test_head_dim_256_tuned_kernel(dt, G, gate):
+    """head_dim 256, 64-token tiles, 16-bit K/V with q of K's type: the cached
+    score- or mask-gated decode and the dense decode run on the per-wave-
+    prologue matrix-core kernel (4-wave workgroups, one wave per SIMD) when a
+    workgroup takes several splits (here splits_per_group = 2); against the
+    oracle, and against the same decode forced onto the portable kernels."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T = 3, 12
+    kd, vd, qd, noise = _d256_case(rows, T, G, dt, seed=17 * G + 3 * len(gate))
+    kv = X.rows_layout(kd, vd)
+    q32, k32, v32 = np32(qd), np32(kd), np32(vd)
+    tmask = None
+    if gate == "cs":
+        thr, ng = _cs_tau(qd, kd, noise, G), N.OC_GATE_CS
+    elif gate == "zeta":
+        thr, ng = 5.0, N.OC_GATE_ZETA
+    elif gate == "mask":
+        thr, ng = 0.0, N.OC_GATE_MASK
+        tmask = (torch.rand(rows, T, generator=torch.Generator().manual_seed(G)) < 0.5).to(torch.uint8)
+        tmask[:, 0] = 1
+    else:
+        thr, ng = 0.0, N.OC_GATE_NONE
+    if gate == "mask":
+        keep = tmask.bool().numpy()
+        ref = np.zeros((rows * G, 256), dtype=np.float32)
+        for r in range(rows):
+            sel = np.repeat(keep[r], 64)
+            for h in range(G):
+                ref[r * G + h] = O.dense_decode(q32[r * G + h:r * G + h + 1], k32[r:r + 1, sel], v32[r:r + 1, sel])[0]
+    else:
+        res = O.decode_rows(q32, k32, v32, gate="none" if gate == "none" else gate, threshold=thr, G=G)
+        ref, keep = res["out"], res["keep"]
+        if gate != "none":
+            assert np.array_equal(keep, noise.numpy() if gate == "cs" else ~noise.numpy())
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    mode = N.OC_MODE_SINGLE_PASS if gate == "none" else N.OC_MODE_CACHED
+    outs = {}
+    for portable in (0, 1):
+        print(f"head_dim 256 {dt} G={G} gate={gate} portable={portable}", flush=True)
+        r = X.decode(kv, qd, G, gate=ng, threshold=thr, mode=mode, scores=(e_low, e_high), num_splits=4,
+                     splits_per_group=2, out_dtype=TORCH_DT[dt], want_keep=gate != "none",
+                     tile_mask=None if tmask is None else tmask.to(DEV), portable=portable)
+        torch.cuda.synchronize()
+        if gate != "none":
+            assert np.array_equal(r.keep.cpu().numpy().astype(bool), keep), portable
+        assert_out(r.out, ref, dt, f"head_dim 256 {'portable' if portable else 'tuned'} {dt} G={G} {gate}")
+        outs[portable] = np32(r.out)
+    # the two kernels agree to the output type's rounding
+    assert np.max(np.abs(outs[0] - outs[1])) <= {"bf16": 1.6e-2, "f16": 2e-3}[dt]
+
+
+def test_head_dim_256_routing_and_full_row():
+    """With the automatic split grouping, head_dim 256 bf16 cached and dense
+    decodes take several splits per workgroup (the tuned kernel's grouping:
+    fewer partials than splits) while the same call forced portable keeps one
+    split per workgroup; the tuned kernel's output on 8 rows x 10240 tokens
+    (160 tiles, P = 40) matches the oracle, both modes."""
+    import ctypes
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T, G = 8, 160, 4
+    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=2560)
+    kv = X.rows_layout(kd, vd)
+    tau = _cs_tau(qd, kd, noise, G)
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    P = X.auto_num_splits(T, qd.device)
+    lib = N.lib()
+    groups = {}
+    for portable in (0, 1):
+        p = N.OcDecodeParams()
+        p.kv = kv.struct()
+        p.q, p.q_dtype, p.G, p.q_row_stride = qd.data_ptr(), N.OC_BF16, G, qd.stride(0)
+        p.gate, p.mode, p.threshold = N.OC_GATE_CS, N.OC_MODE_CACHED, tau
+        p.score_e_low, p.score_e_high, p.score_row_stride = e_low.data_ptr(), e_high.data_ptr(), e_high.stride(0)
+        p.num_splits, p.out_dtype, p.portable = P, N.OC_BF16, portable
+        groups[portable] = lib.oc_decode_num_groups(ctypes.byref(p))
+    assert groups[1] == P and groups[0] < P, (P, groups)
+    q32, k32, v32 = np32(qd), np32(kd), np32(vd)
+    for gate, ng, mode in (("cs", N.OC_GATE_CS, N.OC_MODE_CACHED), ("none", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS)):
+        ref = O.decode_rows(q32, k32, v32, gate=gate, threshold=tau, G=G)
+        print(f"head_dim 256 full row {gate}", flush=True)
+        r = X.decode(kv, qd, G, gate=ng, threshold=tau, mode=mode, scores=(e_low, e_high), num_splits=P,
+                     out_dtype=torch.bfloat16, want_keep=gate == "cs")
+        torch.cuda.synchronize()
+        if gate == "cs":
+            assert np.array_equal(r.keep.cpu().numpy().astype(bool), ref["keep"])
+        assert_out(r.out, ref["out"], "bf16", f"head_dim 256 tuned full row {gate}")
