@@ -491,40 +491,34 @@ static FlatCfg flat_cfg(const oc_decode_params* p) {
 // per split group and merge_kernel combines them.
 static bool flat_layout_tuned(const oc_decode_params* p);
 
-// head_dim 256 with 64-token tiles on the per-wave-prologue kernel
-// (decode_fast_kernel<DT, 256, GT <= 4, PG, 4 waves>): bf16 or f16 K/V with q
-// of K's type, at most 4 query heads per kv row, contiguous rows or pages of
-// >= 16 tokens, 16-byte aligned q, K, V and strides, no q-folded scale,
-// partials internal; a cached decode with a score or mask gate on rows of at
-// most 64 * kFastChunks tiles, or a dense decode; several splits per
-// workgroup or rows of different lengths (the conditions under which
-// decode_impl sets a.fast).  Every other head_dim-256 decode runs on the
-// portable kernels.
-static bool wide_fast(const oc_decode_params* p) {
+// head_dim 256 with 64-token tiles on the matrix-core kernels (4-wave
+// workgroups at one wave per SIMD, a 32 KiB V slot per wave): bf16 or f16
+// K/V with q of K's type, at most 4 query heads per kv row, contiguous rows
+// or pages of >= 16 tokens, 16-byte aligned q, K, V and strides, K not
+// dequantised in the kernel.  The per-wave-prologue kernel takes what it
+// takes at head_dim 64 / 128 (a.fast), the general matrix-core kernel the
+// rest (single-pass gate, partials, one split per workgroup).  Every other
+// head_dim-256 decode runs on the portable kernels.
+static bool wide_route(const oc_decode_params* p) {
   const oc_kv_desc& kv = p->kv;
   const int ts = kv.tile_size > 0 ? kv.tile_size : 64;
   if (p->portable != 0 || kv.head_dim != 256 || ts != 64) return false;
   const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16);
   if (!mq || (kv.v_dtype != 0 && kv.v_dtype != kv.dtype) || p->G < 1 || p->G > 4) return false;
   if (kv.paged && kv.block_size < 16) return false;
-  if (kv.k_scale_mode == OC_KSCALE_Q_FOLD || kv.k_scale_mode == OC_KSCALE_DEQUANT) return false;
-  if ((p->partial_m && p->partial_l && p->partial_acc) || p->split_counts) return false;
+  if (kv.k_scale_mode == OC_KSCALE_DEQUANT) return false;
   auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
   if (!aligned(p->q, 16) || !a16(p->q_row_stride) || !aligned(kv.k, 16) || !aligned(kv.v, 16) ||
       !a16(kv.k_token_stride) || !a16(kv.v_token_stride))
     return false;
-  if (kv.paged ? !(a16(kv.k_block_stride) && a16(kv.k_head_stride) && a16(kv.v_block_stride) &&
-                   a16(kv.v_head_stride))
-               : !(a16(kv.k_row_stride) && a16(kv.v_row_stride)))
-    return false;
-  const bool cached_gate = p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE;
-  if (!(cached_gate && kv.num_tiles <= 64 * kFastChunks) && p->gate != OC_GATE_NONE) return false;
-  return choose_spw_tuned(p) > 1 || flat_layout_tuned(p);
+  return kv.paged ? a16(kv.k_block_stride) && a16(kv.k_head_stride) && a16(kv.v_block_stride) &&
+                        a16(kv.v_head_stride)
+                  : a16(kv.k_row_stride) && a16(kv.v_row_stride);
 }
 
 static bool portable_path(const oc_decode_params* p) {
   return (p->portable == 1 || generic_shape(p->kv.head_dim, p->kv.tile_size > 0 ? p->kv.tile_size : 64)) &&
-         !wide_fast(p);
+         !wide_route(p);
 }
 
 static bool flat_layout(const oc_decode_params* p) {
@@ -727,9 +721,6 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
       a.hk_stats = hk->stats;
     }
   }
-  // head_dim 256 reaches here only through wide_fast, whose conditions are
-  // a.fast's
-  if (D == 256 && !a.fast) return fail(OC_ERR_UNSUPPORTED, "head_dim 256 decode routing (internal)");
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = dispatch_decode(p->kv.dtype, a, D, gt, gchunks, st);
   if (e != hipSuccess) return hip_fail(e, "decode launch");

@@ -30,11 +30,12 @@ constexpr int kThreads = kWave * kWaves;
 // waves of a decode_kernel workgroup: 8 (two per SIMD, <= 256 registers
 // each), or 4 at one per SIMD (512 registers) where 256 do not hold a
 // wave's state: float32 K/V at head_dim 128 (the raw K and V tile alone take
-// 256), and the VALU path at head_dim 128 with two or more heads per
-// workgroup (its tile words, heads' accumulators and states)
+// 256), the VALU path at head_dim 128 with two or more heads per workgroup
+// (its tile words, heads' accumulators and states), and head_dim 256 (the K
+// tile alone takes 128, the 32 KiB V slots fill the LDS at four waves)
 template <int DT, int D, bool MQK = true, int GT = 1>
 struct DecWaves {
-  static constexpr int value = (D == 128 && (DT == OC_F32 || (!MQK && GT >= 2))) ? 4 : 8;
+  static constexpr int value = (D >= 256 || (D == 128 && (DT == OC_F32 || (!MQK && GT >= 2)))) ? 4 : 8;
 };
 constexpr float kM0 = -1e9f;
 constexpr int kMaxBalTiles = 16384;  // tiles per row for the balanced cached decode (1M tokens)
@@ -2811,7 +2812,7 @@ __global__ __launch_bounds__((DecWaves<DT, D, MQK, GT>::value * kWave)) __attrib
     __shared__ float sh_qn[kDW];
     __shared__ int sh_qnan[kDW];
     if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
-    const bool fast_norms = a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
+    const bool fast_norms = D <= 128 && a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
     if (fast_norms) {
       const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
       float ss;
@@ -3223,20 +3224,37 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
   else launch_decode_gt<DT, HD, VDOT2, false, false, false>(a, gt, grid, st);
 }
 
-// head_dim 256: only the per-wave-prologue kernel, 16-bit K/V with q of K's
-// type, at most 4 query heads per workgroup (the fused merge gives each of
-// its 256 threads one column quad of one head); the host routes every other
-// head_dim-256 decode to the portable kernels
+// head_dim 256: the matrix-core kernels only (the per-wave-prologue one,
+// or the general one: attend-every-tile or single-pass gate), 16-bit K/V
+// with q of K's type, 4-wave workgroups, at most 4 query heads per
+// workgroup (the fused merge gives each of its 256 threads one column quad
+// of one head); the host routes every other head_dim-256 decode to the
+// portable kernels
 template <int DT>
-inline void launch_fast256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if constexpr (DT == OC_BF16 || DT == OC_F16) {
     const dim3 block(4 * kWave);
+    const bool loop = (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) || a.gate == OC_GATE_NONE;
     auto go = [&](auto pg) {
       constexpr bool PG = decltype(pg)::value;
-      switch (gt) {
-        case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, DT>), grid, block, 0, st, a); break;
-        case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, DT>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, DT>), grid, block, 0, st, a); break;
+      if (a.fast) {
+        switch (gt) {
+          case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, DT>), grid, block, 0, st, a); break;
+          case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, DT>), grid, block, 0, st, a); break;
+          default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, DT>), grid, block, 0, st, a); break;
+        }
+      } else if (loop) {
+        switch (gt) {
+          case 1: hipLaunchKernelGGL((decode_kernel<DT, 256, 1, true, PG, true, true>), grid, block, 0, st, a); break;
+          case 2: hipLaunchKernelGGL((decode_kernel<DT, 256, 2, true, PG, true, true>), grid, block, 0, st, a); break;
+          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, true>), grid, block, 0, st, a); break;
+        }
+      } else {
+        switch (gt) {
+          case 1: hipLaunchKernelGGL((decode_kernel<DT, 256, 1, true, PG, true, false>), grid, block, 0, st, a); break;
+          case 2: hipLaunchKernelGGL((decode_kernel<DT, 256, 2, true, PG, true, false>), grid, block, 0, st, a); break;
+          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, false>), grid, block, 0, st, a); break;
+        }
       }
     };
     if (a.paged) go(std::true_type{});
@@ -3245,7 +3263,7 @@ inline void launch_fast256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t s
 }
 
 #define OC_DECODE_CASES(DT, DOT2)                                 \
-  if (head_dim == 256) launch_fast256<DT>(a, gt, grid, st);       \
+  if (head_dim == 256) launch_decode256<DT>(a, gt, grid, st);     \
   else if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
   else launch_decode_hd<DT, 64, DOT2>(a, gt, grid, st);
 

@@ -376,13 +376,14 @@ def _cs_tau(qd, kd, noise, G):
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("G", [1, 2, 3, 4])
-@pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none"])
+@pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none", "cs_single_pass", "zeta_single_pass"])
 def test_head_dim_256_tuned_kernel(dt, G, gate):
-    """head_dim 256, 64-token tiles, 16-bit K/V with q of K's type: the cached
-    score- or mask-gated decode and the dense decode run on the per-wave-
-    prologue matrix-core kernel (4-wave workgroups, one wave per SIMD) when a
-    workgroup takes several splits (here splits_per_group = 2); against the
-    oracle, and against the same decode forced onto the portable kernels."""
+    """head_dim 256, 64-token tiles, 16-bit K/V with q of K's type, on the
+    matrix-core kernels (4-wave workgroups, one wave per SIMD): the cached
+    score- or mask-gated decode and the dense decode on the per-wave-prologue
+    kernel (a workgroup takes several splits: splits_per_group = 2), the
+    single-pass gates on the general one; against the oracle, and against the
+    same decode forced onto the portable kernels."""
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
     rows, T = 3, 12
@@ -390,6 +391,8 @@ def test_head_dim_256_tuned_kernel(dt, G, gate):
     kv = X.rows_layout(kd, vd)
     q32, k32, v32 = np32(qd), np32(kd), np32(vd)
     tmask = None
+    single = gate.endswith("_single_pass")
+    gate = gate.replace("_single_pass", "")
     if gate == "cs":
         thr, ng = _cs_tau(qd, kd, noise, G), N.OC_GATE_CS
     elif gate == "zeta":
@@ -413,17 +416,18 @@ def test_head_dim_256_tuned_kernel(dt, G, gate):
         if gate != "none":
             assert np.array_equal(keep, noise.numpy() if gate == "cs" else ~noise.numpy())
     e_low, e_high, _, _ = X.score_tiles(kv)
-    mode = N.OC_MODE_SINGLE_PASS if gate == "none" else N.OC_MODE_CACHED
+    mode = N.OC_MODE_SINGLE_PASS if (gate == "none" or single) else N.OC_MODE_CACHED
     outs = {}
     for portable in (0, 1):
-        print(f"head_dim 256 {dt} G={G} gate={gate} portable={portable}", flush=True)
+        print(f"head_dim 256 {dt} G={G} gate={gate} single={single} portable={portable}", flush=True)
         r = X.decode(kv, qd, G, gate=ng, threshold=thr, mode=mode, scores=(e_low, e_high), num_splits=4,
                      splits_per_group=2, out_dtype=TORCH_DT[dt], want_keep=gate != "none",
                      tile_mask=None if tmask is None else tmask.to(DEV), portable=portable)
         torch.cuda.synchronize()
         if gate != "none":
             assert np.array_equal(r.keep.cpu().numpy().astype(bool), keep), portable
-        assert_out(r.out, ref, dt, f"head_dim 256 {'portable' if portable else 'tuned'} {dt} G={G} {gate}")
+        assert_out(r.out, ref, dt, f"head_dim 256 {'portable' if portable else 'tuned'} {dt} G={G} {gate}"
+                                   f"{' single pass' if single else ''}")
         outs[portable] = np32(r.out)
     # the two kernels agree to the output type's rounding
     assert np.max(np.abs(outs[0] - outs[1])) <= {"bf16": 1.6e-2, "f16": 2e-3}[dt]
@@ -465,3 +469,32 @@ def test_head_dim_256_routing_and_full_row():
         if gate == "cs":
             assert np.array_equal(r.keep.cpu().numpy().astype(bool), ref["keep"])
         assert_out(r.out, ref["out"], "bf16", f"head_dim 256 tuned full row {gate}")
+
+
+def test_head_dim_256_partials_single_pass():
+    """return_partials at head_dim 256 (one workgroup per logical split, the
+    general matrix-core kernel, single-pass CS gate): every split's (m, l,
+    acc) against the oracle's, and the merged output."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T, G = 2, 9, 4
+    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=99)
+    kv = X.rows_layout(kd, vd)
+    tau = _cs_tau(qd, kd, noise, G)
+    print("head_dim 256 partials", flush=True)
+    res = X.decode(kv, qd, G, gate=N.OC_GATE_CS, threshold=tau, num_splits=4, out_dtype=torch.float32,
+                   want_partials=True, want_keep=True)
+    torch.cuda.synchronize()
+    ref = O.decode_rows(np32(qd), np32(kd), np32(vd), gate="cs", threshold=tau, G=G, num_splits=4,
+                        want_partials=True)
+    assert np.array_equal(res.keep.cpu().numpy().astype(bool), ref["keep"])
+    pm, pl, pacc = (np32(t) for t in res.partials)
+    assert np.array_equal(pm == np.float32(-1e9), ref["M"] == np.float32(-1e9))
+    np.testing.assert_allclose(pm, ref["M"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(pl, ref["L"], rtol=1e-5, atol=1e-6)
+    # the matrix-core p.V keeps about 16 bits of each p (a 16-bit high part
+    # plus the 16-bit rounding of the rest): errors of 2^-17 of |p v| per
+    # product, so the accumulator bar scales with the partials' magnitude
+    scale = float(np.abs(ref["ACC"]).max())
+    np.testing.assert_allclose(pacc, ref["ACC"], rtol=1e-5, atol=1e-5 * max(1.0, scale))
+    assert_out(res.out, ref["out"], "f32", "head_dim 256 tuned partials merged")
