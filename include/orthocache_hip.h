@@ -173,8 +173,12 @@ typedef struct oc_kv_desc {
                                paged_eviction.py:346: any power of two; the bands stay
                                the Walsh rows [1, 8) and [32, 64) clipped to the tile).
                                Tiles other than 64 tokens, and head_dim other than 64
-                               and 128, run the portable kernels (oc_generic.hip);
-                               num_tiles and num_tokens count these tiles. */
+                               and 128, run the portable kernels (oc_generic.hip),
+                               except oc_decode at head_dim 256 with 64-token tiles,
+                               bf16/f16 K/V, q of K's type, G <= 4, pages of >= 16
+                               tokens and 16-byte aligned q, K, V and strides (the
+                               matrix-core kernels); num_tiles and num_tokens count
+                               these tiles. */
 } oc_kv_desc;
 
 /*
