@@ -498,3 +498,48 @@ def test_head_dim_256_partials_single_pass():
     scale = float(np.abs(ref["ACC"]).max())
     np.testing.assert_allclose(pacc, ref["ACC"], rtol=1e-5, atol=1e-5 * max(1.0, scale))
     assert_out(res.out, ref["out"], "f32", "head_dim 256 tuned partials merged")
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+@pytest.mark.parametrize("mode", ["cached", "single_pass", "dense"])
+def test_head_dim_256_paged_tuned(bs, mode):
+    """head_dim 256 paged bf16 decode on the matrix-core kernels: 3 sequences
+    x 2 kv heads, G = 4, row lengths with partial tail tiles (the flat layout
+    of rows of different lengths for the cached and dense decodes), a
+    shuffled pool with 16- and 64-token pages; the Cauchy-Schwarz gate at a
+    calibrated tau, against the oracle's decode over the rows' lengths."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import paged_pool
+    B, hkv, G, T, d = 3, 2, 4, 14, 256
+    k, noise = mixed(B * hkv, T, d, 64, seed=256 + bs)
+    g = torch.Generator().manual_seed(bs)
+    v = torch.randn(B * hkv, T * 64, d, generator=g)
+    q = torch.randn(B * hkv * G, d, generator=g)
+    k, v, q = (x.to(torch.bfloat16) for x in (k, v, q))
+    lens = [T * 64, 9 * 64 + 37, 3 * 64 + 5]
+    kc, vc, bt = paged_pool(k, v, hkv, bs, lens, seed=bs)
+    row_lens = [lens[r // hkv] for r in range(B * hkv)]
+    k32, v32, q32 = np32(k), np32(v), np32(q)
+    _, _, _, eh = O.fwht_scores(k32.reshape(-1, d), 0.0)
+    eh = eh.reshape(B * hkv, T)
+    qn = np.array([O.q_norms(q32[r * G:(r + 1) * G]).max() for r in range(B * hkv)])
+    bnd = qn[:, None] * np.sqrt(eh)
+    tau = float(0.5 * (bnd[~noise.numpy()].max() + bnd[noise.numpy()].min()))
+    gate = "none" if mode == "dense" else "cs"
+    ref = O.decode_rows(q32, k32, v32, gate=gate, threshold=tau, G=G, lengths=row_lens)
+    kv = X.paged_layout(kc.to(DEV), vc.to(DEV), bt.to(DEV), T)
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_CS
+    nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
+    print(f"head_dim 256 paged bs={bs} {mode}", flush=True)
+    r = X.decode(kv, q.to(DEV), G, gate=ng, threshold=tau, mode=nm, scores=(e_low, e_high),
+                 out_dtype=torch.float32, want_keep=mode != "dense")
+    torch.cuda.synchronize()
+    if mode != "dense":
+        keep = r.keep.cpu().numpy().astype(bool)
+        for row in range(B * hkv):
+            nt = -(-row_lens[row] // 64)
+            assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
+    assert_out(r.out, ref["out"], "f32", f"head_dim 256 tuned paged bs={bs} {mode}")
