@@ -493,9 +493,9 @@ static bool flat_layout_tuned(const oc_decode_params* p);
 
 // head_dim 256 with 64-token tiles on the matrix-core kernels (4-wave
 // workgroups at one wave per SIMD, a 32 KiB V slot per wave): bf16 or f16
-// K/V with q of K's type, at most 4 query heads per kv row, contiguous rows
-// or pages of >= 16 tokens, 16-byte aligned q, K, V and strides, K not
-// dequantised in the kernel.  The per-wave-prologue kernel takes what it
+// K/V with q of K's type, or fp8 K (fp8 or bf16 V) with bf16 q, at most 4
+// query heads per kv row, contiguous rows or pages of >= 16 tokens, 16-byte
+// aligned q, K, V and strides.  The per-wave-prologue kernel takes what it
 // takes at head_dim 64 / 128 (a.fast), the general matrix-core kernel the
 // rest (single-pass gate, partials, one split per workgroup).  Every other
 // head_dim-256 decode runs on the portable kernels.
@@ -503,17 +503,23 @@ static bool wide_route(const oc_decode_params* p) {
   const oc_kv_desc& kv = p->kv;
   const int ts = kv.tile_size > 0 ? kv.tile_size : 64;
   if (p->portable != 0 || kv.head_dim != 256 || ts != 64) return false;
-  const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16);
-  if (!mq || (kv.v_dtype != 0 && kv.v_dtype != kv.dtype) || p->G < 1 || p->G > 4) return false;
+  const bool f8 = kv.dtype == OC_FP8_E4M3FN;
+  const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16) ||
+                  (f8 && p->q_dtype == OC_BF16);
+  const bool v_ok = kv.v_dtype == 0 || kv.v_dtype == kv.dtype || (f8 && kv.v_dtype == OC_BF16);
+  if (!mq || !v_ok || p->G < 1 || p->G > 4) return false;
   if (kv.paged && kv.block_size < 16) return false;
-  if (kv.k_scale_mode == OC_KSCALE_DEQUANT) return false;
+  if (kv.k_scale_mode == OC_KSCALE_DEQUANT && !f8) return false;
+  const int es = f8 ? 1 : 2, ves = f8 && kv.v_dtype == OC_BF16 ? 2 : es;
   auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
+  auto k16 = [es](int64_t el) { return (el * es) % 16 == 0; };
+  auto v16 = [ves](int64_t el) { return (el * ves) % 16 == 0; };
   if (!aligned(p->q, 16) || !a16(p->q_row_stride) || !aligned(kv.k, 16) || !aligned(kv.v, 16) ||
-      !a16(kv.k_token_stride) || !a16(kv.v_token_stride))
+      !k16(kv.k_token_stride) || !v16(kv.v_token_stride))
     return false;
-  return kv.paged ? a16(kv.k_block_stride) && a16(kv.k_head_stride) && a16(kv.v_block_stride) &&
-                        a16(kv.v_head_stride)
-                  : a16(kv.k_row_stride) && a16(kv.v_row_stride);
+  return kv.paged ? k16(kv.k_block_stride) && k16(kv.k_head_stride) && v16(kv.v_block_stride) &&
+                        v16(kv.v_head_stride)
+                  : k16(kv.k_row_stride) && v16(kv.v_row_stride);
 }
 
 static bool portable_path(const oc_decode_params* p) {

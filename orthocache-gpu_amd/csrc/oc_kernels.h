@@ -975,7 +975,8 @@ struct MState {
 template <int DT, int D>
 __host__ __device__ constexpr int v_xor(int r) {
   if constexpr (DT == OC_FP8_E4M3FN) {
-    if constexpr (D == 128) return (r >> 1) & 7;
+    if constexpr (D == 256) return r & 15;
+    else if constexpr (D == 128) return (r >> 1) & 7;
     else if constexpr (D == 64) return (r >> 2) & 3;
     else return 0;
   } else {
@@ -1012,7 +1013,7 @@ constexpr bool v_xor_pin() {
   return true;
 }
 static_assert(v_xor_pin<OC_BF16, 256>() && v_xor_pin<OC_BF16, 128>() && v_xor_pin<OC_BF16, 64>() &&
-                  v_xor_pin<OC_FP8_E4M3FN, 128>() &&
+                  v_xor_pin<OC_FP8_E4M3FN, 256>() && v_xor_pin<OC_FP8_E4M3FN, 128>() &&
                   v_xor_pin<OC_FP8_E4M3FN, 64>(),
               "v_xor: a transposing V read uses a bank slot more than twice, or a chunk leaves its row");
 
@@ -3226,22 +3227,33 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 
 // head_dim 256: the matrix-core kernels only (the per-wave-prologue one,
 // or the general one: attend-every-tile or single-pass gate), 16-bit K/V
-// with q of K's type, 4-wave workgroups, at most 4 query heads per
+// with q of K's type or fp8 K/V with bf16 q (bf16 V beside fp8 K in the
+// per-wave-prologue kernel), 4-wave workgroups, at most 4 query heads per
 // workgroup (the fused merge gives each of its 256 threads one column quad
 // of one head); the host routes every other head_dim-256 decode to the
 // portable kernels
 template <int DT>
 inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
-  if constexpr (DT == OC_BF16 || DT == OC_F16) {
+  if constexpr (DT == OC_BF16 || DT == OC_F16 || DT == OC_FP8_E4M3FN) {
     const dim3 block(4 * kWave);
     const bool loop = (a.mode == OC_MODE_CACHED && a.gate != OC_GATE_NONE) || a.gate == OC_GATE_NONE;
+    auto fast = [&](auto pg, auto vt) {
+      constexpr bool PG = decltype(pg)::value;
+      constexpr int VT = decltype(vt)::value;
+      switch (gt) {
+        case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, VT>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, VT>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, VT>), grid, block, 0, st, a); break;
+      }
+    };
     auto go = [&](auto pg) {
       constexpr bool PG = decltype(pg)::value;
       if (a.fast) {
-        switch (gt) {
-          case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, DT>), grid, block, 0, st, a); break;
-          case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, DT>), grid, block, 0, st, a); break;
-          default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, DT>), grid, block, 0, st, a); break;
+        if constexpr (DT == OC_FP8_E4M3FN) {
+          if (a.v_bf16) fast(pg, std::integral_constant<int, OC_BF16>{});
+          else fast(pg, std::integral_constant<int, DT>{});
+        } else {
+          fast(pg, std::integral_constant<int, DT>{});
         }
       } else if (loop) {
         switch (gt) {

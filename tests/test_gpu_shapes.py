@@ -543,3 +543,98 @@ def test_head_dim_256_paged_tuned(bs, mode):
             nt = -(-row_lens[row] // 64)
             assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
     assert_out(r.out, ref["out"], "f32", f"head_dim 256 tuned paged bs={bs} {mode}")
+
+
+def _tile_quant(x, ts=64):
+    """per (row, ts-token tile) fp8-e4m3 with scale amax / 448"""
+    d = x.shape[-1]
+    t = x.view(x.shape[0], -1, ts, d)
+    amax = t.abs().amax(dim=(2, 3))
+    s = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    return (t / s[..., None, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(x.shape), s.float()
+
+
+@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("mode", ["cached", "single_pass", "dense"])
+def test_head_dim_256_fp8_tile_scales_tuned(G, mode):
+    """head_dim 256 fp8-e4m3 K and V with one scale per (row, tile) and bf16
+    q on the matrix-core kernels (K widened per instruction, V through the
+    transposing 8-bit LDS read): masks and outputs against the oracle on the
+    decoded values times their scales."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T, d = 3, 12, 256
+    k, noise = mixed(rows, T, d, 64, seed=80 + G)
+    g = torch.Generator().manual_seed(81 + G)
+    v = torch.randn(rows, T * 64, d, generator=g)
+    q = torch.randn(rows * G, d, generator=g).to(torch.bfloat16)
+    kq, ks = _tile_quant(k)
+    vq, vs = _tile_quant(v)
+    tab = O.fp8_e4m3fn_table()
+    kf, vf = tab[kq.view(torch.uint8).numpy()], tab[vq.view(torch.uint8).numpy()]
+    kdeq = (torch.from_numpy(kf).view(rows, T, 64, d) * ks[..., None, None]).numpy().reshape(-1, d)
+    _, _, _, eh = O.fwht_scores(kdeq, 0.0)
+    qn = np.array([O.q_norms(np32(q)[r * G:(r + 1) * G]).max() for r in range(rows)])
+    bnd = qn[:, None] * np.sqrt(eh.reshape(rows, T))
+    tau = float(0.5 * (bnd[~noise.numpy()].max() + bnd[noise.numpy()].min()))
+    gate = "none" if mode == "dense" else "cs"
+    ref = O.decode_rows(np32(q), kf, vf, gate=gate, threshold=tau, G=G, k_scales=ks.numpy(), v_scales=vs.numpy())
+    kv = X.rows_layout(kq.to(DEV), vq.to(DEV))
+    kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(ks.to(DEV), rows, T, DEV)
+    kv.v_scale_mode, kv.v_scales = X.vscale_mode(vs.to(DEV), rows, T, DEV)
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_CS
+    nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
+    print(f"head_dim 256 fp8 tile scales G={G} {mode}", flush=True)
+    r = X.decode(kv, q.to(DEV), G, gate=ng, threshold=tau, mode=nm, scores=(e_low, e_high), num_splits=4,
+                 splits_per_group=2, out_dtype=torch.float32, want_keep=mode != "dense")
+    torch.cuda.synchronize()
+    if mode != "dense":
+        assert np.array_equal(r.keep.cpu().numpy().astype(bool), ref["keep"])
+        assert np.array_equal(ref["keep"], noise.numpy())
+    assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned fp8 tile scales G={G} {mode}")
+
+
+@pytest.mark.parametrize("mode", ["cached", "dense"])
+def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
+    """head_dim 256 paged fp8 K beside a bf16 V with a scalar k_scale (the
+    reference's paged fp8 cache, paged_eviction.py:354-357): K widened in the
+    kernel as bf16(float(fp8) * k_scale), V read as bf16, rows of different
+    lengths (the flat layout), the per-wave-prologue kernel."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import paged_pool
+    B, hkv, G, T, d = 3, 2, 4, 10, 256
+    k, noise = mixed(B * hkv, T, d, 64, seed=901)
+    g = torch.Generator().manual_seed(902)
+    v = torch.randn(B * hkv, T * 64, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(B * hkv * G, d, generator=g).to(torch.bfloat16)
+    ksc = float(k.abs().max()) / 448.0
+    k8 = (k / ksc).clamp(-448, 448).to(torch.float8_e4m3fn)
+    tab = O.fp8_e4m3fn_table()
+    kdeq = np32(torch.from_numpy(tab[k8.view(torch.uint8).numpy()] * np.float32(ksc)).to(torch.bfloat16))
+    lens = [T * 64, 7 * 64 + 11, 2 * 64 + 40]
+    kc, vc, bt = paged_pool(k8, v, hkv, 16, lens, seed=903)
+    row_lens = [lens[r // hkv] for r in range(B * hkv)]
+    _, _, _, eh = O.fwht_scores(kdeq.reshape(-1, d), 0.0)
+    qn = np.array([O.q_norms(np32(q)[r * G:(r + 1) * G]).max() for r in range(B * hkv)])
+    bnd = qn[:, None] * np.sqrt(eh.reshape(B * hkv, T))
+    tau = float(0.5 * (bnd[~noise.numpy()].max() + bnd[noise.numpy()].min()))
+    gate = "none" if mode == "dense" else "cs"
+    ref = O.decode_rows(np32(q), kdeq, np32(v), gate=gate, threshold=tau, G=G, lengths=row_lens)
+    kv = X.paged_layout(kc.to(DEV), vc.to(DEV), bt.to(DEV), T, keep_mixed=True)
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    kv.k_scale_mode, kv.k_scale = N.OC_KSCALE_DEQUANT, ksc
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_CS
+    nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
+    print(f"head_dim 256 paged fp8 K + bf16 V {mode}", flush=True)
+    r = X.decode(kv, q.to(DEV), G, gate=ng, threshold=tau, mode=nm, scores=(e_low, e_high),
+                 out_dtype=torch.float32, want_keep=mode != "dense")
+    torch.cuda.synchronize()
+    if mode != "dense":
+        keep = r.keep.cpu().numpy().astype(bool)
+        for row in range(B * hkv):
+            nt = -(-row_lens[row] // 64)
+            assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
+    assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned paged fp8 K + bf16 V {mode}")
