@@ -611,9 +611,10 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     benchmark configurations): 8 kv rows x 32768 tokens, G = 4, bfloat16,
     half the tiles noise, the Cauchy-Schwarz gate at a calibrated tau (cached
     and single pass) beside the dense decode.  "d256": the library's own
-    routing (cached and dense on the per-wave-prologue matrix-core kernel,
-    the single pass on the portable kernels); "d256_portable": every variant
-    forced onto the portable kernels; the same at head_dim 128 forced
+    routing (the matrix-core kernels: cached and dense on the per-wave-
+    prologue one, the single pass on the general one); "d256_fp8": the same
+    with fp8-e4m3 K/V and one scale per (row, tile); "d256_portable": every
+    variant forced onto the portable kernels; the same at head_dim 128 forced
     portable next to the tuned kernels.  Buffer sets rotate past the Infinity
     Cache."""
     import torch
@@ -624,9 +625,12 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     dev = torch.device("cuda", 0)
     rows, g = 8, 4
     lib, stream = N.lib(), X.current_stream(dev)
-    r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16, 50% noise tiles, Cauchy-Schwarz gate"}
-    for d, portable in ((head_dim, 0), (head_dim, 1), (128, 1), (128, 0)):
-        set_bytes = rows * seq_len * d * 2 * 2
+    r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16 q, bf16 K/V (d256_fp8: fp8-e4m3 K/V with "
+                     f"one scale per (row, tile)), 50% noise tiles, Cauchy-Schwarz gate"}
+    for d, portable, f8 in ((head_dim, 0, False), (head_dim, 0, True), (head_dim, 1, False), (128, 1, False),
+                            (128, 0, False)):
+        es = 1 if f8 else 2
+        set_bytes = rows * seq_len * d * es * 2
         nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
         T = seq_len // 64
         P = X.auto_num_splits(T, dev)
@@ -636,12 +640,16 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
         keep_alive = []
         tau = None
         for i in range(nsets):
-            wl = make_kv(rows, seq_len, d, noise_frac=0.5, dtype=torch.bfloat16, device=dev, seed=seed + 13 * i)
+            wl = make_kv(rows, seq_len, d, noise_frac=0.5, dtype=torch.float8_e4m3fn if f8 else torch.bfloat16,
+                         device=dev, seed=seed + 13 * i)
             q = make_q(rows, g, d, dtype=torch.bfloat16, device=dev, seed=seed + 13 * i + 1)
-            sc = score_tiles(wl.keys)
+            sc = score_tiles(wl.keys, k_scale=wl.k_scales) if f8 else score_tiles(wl.keys)
             if tau is None:
                 tau = calibrate_tau(sc.e_high, q, g)
             kv = X.rows_layout(wl.keys, wl.values)
+            if f8:
+                kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(wl.k_scales, rows, T, dev)
+                kv.v_scale_mode, kv.v_scales = X.vscale_mode(wl.v_scales, rows, T, dev)
             keep_alive.append((wl, q, sc, kv))
             for name, gate, mode in (("cached", N.OC_GATE_CS, N.OC_MODE_CACHED),
                                      ("single_pass", N.OC_GATE_CS, N.OC_MODE_SINGLE_PASS),
@@ -649,12 +657,12 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
                 p = _decode_params(lib, N, kv, q, g, gate, mode, tau, sc, P, out, ws)
                 p.portable = portable
                 params[name].append(p)
-        tile = 64 * d * 2
+        tile = 64 * d * es + (4 if f8 else 0)  # one K or V tile (+ its scale word)
         tiles = rows * T
         kept = tiles // 2
         nbytes = {"cached": 2 * kept * tile + tiles * 4, "single_pass": tiles * tile + kept * tile,
                   "dense": 2 * tiles * tile}
-        key = f"d{d}" + ("_portable" if portable else ("_tuned" if d in (64, 128) else ""))
+        key = f"d{d}" + ("_fp8" if f8 else "") + ("_portable" if portable else ("_tuned" if d in (64, 128) else ""))
         r[key] = {}
         for name, plist in params.items():
             run = lambda i, plist=plist: N.check("oc_decode", lib.oc_decode(ctypes.byref(plist[i % nsets]),

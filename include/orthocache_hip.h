@@ -175,10 +175,10 @@ typedef struct oc_kv_desc {
                                Tiles other than 64 tokens, and head_dim other than 64
                                and 128, run the portable kernels (oc_generic.hip),
                                except oc_decode at head_dim 256 with 64-token tiles,
-                               bf16/f16 K/V, q of K's type, G <= 4, pages of >= 16
-                               tokens and 16-byte aligned q, K, V and strides (the
-                               matrix-core kernels); num_tiles and num_tokens count
-                               these tiles. */
+                               bf16/f16 K/V with q of K's type or fp8 K/V with bf16
+                               q, G <= 4, pages of >= 16 tokens and 16-byte aligned
+                               q, K, V and strides (the matrix-core kernels);
+                               num_tiles and num_tokens count these tiles. */
 } oc_kv_desc;
 
 /*
