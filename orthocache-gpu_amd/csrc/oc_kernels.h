@@ -45,7 +45,6 @@ constexpr int kKeepLds = kMaxBalTiles / 8;  // keep flags staged in LDS (bytes o
 // tile norms, compared in float64
 constexpr int kGateHook = 16;
 constexpr int kFastChunks = 32;  // decode_fast: at most 64 * kFastChunks tiles per row
-constexpr int kFastBatch = 16;   // decode_fast: 64-tile chunks whose scores are in flight at once
 
 // Kernel arguments (byte strides).  Built by oc_api.hip from oc_decode_params.
 struct DecodeArgs {
@@ -2133,17 +2132,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, const RowInfo& 
 
 // The attend-every-tile transposed step on contiguous rows, or on pages of
 // >= 16 tokens (block-table entries of a wave's next tile requested before
-// its current tile is computed), with a barrier-free prologue (a.fast):
+// its current tile is computed), with a short prologue (a.fast):
 // cached decode with a score gate (at most
 // 64 * kFastChunks tiles per row) or dense decode, q of the matrix-core type,
-// all G <= GT query heads of a row in one workgroup.  Every wave forms by
-// itself, from global memory: the matrix-core q operand, the row's q norms,
-// the retained-tile bitmask of the tile range [b0, b1) (lane c holds the
-// bits of tiles b0 + 64c .. + 63, with their inclusive prefix counts over the
-// lanes), the workgroup's even share [r0, r1) of the range's retained tiles
-// (dense: of its tiles; share gidx of npg) and its first rank r0 + wave.  It issues that tile's K and V loads
-// before the workgroup's one barrier, which publishes the LDS counter the
-// later ranks are drawn from (a wave whose tiles arrived sooner takes more).
+// all G <= GT query heads of a row in one workgroup.  Every wave loads the
+// matrix-core q operand and forms the row's q norms; cached, wave w gates the
+// 64-tile chunks w, w + kDW, ... of the tile range [b0, b1) and publishes
+// their keep bits in LDS, and after one barrier every wave holds the range's
+// retained-tile bitmask (lane c: the bits of tiles b0 + 64c .. + 63, with
+// their inclusive prefix counts over the lanes).  From it each wave forms the
+// workgroup's even share [r0, r1) of the range's retained tiles (dense: of
+// its tiles; share gidx of npg) and its first rank r0 + wave.  It issues that
+// tile's K and V loads before a second barrier, which publishes the LDS
+// counter the later ranks are drawn from (a wave whose tiles arrived sooner
+// takes more).
 // The wave's state goes to LDS as decode_body leaves it.
 template <int DT, int D, int GT, bool PAGED, int kDW, int VT>
 __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& ri, int row, int gidx, int npg, int b0, int b1,
@@ -2175,23 +2177,30 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   };
 
   // cached: the row's keep flags, lane c holding the bits of chunk c.  One
-  // copy of the pass per gate, with the gate's tests compiled in.  The first
-  // kFastBatch chunks' scores are requested before q, so that their latency
-  // overlaps q's; indices are clamped into the row and masked after.  (All
-  // kFastChunks chunks in one batch, with uniform branches past the row,
-  // measured no faster on long rows and slower on short ones.)
+  // copy of the pass per gate, with the gate's tests compiled in.  Wave w
+  // gates chunks w + k kDW (k < kCPW), whose scores are all requested before
+  // q, so that their latency overlaps q's (indices clamped into the row), and
+  // writes each chunk's 64 keep bits to sh_keep; one barrier then publishes
+  // them to every wave.  (Every wave gating the whole range by itself, with
+  // no barrier, read each score line kDW times per workgroup and took about
+  // 1.8 us longer per workgroup at 512 tiles per row.)
   const int nch = (b1 - b0 + 63) >> 6;
   uint32_t wlo = 0u, whi = 0u;
+  __shared__ uint64_t sh_keep[kFastChunks];
+  __shared__ float sh_hk[kDW][3];
   auto score_pass = [&](auto gate_tag) {
     constexpr int GATE = decltype(gate_tag)::value;
     constexpr bool HOOK = GATE == kGateHook;
+    constexpr int kCPW = (kFastChunks + kDW - 1) / kDW;
     const int64_t so = (int64_t)row * a.sc_stride;
-    float el[kFastBatch], eh[kFastBatch];
-    auto load_scores = [&](int c0) {
+    float el[kCPW], eh[kCPW];
 #pragma unroll
-      for (int k = 0; k < kFastBatch; ++k) {
-        const int t = min(b0 + (c0 + k) * 64 + lane, b1 - 1);  // b1 > b0 here
-        el[k] = 0.f;
+    for (int k = 0; k < kCPW; ++k) {
+      const int c = wave + k * kDW;
+      el[k] = 0.f;
+      eh[k] = 0.f;
+      if (c < nch) {
+        const int t = min(b0 + c * 64 + lane, b1 - 1);
         if constexpr (HOOK) {
           // the complete tiles' norms (a partial tail reads the last one's)
           eh[k] = a.hk_norms[(int64_t)(row % a.hk_rows) * a.hk_stride + min(t, a.hk_full - 1)];
@@ -2202,8 +2211,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
           if constexpr (GATE == OC_GATE_ZETA) el[k] = a.sc_el[so + t];
         }
       }
-    };
-    if (nch > 0) load_scores(0);
+    }
     load_q();
     // max over the row's G heads of ||q_g||_2 (CS gate; norms below 1e-38
     // count as 0): head x's squares summed over its four lane groups
@@ -2286,52 +2294,75 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     float nev = 0.f, kmax = -__builtin_inff();
     bool knan = false;
     const bool keep_wr = a.keep_out && gidx == 0;
-    for (int c0 = 0; c0 < nch; c0 += kFastBatch) {
-      if (c0 > 0) load_scores(c0);
 #pragma unroll
-      for (int k = 0; k < kFastBatch; ++k) {
-        const int c = c0 + k;
-        if (c < nch) {
-          const int t = b0 + c * 64 + lane;
-          // cached_keep with the gate fixed: a partial last tile is kept
-          // (score gates), the mask byte decides (mask gate)
-          bool keep;
-          if constexpr (HOOK) {
-            const bool full = t < a.hk_full;
-            const bool ev = full && (double)qn * (double)eh[k] <= a.hk_tau;
-            keep = !ev && t < b1;
-            if (full) {
-              nev += ev ? 1.f : 0.f;
-              kmax = fmaxf(kmax, eh[k]);
-              knan = knan || __builtin_isnan(eh[k]);
-            }
-          } else {
-            keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
-            if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
-            keep = keep && t < b1;
+    for (int k = 0; k < kCPW; ++k) {
+      const int c = wave + k * kDW;
+      if (c < nch) {
+        const int t = b0 + c * 64 + lane;
+        // cached_keep with the gate fixed: a partial last tile is kept
+        // (score gates), the mask byte decides (mask gate)
+        bool keep;
+        if constexpr (HOOK) {
+          const bool full = t < a.hk_full;
+          const bool ev = full && (double)qn * (double)eh[k] <= a.hk_tau;
+          keep = !ev && t < b1;
+          if (full) {
+            nev += ev ? 1.f : 0.f;
+            kmax = fmaxf(kmax, eh[k]);
+            knan = knan || __builtin_isnan(eh[k]);
           }
-          const uint64_t m = __ballot(keep);
-          if (lane == c) {
-            wlo = (uint32_t)m;
-            whi = (uint32_t)(m >> 32);
-          }
-          // the keep flags, by the row's first workgroup (chunk c by wave c mod waves)
-          if (keep_wr && (c % kDW) == wave && t < b1) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+        } else {
+          keep = gate_keep(GATE, a.thr, el[k], eh[k], qmax, qnan);
+          if constexpr (GATE != OC_GATE_MASK) keep = keep || (t + 1) * 64 > ri.n_tok;
+          keep = keep && t < b1;
         }
+        const uint64_t m = __ballot(keep);
+        if (lane == 0) sh_keep[c] = m;
+        // the keep flags, by the row's first workgroup
+        if (keep_wr && t < b1) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
       }
     }
     if constexpr (HOOK) {
-      // the row's statistics, by wave 0 of its first workgroup (every wave
-      // holds them): evicted complete tiles, the group norm and the largest
-      // complete tile's norm (NaN if one is NaN, -inf if there are none)
+      // the wave's share of the row's statistics: evicted complete tiles,
+      // the largest complete tile's norm, whether one is NaN
       nev = wave_sum(nev);
       kmax = wave_max(kmax);
       const bool wnan = __ballot(knan) != 0;
+      if (lane == 0) {
+        sh_hk[wave][0] = nev;
+        sh_hk[wave][1] = kmax;
+        sh_hk[wave][2] = wnan ? 1.f : 0.f;
+      }
+    }
+    // publish the chunks' keep bits with a bare barrier after the LDS stores
+    // have completed (loads still in flight, such as the paged block-table
+    // entries, stay in flight across it); the signal fences keep the
+    // compiler from moving LDS accesses across it
+    __builtin_amdgcn_s_waitcnt(kLgkmOnly);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane < min(nch, kFastChunks)) {
+      const uint64_t m = sh_keep[lane];
+      wlo = (uint32_t)m;
+      whi = (uint32_t)(m >> 32);
+    }
+    if constexpr (HOOK) {
+      // the row's statistics, by wave 0 of its first workgroup: evicted
+      // complete tiles, the group norm and the largest complete tile's norm
+      // (NaN if one is NaN, -inf if there are none)
       if (a.hk_stats && gidx == 0 && wave == 0 && lane == 0) {
+        float ev = 0.f, mx = -__builtin_inff();
+        bool nan = false;
+        for (int w = 0; w < kDW; ++w) {
+          ev += sh_hk[w][0];
+          mx = fmaxf(mx, sh_hk[w][1]);
+          nan = nan || sh_hk[w][2] != 0.f;
+        }
         float* o = a.hk_stats + (int64_t)row * 3;
-        o[0] = nev;
+        o[0] = ev;
         o[1] = qn;
-        o[2] = wnan ? __builtin_nanf("") : kmax;
+        o[2] = nan ? __builtin_nanf("") : mx;
       }
     }
   };
@@ -2546,14 +2577,21 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   const int sl = threadIdx.x / NPAIR;
   const int gp = pair / CQ;
   const int cq = pair - gp * CQ;
-  // one buffer descriptor over this head's Pg partial accumulators (D
-  // floats each, qstride * D floats apart)
-  const float* hp = a.pacc + (pbase + (int64_t)(g0 + min(gp, g_active - 1)) * hstride) * D;
+  // one buffer descriptor over the Pg partial accumulators (D floats each,
+  // qstride * D floats apart) of heads g0 .. g0 + g_active - 1 (hstride * D
+  // floats apart), at a base made wave-uniform, so that each load is one
+  // instruction (a per-thread descriptor is applied one distinct value at a
+  // time); the thread's head is in its offset
+  const uint64_t hpa = (uint64_t)(uintptr_t)(a.pacc + (pbase + (int64_t)g0 * hstride) * D);
+  const float* hp = reinterpret_cast<const float*>(
+      (uintptr_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(hpa >> 32)) << 32) |
+                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)hpa)));
+  const int hoff = min(gp, g_active - 1) * hstride * D;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)hp, (short)0, ((Pg - 1) * qstride + 1) * D * (int)sizeof(float), 0x00020000);
+      (void*)hp, (short)0, ((g_active - 1) * hstride + (Pg - 1) * qstride + 1) * D * (int)sizeof(float), 0x00020000);
   auto ld4 = [&](int q) -> float4 {
-    const auto x =
-        __builtin_amdgcn_raw_buffer_load_b128(pr, (q * qstride * D + 4 * cq) * (int)sizeof(float), 0, 16 /* sc1 */);
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, (hoff + q * qstride * D + 4 * cq) * (int)sizeof(float), 0,
+                                                         16 /* sc1 */);
     return make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
   };
   auto ldc = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
