@@ -1531,29 +1531,52 @@ __device__ __forceinline__ void tile_pv_t(f32x4 (&accp)[D / 16], const f32x4 (&c
     const int vrow8 = 32 * tb2 + 8 * kg + (x >> 1);
     const int vx8 = v_xor<DT, D>(vrow8);
     const uint8_t* rowp8 = reinterpret_cast<const uint8_t*>(sv) + vrow8 * D + 8 * (x & 1);
+    // the transposing reads of four column blocks are issued before their
+    // products, so that their latencies overlap (one read ahead of each
+    // product left a wave waiting on LDS latency for most of the step; all
+    // eight blocks of head_dim 128 ahead needed more than 256 registers)
+    constexpr int NW = DT == OC_FP8_E4M3FN ? 2 : 4;
+    constexpr int GS = D / 16 < 4 ? D / 16 : 4;
 #pragma unroll
-    for (int nc = 0; nc < D / 16; ++nc) {
-      uint32_t va[4];
-      if constexpr (DT == OC_FP8_E4M3FN) {
-        typedef int i32x2 __attribute__((ext_vector_type(2)));
-        const i32x2 b8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * (nc ^ vx8)));
-        fp8x4_to_bf16((uint32_t)b8[0], va[0], va[1]);
-        fp8x4_to_bf16((uint32_t)b8[1], va[2], va[3]);
-      } else {
-        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vx)));
-        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vx)));
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
-        va[0] = w0[0];
-        va[1] = w0[1];
-        va[2] = w1[0];
-        va[3] = w1[1];
+    for (int n0 = 0; n0 < D / 16; n0 += GS) {
+      uint32_t raw[GS][NW];
+#pragma unroll
+      for (int j = 0; j < GS; ++j) {
+        const int nc = n0 + j;
+        if constexpr (DT == OC_FP8_E4M3FN) {
+          typedef int i32x2 __attribute__((ext_vector_type(2)));
+          const i32x2 b8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (__attribute__((address_space(3))) i32x2*)(rowp8 + 16 * (nc ^ vx8)));
+          raw[j][0] = (uint32_t)b8[0];
+          raw[j][1] = (uint32_t)b8[1];
+        } else {
+          const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vx)));
+          const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vx)));
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
+          raw[j][0] = w0[0];
+          raw[j][1] = w0[1];
+          raw[j][2] = w1[0];
+          raw[j][3] = w1[1];
+        }
       }
-      accp[nc] = mfma_qk<MfmaT<DT>::value>(va, phi, accp[nc]);
-      accp[nc] = mfma_qk<MfmaT<DT>::value>(va, plo, accp[nc]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
+#pragma unroll
+      for (int j = 0; j < GS; ++j) {
+        const int nc = n0 + j;
+        uint32_t va[4];
+        if constexpr (DT == OC_FP8_E4M3FN) {
+          fp8x4_to_bf16(raw[j][0], va[0], va[1]);
+          fp8x4_to_bf16(raw[j][1], va[2], va[3]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) va[w] = raw[j][w];
+        }
+        accp[nc] = mfma_qk<MfmaT<DT>::value>(va, phi, accp[nc]);
+        accp[nc] = mfma_qk<MfmaT<DT>::value>(va, plo, accp[nc]);
+      }
     }
   }
 }
@@ -2562,6 +2585,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   }
   __syncthreads();
   if (!sh_last) return;
+  Pg = __builtin_amdgcn_readfirstlane(Pg);  // uniform (the flat layout's comes through LDS)
   // the other workgroups' partials are read with agent-scope (sc1) loads,
   // which are coherent across the XCDs' L2s without an L2 invalidate.  All
   // first-round loads (m, l of partials 0..63 and the first PF accumulator
@@ -2589,9 +2613,11 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   const int hoff = min(gp, g_active - 1) * hstride * D;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)hp, (short)0, ((g_active - 1) * hstride + (Pg - 1) * qstride + 1) * D * (int)sizeof(float), 0x00020000);
-  auto ld4 = [&](int q) -> float4 {
-    const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, (hoff + q * qstride * D + 4 * cq) * (int)sizeof(float), 0,
-                                                         16 /* sc1 */);
+  // partial q's column quad, or zeros when !ok (an offset past the
+  // descriptor's range, which the buffer load answers with zeros: no branch)
+  auto ld4 = [&](int q, bool ok) -> float4 {
+    const int off = ok ? (hoff + q * qstride * D + 4 * cq) * (int)sizeof(float) : 0x7ffffff0;
+    const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 16 /* sc1 */);
     return make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
   };
   auto ldc = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
@@ -2605,11 +2631,14 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
     m0[k] = ok ? ldc(a.pm + base + lane * qstride) : -__builtin_inff();
     l0[k] = ok ? ldc(a.pl + base + lane * qstride) : 0.f;
   }
+  // (round i is issued only when some thread of the workgroup has a
+  // partial in it: a uniform test)
   float4 pf[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
     const int q = sl + i * NSLICE;
-    pf[i] = (gp < g_active && q < Pg) ? ld4(q) : make_float4(0.f, 0.f, 0.f, 0.f);
+    pf[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i * NSLICE < Pg) pf[i] = ld4(q, gp < g_active && q < Pg);
   }
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -2643,12 +2672,14 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
     const float* wg = sh_w + g * Pg;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int q = sl + i * NSLICE;
-      const float w = q < Pg ? wg[q] : 0.f;
-      acc.x = __builtin_fmaf(pf[i].x, w, acc.x);
-      acc.y = __builtin_fmaf(pf[i].y, w, acc.y);
-      acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
-      acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
+      if (i * NSLICE < Pg) {
+        const int q = sl + i * NSLICE;
+        const float w = q < Pg ? wg[min(q, Pg - 1)] : 0.f;
+        acc.x = __builtin_fmaf(pf[i].x, w, acc.x);
+        acc.y = __builtin_fmaf(pf[i].y, w, acc.y);
+        acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
+        acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
+      }
     }
     // the rest in rounds of RB independent loads (the same order of
     // additions as one partial at a time)
@@ -2659,7 +2690,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
         const int q = q0 + i * NSLICE;
-        x[i] = q < Pg ? ld4(q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[i] = ld4(q, q < Pg);
       }
 #pragma unroll
       for (int i = 0; i < RB; ++i) {
