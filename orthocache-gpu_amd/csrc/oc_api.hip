@@ -418,13 +418,38 @@ static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 
 // pass, 256 take 115 and 147).
 static bool portable_path(const oc_decode_params* p);
 
+// Whether a score-gated cached decode of p meets every condition of the
+// per-wave-prologue kernel (decode_fast) other than its split grouping: q of
+// K's 16-bit type (bf16 for fp8 K) in 16-byte rows, pages of >= 16 tokens,
+// all query heads of a row in one workgroup, rows of at most 64 *
+// kFastChunks tiles, output merged inside (no partials or per-split counts
+// asked for), no q-folded K scale.
+static bool fast_cached_shape(const oc_decode_params* p) {
+  const oc_kv_desc& kv = p->kv;
+  const int dt = kv.dtype;
+  const bool mq = (dt == OC_BF16 && p->q_dtype == OC_BF16) || (dt == OC_F16 && p->q_dtype == OC_F16) ||
+                  (dt == OC_FP8_E4M3FN && p->q_dtype == OC_BF16);
+  const int qes = p->q_dtype == OC_F32 ? 4 : 2;
+  const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
+  return p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && mq && (!kv.paged || kv.block_size >= 16) &&
+         p->G <= heads_per_group(p->G) && aligned(p->q, 16) && (p->q_row_stride * qes) % 16 == 0 &&
+         kv.k_scale_mode != OC_KSCALE_Q_FOLD && p->out && !partials_given && !p->split_counts &&
+         kv.num_tiles <= 64 * kFastChunks;
+}
+
 // splits per workgroup of the tuned kernels
 static int choose_spw_tuned(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
   const int P = p->num_splits;
   const int64_t cus = device_cus();
   const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G));
-  const int64_t spw = (P * groups + cus - 1) / cus;
+  int64_t spw = (P * groups + cus - 1) / cus;
+  // A short cached decode whose splits alone fill the CUs (one split per
+  // workgroup) still takes two per workgroup, which puts it on the
+  // per-wave-prologue kernel: config 1 at 1K / 2K tokens (32 rows, 4 / 8
+  // splits) took 14.3 / 14.9 us on one split per workgroup and 11.3 / 11.8
+  // on two.
+  if (spw <= 1 && P >= 2 && fast_cached_shape(p)) spw = 2;
   return (int)std::max<int64_t>(1, std::min<int64_t>(spw, P));
 }
 
@@ -582,7 +607,7 @@ static constexpr int kHookNotFused = -1;
 static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, void* stream,
                        const HookGate* hk = nullptr) {
   if (!p) return fail(OC_ERR_INVALID, "params is NULL");
-  DecodeArgs a;
+  DecodeArgs a{};
   int rc = fill_kv(&p->kv, a, true);
   if (rc) return rc;
   if (!p->kv.v) return fail(OC_ERR_INVALID, "V pointer is NULL");
@@ -900,7 +925,7 @@ extern "C" int oc_decode_static(const oc_decode_params* p, void* stream) {
 
 extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_low, float* e_high, float* zeta,
                               uint8_t* keep, int64_t out_row_stride, void* stream) {
-  DecodeArgs a;
+  DecodeArgs a{};
   int rc = fill_kv(kv, a, true);
   if (rc) return rc;
   a.thr = zeta_max;
@@ -921,7 +946,7 @@ extern "C" int oc_score_tiles(const oc_kv_desc* kv, double zeta_max, float* e_lo
 extern "C" int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int32_t count, double zeta_max,
                                    float* e_low, float* e_high, float* zeta, uint8_t* keep, int64_t out_row_stride,
                                    void* stream) {
-  DecodeArgs a;
+  DecodeArgs a{};
   int rc = fill_kv(kv, a, true);
   if (rc) return rc;
   if (first_tile < 0 || count < 0 || (int64_t)first_tile + count > kv->num_tiles)
@@ -944,7 +969,7 @@ extern "C" int oc_score_tile_range(const oc_kv_desc* kv, int32_t first_tile, int
 extern "C" int oc_band_norms(const oc_kv_desc* kv, int32_t first_tile, int32_t count, int32_t band_lo,
                              int32_t band_hi, float* out, int64_t out_row_stride, int32_t* valid_tiles,
                              void* stream) {
-  DecodeArgs a;
+  DecodeArgs a{};
   int rc = fill_kv(kv, a);
   if (rc) return rc;
   if (generic_shape(kv->head_dim, a.ts))
@@ -967,7 +992,7 @@ extern "C" int oc_band_norms(const oc_kv_desc* kv, int32_t first_tile, int32_t c
 }
 
 extern "C" int oc_fwht_tiles(const oc_kv_desc* kv, float* out, void* stream) {
-  DecodeArgs a;
+  DecodeArgs a{};
   int rc = fill_kv(kv, a);
   if (rc) return rc;
   if (!out) return fail(OC_ERR_INVALID, "out is NULL");
