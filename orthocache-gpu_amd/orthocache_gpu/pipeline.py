@@ -95,8 +95,8 @@ class GPUProfile:
 # 4096 and 1.03-1.08x at 8192 (1.21x at 32768): between 2048 and 8192 the two
 # are within a few percent, box to box.  The bypass takes the band's lower
 # end, 2048, below which dense is faster on every run.  The cached-score
-# decode is level at 1024 tokens (0.99-1.01x) and ahead from 2048 on
-# (1.05x; 1.3x at 4096, 1.77x at 32768).
+# decode is ahead from 1024 tokens on (1.27x at 1024, 1.32x at 2048, 1.4x
+# at 4096, 1.83x at 32768).
 MI355X_CROSSOVER = 2048
 MI355X_CROSSOVER_BAND = (2048, 8192)
 MI355X_PEAK_GBPS = 8000.0
