@@ -2200,13 +2200,15 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   };
 
   // cached: the row's keep flags, lane c holding the bits of chunk c.  One
-  // copy of the pass per gate, with the gate's tests compiled in.  Wave w
-  // gates chunks w + k kDW (k < kCPW), whose scores are all requested before
-  // q, so that their latency overlaps q's (indices clamped into the row), and
-  // writes each chunk's 64 keep bits to sh_keep; one barrier then publishes
-  // them to every wave.  (Every wave gating the whole range by itself, with
-  // no barrier, read each score line kDW times per workgroup and took about
-  // 1.8 us longer per workgroup at 512 tiles per row.)
+  // copy of the pass per gate, with the gate's tests compiled in.  On ranges
+  // of more than two chunks (shared) wave w gates chunks w + k kDW (k <
+  // kCPW), whose scores are all requested before q, so that their latency
+  // overlaps q's (indices clamped into the row), and writes each chunk's 64
+  // keep bits to sh_keep; one barrier then publishes them to every wave.
+  // (Every wave gating the whole range by itself, with no barrier, read each
+  // score line kDW times per workgroup and took about 1.8 us longer per
+  // workgroup at 512 tiles per row.)  On one or two chunks every wave gates
+  // them all itself, with no barrier.
   const int nch = (b1 - b0 + 63) >> 6;
   uint32_t wlo = 0u, whi = 0u;
   __shared__ uint64_t sh_keep[kFastChunks];
@@ -2215,11 +2217,13 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     constexpr int GATE = decltype(gate_tag)::value;
     constexpr bool HOOK = GATE == kGateHook;
     constexpr int kCPW = (kFastChunks + kDW - 1) / kDW;
+    static_assert(kCPW >= 2, "the unshared pass gates two chunks");
+    const bool shared = nch > 2;
     const int64_t so = (int64_t)row * a.sc_stride;
     float el[kCPW], eh[kCPW];
 #pragma unroll
     for (int k = 0; k < kCPW; ++k) {
-      const int c = wave + k * kDW;
+      const int c = shared ? wave + k * kDW : k;
       el[k] = 0.f;
       eh[k] = 0.f;
       if (c < nch) {
@@ -2319,7 +2323,7 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
     const bool keep_wr = a.keep_out && gidx == 0;
 #pragma unroll
     for (int k = 0; k < kCPW; ++k) {
-      const int c = wave + k * kDW;
+      const int c = shared ? wave + k * kDW : k;
       if (c < nch) {
         const int t = b0 + c * 64 + lane;
         // cached_keep with the gate fixed: a partial last tile is kept
@@ -2340,47 +2344,61 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
           keep = keep && t < b1;
         }
         const uint64_t m = __ballot(keep);
-        if (lane == 0) sh_keep[c] = m;
-        // the keep flags, by the row's first workgroup
-        if (keep_wr && t < b1) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
+        if (shared) {
+          if (lane == 0) sh_keep[c] = m;
+        } else if (lane == c) {
+          wlo = (uint32_t)m;
+          whi = (uint32_t)(m >> 32);
+        }
+        // the keep flags, by the row's first workgroup (unshared: chunk c by
+        // wave c)
+        if (keep_wr && (shared || c == wave) && t < b1) a.keep_out[(int64_t)row * a.keep_stride + t] = keep ? 1 : 0;
       }
     }
+    // the wave's statistics (hook gate): evicted complete tiles, the largest
+    // complete tile's norm, whether one is NaN; shared: of its chunks
+    bool wnan = false;
     if constexpr (HOOK) {
-      // the wave's share of the row's statistics: evicted complete tiles,
-      // the largest complete tile's norm, whether one is NaN
       nev = wave_sum(nev);
       kmax = wave_max(kmax);
-      const bool wnan = __ballot(knan) != 0;
-      if (lane == 0) {
+      wnan = __ballot(knan) != 0;
+      if (shared && lane == 0) {
         sh_hk[wave][0] = nev;
         sh_hk[wave][1] = kmax;
         sh_hk[wave][2] = wnan ? 1.f : 0.f;
       }
     }
-    // publish the chunks' keep bits with a bare barrier after the LDS stores
-    // have completed (loads still in flight, such as the paged block-table
-    // entries, stay in flight across it); the signal fences keep the
-    // compiler from moving LDS accesses across it
-    __builtin_amdgcn_s_waitcnt(kLgkmOnly);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane < min(nch, kFastChunks)) {
-      const uint64_t m = sh_keep[lane];
-      wlo = (uint32_t)m;
-      whi = (uint32_t)(m >> 32);
+    if (shared) {
+      // publish the chunks' keep bits with a bare barrier after the LDS
+      // stores have completed (loads still in flight, such as the paged
+      // block-table entries, stay in flight across it); the signal fences
+      // keep the compiler from moving LDS accesses across it
+      __builtin_amdgcn_s_waitcnt(kLgkmOnly);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (lane < min(nch, kFastChunks)) {
+        const uint64_t m = sh_keep[lane];
+        wlo = (uint32_t)m;
+        whi = (uint32_t)(m >> 32);
+      }
     }
     if constexpr (HOOK) {
       // the row's statistics, by wave 0 of its first workgroup: evicted
       // complete tiles, the group norm and the largest complete tile's norm
       // (NaN if one is NaN, -inf if there are none)
       if (a.hk_stats && gidx == 0 && wave == 0 && lane == 0) {
-        float ev = 0.f, mx = -__builtin_inff();
-        bool nan = false;
-        for (int w = 0; w < kDW; ++w) {
-          ev += sh_hk[w][0];
-          mx = fmaxf(mx, sh_hk[w][1]);
-          nan = nan || sh_hk[w][2] != 0.f;
+        float ev = nev, mx = kmax;
+        bool nan = wnan;
+        if (shared) {
+          ev = 0.f;
+          mx = -__builtin_inff();
+          nan = false;
+          for (int w = 0; w < kDW; ++w) {
+            ev += sh_hk[w][0];
+            mx = fmaxf(mx, sh_hk[w][1]);
+            nan = nan || sh_hk[w][2] != 0.f;
+          }
         }
         float* o = a.hk_stats + (int64_t)row * 3;
         o[0] = ev;
