@@ -27,6 +27,7 @@ namespace {
 constexpr int kPfWaves = 8;
 constexpr int kPfRows = 16 * kPfWaves;  // query positions per workgroup
 constexpr int kPfThreads = kPfWaves * kWave;
+constexpr int kPfPvGroup = 4;  // p.V column pairs whose V reads are in flight together
 // work items of a call that splits its longest causal windows (beyond: no split)
 constexpr int kPfMaxItems = 512;
 // -(1e-10) * ln(1e-10): what one zero probability adds to the entropy of a
@@ -399,17 +400,31 @@ __device__ __forceinline__ void pf_pv(f32x4 (&acc)[D / 16], const f32x4 (&c)[4],
       const int vrow = 32 * j + 8 * kg + (x >> 2);
       const int vt = PfTile<DT, D>::vswz(vrow);
       const uint16_t* rowp = sv + vrow * D + 4 * (x & 3);
+      // the transposing reads of GS column pairs are issued before their
+      // products, so that their latencies overlap
 #pragma unroll
-      for (int nc = 0; nc < D / 16; ++nc) {
-        const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vt)));
-        const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vt)));
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
-        const uint32_t av[4] = {w0[0], w0[1], w1[0], w1[1]};
-        acc[nc] = mfma_qk<DT>(av, bhi, acc[nc]);
-        if constexpr (DT == OC_BF16) acc[nc] = mfma_qk<DT>(av, blo, acc[nc]);
+      for (int n0 = 0; n0 < D / 16; n0 += kPfPvGroup) {
+        uint32_t av[kPfPvGroup][4];
+#pragma unroll
+        for (int g = 0; g < kPfPvGroup; ++g) {
+          const int nc = n0 + g;
+          const s16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(rowp + 16 * (nc ^ vt)));
+          const s16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(rowp + 4 * D + 16 * (nc ^ vt)));
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 w0 = __builtin_bit_cast(u32x2, b0), w1 = __builtin_bit_cast(u32x2, b1);
+          av[g][0] = w0[0];
+          av[g][1] = w0[1];
+          av[g][2] = w1[0];
+          av[g][3] = w1[1];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int g = 0; g < kPfPvGroup; ++g) {
+          acc[n0 + g] = mfma_qk<DT>(av[g], bhi, acc[n0 + g]);
+          if constexpr (DT == OC_BF16) acc[n0 + g] = mfma_qk<DT>(av[g], blo, acc[n0 + g]);
+        }
       }
     }
   }
