@@ -172,8 +172,7 @@ class Setup:
 
     def time(self, variant, steps, warmup):
         torch = self.torch
-        for i in range(warmup):
-            self.run(variant, i)
+        _warm(lambda i: self.run(variant, i), warmup)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -323,8 +322,7 @@ class ExtraConfig:
         torch = self.torch
         p = self.params[variant]
         run = lambda: self.N.check("oc_decode", self.lib.oc_decode(ctypes.byref(p), ctypes.c_void_p(self.stream)))
-        for _ in range(warmup):
-            run()
+        _warm(lambda i: run(), warmup)
         torch.cuda.synchronize()
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0.record()
@@ -725,12 +723,34 @@ def cpu_baseline(setup, seconds):
             "host_cpus": os.cpu_count()}
 
 
-def _event_us_i(fn, steps, warmup):
-    """Mean µs of fn(i) over `steps` back-to-back calls between two HIP
-    events, after `warmup` calls."""
+# Seconds of extra warmup calls before a secondary measurement (0 for the
+# primary line, which keeps its --warmup): the clocks take on the order of
+# 10 ms of back-to-back calls to settle after host-side set-up.
+SETTLE_S = 0.0
+
+
+def _warm(fn, warmup):
+    """`warmup` calls of fn(i), then more, 32 at a time, until SETTLE_S
+    seconds have passed."""
     import torch
     for i in range(warmup):
         fn(i)
+    if SETTLE_S > 0:
+        t0, i = time.perf_counter(), warmup
+        while True:
+            for _ in range(32):
+                fn(i)
+                i += 1
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= SETTLE_S:
+                break
+
+
+def _event_us_i(fn, steps, warmup):
+    """Mean µs of fn(i) over `steps` back-to-back calls between two HIP
+    events, after `warmup` calls (and SETTLE_S)."""
+    import torch
+    _warm(fn, warmup)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -743,8 +763,7 @@ def _event_us_i(fn, steps, warmup):
 
 def _event_us(fn, steps, warmup):
     import torch
-    for _ in range(warmup):
-        fn()
+    _warm(lambda i: fn(), warmup)
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -1025,6 +1044,7 @@ def traffic_from_profiles():
 
 SECONDARY_STEPS, SECONDARY_WARMUP = 200, 50
 SETTLED_STEPS, SETTLED_WARMUP = 400, 200
+SECONDARY_SETTLE_S = 0.02
 
 
 def main():
@@ -1097,12 +1117,15 @@ def main():
     # keeps the --warmup it is given.  Reported beside it, not as `value`.
     settled_us = primary.time("cached", SETTLED_STEPS, SETTLED_WARMUP)
     cpu = cpu_baseline(primary, args.cpu_seconds) if args.cpu_seconds > 0 else None
-    # the secondary lines (batch 1, configs 2-4, the config-1 sweep) time at
-    # least 200 steps after at least 50 warmup steps per variant: each starts
-    # after host-side set-up with the GPU idle, and the clocks take tens of
+    # the secondary lines (batch 1, configs 2-4, the config-1 sweep, ...)
+    # time at least 200 steps after at least 50 warmup steps per variant and
+    # then SECONDARY_SETTLE_S seconds more of warmup calls: each starts after
+    # host-side set-up with the GPU idle, and the clocks take about 10 ms of
     # calls to settle (config 3 cached: 297 us at 20 steps after 5 warmup
     # steps, 248-257 us settled); the primary line keeps --steps / --warmup
     s_steps, s_warm = max(args.steps, SECONDARY_STEPS), max(args.warmup, SECONDARY_WARMUP)
+    global SETTLE_S
+    SETTLE_S = SECONDARY_SETTLE_S
     extra = None
     if args.extra_batch:
         del primary
