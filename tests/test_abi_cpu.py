@@ -207,3 +207,38 @@ def test_walsh_matrix_api():
     w = generate_walsh_matrix(64)
     assert torch.allclose(w @ w.T, torch.eye(64), atol=1e-6)
     assert torch.all(w[0] == 0.125)
+
+
+def test_split_grouping_of_short_cached_decodes():
+    """oc_decode_num_groups (host logic only): a cached decode whose splits
+    alone fill the CUs (one split per workgroup) takes two splits per
+    workgroup, which puts it on the per-wave-prologue kernel; partials asked
+    for, a dense decode, or a caller's own grouping keep one split per
+    group."""
+    import ctypes
+    from orthocache_gpu import _native as N
+    lib = N.lib()
+
+    def params(**kw):
+        p = N.OcDecodeParams()
+        p.kv.k, p.kv.v = 1 << 20, 1 << 21
+        p.kv.dtype, p.kv.head_dim, p.kv.num_rows, p.kv.num_tiles = N.OC_BF16, 128, 32, 16
+        p.kv.k_row_stride = p.kv.v_row_stride = 16 * 64 * 128
+        p.kv.k_token_stride = p.kv.v_token_stride = 128
+        p.q, p.q_dtype, p.G, p.q_row_stride = 1 << 22, N.OC_BF16, 1, 128
+        p.gate, p.mode = N.OC_GATE_CS, N.OC_MODE_CACHED
+        p.score_e_low, p.score_e_high, p.score_row_stride = 1 << 23, 1 << 24, 16
+        p.num_splits, p.out_dtype, p.out = 4, N.OC_BF16, 1 << 25
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+    groups = lambda p: lib.oc_decode_num_groups(ctypes.byref(p))
+    assert groups(params()) == 2                                   # 32 rows x 4 splits: two per workgroup
+    assert groups(params(num_splits=8)) == 4
+    assert groups(params(gate=N.OC_GATE_NONE, mode=N.OC_MODE_SINGLE_PASS)) == 4   # dense: one per group
+    assert groups(params(mode=N.OC_MODE_SINGLE_PASS)) == 4         # single pass: one per group
+    assert groups(params(splits_per_group=1)) == 4                 # the caller's grouping
+    assert groups(params(partial_m=1 << 26, partial_l=1 << 27, partial_acc=1 << 28)) == 4
+    assert groups(params(q=(1 << 22) + 2)) == 4                    # q rows not 16-byte pieces
+    assert groups(params(num_splits=1)) == 1
