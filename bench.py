@@ -615,8 +615,9 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     prologue one, the single pass on the general one); "d256_fp8": the same
     with fp8-e4m3 K/V and one scale per (row, tile); "d256_portable": every
     variant forced onto the portable kernels; the same at head_dim 128 forced
-    portable next to the tuned kernels.  Buffer sets rotate past the Infinity
-    Cache."""
+    portable next to the tuned kernels, and at head_dim 32 ("d32": the
+    matrix-core kernels of head_dim 64 / 128, "d32_portable").  Buffer sets
+    rotate past the Infinity Cache."""
     import torch
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
@@ -628,7 +629,7 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16 q, bf16 K/V (d256_fp8: fp8-e4m3 K/V with "
                      f"one scale per (row, tile)), 50% noise tiles, Cauchy-Schwarz gate"}
     for d, portable, f8 in ((head_dim, 0, False), (head_dim, 0, True), (head_dim, 1, False), (128, 1, False),
-                            (128, 0, False)):
+                            (128, 0, False), (32, 0, False), (32, 1, False)):
         es = 1 if f8 else 2
         set_bytes = rows * seq_len * d * es * 2
         nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))

@@ -511,9 +511,10 @@ static FlatCfg flat_cfg(const oc_decode_params* p) {
   return p->mode == OC_MODE_SINGLE_PASS && p->gate != OC_GATE_NONE ? kFlatSinglePass : kFlat;
 }
 
-// The portable kernels (oc_generic.hip): head_dim other than 64 / 128, tiles
-// other than 64 tokens, or asked for (p->portable).  They write one partial
-// per split group and merge_kernel combines them.
+// The portable kernels (oc_generic.hip): head_dim other than 64 / 128 (and
+// 32 / 256 outside the matrix-core routes below), tiles other than 64
+// tokens, or asked for (p->portable).  They write one partial per split
+// group and merge_kernel combines them.
 static bool flat_layout_tuned(const oc_decode_params* p);
 
 // head_dim 256 with 64-token tiles on the matrix-core kernels (4-wave
@@ -547,9 +548,31 @@ static bool wide_route(const oc_decode_params* p) {
                   : k16(kv.k_row_stride) && v16(kv.v_row_stride);
 }
 
+// head_dim 32 with 64-token tiles on the matrix-core kernels of head_dim 64
+// / 128 (8-wave workgroups, the per-wave-prologue kernel where a.fast, the
+// general one otherwise): bf16 or f16 K/V with q of K's type (no fp8 or
+// float32 K/V: a lane's 64-byte row piece holds 2 fp8 bytes), contiguous
+// rows or pages of >= 16 tokens, 16-byte aligned q, K, V and strides.
+// Every other head_dim-32 decode runs on the portable kernels.
+static bool narrow_route(const oc_decode_params* p) {
+  const oc_kv_desc& kv = p->kv;
+  const int ts = kv.tile_size > 0 ? kv.tile_size : 64;
+  if (p->portable != 0 || kv.head_dim != 32 || ts != 64) return false;
+  const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16);
+  if (!mq || (kv.v_dtype != 0 && kv.v_dtype != kv.dtype)) return false;
+  if (kv.paged && kv.block_size < 16) return false;
+  auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
+  if (!aligned(p->q, 16) || !a16(p->q_row_stride) || !aligned(kv.k, 16) || !aligned(kv.v, 16) ||
+      !a16(kv.k_token_stride) || !a16(kv.v_token_stride))
+    return false;
+  return kv.paged ? a16(kv.k_block_stride) && a16(kv.k_head_stride) && a16(kv.v_block_stride) &&
+                        a16(kv.v_head_stride)
+                  : a16(kv.k_row_stride) && a16(kv.v_row_stride);
+}
+
 static bool portable_path(const oc_decode_params* p) {
   return (p->portable == 1 || generic_shape(p->kv.head_dim, p->kv.tile_size > 0 ? p->kv.tile_size : 64)) &&
-         !wide_route(p);
+         !wide_route(p) && !narrow_route(p);
 }
 
 static bool flat_layout(const oc_decode_params* p) {
@@ -742,7 +765,7 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
                                       "type (convert one of them, or decode cached / dense)");
     if (hk) {
       // the row statistics come from a pass over the whole row (not flat)
-      if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1 || D > 128) return kHookNotFused;
+      if (!a.fast || a.flat || dt == OC_FP8_E4M3FN || hk->full < 1 || (D != 64 && D != 128)) return kHookNotFused;
       a.gate = kGateHook;
       a.hk_norms = hk->norms;
       a.hk_stride = hk->stride;

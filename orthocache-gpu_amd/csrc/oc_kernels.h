@@ -982,6 +982,9 @@ __host__ __device__ constexpr int v_xor(int r) {
     // 128 and 256 (512-byte rows: the same pairs of rows share a bank line)
     if constexpr (D == 128 || D == 256) return 2 * ((r & 3) + 4 * ((r >> 3) & 1));
     else if constexpr (D == 64) return 2 * (((r & 3) >> 1) + 2 * ((r >> 3) & 1));
+    // 32 (64-byte rows, four to a bank line): rows r and r + 8 of one read
+    // take the two halves of the line in opposite order
+    else if constexpr (D == 32) return 2 * ((r >> 3) & 1);
     else return 0;
   }
 }
@@ -1012,7 +1015,7 @@ constexpr bool v_xor_pin() {
   return true;
 }
 static_assert(v_xor_pin<OC_BF16, 256>() && v_xor_pin<OC_BF16, 128>() && v_xor_pin<OC_BF16, 64>() &&
-                  v_xor_pin<OC_FP8_E4M3FN, 256>() && v_xor_pin<OC_FP8_E4M3FN, 128>() &&
+                  v_xor_pin<OC_BF16, 32>() && v_xor_pin<OC_FP8_E4M3FN, 256>() && v_xor_pin<OC_FP8_E4M3FN, 128>() &&
                   v_xor_pin<OC_FP8_E4M3FN, 64>(),
               "v_xor: a transposing V read uses a bank slot more than twice, or a chunk leaves its row");
 
@@ -2420,8 +2423,8 @@ __device__ __forceinline__ void decode_fast(const DecodeArgs& a, const RowInfo& 
   }
   if (!cached) load_q();
   else if (a.gate == OC_GATE_CS) score_pass(std::integral_constant<int, OC_GATE_CS>{});
-  else if (!F8 && D <= 128 && a.gate == kGateHook)
-    score_pass(std::integral_constant<int, (F8 || D > 128) ? OC_GATE_CS : kGateHook>{});
+  else if (!F8 && (D == 64 || D == 128) && a.gate == kGateHook)
+    score_pass(std::integral_constant<int, (F8 || (D != 64 && D != 128)) ? OC_GATE_CS : kGateHook>{});
   else if (a.gate == OC_GATE_ZETA) score_pass(std::integral_constant<int, OC_GATE_ZETA>{});
   else score_pass(std::integral_constant<int, OC_GATE_MASK>{});
   const int cnt = __popc(wlo) + __popc(whi);
@@ -2724,13 +2727,29 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   sh_red[threadIdx.x] = acc;
   __syncthreads();
   if (threadIdx.x < NPAIR && g < g_active) {
-#pragma unroll
-    for (int k = 1; k < NSLICE; ++k) {
-      const float4 y = sh_red[k * NPAIR + threadIdx.x];
+    auto add = [&](const float4 y) {
       acc.x += y.x;
       acc.y += y.y;
       acc.z += y.z;
       acc.w += y.w;
+    };
+    if constexpr (NSLICE > 32) {
+      // (head_dim 32, one head: 64 slices) rounds of 16 reads, the same
+      // order of additions; all 63 reads at once would take 252 registers
+      constexpr int RS = 16;
+#pragma unroll 1
+      for (int k0 = 1; k0 < NSLICE; k0 += RS) {
+        float4 y[RS];
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+          if (k0 + j < NSLICE) y[j] = sh_red[(k0 + j) * NPAIR + threadIdx.x];
+#pragma unroll
+        for (int j = 0; j < RS; ++j)
+          if (k0 + j < NSLICE) add(y[j]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 1; k < NSLICE; ++k) add(sh_red[k * NPAIR + threadIdx.x]);
     }
     const float inv = sh_inv[g];
     const int es = a.out_dtype == OC_F32 ? 4 : 2;
@@ -2900,7 +2919,7 @@ __global__ __launch_bounds__((DecWaves<DT, D, MQK, GT>::value * kWave)) __attrib
     __shared__ float sh_qn[kDW];
     __shared__ int sh_qnan[kDW];
     if (threadIdx.x == 0) sh_cnt[kDW] = kDW;
-    const bool fast_norms = D <= 128 && a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
+    const bool fast_norms = (D == 64 || D == 128) && a.gate == OC_GATE_CS && a.G <= GT && GT * D / 2 <= kDT;
     if (fast_norms) {
       const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
       float ss;
@@ -3361,9 +3380,24 @@ inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
   }
 }
 
+// head_dim 32: the matrix-core kernels only, 16-bit K/V with q of K's type
+// (8-wave workgroups as at head_dim 64, a 4 KiB V slot per wave); the host
+// routes every other head_dim-32 decode (fp8 or float32 K/V, another q type)
+// to the portable kernels
+template <int DT>
+constexpr bool kNarrowMfma = DT == OC_BF16 || DT == OC_F16;
+template <int DT>
+inline void launch_decode32(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
+  if constexpr (kNarrowMfma<DT>) {
+    if (a.paged) launch_decode_mq<DT, 32, true>(a, gt, grid, st);
+    else launch_decode_mq<DT, 32, false>(a, gt, grid, st);
+  }
+}
+
 #define OC_DECODE_CASES(DT, DOT2)                                 \
   if (head_dim == 256) launch_decode256<DT>(a, gt, grid, st);     \
   else if (head_dim == 128) launch_decode_hd<DT, 128, DOT2>(a, gt, grid, st); \
+  else if (head_dim == 32) launch_decode32<DT>(a, gt, grid, st);  \
   else launch_decode_hd<DT, 64, DOT2>(a, gt, grid, st);
 
 // q . k on 16-bit operands (matrix cores, or v_dot2 on the VALU path) when
@@ -3379,6 +3413,8 @@ constexpr int kDot2Q = DT == OC_FP8_E4M3FN ? OC_BF16 : DT;
                                hipStream_t st) {                                                  \
     const dim3 grid = a.flat ? dim3(a.fast || !a.bal ? a.flat_slots : a.flat_target + a.num_rows, 1, gchunks)      \
                              : dim3(a.Pg, a.num_rows, gchunks);                                   \
+    /* head_dim 32: 16-bit K/V with q of K's type only */                                        \
+    if (head_dim == 32 && !(kNarrowMfma<DT> && a.q_dtype == DT)) return hipErrorInvalidValue;    \
     if (kHasDot2<DT> && a.q_dtype == kDot2Q<DT>) {                                               \
       OC_DECODE_CASES(DT, kHasDot2<DT>)                                                           \
     } else {                                                                                      \

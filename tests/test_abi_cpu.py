@@ -242,3 +242,45 @@ def test_split_grouping_of_short_cached_decodes():
     assert groups(params(partial_m=1 << 26, partial_l=1 << 27, partial_acc=1 << 28)) == 4
     assert groups(params(q=(1 << 22) + 2)) == 4                    # q rows not 16-byte pieces
     assert groups(params(num_splits=1)) == 1
+
+
+def test_head_dim_32_and_256_routes():
+    """oc_decode_num_groups (host logic only): head_dim 32 and 256 decodes
+    of 16-bit K/V with q of K's type take the matrix-core kernels' split
+    grouping (fewer groups than splits); fp8 K at head_dim 32, float32 K/V,
+    another q type, q rows that are not 16-byte pieces, tiles other than 64
+    tokens or the portable switch keep the portable kernels' one split per
+    group."""
+    import ctypes
+    from orthocache_gpu import _native as N
+    lib = N.lib()
+
+    def params(d, **kw):
+        p = N.OcDecodeParams()
+        p.kv.k, p.kv.v = 1 << 20, 1 << 21
+        p.kv.dtype, p.kv.head_dim, p.kv.num_rows, p.kv.num_tiles = N.OC_BF16, d, 32, 160
+        p.kv.k_row_stride = p.kv.v_row_stride = 160 * 64 * d
+        p.kv.k_token_stride = p.kv.v_token_stride = d
+        p.q, p.q_dtype, p.G, p.q_row_stride = 1 << 22, N.OC_BF16, 1, d
+        p.gate, p.mode = N.OC_GATE_CS, N.OC_MODE_CACHED
+        p.score_e_low, p.score_e_high, p.score_row_stride = 1 << 23, 1 << 24, 160
+        p.num_splits, p.out_dtype, p.out = 40, N.OC_BF16, 1 << 25
+        for k, v in kw.items():
+            if k.startswith("kv_"):
+                setattr(p.kv, k[3:], v)
+            else:
+                setattr(p, k, v)
+        return p
+
+    groups = lambda p: lib.oc_decode_num_groups(ctypes.byref(p))
+    for d in (32, 256):
+        assert groups(params(d)) < 40, d                                     # matrix cores
+        assert groups(params(d, kv_dtype=N.OC_F16, q_dtype=N.OC_F16)) < 40, d
+        assert groups(params(d, portable=1)) == 40, d
+        assert groups(params(d, q_dtype=N.OC_F32)) == 40, d                  # q not of K's type
+        assert groups(params(d, kv_dtype=N.OC_F32, q_dtype=N.OC_F32)) == 40, d
+        assert groups(params(d, q=(1 << 22) + 2)) == 40, d                    # q rows not 16-byte pieces
+    assert groups(params(32, kv_dtype=N.OC_FP8_E4M3FN)) == 40                # fp8 K: portable at 32
+    assert groups(params(256, kv_dtype=N.OC_FP8_E4M3FN)) < 40                # (matrix cores at 256)
+    assert groups(params(32, kv_tile_size=32, kv_num_tiles=320, score_row_stride=320)) == 40
+    assert groups(params(16)) == 40 and groups(params(512)) == 40            # portable head dims

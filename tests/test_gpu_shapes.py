@@ -638,3 +638,195 @@ def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
             nt = -(-row_lens[row] // 64)
             assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
     assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned paged fp8 K + bf16 V {mode}")
+
+
+# ------------------------------------------------ head_dim 32, tuned kernels
+
+def _d32_case(rows, T, G, dt, seed):
+    k, noise = mixed(rows, T, 32, 64, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    v = torch.randn(rows, T * 64, 32, generator=g)
+    q = torch.randn(rows * G, 32, generator=g)
+    kd, vd, qd = (x.to(TORCH_DT[dt]).to(DEV) for x in (k, v, q))
+    return kd, vd, qd, noise
+
+
+def _cs_tau_d(qd, kd, noise, G):
+    rows, d = kd.shape[0], kd.shape[-1]
+    _, _, _, eh = O.fwht_scores(np32(kd).reshape(-1, d), 0.0)
+    eh = eh.reshape(rows, -1)
+    qn = np.array([O.q_norms(np32(qd)[r * G:(r + 1) * G]).max() for r in range(rows)])
+    b = qn[:, None] * np.sqrt(eh)
+    return float(0.5 * (b[~noise.numpy()].max() + b[noise.numpy()].min()))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 8, 12])
+@pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none", "cs_single_pass", "zeta_single_pass"])
+def test_head_dim_32_tuned_kernel(dt, G, gate):
+    """head_dim 32, 64-token tiles, 16-bit K/V with q of K's type, on the
+    matrix-core kernels of head_dim 64 / 128 (8-wave workgroups, a 4 KiB V
+    slot per wave): the cached score- or mask-gated decode and the dense
+    decode on the per-wave-prologue kernel (splits_per_group = 2; G = 12 is
+    two head chunks, the general kernel), the single-pass gates on the
+    general one; against the oracle, and against the same decode forced onto
+    the portable kernels."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T = 3, 12
+    kd, vd, qd, noise = _d32_case(rows, T, G, dt, seed=19 * G + 5 * len(gate))
+    kv = X.rows_layout(kd, vd)
+    q32, k32, v32 = np32(qd), np32(kd), np32(vd)
+    tmask = None
+    single = gate.endswith("_single_pass")
+    gate = gate.replace("_single_pass", "")
+    if gate == "cs":
+        thr, ng = _cs_tau_d(qd, kd, noise, G), N.OC_GATE_CS
+    elif gate == "zeta":
+        thr, ng = 5.0, N.OC_GATE_ZETA
+    elif gate == "mask":
+        thr, ng = 0.0, N.OC_GATE_MASK
+        tmask = (torch.rand(rows, T, generator=torch.Generator().manual_seed(G)) < 0.5).to(torch.uint8)
+        tmask[:, 0] = 1
+    else:
+        thr, ng = 0.0, N.OC_GATE_NONE
+    if gate == "mask":
+        keep = tmask.bool().numpy()
+        ref = np.zeros((rows * G, 32), dtype=np.float32)
+        for r in range(rows):
+            sel = np.repeat(keep[r], 64)
+            for h in range(G):
+                ref[r * G + h] = O.dense_decode(q32[r * G + h:r * G + h + 1], k32[r:r + 1, sel], v32[r:r + 1, sel])[0]
+    else:
+        res = O.decode_rows(q32, k32, v32, gate="none" if gate == "none" else gate, threshold=thr, G=G)
+        ref, keep = res["out"], res["keep"]
+        if gate != "none":
+            assert np.array_equal(keep, noise.numpy() if gate == "cs" else ~noise.numpy())
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    mode = N.OC_MODE_SINGLE_PASS if (gate == "none" or single) else N.OC_MODE_CACHED
+    outs = {}
+    for portable in (0, 1):
+        print(f"head_dim 32 {dt} G={G} gate={gate} single={single} portable={portable}", flush=True)
+        r = X.decode(kv, qd, G, gate=ng, threshold=thr, mode=mode, scores=(e_low, e_high), num_splits=4,
+                     splits_per_group=2, out_dtype=TORCH_DT[dt], want_keep=gate != "none",
+                     tile_mask=None if tmask is None else tmask.to(DEV), portable=portable)
+        torch.cuda.synchronize()
+        if gate != "none":
+            assert np.array_equal(r.keep.cpu().numpy().astype(bool), keep), portable
+        assert_out(r.out, ref, dt, f"head_dim 32 {'portable' if portable else 'tuned'} {dt} G={G} {gate}"
+                                   f"{' single pass' if single else ''}")
+        outs[portable] = np32(r.out)
+    # the two kernels agree to the output type's rounding
+    assert np.max(np.abs(outs[0] - outs[1])) <= {"bf16": 1.6e-2, "f16": 2e-3}[dt]
+
+
+def test_head_dim_32_routing_and_full_row():
+    """With the automatic split grouping, head_dim 32 bf16 cached decodes take
+    several splits per workgroup (the tuned kernels' grouping: fewer
+    partials than splits) while the same call forced portable keeps one
+    split per workgroup; the tuned kernels' output on 8 rows x 10240 tokens
+    (160 tiles) matches the oracle, cached and dense, with the fused merge
+    over one head (64 merge slices of 512 threads) and over four."""
+    import ctypes
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T = 8, 160
+    lib = N.lib()
+    for G in (1, 4):
+        kd, vd, qd, noise = _d32_case(rows, T, G, "bf16", seed=320 + G)
+        kv = X.rows_layout(kd, vd)
+        tau = _cs_tau_d(qd, kd, noise, G)
+        e_low, e_high, _, _ = X.score_tiles(kv)
+        P = X.auto_num_splits(T, qd.device)
+        groups = {}
+        for portable in (0, 1):
+            p = N.OcDecodeParams()
+            p.kv = kv.struct()
+            p.q, p.q_dtype, p.G, p.q_row_stride = qd.data_ptr(), N.OC_BF16, G, qd.stride(0)
+            p.gate, p.mode, p.threshold = N.OC_GATE_CS, N.OC_MODE_CACHED, tau
+            p.score_e_low, p.score_e_high, p.score_row_stride = e_low.data_ptr(), e_high.data_ptr(), e_high.stride(0)
+            p.num_splits, p.out_dtype, p.portable = P, N.OC_BF16, portable
+            groups[portable] = lib.oc_decode_num_groups(ctypes.byref(p))
+        assert groups[1] == P and groups[0] < P, (P, groups)
+        q32, k32, v32 = np32(qd), np32(kd), np32(vd)
+        for gate, ng, mode in (("cs", N.OC_GATE_CS, N.OC_MODE_CACHED), ("none", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS)):
+            ref = O.decode_rows(q32, k32, v32, gate=gate, threshold=tau, G=G)
+            print(f"head_dim 32 full row G={G} {gate}", flush=True)
+            r = X.decode(kv, qd, G, gate=ng, threshold=tau, mode=mode, scores=(e_low, e_high), num_splits=P,
+                         out_dtype=torch.bfloat16, want_keep=gate == "cs")
+            torch.cuda.synchronize()
+            if gate == "cs":
+                assert np.array_equal(r.keep.cpu().numpy().astype(bool), ref["keep"])
+            assert_out(r.out, ref["out"], "bf16", f"head_dim 32 tuned full row G={G} {gate}")
+
+
+def test_head_dim_32_partials_single_pass():
+    """return_partials at head_dim 32 (one workgroup per logical split, the
+    general matrix-core kernel, single-pass CS gate): every split's (m, l,
+    acc) against the oracle's, and the merged output."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T, G = 2, 9, 4
+    kd, vd, qd, noise = _d32_case(rows, T, G, "bf16", seed=32)
+    kv = X.rows_layout(kd, vd)
+    tau = _cs_tau_d(qd, kd, noise, G)
+    print("head_dim 32 partials", flush=True)
+    res = X.decode(kv, qd, G, gate=N.OC_GATE_CS, threshold=tau, num_splits=4, out_dtype=torch.float32,
+                   want_partials=True, want_keep=True)
+    torch.cuda.synchronize()
+    ref = O.decode_rows(np32(qd), np32(kd), np32(vd), gate="cs", threshold=tau, G=G, num_splits=4,
+                        want_partials=True)
+    assert np.array_equal(res.keep.cpu().numpy().astype(bool), ref["keep"])
+    pm, pl, pacc = (np32(t) for t in res.partials)
+    assert np.array_equal(pm == np.float32(-1e9), ref["M"] == np.float32(-1e9))
+    np.testing.assert_allclose(pm, ref["M"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(pl, ref["L"], rtol=1e-5, atol=1e-6)
+    # about 16 bits of each p in the matrix-core p.V (see the head_dim 256 case)
+    scale = float(np.abs(ref["ACC"]).max())
+    np.testing.assert_allclose(pacc, ref["ACC"], rtol=1e-5, atol=1e-5 * max(1.0, scale))
+    assert_out(res.out, ref["out"], "f32", "head_dim 32 tuned partials merged")
+
+
+@pytest.mark.parametrize("bs", [16, 64])
+@pytest.mark.parametrize("mode", ["cached", "single_pass", "dense"])
+def test_head_dim_32_paged_tuned(bs, mode):
+    """head_dim 32 paged f16 decode on the matrix-core kernels: 3 sequences x
+    2 kv heads, G = 4, row lengths with partial tail tiles (the flat layout
+    of rows of different lengths for the cached and dense decodes), a
+    shuffled pool with 16- and 64-token pages; the Cauchy-Schwarz gate at a
+    calibrated tau, against the oracle's decode over the rows' lengths."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    from orthocache_gpu.workloads import paged_pool
+    B, hkv, G, T, d = 3, 2, 4, 14, 32
+    k, noise = mixed(B * hkv, T, d, 64, seed=32 + bs)
+    g = torch.Generator().manual_seed(3 * bs)
+    v = torch.randn(B * hkv, T * 64, d, generator=g)
+    q = torch.randn(B * hkv * G, d, generator=g)
+    k, v, q = (x.to(torch.float16) for x in (k, v, q))
+    lens = [T * 64, 9 * 64 + 37, 3 * 64 + 5]
+    kc, vc, bt = paged_pool(k, v, hkv, bs, lens, seed=bs + 1)
+    row_lens = [lens[r // hkv] for r in range(B * hkv)]
+    k32, v32, q32 = np32(k), np32(v), np32(q)
+    _, _, _, eh = O.fwht_scores(k32.reshape(-1, d), 0.0)
+    eh = eh.reshape(B * hkv, T)
+    qn = np.array([O.q_norms(q32[r * G:(r + 1) * G]).max() for r in range(B * hkv)])
+    bnd = qn[:, None] * np.sqrt(eh)
+    tau = float(0.5 * (bnd[~noise.numpy()].max() + bnd[noise.numpy()].min()))
+    gate = "none" if mode == "dense" else "cs"
+    ref = O.decode_rows(q32, k32, v32, gate=gate, threshold=tau, G=G, lengths=row_lens)
+    kv = X.paged_layout(kc.to(DEV), vc.to(DEV), bt.to(DEV), T)
+    kv.lengths = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_CS
+    nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
+    print(f"head_dim 32 paged bs={bs} {mode}", flush=True)
+    r = X.decode(kv, q.to(DEV), G, gate=ng, threshold=tau, mode=nm, scores=(e_low, e_high),
+                 out_dtype=torch.float32, want_keep=mode != "dense")
+    torch.cuda.synchronize()
+    if mode != "dense":
+        keep = r.keep.cpu().numpy().astype(bool)
+        for row in range(B * hkv):
+            nt = -(-row_lens[row] // 64)
+            assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
+    assert_out(r.out, ref["out"], "f32", f"head_dim 32 tuned paged bs={bs} {mode}")
