@@ -176,8 +176,11 @@ typedef struct oc_kv_desc {
                                and 128, run the portable kernels (oc_generic.hip),
                                except oc_decode at head_dim 256 with 64-token tiles,
                                bf16/f16 K/V with q of K's type or fp8 K/V with bf16
-                               q, G <= 4, pages of >= 16 tokens and 16-byte aligned
-                               q, K, V and strides (the matrix-core kernels);
+                               q (bf16 V beside fp8 K and in-kernel dequantisation:
+                               G <= 4), pages of >= 16 tokens and 16-byte aligned
+                               q, K, V and strides, and at head_dim 32 with 64-token
+                               tiles, bf16/f16 K/V with q of K's type under the same
+                               page and alignment conditions (the matrix-core kernels);
                                num_tiles and num_tokens count these tiles. */
 } oc_kv_desc;
 

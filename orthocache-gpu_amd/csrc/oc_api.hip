@@ -406,8 +406,16 @@ static int device_cus() {
   return cache[dev];
 }
 
-// query heads per decode workgroup for G heads per kv row
-static int heads_per_group(int G) { return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G)); }
+static bool wide_route(const oc_decode_params* p);
+
+// query heads per decode workgroup for G heads per kv row: chunks of up to
+// 8, of up to 4 on the head_dim-256 matrix-core kernels (whose fused merge
+// gives each of 256 threads one column quad of one head)
+static int heads_per_group(const oc_decode_params* p) {
+  const int G = p->G;
+  const int g = G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G));
+  return g > 4 && wide_route(p) ? 4 : g;
+}
 
 // Splits per workgroup: as many as keep the workgroup count at or below the
 // CU count, so that the decode runs as one round of workgroups (one
@@ -432,7 +440,7 @@ static bool fast_cached_shape(const oc_decode_params* p) {
   const int qes = p->q_dtype == OC_F32 ? 4 : 2;
   const bool partials_given = p->partial_m && p->partial_l && p->partial_acc;
   return p->mode == OC_MODE_CACHED && p->gate != OC_GATE_NONE && mq && (!kv.paged || kv.block_size >= 16) &&
-         p->G <= heads_per_group(p->G) && aligned(p->q, 16) && (p->q_row_stride * qes) % 16 == 0 &&
+         p->G <= heads_per_group(p) && aligned(p->q, 16) && (p->q_row_stride * qes) % 16 == 0 &&
          kv.k_scale_mode != OC_KSCALE_Q_FOLD && p->out && !partials_given && !p->split_counts &&
          kv.num_tiles <= 64 * kFastChunks;
 }
@@ -442,7 +450,7 @@ static int choose_spw_tuned(const oc_decode_params* p) {
   if (p->splits_per_group > 0) return std::min(p->splits_per_group, p->num_splits);
   const int P = p->num_splits;
   const int64_t cus = device_cus();
-  const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G));
+  const int64_t groups = (int64_t)p->kv.num_rows * ((p->G + heads_per_group(p) - 1) / heads_per_group(p));
   int64_t spw = (P * groups + cus - 1) / cus;
   // A short cached decode whose splits alone fill the CUs (one split per
   // workgroup) still takes two per workgroup, which puts it on the
@@ -483,7 +491,7 @@ static constexpr size_t kCounterBytes = 64 << 10;
 // merge weights (GT * Pg floats in the kernel's 4 * GT * D wave-merge LDS)
 // fit; otherwise merge_kernel runs after it.
 static int gchunks_of(const oc_decode_params* p) {
-  return (p->G + heads_per_group(p->G) - 1) / heads_per_group(p->G);
+  return (p->G + heads_per_group(p) - 1) / heads_per_group(p);
 }
 
 static bool fused_merge(const oc_decode_params* p, int pg) {
@@ -519,12 +527,15 @@ static bool flat_layout_tuned(const oc_decode_params* p);
 
 // head_dim 256 with 64-token tiles on the matrix-core kernels (4-wave
 // workgroups at one wave per SIMD, a 32 KiB V slot per wave): bf16 or f16
-// K/V with q of K's type, or fp8 K (fp8 or bf16 V) with bf16 q, at most 4
-// query heads per kv row, contiguous rows or pages of >= 16 tokens, 16-byte
-// aligned q, K, V and strides.  The per-wave-prologue kernel takes what it
-// takes at head_dim 64 / 128 (a.fast), the general matrix-core kernel the
-// rest (single-pass gate, partials, one split per workgroup).  Every other
-// head_dim-256 decode runs on the portable kernels.
+// K/V with q of K's type, or fp8 K (fp8 or bf16 V) with bf16 q, contiguous
+// rows or pages of >= 16 tokens, 16-byte aligned q, K, V and strides.  A
+// workgroup takes at most 4 query heads: the per-wave-prologue kernel takes
+// what it takes at head_dim 64 / 128 (a.fast) for G <= 4, the general
+// matrix-core kernel the rest (single-pass gate, partials, one split per
+// workgroup, and G > 4 as chunks of 4 heads, each reading the row's K and
+// V).  bf16 V beside fp8 K and the in-kernel K dequantisation, which only
+// the per-wave-prologue kernel does, need G <= 4.  Every other head_dim-256
+// decode runs on the portable kernels.
 static bool wide_route(const oc_decode_params* p) {
   const oc_kv_desc& kv = p->kv;
   const int ts = kv.tile_size > 0 ? kv.tile_size : 64;
@@ -533,9 +544,11 @@ static bool wide_route(const oc_decode_params* p) {
   const bool mq = (kv.dtype == OC_BF16 && p->q_dtype == OC_BF16) || (kv.dtype == OC_F16 && p->q_dtype == OC_F16) ||
                   (f8 && p->q_dtype == OC_BF16);
   const bool v_ok = kv.v_dtype == 0 || kv.v_dtype == kv.dtype || (f8 && kv.v_dtype == OC_BF16);
-  if (!mq || !v_ok || p->G < 1 || p->G > 4) return false;
+  if (!mq || !v_ok || p->G < 1 || p->G > 64) return false;
   if (kv.paged && kv.block_size < 16) return false;
   if (kv.k_scale_mode == OC_KSCALE_DEQUANT && !f8) return false;
+  const bool v_bf16 = f8 && kv.v_dtype == OC_BF16;
+  if (p->G > 4 && (v_bf16 || kv.k_scale_mode == OC_KSCALE_DEQUANT)) return false;
   const int es = f8 ? 1 : 2, ves = f8 && kv.v_dtype == OC_BF16 ? 2 : es;
   auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
   auto k16 = [es](int64_t el) { return (el * es) % 16 == 0; };
@@ -721,7 +734,7 @@ static int decode_impl(const oc_decode_params* p, void* ws, size_t ws_bytes, voi
   a.out_dtype = p->out_dtype;
   a.out_stride = p->out_row_stride * oes;
   if (a.num_rows == 0) return OC_OK;
-  const int gt = heads_per_group(p->G);
+  const int gt = heads_per_group(p);
   const int gchunks = (p->G + gt - 1) / gt;
   if (portable) {
     // every gate, mode, scale mode and layout, in float32 on the VALU; the

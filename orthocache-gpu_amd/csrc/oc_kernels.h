@@ -3336,8 +3336,8 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 // with q of K's type or fp8 K/V with bf16 q (bf16 V beside fp8 K in the
 // per-wave-prologue kernel), 4-wave workgroups, at most 4 query heads per
 // workgroup (the fused merge gives each of its 256 threads one column quad
-// of one head); the host routes every other head_dim-256 decode to the
-// portable kernels
+// of one head: more heads run as chunks of 4 on the general kernel); the
+// host routes every other head_dim-256 decode to the portable kernels
 template <int DT>
 inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if constexpr (DT == OC_BF16 || DT == OC_F16 || DT == OC_FP8_E4M3FN) {

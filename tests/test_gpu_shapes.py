@@ -375,15 +375,16 @@ def _cs_tau(qd, kd, noise, G):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("G", [1, 2, 3, 4])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8])
 @pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none", "cs_single_pass", "zeta_single_pass"])
 def test_head_dim_256_tuned_kernel(dt, G, gate):
     """head_dim 256, 64-token tiles, 16-bit K/V with q of K's type, on the
     matrix-core kernels (4-wave workgroups, one wave per SIMD): the cached
     score- or mask-gated decode and the dense decode on the per-wave-prologue
     kernel (a workgroup takes several splits: splits_per_group = 2), the
-    single-pass gates on the general one; against the oracle, and against the
-    same decode forced onto the portable kernels."""
+    single-pass gates on the general one, and G = 6, 8 on the general one in
+    two chunks of up to 4 heads; against the oracle, and against the same
+    decode forced onto the portable kernels."""
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
     rows, T = 3, 12
@@ -554,7 +555,7 @@ def _tile_quant(x, ts=64):
     return (t / s[..., None, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(x.shape), s.float()
 
 
-@pytest.mark.parametrize("G", [1, 4])
+@pytest.mark.parametrize("G", [1, 4, 8])
 @pytest.mark.parametrize("mode", ["cached", "single_pass", "dense"])
 def test_head_dim_256_fp8_tile_scales_tuned(G, mode):
     """head_dim 256 fp8-e4m3 K and V with one scale per (row, tile) and bf16
