@@ -177,7 +177,7 @@ typedef struct oc_kv_desc {
                                except oc_decode at head_dim 256 with 64-token tiles,
                                bf16/f16 K/V with q of K's type or fp8 K/V with bf16
                                q (bf16 V beside fp8 K and in-kernel dequantisation:
-                               G <= 4), pages of >= 16 tokens and 16-byte aligned
+                               G <= 8), pages of >= 16 tokens and 16-byte aligned
                                q, K, V and strides, and at head_dim 32 with 64-token
                                tiles, bf16/f16 K/V with q of K's type under the same
                                page and alignment conditions (the matrix-core kernels);

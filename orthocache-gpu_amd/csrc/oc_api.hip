@@ -406,15 +406,10 @@ static int device_cus() {
   return cache[dev];
 }
 
-static bool wide_route(const oc_decode_params* p);
-
-// query heads per decode workgroup for G heads per kv row: chunks of up to
-// 8, of up to 4 on the head_dim-256 matrix-core kernels (whose fused merge
-// gives each of 256 threads one column quad of one head)
+// query heads per decode workgroup for G heads per kv row (chunks of up to 8)
 static int heads_per_group(const oc_decode_params* p) {
   const int G = p->G;
-  const int g = G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G));
-  return g > 4 && wide_route(p) ? 4 : g;
+  return G >= 8 ? 8 : (G >= 4 ? (G == 4 ? 4 : 8) : (G == 3 ? 4 : G));
 }
 
 // Splits per workgroup: as many as keep the workgroup count at or below the
@@ -528,13 +523,12 @@ static bool flat_layout_tuned(const oc_decode_params* p);
 // head_dim 256 with 64-token tiles on the matrix-core kernels (4-wave
 // workgroups at one wave per SIMD, a 32 KiB V slot per wave): bf16 or f16
 // K/V with q of K's type, or fp8 K (fp8 or bf16 V) with bf16 q, contiguous
-// rows or pages of >= 16 tokens, 16-byte aligned q, K, V and strides.  A
-// workgroup takes at most 4 query heads: the per-wave-prologue kernel takes
-// what it takes at head_dim 64 / 128 (a.fast) for G <= 4, the general
-// matrix-core kernel the rest (single-pass gate, partials, one split per
-// workgroup, and G > 4 as chunks of 4 heads, each reading the row's K and
-// V).  bf16 V beside fp8 K and the in-kernel K dequantisation, which only
-// the per-wave-prologue kernel does, need G <= 4.  Every other head_dim-256
+// rows or pages of >= 16 tokens, 16-byte aligned q, K, V and strides.  The
+// per-wave-prologue kernel takes what it takes at head_dim 64 / 128 (a.fast,
+// G <= 8), the general matrix-core kernel the rest (single-pass gate,
+// partials, one split per workgroup, G > 8 in chunks of 8 heads).  bf16 V
+// beside fp8 K and the in-kernel K dequantisation, which only the
+// per-wave-prologue kernel does, need G <= 8.  Every other head_dim-256
 // decode runs on the portable kernels.
 static bool wide_route(const oc_decode_params* p) {
   const oc_kv_desc& kv = p->kv;
@@ -548,7 +542,7 @@ static bool wide_route(const oc_decode_params* p) {
   if (kv.paged && kv.block_size < 16) return false;
   if (kv.k_scale_mode == OC_KSCALE_DEQUANT && !f8) return false;
   const bool v_bf16 = f8 && kv.v_dtype == OC_BF16;
-  if (p->G > 4 && (v_bf16 || kv.k_scale_mode == OC_KSCALE_DEQUANT)) return false;
+  if (p->G > 8 && (v_bf16 || kv.k_scale_mode == OC_KSCALE_DEQUANT)) return false;
   const int es = f8 ? 1 : 2, ves = f8 && kv.v_dtype == OC_BF16 ? 2 : es;
   auto a16 = [](int64_t el) { return (el * 2) % 16 == 0; };
   auto k16 = [es](int64_t el) { return (el * es) % 16 == 0; };

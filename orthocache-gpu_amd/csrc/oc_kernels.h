@@ -2614,14 +2614,18 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   constexpr int CQ = D / 4;
-  constexpr int NPAIR = GT * CQ;
   constexpr int kDT = kDW * kWave;
+  // the (head, column quad) pairs in NPASS passes of NPAIR, each pair of a
+  // pass summed by NSLICE threads (two passes at head_dim 256 with 8 heads,
+  // one otherwise)
+  constexpr int NPASS = (GT * CQ + kDT - 1) / kDT;
+  constexpr int NPAIR = GT * CQ / NPASS;
   constexpr int NSLICE = kDT / NPAIR;
+  static_assert(NPAIR * NPASS == GT * CQ && NPAIR * NSLICE == kDT, "merge passes");
   constexpr int PF = D >= 128 ? 32 : 8;  // the D = 64 kernels keep more waves per SIMD
-  const int pair = threadIdx.x % NPAIR;
   const int sl = threadIdx.x / NPAIR;
-  const int gp = pair / CQ;
-  const int cq = pair - gp * CQ;
+  int gp = (threadIdx.x % NPAIR) / CQ;
+  int cq = (threadIdx.x % NPAIR) - gp * CQ;
   // one buffer descriptor over the Pg partial accumulators (D floats each,
   // qstride * D floats apart) of heads g0 .. g0 + g_active - 1 (hstride * D
   // floats apart), at a base made wave-uniform, so that each load is one
@@ -2631,7 +2635,7 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   const float* hp = reinterpret_cast<const float*>(
       (uintptr_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(hpa >> 32)) << 32) |
                   (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)hpa)));
-  const int hoff = min(gp, g_active - 1) * hstride * D;
+  int hoff = min(gp, g_active - 1) * hstride * D;
   const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)hp, (short)0, ((g_active - 1) * hstride + (Pg - 1) * qstride + 1) * D * (int)sizeof(float), 0x00020000);
   // partial q's column quad, or zeros when !ok (an offset past the
@@ -2655,12 +2659,15 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   // (round i is issued only when some thread of the workgroup has a
   // partial in it: a uniform test)
   float4 pf[PF];
+  auto prefetch = [&]() {
 #pragma unroll
-  for (int i = 0; i < PF; ++i) {
-    const int q = sl + i * NSLICE;
-    pf[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (i * NSLICE < Pg) pf[i] = ld4(q, gp < g_active && q < Pg);
-  }
+    for (int i = 0; i < PF; ++i) {
+      const int q = sl + i * NSLICE;
+      pf[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i * NSLICE < Pg) pf[i] = ld4(q, gp < g_active && q < Pg);
+    }
+  };
+  prefetch();
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int g = wave + k * kDW;
@@ -2684,80 +2691,92 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
     if (lane == 0) sh_inv[g] = fmaxf(ls, 1e-9f);
   }
   __syncthreads();
-  // weighted sum over the Pg partials: thread (slice, g, column quad) adds
-  // partials q = slice, slice + nslice, ... with all its loads independent;
-  // the slices are then added in a fixed order (deterministic result)
-  const int g = gp;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (g < g_active) {
-    const float* wg = sh_w + g * Pg;
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      if (i * NSLICE < Pg) {
-        const int q = sl + i * NSLICE;
-        const float w = q < Pg ? wg[min(q, Pg - 1)] : 0.f;
-        acc.x = __builtin_fmaf(pf[i].x, w, acc.x);
-        acc.y = __builtin_fmaf(pf[i].y, w, acc.y);
-        acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
-        acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
-      }
+  for (int ps = 0; ps < NPASS; ++ps) {
+    if (ps > 0) {
+      // the next pass's pairs, once every thread has read the last pass's
+      // slices from sh_red
+      __syncthreads();
+      const int pair = ps * NPAIR + threadIdx.x % NPAIR;
+      gp = pair / CQ;
+      cq = pair - gp * CQ;
+      hoff = min(gp, g_active - 1) * hstride * D;
+      prefetch();
     }
-    // the rest in rounds of RB independent loads (the same order of
-    // additions as one partial at a time)
-    constexpr int RB = 16;
+    // weighted sum over the Pg partials: thread (slice, g, column quad) adds
+    // partials q = slice, slice + nslice, ... with all its loads independent;
+    // the slices are then added in a fixed order (deterministic result)
+    const int g = gp;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (g < g_active) {
+      const float* wg = sh_w + g * Pg;
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        if (i * NSLICE < Pg) {
+          const int q = sl + i * NSLICE;
+          const float w = q < Pg ? wg[min(q, Pg - 1)] : 0.f;
+          acc.x = __builtin_fmaf(pf[i].x, w, acc.x);
+          acc.y = __builtin_fmaf(pf[i].y, w, acc.y);
+          acc.z = __builtin_fmaf(pf[i].z, w, acc.z);
+          acc.w = __builtin_fmaf(pf[i].w, w, acc.w);
+        }
+      }
+      // the rest in rounds of RB independent loads (the same order of
+      // additions as one partial at a time)
+      constexpr int RB = 16;
 #pragma unroll 1
-    for (int q0 = sl + PF * NSLICE; q0 < Pg; q0 += RB * NSLICE) {
-      float4 x[RB];
+      for (int q0 = sl + PF * NSLICE; q0 < Pg; q0 += RB * NSLICE) {
+        float4 x[RB];
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int q = q0 + i * NSLICE;
-        x[i] = ld4(q, q < Pg);
-      }
+        for (int i = 0; i < RB; ++i) {
+          const int q = q0 + i * NSLICE;
+          x[i] = ld4(q, q < Pg);
+        }
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        const int q = q0 + i * NSLICE;
-        const float w = q < Pg ? wg[q] : 0.f;
-        acc.x = __builtin_fmaf(x[i].x, w, acc.x);
-        acc.y = __builtin_fmaf(x[i].y, w, acc.y);
-        acc.z = __builtin_fmaf(x[i].z, w, acc.z);
-        acc.w = __builtin_fmaf(x[i].w, w, acc.w);
+        for (int i = 0; i < RB; ++i) {
+          const int q = q0 + i * NSLICE;
+          const float w = q < Pg ? wg[q] : 0.f;
+          acc.x = __builtin_fmaf(x[i].x, w, acc.x);
+          acc.y = __builtin_fmaf(x[i].y, w, acc.y);
+          acc.z = __builtin_fmaf(x[i].z, w, acc.z);
+          acc.w = __builtin_fmaf(x[i].w, w, acc.w);
+        }
       }
     }
-  }
-  sh_red[threadIdx.x] = acc;
-  __syncthreads();
-  if (threadIdx.x < NPAIR && g < g_active) {
-    auto add = [&](const float4 y) {
-      acc.x += y.x;
-      acc.y += y.y;
-      acc.z += y.z;
-      acc.w += y.w;
-    };
-    if constexpr (NSLICE > 32) {
-      // (head_dim 32, one head: 64 slices) rounds of 16 reads, the same
-      // order of additions; all 63 reads at once would take 252 registers
-      constexpr int RS = 16;
+    sh_red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x < NPAIR && g < g_active) {
+      auto add = [&](const float4 y) {
+        acc.x += y.x;
+        acc.y += y.y;
+        acc.z += y.z;
+        acc.w += y.w;
+      };
+      if constexpr (NSLICE > 32) {
+        // (head_dim 32, one head: 64 slices) rounds of 16 reads, the same
+        // order of additions; all 63 reads at once would take 252 registers
+        constexpr int RS = 16;
 #pragma unroll 1
-      for (int k0 = 1; k0 < NSLICE; k0 += RS) {
-        float4 y[RS];
+        for (int k0 = 1; k0 < NSLICE; k0 += RS) {
+          float4 y[RS];
 #pragma unroll
-        for (int j = 0; j < RS; ++j)
-          if (k0 + j < NSLICE) y[j] = sh_red[(k0 + j) * NPAIR + threadIdx.x];
+          for (int j = 0; j < RS; ++j)
+            if (k0 + j < NSLICE) y[j] = sh_red[(k0 + j) * NPAIR + threadIdx.x];
 #pragma unroll
-        for (int j = 0; j < RS; ++j)
-          if (k0 + j < NSLICE) add(y[j]);
+          for (int j = 0; j < RS; ++j)
+            if (k0 + j < NSLICE) add(y[j]);
+        }
+      } else {
+#pragma unroll
+        for (int k = 1; k < NSLICE; ++k) add(sh_red[k * NPAIR + threadIdx.x]);
       }
-    } else {
-#pragma unroll
-      for (int k = 1; k < NSLICE; ++k) add(sh_red[k * NPAIR + threadIdx.x]);
+      const float inv = sh_inv[g];
+      const int es = a.out_dtype == OC_F32 ? 4 : 2;
+      char* o = a.out + ((int64_t)row * a.G + g0 + g) * a.out_stride + (int64_t)(4 * cq) * es;
+      store_scalar(o, a.out_dtype, acc.x / inv);
+      store_scalar(o + es, a.out_dtype, acc.y / inv);
+      store_scalar(o + 2 * es, a.out_dtype, acc.z / inv);
+      store_scalar(o + 3 * es, a.out_dtype, acc.w / inv);
     }
-    const float inv = sh_inv[g];
-    const int es = a.out_dtype == OC_F32 ? 4 : 2;
-    char* o = a.out + ((int64_t)row * a.G + g0 + g) * a.out_stride + (int64_t)(4 * cq) * es;
-    store_scalar(o, a.out_dtype, acc.x / inv);
-    store_scalar(o + es, a.out_dtype, acc.y / inv);
-    store_scalar(o + 2 * es, a.out_dtype, acc.z / inv);
-    store_scalar(o + 3 * es, a.out_dtype, acc.w / inv);
   }
 }
 
@@ -3334,10 +3353,10 @@ inline void launch_decode_hd(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
 // head_dim 256: the matrix-core kernels only (the per-wave-prologue one,
 // or the general one: attend-every-tile or single-pass gate), 16-bit K/V
 // with q of K's type or fp8 K/V with bf16 q (bf16 V beside fp8 K in the
-// per-wave-prologue kernel), 4-wave workgroups, at most 4 query heads per
+// per-wave-prologue kernel), 4-wave workgroups, up to 8 query heads per
 // workgroup (the fused merge gives each of its 256 threads one column quad
-// of one head: more heads run as chunks of 4 on the general kernel); the
-// host routes every other head_dim-256 decode to the portable kernels
+// of one head per pass: two passes for 8 heads); the host routes every
+// other head_dim-256 decode to the portable kernels
 template <int DT>
 inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t st) {
   if constexpr (DT == OC_BF16 || DT == OC_F16 || DT == OC_FP8_E4M3FN) {
@@ -3349,7 +3368,8 @@ inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
       switch (gt) {
         case 1: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 1, PG, 4, VT>), grid, block, 0, st, a); break;
         case 2: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 2, PG, 4, VT>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, VT>), grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 4, PG, 4, VT>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((decode_fast_kernel<DT, 256, 8, PG, 4, VT>), grid, block, 0, st, a); break;
       }
     };
     auto go = [&](auto pg) {
@@ -3365,13 +3385,15 @@ inline void launch_decode256(const DecodeArgs& a, int gt, dim3 grid, hipStream_t
         switch (gt) {
           case 1: hipLaunchKernelGGL((decode_kernel<DT, 256, 1, true, PG, true, true>), grid, block, 0, st, a); break;
           case 2: hipLaunchKernelGGL((decode_kernel<DT, 256, 2, true, PG, true, true>), grid, block, 0, st, a); break;
-          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, true>), grid, block, 0, st, a); break;
+          case 4: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, true>), grid, block, 0, st, a); break;
+          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 8, true, PG, true, true>), grid, block, 0, st, a); break;
         }
       } else {
         switch (gt) {
           case 1: hipLaunchKernelGGL((decode_kernel<DT, 256, 1, true, PG, true, false>), grid, block, 0, st, a); break;
           case 2: hipLaunchKernelGGL((decode_kernel<DT, 256, 2, true, PG, true, false>), grid, block, 0, st, a); break;
-          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, false>), grid, block, 0, st, a); break;
+          case 4: hipLaunchKernelGGL((decode_kernel<DT, 256, 4, true, PG, true, false>), grid, block, 0, st, a); break;
+          default: hipLaunchKernelGGL((decode_kernel<DT, 256, 8, true, PG, true, false>), grid, block, 0, st, a); break;
         }
       }
     };

@@ -282,10 +282,10 @@ def test_head_dim_32_and_256_routes():
         assert groups(params(d, q=(1 << 22) + 2)) == 40, d                    # q rows not 16-byte pieces
     assert groups(params(32, kv_dtype=N.OC_FP8_E4M3FN)) == 40                # fp8 K: portable at 32
     assert groups(params(256, kv_dtype=N.OC_FP8_E4M3FN)) < 40                # (matrix cores at 256)
-    # head_dim 256 with G > 4: the general matrix-core kernel in chunks of 4
+    # head_dim 256 with G > 8: the general matrix-core kernel in chunks of 8
     # heads, except bf16 V beside fp8 K (per-wave-prologue kernel only)
-    assert groups(params(256, G=8, q_row_stride=256)) < 40
-    assert groups(params(256, G=8, kv_dtype=N.OC_FP8_E4M3FN, kv_v_dtype=N.OC_BF16)) == 40
-    assert groups(params(256, G=4, kv_dtype=N.OC_FP8_E4M3FN, kv_v_dtype=N.OC_BF16)) < 40
+    assert groups(params(256, G=8)) < 40 and groups(params(256, G=12)) < 40
+    assert groups(params(256, G=8, kv_dtype=N.OC_FP8_E4M3FN, kv_v_dtype=N.OC_BF16)) < 40
+    assert groups(params(256, G=12, kv_dtype=N.OC_FP8_E4M3FN, kv_v_dtype=N.OC_BF16)) == 40
     assert groups(params(32, kv_tile_size=32, kv_num_tiles=320, score_row_stride=320)) == 40
     assert groups(params(16)) == 40 and groups(params(512)) == 40            # portable head dims

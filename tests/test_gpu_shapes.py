@@ -375,16 +375,17 @@ def _cs_tau(qd, kd, noise, G):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 6, 8, 12])
 @pytest.mark.parametrize("gate", ["cs", "zeta", "mask", "none", "cs_single_pass", "zeta_single_pass"])
 def test_head_dim_256_tuned_kernel(dt, G, gate):
     """head_dim 256, 64-token tiles, 16-bit K/V with q of K's type, on the
     matrix-core kernels (4-wave workgroups, one wave per SIMD): the cached
     score- or mask-gated decode and the dense decode on the per-wave-prologue
-    kernel (a workgroup takes several splits: splits_per_group = 2), the
-    single-pass gates on the general one, and G = 6, 8 on the general one in
-    two chunks of up to 4 heads; against the oracle, and against the same
-    decode forced onto the portable kernels."""
+    kernel (a workgroup takes several splits: splits_per_group = 2; G = 6, 8
+    merged in two passes of 4 heads), the single-pass gates on the general
+    one, and G = 12 on the general one in two chunks of up to 8 heads;
+    against the oracle, and against the same decode forced onto the portable
+    kernels."""
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
     rows, T = 3, 12
@@ -596,8 +597,9 @@ def test_head_dim_256_fp8_tile_scales_tuned(G, mode):
     assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned fp8 tile scales G={G} {mode}")
 
 
+@pytest.mark.parametrize("G", [4, 8])
 @pytest.mark.parametrize("mode", ["cached", "dense"])
-def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
+def test_head_dim_256_paged_fp8k_bf16v_tuned(G, mode):
     """head_dim 256 paged fp8 K beside a bf16 V with a scalar k_scale (the
     reference's paged fp8 cache, paged_eviction.py:354-357): K widened in the
     kernel as bf16(float(fp8) * k_scale), V read as bf16, rows of different
@@ -605,7 +607,7 @@ def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
     from orthocache_gpu.workloads import paged_pool
-    B, hkv, G, T, d = 3, 2, 4, 10, 256
+    B, hkv, T, d = 3, 2, 10, 256
     k, noise = mixed(B * hkv, T, d, 64, seed=901)
     g = torch.Generator().manual_seed(902)
     v = torch.randn(B * hkv, T * 64, d, generator=g).to(torch.bfloat16)
@@ -629,7 +631,7 @@ def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
     e_low, e_high, _, _ = X.score_tiles(kv)
     ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_CS
     nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
-    print(f"head_dim 256 paged fp8 K + bf16 V {mode}", flush=True)
+    print(f"head_dim 256 paged fp8 K + bf16 V G={G} {mode}", flush=True)
     r = X.decode(kv, q.to(DEV), G, gate=ng, threshold=tau, mode=nm, scores=(e_low, e_high),
                  out_dtype=torch.float32, want_keep=mode != "dense")
     torch.cuda.synchronize()
@@ -638,7 +640,7 @@ def test_head_dim_256_paged_fp8k_bf16v_tuned(mode):
         for row in range(B * hkv):
             nt = -(-row_lens[row] // 64)
             assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
-    assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned paged fp8 K + bf16 V {mode}")
+    assert_out(r.out, ref["out"], "fp8", f"head_dim 256 tuned paged fp8 K + bf16 V G={G} {mode}")
 
 
 # ------------------------------------------------ head_dim 32, tuned kernels
