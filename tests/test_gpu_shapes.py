@@ -435,17 +435,20 @@ def test_head_dim_256_tuned_kernel(dt, G, gate):
     assert np.max(np.abs(outs[0] - outs[1])) <= {"bf16": 1.6e-2, "f16": 2e-3}[dt]
 
 
-def test_head_dim_256_routing_and_full_row():
+@pytest.mark.parametrize("G", [4, 8])
+def test_head_dim_256_routing_and_full_row(G):
     """With the automatic split grouping, head_dim 256 bf16 cached and dense
     decodes take several splits per workgroup (the tuned kernel's grouping:
     fewer partials than splits) while the same call forced portable keeps one
     split per workgroup; the tuned kernel's output on 8 rows x 10240 tokens
-    (160 tiles, P = 40) matches the oracle, both modes."""
+    (160 tiles, P = 40) matches the oracle, both modes, and with one split
+    per tile and per workgroup (160 partials per row in the fused merge,
+    two passes of 4 heads at G = 8)."""
     import ctypes
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
-    rows, T, G = 8, 160, 4
-    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=2560)
+    rows, T = 8, 160
+    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=2560 + G)
     kv = X.rows_layout(kd, vd)
     tau = _cs_tau(qd, kd, noise, G)
     e_low, e_high, _, _ = X.score_tiles(kv)
@@ -462,15 +465,17 @@ def test_head_dim_256_routing_and_full_row():
         groups[portable] = lib.oc_decode_num_groups(ctypes.byref(p))
     assert groups[1] == P and groups[0] < P, (P, groups)
     q32, k32, v32 = np32(qd), np32(kd), np32(vd)
-    for gate, ng, mode in (("cs", N.OC_GATE_CS, N.OC_MODE_CACHED), ("none", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS)):
+    for gate, ng, mode, ns, spg in (("cs", N.OC_GATE_CS, N.OC_MODE_CACHED, P, 0),
+                                    ("none", N.OC_GATE_NONE, N.OC_MODE_SINGLE_PASS, P, 0),
+                                    ("cs", N.OC_GATE_CS, N.OC_MODE_CACHED, T, 1)):
         ref = O.decode_rows(q32, k32, v32, gate=gate, threshold=tau, G=G)
-        print(f"head_dim 256 full row {gate}", flush=True)
-        r = X.decode(kv, qd, G, gate=ng, threshold=tau, mode=mode, scores=(e_low, e_high), num_splits=P,
-                     out_dtype=torch.bfloat16, want_keep=gate == "cs")
+        print(f"head_dim 256 full row G={G} {gate} P={ns} spg={spg}", flush=True)
+        r = X.decode(kv, qd, G, gate=ng, threshold=tau, mode=mode, scores=(e_low, e_high), num_splits=ns,
+                     splits_per_group=spg, out_dtype=torch.bfloat16, want_keep=gate == "cs")
         torch.cuda.synchronize()
         if gate == "cs":
             assert np.array_equal(r.keep.cpu().numpy().astype(bool), ref["keep"])
-        assert_out(r.out, ref["out"], "bf16", f"head_dim 256 tuned full row {gate}")
+        assert_out(r.out, ref["out"], "bf16", f"head_dim 256 tuned full row G={G} {gate} P={ns} spg={spg}")
 
 
 def test_head_dim_256_partials_single_pass():
