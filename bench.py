@@ -615,21 +615,23 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
     prologue one, the single pass on the general one); "d256_fp8": the same
     with fp8-e4m3 K/V and one scale per (row, tile); "d256_portable": every
     variant forced onto the portable kernels; the same at head_dim 128 forced
-    portable next to the tuned kernels, and at head_dim 32 ("d32": the
-    matrix-core kernels of head_dim 64 / 128, "d32_portable").  Buffer sets
-    rotate past the Infinity Cache."""
+    portable next to the tuned kernels, at head_dim 32 ("d32": the
+    matrix-core kernels of head_dim 64 / 128, "d32_portable"), and head_dim
+    256 with G = 8 ("d256_g8", "d256_g8_portable").  Buffer sets rotate past
+    the Infinity Cache."""
     import torch
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
     from orthocache_gpu.triton_kernels.fwht_fused_prototype import score_tiles
     from orthocache_gpu.workloads import calibrate_tau, make_kv, make_q
     dev = torch.device("cuda", 0)
-    rows, g = 8, 4
+    rows = 8
     lib, stream = N.lib(), X.current_stream(dev)
-    r = {"workload": f"{rows} kv rows x {seq_len} tokens, G={g}, bf16 q, bf16 K/V (d256_fp8: fp8-e4m3 K/V with "
-                     f"one scale per (row, tile)), 50% noise tiles, Cauchy-Schwarz gate"}
-    for d, portable, f8 in ((head_dim, 0, False), (head_dim, 0, True), (head_dim, 1, False), (128, 1, False),
-                            (128, 0, False), (32, 0, False), (32, 1, False)):
+    r = {"workload": f"{rows} kv rows x {seq_len} tokens, G=4 (the _g8 keys: G=8), bf16 q, bf16 K/V (d256_fp8: "
+                     f"fp8-e4m3 K/V with one scale per (row, tile)), 50% noise tiles, Cauchy-Schwarz gate"}
+    for d, portable, f8, g in ((head_dim, 0, False, 4), (head_dim, 0, True, 4), (head_dim, 1, False, 4),
+                               (128, 1, False, 4), (128, 0, False, 4), (32, 0, False, 4), (32, 1, False, 4),
+                               (head_dim, 0, False, 8), (head_dim, 1, False, 8)):
         es = 1 if f8 else 2
         set_bytes = rows * seq_len * d * es * 2
         nsets = max(2, math.ceil(3 * MALL_BYTES / set_bytes))
@@ -663,7 +665,8 @@ def portable_measure(steps, warmup, head_dim=256, seq_len=32768, seed=900):
         kept = tiles // 2
         nbytes = {"cached": 2 * kept * tile + tiles * 4, "single_pass": tiles * tile + kept * tile,
                   "dense": 2 * tiles * tile}
-        key = f"d{d}" + ("_fp8" if f8 else "") + ("_portable" if portable else ("_tuned" if d in (64, 128) else ""))
+        key = (f"d{d}" + ("_fp8" if f8 else "") + ("_g8" if g == 8 else "")
+               + ("_portable" if portable else ("_tuned" if d in (64, 128) else "")))
         r[key] = {}
         for name, plist in params.items():
             run = lambda i, plist=plist: N.check("oc_decode", lib.oc_decode(ctypes.byref(plist[i % nsets]),
