@@ -91,12 +91,12 @@ class GPUProfile:
 # float16, half the tiles evicted) stops losing to this build's own dense
 # decode on MI355X.  It is a band, not a point: in the config1_sweep of the
 # default bench.py line on fresh boxes (reference config 1) the single pass
-# is at 0.93-0.99x dense at 1024 tokens, 0.98-1.05x at 2048, 0.97-1.06x at
-# 4096 and 1.03-1.08x at 8192 (1.21x at 32768): between 2048 and 8192 the two
-# are within a few percent, box to box.  The bypass takes the band's lower
-# end, 2048, below which dense is faster on every run.  The cached-score
-# decode is ahead from 1024 tokens on (1.27x at 1024, 1.32x at 2048, 1.4x
-# at 4096, 1.83x at 32768).
+# is at 0.93-0.99x dense at 1024 tokens, 0.98-1.05x at 2048, 0.93-1.06x at
+# 4096 and 1.00-1.08x at 8192 (1.15-1.21x at 32768): between 2048 and 8192
+# the two are within a few percent, box to box.  The bypass takes the band's
+# lower end, 2048, below which dense is faster on every run.  The
+# cached-score decode is ahead from 1024 tokens on (1.27x at 1024, 1.32x at
+# 2048, 1.4x at 4096, 1.77-1.83x at 32768).
 MI355X_CROSSOVER = 2048
 MI355X_CROSSOVER_BAND = (2048, 8192)
 MI355X_PEAK_GBPS = 8000.0
