@@ -2650,51 +2650,57 @@ __device__ __forceinline__ void merge_if_last(const DecodeArgs& a, int row, int 
   if (Pg <= kMergeFew) {
     // few partials (a uniform test): one thread per (head, column quad)
     // pair requests every partial's m, l and quad at once and forms the
-    // output itself (no LDS weights, wave reductions or slice sums)
+    // output itself (no LDS weights, wave reductions or slice sums); N load
+    // slots, 4 when they hold every partial
+    auto few = [&](auto n_tag) {
+      constexpr int N = decltype(n_tag)::value;
 #pragma unroll
-    for (int p0 = 0; p0 < GT * CQ; p0 += kDT) {
-      const int pr0 = p0 + (int)threadIdx.x;
-      const int hg = pr0 / CQ;
-      const int hq = pr0 - hg * CQ;
-      if (pr0 < GT * CQ && hg < g_active) {
-        const int64_t base = pbase + (int64_t)(g0 + hg) * hstride;
-        float mq[kMergeFew], lq[kMergeFew];
-        float4 xq[kMergeFew];
+      for (int p0 = 0; p0 < GT * CQ; p0 += kDT) {
+        const int pr0 = p0 + (int)threadIdx.x;
+        const int hg = pr0 / CQ;
+        const int hq = pr0 - hg * CQ;
+        if (pr0 < GT * CQ && hg < g_active) {
+          const int64_t base = pbase + (int64_t)(g0 + hg) * hstride;
+          float mq[N], lq[N];
+          float4 xq[N];
 #pragma unroll
-        for (int q = 0; q < kMergeFew; ++q) {
-          const bool ok = q < Pg;
-          mq[q] = ok ? ldc(a.pm + base + q * qstride) : -__builtin_inff();
-          lq[q] = ok ? ldc(a.pl + base + q * qstride) : 0.f;
-          const int off = ok ? ((hg * hstride + q * qstride) * D + 4 * hq) * (int)sizeof(float) : 0x7ffffff0;
-          const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 16 /* sc1 */);
-          xq[q] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
-                              __uint_as_float(x[3]));
-        }
-        float mx = mq[0];
-#pragma unroll
-        for (int q = 1; q < kMergeFew; ++q) mx = fmaxf(mx, mq[q]);
-        float ls = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int q = 0; q < kMergeFew; ++q) {
-          if (q < Pg) {
-            const float w = __expf(mq[q] - mx);
-            ls = __builtin_fmaf(w, lq[q], ls);
-            acc.x = __builtin_fmaf(xq[q].x, w, acc.x);
-            acc.y = __builtin_fmaf(xq[q].y, w, acc.y);
-            acc.z = __builtin_fmaf(xq[q].z, w, acc.z);
-            acc.w = __builtin_fmaf(xq[q].w, w, acc.w);
+          for (int q = 0; q < N; ++q) {
+            const bool ok = q < Pg;
+            mq[q] = ok ? ldc(a.pm + base + q * qstride) : -__builtin_inff();
+            lq[q] = ok ? ldc(a.pl + base + q * qstride) : 0.f;
+            const int off = ok ? ((hg * hstride + q * qstride) * D + 4 * hq) * (int)sizeof(float) : 0x7ffffff0;
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 16 /* sc1 */);
+            xq[q] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                                __uint_as_float(x[3]));
           }
+          float mx = mq[0];
+#pragma unroll
+          for (int q = 1; q < N; ++q) mx = fmaxf(mx, mq[q]);
+          float ls = 0.f;
+          float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int q = 0; q < N; ++q) {
+            if (q < Pg) {
+              const float w = __expf(mq[q] - mx);
+              ls = __builtin_fmaf(w, lq[q], ls);
+              acc.x = __builtin_fmaf(xq[q].x, w, acc.x);
+              acc.y = __builtin_fmaf(xq[q].y, w, acc.y);
+              acc.z = __builtin_fmaf(xq[q].z, w, acc.z);
+              acc.w = __builtin_fmaf(xq[q].w, w, acc.w);
+            }
+          }
+          const float inv = fmaxf(ls, 1e-9f);
+          const int es = a.out_dtype == OC_F32 ? 4 : 2;
+          char* o = a.out + ((int64_t)row * a.G + g0 + hg) * a.out_stride + (int64_t)(4 * hq) * es;
+          store_scalar(o, a.out_dtype, acc.x / inv);
+          store_scalar(o + es, a.out_dtype, acc.y / inv);
+          store_scalar(o + 2 * es, a.out_dtype, acc.z / inv);
+          store_scalar(o + 3 * es, a.out_dtype, acc.w / inv);
         }
-        const float inv = fmaxf(ls, 1e-9f);
-        const int es = a.out_dtype == OC_F32 ? 4 : 2;
-        char* o = a.out + ((int64_t)row * a.G + g0 + hg) * a.out_stride + (int64_t)(4 * hq) * es;
-        store_scalar(o, a.out_dtype, acc.x / inv);
-        store_scalar(o + es, a.out_dtype, acc.y / inv);
-        store_scalar(o + 2 * es, a.out_dtype, acc.z / inv);
-        store_scalar(o + 3 * es, a.out_dtype, acc.w / inv);
       }
-    }
+    };
+    if (Pg <= 4) few(std::integral_constant<int, 4>{});
+    else few(std::integral_constant<int, kMergeFew>{});
     return;
   }
   static_assert(GT <= 2 * kDW, "a wave merges at most two heads");
