@@ -478,17 +478,19 @@ def test_head_dim_256_routing_and_full_row(G):
         assert_out(r.out, ref["out"], "bf16", f"head_dim 256 tuned full row G={G} {gate} P={ns} spg={spg}")
 
 
-def test_head_dim_256_partials_single_pass():
+@pytest.mark.parametrize("G", [4, 8])
+def test_head_dim_256_partials_single_pass(G):
     """return_partials at head_dim 256 (one workgroup per logical split, the
-    general matrix-core kernel, single-pass CS gate): every split's (m, l,
-    acc) against the oracle's, and the merged output."""
+    general matrix-core kernel, single-pass CS gate; 8 heads in one
+    workgroup): every split's (m, l, acc) against the oracle's, and the
+    merged output."""
     from orthocache_gpu import _launch as X
     from orthocache_gpu import _native as N
-    rows, T, G = 2, 9, 4
-    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=99)
+    rows, T = 2, 9
+    kd, vd, qd, noise = _d256_case(rows, T, G, "bf16", seed=99 + G)
     kv = X.rows_layout(kd, vd)
     tau = _cs_tau(qd, kd, noise, G)
-    print("head_dim 256 partials", flush=True)
+    print(f"head_dim 256 partials G={G}", flush=True)
     res = X.decode(kv, qd, G, gate=N.OC_GATE_CS, threshold=tau, num_splits=4, out_dtype=torch.float32,
                    want_partials=True, want_keep=True)
     torch.cuda.synchronize()
