@@ -840,3 +840,50 @@ def test_head_dim_32_paged_tuned(bs, mode):
             nt = -(-row_lens[row] // 64)
             assert np.array_equal(keep[row, :nt], ref["keep"][row, :nt]), row
     assert_out(r.out, ref["out"], "f32", f"head_dim 32 tuned paged bs={bs} {mode}")
+
+
+@pytest.mark.parametrize("scale", ["q_fold", "tile"])
+@pytest.mark.parametrize("mode", ["cached", "single_pass", "dense"])
+def test_head_dim_32_scale_modes(scale, mode):
+    """head_dim 32 bf16 on the matrix-core kernels with a scalar k_scale folded
+    into q (the reference's semantics) or per-(row, tile) K and V scales: keep
+    flags and outputs equal, to the output's rounding, to the same call on the
+    portable kernels; the tile-scale outputs also against the oracle on the
+    scaled values (the zeta gate, whose ratio the tile scales leave as it is)."""
+    from orthocache_gpu import _launch as X
+    from orthocache_gpu import _native as N
+    rows, T, G, d = 3, 12, 4, 32
+    k, noise = mixed(rows, T, d, 64, seed=3200 + len(mode) + len(scale))
+    g = torch.Generator().manual_seed(3201)
+    v = torch.randn(rows, T * 64, d, generator=g)
+    q = torch.randn(rows * G, d, generator=g)
+    kd, vd, qd = (x.to(torch.bfloat16).to(DEV) for x in (k, v, q))
+    kv = X.rows_layout(kd, vd)
+    ks = vs = None
+    if scale == "tile":
+        ks = 0.5 + torch.rand(rows, T, generator=g)
+        vs = 0.5 + torch.rand(rows, T, generator=g)
+        kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(ks.to(DEV), rows, T, DEV)
+        kv.v_scale_mode, kv.v_scales = X.vscale_mode(vs.to(DEV), rows, T, DEV)
+    else:
+        kv.k_scale_mode, kv.k_scale, kv.k_scales = X.kscale_mode(1.25, rows, T, DEV)
+    e_low, e_high, _, _ = X.score_tiles(kv)
+    ng = N.OC_GATE_NONE if mode == "dense" else N.OC_GATE_ZETA
+    nm = N.OC_MODE_CACHED if mode == "cached" else N.OC_MODE_SINGLE_PASS
+    outs, keeps = {}, {}
+    for portable in (0, 1):
+        print(f"head_dim 32 {scale} {mode} portable={portable}", flush=True)
+        r = X.decode(kv, qd, G, gate=ng, threshold=5.0, mode=nm, scores=(e_low, e_high), num_splits=4,
+                     splits_per_group=2, out_dtype=torch.float32, want_keep=mode != "dense", portable=portable)
+        torch.cuda.synchronize()
+        outs[portable] = np32(r.out)
+        if mode != "dense":
+            keeps[portable] = r.keep.cpu().numpy().astype(bool)
+    if mode != "dense":
+        assert np.array_equal(keeps[0], keeps[1])
+        assert np.array_equal(keeps[0], ~noise.numpy())
+    assert np.max(np.abs(outs[0] - outs[1])) <= 2e-3, scale
+    if scale == "tile":
+        ref = O.decode_rows(np32(qd), np32(kd), np32(vd), gate="none" if mode == "dense" else "zeta", threshold=5.0,
+                            G=G, k_scales=ks.numpy(), v_scales=vs.numpy())
+        assert_out(outs[0], ref["out"], "f32", f"head_dim 32 tuned tile scales {mode}")
